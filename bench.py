@@ -1,0 +1,368 @@
+"""Benchmark of the MI355X kernel path on the BASELINE.json configs.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME|all]
+
+Prints ONE JSON line. The headline (metric/value) is the workload named by --workload; with
+"all" (default) it is the dense GEMM 4096^3 and every other config is
+reported in "configs". A step is one pass of the config's kernel(s) over one batch of synthetic
+input already resident in HBM. For working sets that fit the 256 MB Infinity Cache, steps rotate
+over enough input copies (> 512 MiB in total) that no step reads another step's data from cache.
+
+roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch duration, the duration
+measured with HIP events recorded on the stream the kernels run on (torch's current stream),
+each launch preceded by a 512 MiB cache flush. cpu_baseline = the oracle (restated reference
+torch path) on a bounded sample, timed on this host's cores.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tilelang-tpu_amd"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0}  # dense TFLOP/s (AMD spec)
+FLUSH_BYTES = 512 << 20
+CACHE_EVICT_BYTES = 512 << 20
+
+METRIC = "TFLOP/s (% MFMA peak) GEMM/FA/FP8-MLA; GB/s (% HBM peak) norm/rope/swiglu"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------------------------------------
+# timing helpers
+
+
+def _copies_for(nbytes):
+    return max(1, math.ceil(CACHE_EVICT_BYTES / max(nbytes, 1)))
+
+
+def time_steps(fns, steps, warmup):
+    """Run fns[i % len] warmup times then steps times; return ms per step (device-synchronised)."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_launches(fn, reps, flush):
+    """Mean duration (ms) of single launches of fn, HIP events on the current stream, cache
+    flushed before each launch."""
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    fn()
+    torch.cuda.synchronize()
+    for i in range(reps):
+        flush.zero_()
+        st[i].record()
+        fn()
+        en[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in zip(st, en))
+    return sum(ts) / len(ts), ts[len(ts) // 2]
+
+
+def cpu_time(fn, reps=3):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def roofline(bound, achieved, unit, peak, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ------------------------------------------------------------------------------------------------
+# configs
+
+
+def bench_rmsnorm(args, dev, flush, cpu):
+    import tilelang
+    from tilelang.testing import programs, workloads
+    w = workloads.rmsnorm(4096, 4096)
+    k = tilelang.compile(programs.rms_norm(4096, 4096, 1, "float16", eps=1e-6, with_weight=True),
+                         out_idx=-1, target="mi355x")
+    nbytes = 2 * 4096 * 4096 * 2 + 4096 * 2
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        x = w.tensors["x"].to(dev)
+        wt = w.tensors["w"].to(dev)
+        y = torch.empty_like(x)
+        sets.append((x, wt, y))
+    fns = [lambda s=s: k(*s) for s in sets]
+    ms = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns[0], 50, flush)
+    res = {"workload": "rmsnorm_fp16_4096x4096", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms, "dtype": "f16",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        xs, ws = w.tensors["x"], w.tensors["w"]
+        t = cpu_time(lambda: ref.rmsnorm_ref(xs, ws, 1e-6))
+        res["cpu_baseline"] = {"value": nbytes / t / 1e9, "unit": "GB/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "full 4096x4096 config, oracle.ref.rmsnorm_ref"}
+    return res
+
+
+def bench_swiglu(args, dev, flush, cpu):
+    import tilelang
+    from tilelang.testing import programs, workloads
+    rows, cols = 8192, 14336
+    w = workloads.swiglu(rows, cols)
+    k = tilelang.compile(programs.swi_glu(32, 32, rows, cols), out_idx=-1)
+    nbytes = 3 * rows * cols * 2
+    g, u = w.tensors["gate"].to(dev), w.tensors["up"].to(dev)
+    o = torch.empty_like(g)
+    fns = [lambda: k(g, u, o)]
+    ms = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns[0], 30, flush)
+    res = {"workload": "swiglu_bf16_8192x14336", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms, "dtype": "bf16",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        gs, us = w.tensors["gate"][:1024], w.tensors["up"][:1024]
+        t = cpu_time(lambda: ref.swiglu_ref(gs, us))
+        sb = 3 * gs.numel() * 2
+        res["cpu_baseline"] = {"value": sb / t / 1e9, "unit": "GB/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "first 1024 of 8192 rows, oracle.ref.swiglu_ref"}
+    return res
+
+
+def bench_rope(args, dev, flush, cpu):
+    import tilelang
+    from tilelang.testing import programs, workloads
+    T_, H, D = 8192, 32, 128
+    w = workloads.rope(T_, H, D)
+    k = tilelang.compile(programs.rope_qk(T_, H, H, D), out_idx=[4, 5])
+    nbytes = 4 * T_ * H * D * 2 + 2 * T_ * D * 2
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        t = {n: w.tensors[n].to(dev) for n in ("q", "k", "cos", "sin")}
+        sets.append((t["q"], t["k"], t["cos"], t["sin"], torch.empty_like(t["q"]),
+                     torch.empty_like(t["k"])))
+    fns = [lambda s=s: k(*s) for s in sets]
+    ms = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns[0], 50, flush)
+    res = {"workload": "rope_qk_bf16_8192x32x128", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms, "dtype": "bf16",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        q, kk, c, s = (w.tensors[n][:1024] for n in ("q", "k", "cos", "sin"))
+        t = cpu_time(lambda: (ref.rope_ref(q, c, s), ref.rope_ref(kk, c, s)))
+        sb = 4 * q.numel() * 2 + 2 * c.numel() * 2
+        res["cpu_baseline"] = {"value": sb / t / 1e9, "unit": "GB/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "first 1024 of 8192 tokens, oracle.ref.rope_ref on q,k"}
+    return res
+
+
+def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float16):
+    import tilelang
+    from tilelang.testing import programs, workloads
+    w = workloads.gemm(M, N, K, dtype=dtype)
+    dn = "float16" if dtype == torch.float16 else "bfloat16"
+    k = tilelang.compile(programs.matmul(M, N, K, 128, 128, 64, dn, "float16"), out_idx=-1)
+    flops = 2 * M * N * K
+    nbytes = 2 * (M * K + K * N + M * N)
+    a, b = w.tensors["a"].to(dev), w.tensors["b"].to(dev)
+    c = torch.empty(M, N, dtype=torch.float16, device=dev)
+    fns = [lambda: k(a, b, c)]
+    ms = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns[0], 30, flush)
+    skinny = M <= 64
+    if skinny:
+        rl = roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS)
+    else:
+        rl = roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s", MFMA_PEAK["fp16"])
+    res = {"workload": f"gemm_{dn}_{M}x{N}x{K}", "value": flops / (ms * 1e-3) / 1e12,
+           "unit": "TFLOP/s", "ms_per_step": ms, "dtype": "f16" if dn == "float16" else "bf16",
+           "roofline": rl, "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        rows = min(M, 512)
+        a_s, b_s = w.tensors["a"][:rows], w.tensors["b"]
+        t = cpu_time(lambda: ref.matmul_ref(a_s, b_s), reps=1)
+        res["cpu_baseline"] = {"value": 2 * rows * N * K / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"first {rows} rows of A, oracle.ref.matmul_ref (fp32 "
+                                         f"accumulate)"}
+    return res
+
+
+def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
+    import tilelang
+    from tilelang.testing import programs, workloads
+    B, H, D = 8, 32, 128
+    w = workloads.flashattn(B, S, H, D, causal=causal)
+    k = tilelang.compile(programs.flashattn(B, H, S, D, causal), out_idx=-1)
+    flops = 4 * B * H * S * S * D * (0.5 if causal else 1.0)
+    q, kk, v = (w.tensors[n].to(dev) for n in ("q", "k", "v"))
+    o = torch.empty_like(q)
+    fns = [lambda: k(q, kk, v, o)]
+    ms = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns[0], 10, flush)
+    res = {"workload": f"flashattn_bf16_b{B}h{H}s{S}d{D}_{'causal' if causal else 'full'}",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "dtype": "bf16",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["bf16"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_flops": flops}
+    if cpu:
+        from oracle import ref
+        t = cpu_time(lambda: ref.flashattn_ref(w.tensors["q"], w.tensors["k"], w.tensors["v"],
+                                               causal, batches=[0], heads=[0, 1]), reps=1)
+        sf = flops / (B * H) * 2
+        res["cpu_baseline"] = {"value": sf / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "batch 0, heads 0-1, oracle.ref.flashattn_ref"}
+    return res
+
+
+def bench_mla(args, dev, flush, cpu):
+    from tilelang.jit.adapter.mi355x import ops
+    from tilelang.testing import workloads
+    w = workloads.mla()
+    a = w.attrs
+    B, Hq, dv, dpe = a["B"], a["Hq"], a["dv"], a["dpe"]
+    sum_l = int(w.tensors["seqlens"].sum())
+    nbytes = sum_l * (dv + dpe) + B * Hq * (dv + dpe) * 2 + B * Hq * dv * 2 + \
+        w.tensors["block_table"].numel() * 4 + B * 4
+    flops = sum_l * Hq * (dv + dpe + dv) * 2
+    num_split = args.mla_splits
+    t = {n: x.to(dev) for n, x in w.tensors.items()}
+    out = torch.empty(B, Hq, dv, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(ops.mla_workspace_bytes(B, Hq, dv, num_split), dtype=torch.uint8,
+                     device=dev)
+    q, kv = t["q"], t["kv"]
+
+    def run():
+        ops.mla_decode(q[..., :dv], q[..., dv:], kv[:, :dv], kv[:, dv:], t["block_table"],
+                       t["seqlens"], out, ws, a["page"], num_split, a["sm_scale"], t["kv_scale"])
+
+    ms = time_steps([run], args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(run, 50, flush)
+    res = {"workload": "mla_decode_fp8_b64_h128_d576", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms, "dtype": "fp8e4m3-kv/bf16-q",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "tflops": flops / (mean_ms * 1e-3) / 1e12, "kernel_ms_mean": mean_ms,
+           "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes, "sum_seqlens": sum_l,
+           "num_split": num_split}
+    if cpu:
+        from oracle import ref
+        nb = 4
+        t0 = cpu_time(lambda: ref.mla_decode_ref(
+            w.tensors["q"][:nb, :, :dv], w.tensors["q"][:nb, :, dv:], w.tensors["kv"][:, :dv],
+            w.tensors["kv"][:, dv:], w.tensors["block_table"], w.tensors["seqlens"][:nb],
+            a["page"], a["sm_scale"], float(w.tensors["kv_scale"])), reps=1)
+        sl = int(w.tensors["seqlens"][:nb].sum())
+        sb = sl * (dv + dpe) + nb * Hq * (dv + dpe) * 2 + nb * Hq * dv * 2
+        res["cpu_baseline"] = {"value": sb / t0 / 1e9, "unit": "GB/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"first {nb} of {B} sequences ({sl} tokens), "
+                                         f"oracle.ref.mla_decode_ref"}
+    return res
+
+
+BENCHES = {
+    "gemm": bench_gemm,
+    "gemm_skinny": lambda a, d, f, c: bench_gemm(a, d, f, c, M=16, N=14336, K=4096),
+    "rmsnorm": bench_rmsnorm,
+    "rope": bench_rope,
+    "swiglu": bench_swiglu,
+    "flashattn": bench_flashattn,
+    "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
+    "mla": bench_mla,
+}
+ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
+         "mla"]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="all", choices=["all"] + ORDER)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--mla-splits", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only (every kernel here is a "
+                                   "single-GPU kernel); run with --gpus 1"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    torch.set_num_threads(os.cpu_count() or 1)
+    flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+    names = ORDER if args.workload == "all" else [args.workload]
+    results = {}
+    for n in names:
+        log(f"[bench] {n} ...")
+        try:
+            results[n] = BENCHES[n](args, dev, flush, not args.no_cpu)
+            log(f"[bench] {n}: {results[n]['value']:.1f} {results[n]['unit']} "
+                f"(roofline {results[n]['roofline']['frac'] * 100:.1f}%)")
+        except Exception as e:  # a family without a kernel yet is reported, not fatal
+            results[n] = {"workload": n, "error": f"{type(e).__name__}: {e}"}
+            log(f"[bench] {n}: ERROR {e}")
+        torch.cuda.empty_cache()
+    head_name = "gemm" if args.workload == "all" else args.workload
+    head = results.get(head_name, {})
+    if "error" in head:
+        ok = [n for n in names if "error" not in results[n]]
+        head_name = ok[0] if ok else head_name
+        head = results.get(head_name, {})
+    line = {
+        "metric": METRIC,
+        "value": head.get("value"),
+        "unit": head.get("unit"),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head.get("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head.get("dtype"),
+        "data": "synthetic (seed 0, BASELINE.json configs)",
+        "config": {"workload": head.get("workload", head_name), "device": torch.cuda.get_device_name(dev)},
+        "roofline": head.get("roofline"),
+        "cpu_baseline": head.get("cpu_baseline"),
+        "configs": [results[n] for n in names],
+        "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,144 @@
+/*
+ * tlmi355x.h — C ABI of libtlmi355x.so, the gfx950 (MI355X) kernels that sit behind
+ * `tilelang.compile(..., target="mi355x")`.
+ *
+ * The reference crosses its process/device boundary through one generated entry point,
+ *   extern "C" int tilelang_tpu_run(void** args)
+ * (reference: src/tl_templates/tpu/main_template.cpp:39, bound by ctypes at
+ *  tilelang/jit/adapter/cython/adapter.py:214-216 with argtypes=[POINTER(c_void_p)],
+ *  restype=c_int), which is regenerated per kernel from templates
+ * (tilelang/jit/adapter/wrapper.py:617-834). This library replaces that per-kernel
+ * codegen with one fixed entry point per operator family. The Python adapter binds
+ * these with ctypes exactly as the reference binds tilelang_tpu_run.
+ *
+ * Conventions (all entry points):
+ *  - every pointer is a DEVICE pointer owned by the caller (torch allocates); the
+ *    library allocates nothing on the hot path (MLA takes its workspace from the caller);
+ *  - tensors are dense, row-major (C-contiguous) unless a stride argument says otherwise;
+ *  - return 0 on success or a negative TLM_E* code; the message is available from
+ *    tlm_last_error() (thread-local). Nothing aborts or prints;
+ *  - argument validation runs BEFORE any HIP call, so every error path is testable on a
+ *    host without a GPU;
+ *  - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream), NULL = default;
+ *  - calls are reentrant; per-device state is initialised once (std::call_once).
+ */
+#ifndef TLMI355X_H
+#define TLMI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. Mirrors the reference's dtype table for generated wrappers
+ * (tilelang/jit/adapter/wrapper.py:622-648) restricted to what the kernels take. */
+enum tlm_dtype {
+  TLM_F16 = 0,
+  TLM_BF16 = 1,
+  TLM_F32 = 2,
+  TLM_F8E4M3 = 3, /* OCP e4m3fn (gfx950 native), not the FNUZ variant of gfx942 */
+  TLM_I32 = 4,
+};
+
+/* Error codes. The reference returns -1 (init), -2 (module load), 1 (launch)
+ * (main_template.cpp:15-31, 64-67); here every failure is negative. */
+enum tlm_status {
+  TLM_OK = 0,
+  TLM_EINVAL = -1,       /* null/misaligned pointer, bad size or dtype */
+  TLM_EUNSUPPORTED = -2, /* valid request that no kernel here implements */
+  TLM_EHIP = -3,         /* a HIP runtime call failed (message names it) */
+  TLM_EWORKSPACE = -4,   /* caller workspace too small */
+};
+
+/* Library version (major*10000 + minor*100 + patch). No reference counterpart. */
+int tlm_version(void);
+
+/* Select and initialise `device` (hipSetDevice + property query, once per device).
+ * Replaces init() of main_template.cpp:14-32 (tpuRtInit/tpuRtSetDevice). */
+int tlm_init(int device);
+
+/* Message for the last failing call on this thread ("" if none). Replaces the
+ * GPU-side get_last_error() convention (wrapper.py:22-42). */
+const char* tlm_last_error(void);
+
+/* Number of compute units of the current device (0 if unknown). */
+int tlm_num_cus(void);
+
+/* RMSNorm over the last dim: y[r,:] = cast(x[r,:] * rsqrt(mean_fp32(x[r,:]^2) + eps) * w).
+ * Reference program: tpu_demo/rms_norm/rms_norm_fp16.py:9-35 (no weight, eps 1e-12);
+ * oracle rms_norm_fp16.py:51-54. `w` may be NULL (reference behaviour). dtype: F16 | BF16. */
+int tlm_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
+                int dtype, void* stream);
+
+/* SwiGLU: out = cast(up * gate / (1 + exp(-gate))) in fp32.
+ * Reference program tpu_demo/tpu_test_swiglu_bf16.py:5-54 (param order gate, up, out),
+ * oracle :68 (b * F.silu(a)). dtype: BF16 | F16. n = number of elements. */
+int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* Interleaved RoPE on x[tokens, heads, dim] with tables cos/sin[tokens, dim] shared by all
+ * heads (pairs (2i, 2i+1) rotate by the angle stored at cos[t,2i] / sin[t,2i]):
+ *   out[2i]   = x[2i]*c - x[2i+1]*s,   out[2i+1] = x[2i+1]*c + x[2i]*s   (fp32, one rounding).
+ * Reference program tpu_demo/tpu_test_rope_bf16.py:5-51 (ppl_rope_add), oracle :76-92.
+ * The reference's [C, W] program is the case heads == 1. `k`/`k_out` may be NULL; when
+ * given, k[tokens, heads_k, dim] is rotated in the same launch. dtype: BF16 | F16. */
+int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t, void* q_out,
+             void* k_out, int64_t tokens, int64_t heads_q, int64_t heads_k, int64_t dim, int dtype,
+             void* stream);
+
+/* GEMM: C[M,N] = A[M,K] * B (fp32 accumulation, one rounding to out_dtype).
+ * trans_b == 0: B is [K,N] row-major (reference ppl_gemm transpose_B=False,
+ *   tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31, src/target/codegen_ppl.cc:1244-1279).
+ * trans_b == 1: B is [N,K] row-major (ppl_gemm transpose_B=True).
+ * in_dtype: F16 | BF16; out_dtype: F16 | BF16 | F32. */
+int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
+             int out_dtype, int trans_b, void* stream);
+
+/* FlashAttention forward, BSHD layout: q,k,v,o [B, S, H, D]; softmax in fp32 with scale
+ * sm_scale; P rounded to the input dtype before P*V; causal masks key j > query i.
+ * Reference: tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (oracle :171-182),
+ * element mask per examples/flash_attention/example_mha_fwd_bshd.py:50-53.
+ * dtype: BF16 | F16; D == 128 (64 also accepted). */
+int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t S,
+                       int64_t H, int64_t D, int causal, float sm_scale, int dtype, void* stream);
+
+/* MLA paged decode (one query token per sequence, one shared latent KV head).
+ * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,
+ * LSE combine :186-221, params :224-256), torch oracle :259-308.
+ *   q      [B, Hq, q_stride] (q_stride >= dqk): q[..., :dv] is the latent part, q[..., dv:dqk]
+ *          the rope part; q_pe may point elsewhere (q_pe_stride) to take the reference's
+ *          separate Q / Q_pe tensors; pass q_pe = q + dv elements for a fused [.., 576] tensor.
+ *   kv     token rows of the paged cache; row t at kv + t*kv_stride holds the dv latent values,
+ *   k_pe   row t at k_pe + t*kpe_stride holds the dpe rope values (same convention as q_pe).
+ *   block_table int32 [B, max_pages]: token j of sequence b lives in row
+ *          block_table[b, j / page] * page + j % page   (example_mla_decode_paged.py:62-63).
+ *   seqlens int32 [B], each in [1, max_pages*page].
+ *   o      [B, Hq, dv] out dtype (F16 | BF16).
+ * kv_dtype: F8E4M3 (value = e4m3 decode of the byte times *kv_scale, a DEVICE fp32 scalar so
+ *   that no host sync is needed; NULL means 1) | F16 | BF16 (kv_scale may be NULL).
+ * q_dtype: BF16 | F16. The softmax uses sm_scale (natural-log domain).
+ * num_split >= 1 KV splits per sequence, combined by an LSE pass through `ws`;
+ * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned). */
+int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                   const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                   const int32_t* block_table, const int32_t* seqlens, void* o, void* ws,
+                   size_t ws_bytes, int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
+                   int64_t max_pages, int num_split, float sm_scale, const float* kv_scale,
+                   int q_dtype, int kv_dtype, int o_dtype, void* stream);
+
+/* Workspace bytes that tlm_mla_decode needs for (B, Hq, dv, num_split). */
+size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split);
+
+/* Integer-path check: out[i, :] = kv_bytes[row(i), :] for every token i of every sequence,
+ * rows resolved through the block table exactly as tlm_mla_decode does; tokens of sequence b
+ * are written at out + (cu_seqlens[b] + j) * row_bytes with cu_seqlens the exclusive prefix
+ * sum of seqlens (computed on the host by the caller and passed in). Bit-exact by contract. */
+int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, const int32_t* block_table,
+                     const int32_t* seqlens, const int64_t* cu_seqlens, void* out, int64_t B,
+                     int64_t page, int64_t max_pages, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TLMI355X_H */

@@ -1,0 +1,226 @@
+"""CPU oracle: restatements of the reference's own torch reference functions for the kernel path.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+import this module, as the checker / CPU baseline — never as the thing measured or shipped.
+The product path (tilelang -> libtlmi355x.so) never imports it and has no CPU fallback.
+
+Each function cites the reference file:line it restates. Stated deviations from the reference
+(all listed in the module-level notes of each function) follow the benchmark configs:
+  * rmsnorm: weight and eps are parameters (the demo has no weight and eps 1e-12);
+  * rope tables are computed in fp32 then cast (the demo computes angles in bf16, which cannot
+    represent positions > 256 exactly) and the rotation is evaluated in fp32 with one rounding;
+  * flash attention causal masking is the element mask of ref_program (tril);
+  * mla gathers tokens through the block table (the reference oracle assumes an identity
+    table, begin = i*max_seqlen_pad) and dequantises fp8 KV with a per-tensor scale.
+
+How each function is pinned (checks that do not retype the formula) is in tests/test_oracle.py.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+LOG2E_REF = 1.44269504  # constant used by the reference's MLA programs (example_mla_decode_paged.py:12)
+
+
+# ------------------------------------------------------------------------------------------------
+# RMSNorm — tpu_demo/rms_norm/rms_norm_fp16.py:51-54:
+#   ref_fp32 = a_fp32 / sqrt(mean(a_fp32*a_fp32, dim=1, keepdim=True) + eps); ref = ref_fp32.to(dtype)
+def rmsnorm_ref(x: torch.Tensor, w: Optional[torch.Tensor] = None, eps: float = 1e-12):
+    xf = x.float()
+    y = xf / torch.sqrt(torch.mean(xf * xf, dim=-1, keepdim=True) + eps)
+    if w is not None:
+        y = y * w.float()
+    return y.to(x.dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# GEMM — tpu_demo/matmul/tpu_test_matmul_fp16.py:45 (ref = torch.matmul(a, b).half()), with the
+# fp32 accumulation of the program (ppl_gemm C is fp32, tpu_test_matmul_fp16.py:19-29) and of
+# testing/python/amd/test_tilelang_test_amd.py:90-99 (a.float() @ b.float()).
+def matmul_ref(a: torch.Tensor, b: torch.Tensor, out_dtype=torch.float16, trans_b=False):
+    bf = b.float().t() if trans_b else b.float()
+    return (a.float() @ bf).to(out_dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# RoPE — tables per tpu_demo/tpu_test_rope_bf16.py:53-74 (make_rope_cos_sin), computed in fp32;
+# rotation per rope_ref_torch (:76-92).
+def rope_cos_sin(C: int, W: int, base: float = 10000.0, pos_start: int = 0,
+                 dtype=torch.bfloat16):
+    assert W % 2 == 0
+    k = torch.arange(W // 2, dtype=torch.float32)
+    inv_freq = base ** (-2.0 * k / W)
+    pos = torch.arange(pos_start, pos_start + C, dtype=torch.float32).unsqueeze(1)
+    theta = pos * inv_freq
+    c, s = torch.cos(theta), torch.sin(theta)
+    cos = torch.repeat_interleave(c, 2, dim=1)
+    sin = torch.repeat_interleave(s, 2, dim=1)
+    return cos.to(dtype).contiguous(), sin.to(dtype).contiguous()
+
+
+def rope_ref(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [..., tokens?, W] with cos/sin broadcastable as [tokens, 1.., W] (or x's shape)."""
+    xf, cf, sf = x.float(), cos.float(), sin.float()
+    if cf.shape != xf.shape:  # tables [T, W] shared across heads of x [T, H, W]
+        cf = cf.view(cf.shape[0], *([1] * (xf.dim() - 2)), cf.shape[-1])
+        sf = sf.view(sf.shape[0], *([1] * (xf.dim() - 2)), sf.shape[-1])
+    xe, xo = xf[..., 0::2], xf[..., 1::2]
+    c, s = cf[..., 0::2], sf[..., 0::2]
+    out = torch.empty_like(xf.expand(*torch.broadcast_shapes(xf.shape, cf.shape)))
+    out[..., 0::2] = xe * c - xo * s
+    out[..., 1::2] = xo * c + xe * s
+    return out.to(x.dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# SwiGLU — tpu_demo/tpu_test_swiglu_bf16.py:68: ref = b * F.silu(a), evaluated in fp32 (the
+# program computes in fp32, :37-52) with one rounding.
+def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    return (up.float() * F.silu(gate.float())).to(gate.dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# FlashAttention — tpu_demo/flashattn/tpu_test_flashattn_bf16.py:171-182 (ref_program):
+#   scores = einsum('bqhd,bkhd->bhqk', Q.float(), K.float()) / sqrt(dim); causal tril mask;
+#   softmax; out = einsum('bhqk,bkhd->bqhd', P, V.float()).bfloat16()
+# Evaluated one (batch, head) at a time so the [S, S] scores fit in host memory.
+def flashattn_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None,
+                  heads: Optional[list] = None, batches: Optional[list] = None):
+    B, S, H, D = Q.shape
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else sm_scale
+    out = torch.empty(B, S, H, D, dtype=torch.float32)
+    mask = None
+    if causal:
+        mask = torch.ones(S, S, dtype=torch.bool).tril()
+    bs = range(B) if batches is None else batches
+    hs = range(H) if heads is None else heads
+    for b in bs:
+        for h in hs:
+            q = Q[b, :, h, :].float()
+            k = K[b, :, h, :].float()
+            v = V[b, :, h, :].float()
+            s = (q @ k.t()) * scale
+            if mask is not None:
+                s = s.masked_fill(~mask, float("-inf"))
+            out[b, :, h, :] = torch.softmax(s, dim=-1) @ v
+    return out.to(Q.dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# MLA decode — examples/deepseek_mla/example_mla_decode_paged.py:259-308 (run_torch_mla /
+# scaled_dot_product_attention): per sequence, fp32 attention of q [h_q, d] over the sequence's
+# KV rows, shared latent head (h_kv = 1), value = first dv columns of the key rows.
+# The rows are gathered through the block table: token j -> BT[b, j // page] * page + j % page
+# (the kernel's addressing, :62-63, 147-148). fp8 KV is dequantised as decode(byte) * kv_scale.
+def paged_rows(block_table: torch.Tensor, seqlen: int, b: int, page: int) -> torch.Tensor:
+    j = torch.arange(seqlen, dtype=torch.int64)
+    return block_table[b, j // page].to(torch.int64) * page + j % page
+
+
+def mla_decode_ref(q, q_pe, kv, k_pe, block_table, seqlens, page: int, sm_scale: float,
+                   kv_scale: float = 1.0, out_dtype=torch.bfloat16, return_lse=False):
+    """q [B,Hq,dv], q_pe [B,Hq,dpe], kv [rows,dv] / k_pe [rows,dpe] (any dtype incl. fp8),
+    block_table int32 [B,P], seqlens int32 [B]. Returns [B,Hq,dv] (and lse [B,Hq], natural log)."""
+    B, Hq, dv = q.shape
+    kvf = kv.reshape(kv.shape[0], -1).float() * kv_scale
+    kpf = k_pe.reshape(k_pe.shape[0], -1).float() * kv_scale
+    out = torch.empty(B, Hq, dv, dtype=torch.float32)
+    lse = torch.empty(B, Hq, dtype=torch.float32)
+    for b in range(B):
+        L = int(seqlens[b])
+        rows = paged_rows(block_table, L, b, page)
+        kb = torch.cat([kvf[rows], kpf[rows]], dim=1)  # [L, dv+dpe]
+        qb = torch.cat([q[b].float(), q_pe[b].float()], dim=1)  # [Hq, dv+dpe]
+        s = (qb @ kb.t()) * sm_scale
+        lse[b] = torch.logsumexp(s, dim=-1)
+        out[b] = torch.softmax(s, dim=-1) @ kvf[rows]
+    o = out.to(out_dtype)
+    return (o, lse) if return_lse else o
+
+
+# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial
+# outputs with log2-domain LSE, then the LSE-weighted combine. Restated over explicit splits of
+# the token range (the kernel's partition, example_mla_decode_paged.py:140-144: blocks of
+# block_N tokens, the first `total % num_split` splits take one extra block).
+def mla_split_partition(seqlen: int, num_split: int, block_n: int):
+    total = -(-seqlen // block_n)
+    per, rem = divmod(total, num_split)
+    bounds = []
+    for s in range(num_split):
+        nblk = per + (1 if s < rem else 0)
+        start = (per * s + min(s, rem)) * block_n
+        bounds.append((start, min(start + nblk * block_n, seqlen)))
+    return bounds
+
+
+def mla_split_combine_ref(q, q_pe, kv, k_pe, block_table, seqlens, page, sm_scale, num_split,
+                          block_n=64, kv_scale=1.0, out_dtype=torch.bfloat16):
+    B, Hq, dv = q.shape
+    kvf = kv.reshape(kv.shape[0], -1).float() * kv_scale
+    kpf = k_pe.reshape(k_pe.shape[0], -1).float() * kv_scale
+    out = torch.zeros(B, Hq, dv, dtype=torch.float32)
+    log2e = 1.0 / math.log(2.0)
+    for b in range(B):
+        L = int(seqlens[b])
+        rows = paged_rows(block_table, L, b, page)
+        qb = torch.cat([q[b].float(), q_pe[b].float()], dim=1)
+        parts, lses = [], []
+        for (st, en) in mla_split_partition(L, num_split, block_n):
+            if en <= st:
+                parts.append(torch.zeros(Hq, dv))
+                lses.append(torch.full((Hq,), float("-inf")))
+                continue
+            r = rows[st:en]
+            s = (qb @ torch.cat([kvf[r], kpf[r]], 1).t()) * sm_scale * log2e  # log2 domain
+            m = s.max(dim=-1).values
+            p = torch.exp2(s - m[:, None])
+            l = p.sum(-1)
+            parts.append((p @ kvf[r]) / l[:, None])
+            lses.append(torch.log2(l) + m)
+        g = torch.stack(lses, -1)  # [Hq, ns]
+        gmax = g.max(-1).values
+        lse = torch.log2(torch.exp2(g - gmax[:, None]).sum(-1)) + gmax
+        for i, part in enumerate(parts):
+            out[b] += part * torch.exp2(g[:, i] - lse)[:, None]
+    return out.to(out_dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# FP8 e4m3fn (OCP) decode, numpy closed form: sign, 4-bit exponent (bias 7), 3-bit mantissa;
+# exponent 0 is subnormal (m/8 * 2^-6); 0x7F / 0xFF are NaN; there is no infinity.
+def fp8_e4m3fn_table() -> np.ndarray:
+    t = np.empty(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 0x7
+        if e == 0xF and m == 0x7:
+            t[b] = np.nan
+        elif e == 0:
+            t[b] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            t[b] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+def fp8_quantize(x: torch.Tensor):
+    """Per-tensor e4m3 quantisation used by the MLA config: scale = amax / 448."""
+    scale = float(x.abs().max()) / 448.0
+    q = (x / scale).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def paged_gather_ref(kv_bytes: np.ndarray, block_table: np.ndarray, seqlens: np.ndarray,
+                     page: int) -> np.ndarray:
+    """Concatenate every sequence's rows in token order (uint8 rows), numpy."""
+    rows = []
+    for b in range(block_table.shape[0]):
+        j = np.arange(int(seqlens[b]))
+        rows.append(block_table[b, j // page].astype(np.int64) * page + j % page)
+    idx = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+    return kv_bytes[idx]

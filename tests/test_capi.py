@@ -1,0 +1,125 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol declared in
+include/tlmi355x.h, and rejects bad arguments before touching HIP (error paths modelled on the
+reference's ValueError / status-code conventions, cython_wrapper.pyx:76-79, 130-150 and
+main_template.cpp:15-31, 64-67)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+from tilelang.jit.adapter.mi355x import lib
+
+HEADER = os.path.join(ROOT, "include", "tlmi355x.h")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tlm_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
+              "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
+              "tlm_paged_gather"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.load()
+    missing = [s for s in declared_symbols() if not hasattr(L, s)]
+    assert not missing, f"libtlmi355x.so lacks {missing}"
+    # and the ctypes table covers them all
+    assert set(declared_symbols()) <= set(lib.EXPORTED)
+
+
+def test_version():
+    assert lib.load().tlm_version() >= 100
+
+
+def _err():
+    return lib.load().tlm_last_error().decode()
+
+
+def test_rmsnorm_rejects_null_and_dtype():
+    L = lib.load()
+    assert L.tlm_rmsnorm(None, None, None, 4, 4, 1e-6, lib.F16, None) == -1
+    assert "null" in _err()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_rmsnorm(p, None, p, 4, 4, 1e-6, lib.F32, None) == -2
+    assert "dtype" in _err()
+    assert L.tlm_rmsnorm(p, None, p, -1, 4, 1e-6, lib.F16, None) == -1
+    assert L.tlm_rmsnorm(ctypes.c_void_p(0x1001), None, p, 4, 4, 1e-6, lib.F16, None) == -1
+    assert "aligned" in _err()
+    assert L.tlm_rmsnorm(p, None, p, 4, 4, -1.0, lib.F16, None) == -1
+
+
+def test_swiglu_rope_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_swiglu(p, None, p, 8, lib.BF16, None) == -1
+    assert L.tlm_swiglu(p, p, p, -8, lib.BF16, None) == -1
+    assert L.tlm_swiglu(p, p, p, 8, lib.F8E4M3, None) == -2
+    # zero-size is a successful no-op that never reaches HIP
+    assert L.tlm_swiglu(p, p, p, 0, lib.BF16, None) == 0
+    assert L.tlm_rope(p, p, p, p, p, None, 4, 2, 2, 128, lib.BF16, None) == -1  # k_out missing
+    assert L.tlm_rope(p, None, p, p, p, None, 4, 2, 0, 127, lib.BF16, None) == -1  # odd dim
+    assert L.tlm_rope(p, None, p, p, p, None, 0, 2, 0, 128, lib.BF16, None) == 0
+
+
+@pytest.mark.parametrize("args,code", [
+    # null pointers
+    ((None, None, None, 16, 16, 16, lib.F16, lib.F16, 0), -1),
+    # bad in dtype
+    ((0x1000, 0x1000, 0x1000, 16, 16, 16, lib.F32, lib.F16, 0), -2),
+    # bad trans flag
+    ((0x1000, 0x1000, 0x1000, 16, 16, 16, lib.F16, lib.F16, 2), -1),
+    # negative size
+    ((0x1000, 0x1000, 0x1000, -1, 16, 16, lib.F16, lib.F16, 0), -1),
+])
+def test_gemm_validation(args, code):
+    L = lib.load()
+    a = [ctypes.c_void_p(x) if isinstance(x, int) and i < 3 else x for i, x in enumerate(args)]
+    assert L.tlm_gemm(*a, None) == code
+
+
+def test_flash_attn_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_flash_attn_fwd(None, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.BF16, None) == -1
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 96, 0, 0.1, lib.BF16, None) == -2
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.F32, None) == -2
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 128, 0, 0.1, lib.BF16, None) == 0
+
+
+def test_mla_validation_and_workspace():
+    L = lib.load()
+    ws = L.tlm_mla_workspace_bytes(64, 128, 512, 4)
+    assert ws >= 64 * 128 * 4 * (512 + 1) * 4
+    p = ctypes.c_void_p(0x1000)
+    # workspace too small
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, p, p, p, p, 16, 2, 128, 512, 64, 64, 4,
+                          2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    assert rc == -4 and "workspace" in _err()
+    # unsupported head dims
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, p, p, p, p, 1 << 30, 2, 128, 256, 64,
+                          64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    assert rc == -2
+    # null block table
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, None, p, p, p, 1 << 30, 2, 128, 512,
+                          64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    assert rc == -1
+
+
+def test_init_without_gpu_reports_error():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    L = lib.load()
+    assert L.tlm_init(0) != 0
+    assert _err()
+    assert L.tlm_init(-1) == -1

@@ -1,0 +1,126 @@
+"""The mi355x kernel adapter: the callable that ``tilelang.compile`` returns.
+
+Both call conventions of the reference are kept:
+  * TPU convention (tilelang/jit/adapter/cython/adapter.py:218-246): the caller passes ALL
+    parameters in prim_func order; outputs are written in place; the call returns ``0``.
+    Tensors may live on the host (the demos pass CPU tensors): they are copied to the GPU and
+    the outputs copied back, as the reference copies through host buffers.
+  * GPU convention (tilelang/jit/adapter/cython/cython_wrapper.pyx:68-163): the caller passes
+    the inputs only; outputs are allocated on the inputs' device and returned (one tensor, or a
+    list for several outputs). Count, dtype, static shape and device mismatches raise ValueError.
+The convention is chosen by the number of arguments.
+"""
+from typing import Any, List
+
+import torch
+
+from ..base import BaseKernelAdapter
+from . import ops
+
+
+def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
+    a = plan.attrs
+    f = plan.family
+    if f == "rmsnorm":
+        w = None if a["w"] is None else t[a["w"]]
+        ops.rmsnorm(t[a["x"]], w, t[a["y"]], a["eps"])
+    elif f == "swiglu":
+        ops.swiglu(t[a["gate"]], t[a["up"]], t[a["out"]])
+    elif f == "rope":
+        k = None if a["k"] is None else t[a["k"]]
+        ko = None if a["k_out"] is None else t[a["k_out"]]
+        ops.rope(t[a["q"]], t[a["cos"]], t[a["sin"]], t[a["q_out"]], k, ko)
+    elif f == "gemm":
+        ops.gemm(t[a["a"]], t[a["b"]], t[a["c"]], a["trans_b"])
+    elif f == "flashattn":
+        ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"])
+    elif f == "mla":
+        q = t[a["q"]]
+        dev = q.device
+        need = ops.mla_workspace_bytes(a["B"], a["Hq"], a["dv"], a["num_split"])
+        ws = workspace_cache.get(dev)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+            workspace_cache[dev] = ws
+        kvs = None if a["kv_scale"] is None else t[a["kv_scale"]]
+        ops.mla_decode(q, t[a["q_pe"]], t[a["kv"]], t[a["k_pe"]], t[a["block_table"]],
+                       t[a["seqlens"]], t[a["o"]], ws, a["page"], a["num_split"], a["sm_scale"],
+                       kvs)
+    else:  # pragma: no cover - recognizer only emits the families above
+        raise RuntimeError(f"no runner for family {f}")
+
+
+class MI355XKernelAdapter(BaseKernelAdapter):
+
+    def __init__(self, params, result_idx, plan, prim_func=None):
+        self.plan = plan
+        self.prim_func = prim_func
+        self._ws = {}
+        super().__init__(None, params, result_idx)
+        # the recognizer knows which parameters the program writes
+        if not self.result_idx:
+            self.result_idx = list(plan.out_idx)
+
+    def get_kernel_source(self, kernel_only: bool = False) -> str:
+        return (f"// gfx950 kernel family {self.plan.describe()}\n"
+                f"// dispatched through libtlmi355x.so (include/tlmi355x.h)\n")
+
+    def _check(self, i, t):
+        p = self.params[i]
+        if not isinstance(t, torch.Tensor):
+            raise ValueError(f"parameter {i} must be a torch.Tensor, got {type(t)}")
+        if t.dtype != p.dtype:
+            raise ValueError(f"Buffer dtype mismatch for parameter {i}: expected {p.dtype}, "
+                             f"got {t.dtype}")
+        if list(t.shape) != [int(s) for s in p.shape]:
+            raise ValueError(f"Static shape mismatch for parameter {i}: expected "
+                             f"{list(p.shape)}, got {list(t.shape)}")
+
+    def _convert_torch_func(self):
+
+        def forward(*args: Any):
+            n = len(self.params)
+            outs = self.result_idx
+            if len(args) == n:
+                inplace = True
+                full = list(args)
+            elif len(args) == n - len(outs):
+                inplace = False
+                it = iter(args)
+                full = [None if i in outs else next(it) for i in range(n)]
+            else:
+                raise ValueError(f"Expected {n} arguments (all parameters, outputs written in "
+                                 f"place) or {n - len(outs)} (inputs only), got {len(args)}")
+            for i, t in enumerate(full):
+                if t is not None:
+                    self._check(i, t)
+            ins = [t for t in full if t is not None]
+            if not torch.cuda.is_available():
+                raise RuntimeError("no HIP device visible: the mi355x target runs on gfx950 only "
+                                   "and has no CPU fallback")
+            devs = {t.device for t in ins}
+            if len(devs) > 1:
+                raise ValueError(f"Buffer device mismatch: arguments on {sorted(map(str, devs))}")
+            home = next(iter(devs)) if devs else torch.device("cuda", torch.cuda.current_device())
+            gpu = home if home.type == "cuda" else torch.device(
+                "cuda", torch.cuda.current_device())
+            dev_t = []
+            for i, t in enumerate(full):
+                if t is None:
+                    p = self.params[i]
+                    dev_t.append(torch.empty([int(s) for s in p.shape], dtype=p.dtype,
+                                             device=gpu))
+                elif t.device != gpu:
+                    dev_t.append(t.to(gpu))
+                else:
+                    dev_t.append(t)
+            _run_plan(self.plan, dev_t, self._ws)
+            if inplace:
+                for i in outs:
+                    if full[i].data_ptr() != dev_t[i].data_ptr():
+                        full[i].copy_(dev_t[i])
+                return 0
+            res = [dev_t[i] if home.type == "cuda" else dev_t[i].to(home) for i in outs]
+            return res[0] if len(res) == 1 else res
+
+        return forward

@@ -1,0 +1,211 @@
+"""Torch-tensor front of each C-ABI entry point.
+
+These functions take device tensors that the caller allocated (torch is only the allocator and
+the stream provider), check dtype/shape/contiguity, and call libtlmi355x.so on the current
+stream. They are what the mi355x kernel adapter dispatches to, and can be called directly.
+"""
+from typing import Optional
+
+import torch
+
+from . import lib
+
+_DT = {torch.float16: lib.F16, torch.bfloat16: lib.BF16, torch.float32: lib.F32,
+       torch.float8_e4m3fn: lib.F8E4M3, torch.int32: lib.I32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt not in _DT:
+        raise ValueError(f"dtype {dt} is not supported by the mi355x kernels")
+    return _DT[dt]
+
+
+def _dev(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a torch.Tensor, got {type(t)}")
+        if t.device.type != "cuda":
+            raise ValueError(f"tensor on {t.device}: the mi355x kernels take HIP device tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    lib.ensure_device(dev.index if dev.index is not None else torch.cuda.current_device())
+    return dev
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _contig(name, t):
+    if t is not None and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def rmsnorm(x: torch.Tensor, w: Optional[torch.Tensor], y: torch.Tensor, eps: float):
+    """y = cast(x * rsqrt(mean(x^2) + eps) * w) over the last dim."""
+    dev = _dev(x, w, y)
+    for n, t in (("x", x), ("w", w), ("y", y)):
+        _contig(n, t)
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError("y must match x in shape and dtype")
+    if w is not None and (w.numel() != cols or w.dtype != x.dtype):
+        raise ValueError(f"w must have {cols} elements of dtype {x.dtype}")
+    lib.call("tlm_rmsnorm", _ptr(x), _ptr(w), _ptr(y), rows, cols, float(eps),
+             dtype_code(x.dtype), _stream(dev))
+    return y
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor):
+    """out = up * silu(gate), fp32 math."""
+    dev = _dev(gate, up, out)
+    for n, t in (("gate", gate), ("up", up), ("out", out)):
+        _contig(n, t)
+    if not (gate.shape == up.shape == out.shape) or not (gate.dtype == up.dtype == out.dtype):
+        raise ValueError("gate, up and out must share shape and dtype")
+    lib.call("tlm_swiglu", _ptr(gate), _ptr(up), _ptr(out), gate.numel(), dtype_code(gate.dtype),
+             _stream(dev))
+    return out
+
+
+def rope(q: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, q_out: torch.Tensor,
+         k: Optional[torch.Tensor] = None, k_out: Optional[torch.Tensor] = None):
+    """Interleaved RoPE. q/k are [tokens, heads, dim] (or [tokens, dim]); cos/sin [tokens, dim]."""
+    dev = _dev(q, cos, sin, q_out, k, k_out)
+    for n, t in (("q", q), ("cos", cos), ("sin", sin), ("q_out", q_out), ("k", k),
+                 ("k_out", k_out)):
+        _contig(n, t)
+    dim = q.shape[-1]
+    tokens = cos.numel() // dim if dim else 0
+    if cos.shape != sin.shape or cos.shape[-1] != dim:
+        raise ValueError("cos and sin must be [tokens, dim]")
+    hq = q.numel() // (tokens * dim) if tokens else 1
+    if hq * tokens * dim != q.numel() or q_out.shape != q.shape:
+        raise ValueError(f"q {tuple(q.shape)} does not split into {tokens} tokens x heads x {dim}")
+    hk = 0
+    if k is not None:
+        hk = k.numel() // (tokens * dim) if tokens else 1
+        if hk * tokens * dim != k.numel() or k_out is None or k_out.shape != k.shape:
+            raise ValueError("k/k_out do not match the token count of the tables")
+    dts = {t.dtype for t in (q, cos, sin, q_out, k, k_out) if t is not None}
+    if len(dts) != 1:
+        raise ValueError(f"all RoPE tensors must share one dtype, got {dts}")
+    lib.call("tlm_rope", _ptr(q), _ptr(k), _ptr(cos), _ptr(sin), _ptr(q_out), _ptr(k_out), tokens,
+             hq, hk, dim, dtype_code(q.dtype), _stream(dev))
+    return q_out
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = False):
+    """c = a @ b (trans_b=False, b [K,N]) or a @ b.T (trans_b=True, b [N,K]); fp32 accumulate."""
+    dev = _dev(a, b, c)
+    for n, t in (("A", a), ("B", b), ("C", c)):
+        _contig(n, t)
+    M, K = a.shape
+    N = b.shape[0] if trans_b else b.shape[1]
+    kb = b.shape[1] if trans_b else b.shape[0]
+    if kb != K or tuple(c.shape) != (M, N):
+        raise ValueError(f"shape mismatch A{tuple(a.shape)} B{tuple(b.shape)} C{tuple(c.shape)}")
+    if a.dtype != b.dtype:
+        raise ValueError("A and B must share a dtype")
+    lib.call("tlm_gemm", _ptr(a), _ptr(b), _ptr(c), M, N, K, dtype_code(a.dtype),
+             dtype_code(c.dtype), 1 if trans_b else 0, _stream(dev))
+    return c
+
+
+def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float):
+    """BSHD attention forward: q,k,v,o [B, S, H, D]."""
+    dev = _dev(q, k, v, o)
+    for n, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
+        _contig(n, t)
+    if not (q.shape == k.shape == v.shape == o.shape):
+        raise ValueError("Q, K, V and O must share the [B, S, H, D] shape")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype):
+        raise ValueError("Q, K, V and O must share a dtype")
+    B, S, H, D = q.shape
+    lib.call("tlm_flash_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, S, H, D,
+             1 if causal else 0, float(sm_scale), dtype_code(q.dtype), _stream(dev))
+    return o
+
+
+def mla_workspace_bytes(B, Hq, dv, num_split) -> int:
+    return int(lib.load().tlm_mla_workspace_bytes(B, Hq, dv, num_split))
+
+
+def _rows(name, t, width):
+    """Row pointer and row stride (elements) of a [..., width] tensor whose last dim is dense."""
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name}: last dim must be contiguous")
+    if t.shape[-1] != width:
+        raise ValueError(f"{name}: last dim must be {width}, got {t.shape[-1]}")
+    # every leading dim must collapse onto one row stride
+    rs = None
+    expect = None
+    for d in range(t.dim() - 2, -1, -1):
+        if t.shape[d] == 1:
+            continue
+        if rs is None:
+            rs = t.stride(d)
+            expect = rs * t.shape[d]
+        else:
+            if t.stride(d) != expect:
+                raise ValueError(f"{name}: leading dims do not form uniform rows")
+            expect = t.stride(d) * t.shape[d]
+    return t.data_ptr(), (rs if rs is not None else width)
+
+
+def mla_decode(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, page: int,
+               num_split: int, sm_scale: float, kv_scale: Optional[torch.Tensor] = None):
+    """Paged MLA decode. q [B,Hq,dv], q_pe [B,Hq,dpe], kv [rows,...,dv], k_pe [rows,...,dpe]
+    (any uniform row stride), block_table int32 [B, max_pages], seqlens int32 [B],
+    out [B, Hq, dv]. kv_scale: device fp32 scalar for fp8 KV (None -> 1)."""
+    dev = _dev(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, kv_scale)
+    B, Hq, dv = q.shape
+    dpe = q_pe.shape[-1]
+    if tuple(q_pe.shape[:2]) != (B, Hq) or tuple(out.shape) != (B, Hq, dv):
+        raise ValueError("q_pe/out shapes do not match q")
+    q_ptr, q_rs = _rows("Q", q, dv)
+    qpe_ptr, qpe_rs = _rows("Q_pe", q_pe, dpe)
+    if q_rs % 1 or q.stride(1) != q_rs or q_pe.stride(1) != qpe_rs:
+        raise ValueError("Q/Q_pe rows must be uniform over (batch, head)")
+    kv_ptr, kv_rs = _rows("KV", kv, dv)
+    kpe_ptr, kpe_rs = _rows("K_pe", k_pe, dpe)
+    _contig("block_table", block_table)
+    _contig("cache_seqlens", seqlens)
+    _contig("Output", out)
+    if block_table.dtype != torch.int32 or seqlens.dtype != torch.int32:
+        raise ValueError("block_table and cache_seqlens must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] != B or seqlens.numel() != B:
+        raise ValueError("block_table must be [B, max_pages] and cache_seqlens [B]")
+    if q.dtype != q_pe.dtype or kv.dtype != k_pe.dtype:
+        raise ValueError("Q/Q_pe and KV/K_pe must share dtypes")
+    if kv.dtype == torch.float8_e4m3fn:
+        if kv_scale is None:
+            raise ValueError("fp8 KV needs a kv_scale tensor")
+    if kv_scale is not None and (kv_scale.dtype != torch.float32 or kv_scale.numel() != 1):
+        raise ValueError("kv_scale must be a one-element float32 tensor")
+    ws_bytes = workspace.numel() * workspace.element_size()
+    lib.call("tlm_mla_decode", q_ptr, qpe_ptr, q_rs, qpe_rs, kv_ptr, kpe_ptr, kv_rs, kpe_rs,
+             _ptr(block_table), _ptr(seqlens), _ptr(out), _ptr(workspace), ws_bytes, B, Hq, dv,
+             dpe, page, block_table.shape[1], num_split, float(sm_scale), _ptr(kv_scale),
+             dtype_code(q.dtype), dtype_code(kv.dtype), dtype_code(out.dtype), _stream(dev))
+    return out
+
+
+def paged_gather(kv_bytes: torch.Tensor, block_table, seqlens, cu_seqlens, out, page: int):
+    """Bit-exact gather of every sequence's token rows through the block table."""
+    dev = _dev(kv_bytes, block_table, seqlens, cu_seqlens, out)
+    row_bytes = kv_bytes.shape[-1] * kv_bytes.element_size()
+    lib.call("tlm_paged_gather", _ptr(kv_bytes), row_bytes, _ptr(block_table), _ptr(seqlens),
+             _ptr(cu_seqlens), _ptr(out), block_table.shape[0], page, block_table.shape[1],
+             _stream(dev))
+    return out

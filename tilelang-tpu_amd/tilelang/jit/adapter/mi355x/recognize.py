@@ -1,0 +1,468 @@
+"""Match a traced prim_func to one of the operator families that have gfx950 kernels.
+
+The reference lowers any TIR program through its PPL code generator (src/target/codegen_ppl.cc).
+This build has hand-written kernels for six families only, so compilation is recognition: the op
+trace is fingerprinted (which tile ops occur, how data flows from parameters through tiles), the
+family's static parameters (shapes, dtypes, eps, scale, causal, page size, splits) are read out
+of the program, and anything that does not fit a family is rejected with a clear error. There is
+no generic code generation and no fallback.
+
+Families and the reference programs they accept:
+  rmsnorm  tpu_demo/rms_norm/rms_norm_fp16.py:9-35 (+ bf16 twin; optional weight parameter)
+  gemm     tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31 (+ bf16 / fp32-out variants)
+  rope     tpu_demo/tpu_test_rope_bf16.py:5-51 (4 params) and a fused q+k form (6 params)
+  swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54
+  flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 and the upstream
+           examples/flash_attention/example_mha_fwd_bshd.py:30-151 structure
+  mla      examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split and no-split forms),
+           with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+from ....language import ir
+from ....language.ir import Buffer, BufferAccess, Expr
+
+LOG2E_REF = 1.44269504  # the constant the reference programs fold into exp2 scales
+
+
+class UnsupportedProgram(ValueError):
+    """The traced program matches no operator family implemented for gfx950."""
+
+
+@dataclass
+class Plan:
+    family: str
+    params: List[Buffer]
+    out_idx: List[int]
+    attrs: Dict = field(default_factory=dict)
+
+    def describe(self) -> str:
+        a = ", ".join(f"{k}={v}" for k, v in self.attrs.items())
+        return f"{self.family}({a})"
+
+
+# ------------------------------------------------------------------------------------------------
+# trace helpers
+
+_COPY = ("ppl_copy", "copy")
+_GEMM = ("ppl_gemm", "gemm")
+_STRUCTURAL = ("loop_begin", "loop_end", "alloc", "branch")
+
+
+def _ops(pf, names=None):
+    for op in pf.ops:
+        if op.name in _STRUCTURAL:
+            continue
+        if names is None or op.name in names:
+            yield op
+
+
+def _buf(x) -> Optional[Buffer]:
+    if isinstance(x, Buffer):
+        return x
+    if isinstance(x, BufferAccess):
+        return x.buffer
+    return None
+
+
+def _op_names(pf):
+    return [op.name for op in _ops(pf)]
+
+
+def _source_param(pf, buf: Buffer, depth=0) -> Optional[Buffer]:
+    """Follow tile copies backwards from ``buf`` to the global parameter it was loaded from."""
+    if buf is None or depth > 8:
+        return None
+    if buf.scope == "global":
+        return buf
+    for op in _ops(pf, _COPY):
+        if _buf(op.args[1]) is buf:
+            src = _source_param(pf, _buf(op.args[0]), depth + 1)
+            if src is not None:
+                return src
+    return None
+
+
+def _sink_param(pf, buf: Buffer, depth=0) -> Optional[Buffer]:
+    """Follow tile copies forwards from ``buf`` to the global parameter it is stored to."""
+    if buf is None or depth > 8:
+        return None
+    if buf.scope == "global":
+        return buf
+    for op in _ops(pf, _COPY):
+        if _buf(op.args[0]) is buf:
+            dst = _sink_param(pf, _buf(op.args[1]), depth + 1)
+            if dst is not None:
+                return dst
+    return None
+
+
+def _written_params(pf):
+    out = []
+    for op in _ops(pf):
+        b = None
+        if op.name in _COPY:
+            b = _buf(op.args[1])
+        elif op.name == "store":
+            b = op.args[0]
+        if b is not None and b.scope == "global" and all(b is not o for o in out):
+            out.append(b)
+    return out
+
+
+def _index(pf, buf) -> int:
+    for i, p in enumerate(pf.params):
+        if p is buf:
+            return i
+    raise UnsupportedProgram(f"{buf!r} is not a parameter")
+
+
+def _shape(b: Buffer):
+    return tuple(int(ir.const_value(s)) for s in b.shape)
+
+
+def _const(x) -> float:
+    if isinstance(x, Expr) and x.op == "const":
+        return float(x.args[0])
+    if isinstance(x, (int, float)):
+        return float(x)
+    raise UnsupportedProgram(f"expected a compile-time constant, got {x!r}")
+
+
+def _fail(family, msg):
+    raise UnsupportedProgram(f"{family}: {msg}")
+
+
+# ------------------------------------------------------------------------------------------------
+# families
+
+
+def _rmsnorm(pf, names) -> Plan:
+    fam = "rmsnorm"
+    red = [op for op in _ops(pf, ("ppl_reduce_sum",))]
+    if len(red) != 1 or red[0].kwargs.get("dim", 1) not in (1, -1):
+        _fail(fam, "expected one row reduce_sum over the last dim")
+    acc = _buf(red[0].args[1])
+    sq = _buf(red[0].args[0])
+    # eps and 1/N applied to the reduced buffer
+    eps = None
+    inv = None
+    for op in _ops(pf, ("ppl_add_C", "ppl_mul_C")):
+        if _buf(op.args[1]) is acc:
+            if op.name == "ppl_add_C":
+                eps = _const(op.args[2])
+            else:
+                inv = _const(op.args[2])
+    if eps is None or inv is None:
+        _fail(fam, "could not read eps / 1/N from ppl_add_C / ppl_mul_C on the row sum")
+    # x is what the squared tile was computed from
+    mul = [op for op in _ops(pf, ("ppl_mul",)) if _buf(op.args[0]) is sq]
+    if not mul:
+        _fail(fam, "no x*x feeding the reduction")
+    x = _source_param(pf, _buf(mul[0].args[1]))
+    writes = _written_params(pf)
+    if x is None or len(writes) != 1:
+        _fail(fam, "expected one input x and one output y")
+    y = writes[0]
+    if len(x.shape) < 2 or _shape(x) != _shape(y) or x.dtype != y.dtype:
+        _fail(fam, f"x {x!r} and y {y!r} must match")
+    N = _shape(x)[-1]
+    if abs(inv * N - 1.0) > 1e-6:
+        _fail(fam, f"mean scale {inv} is not 1/{N}")
+    if x.dtype not in ("float16", "bfloat16"):
+        _fail(fam, f"dtype {x.dtype} (float16/bfloat16 kernels only)")
+    w = None
+    for p in pf.params:
+        if p is x or p is y:
+            continue
+        if math.prod(_shape(p)) == N and p.dtype == x.dtype:
+            w = p
+        else:
+            _fail(fam, f"unexpected parameter {p!r}")
+    outs = [_index(pf, y)]
+    return Plan(fam, pf.params, outs, dict(
+        x=_index(pf, x), w=None if w is None else _index(pf, w), y=outs[0], eps=eps,
+        rows=math.prod(_shape(x)[:-1]), cols=N, dtype=x.dtype))
+
+
+def _swiglu(pf, names) -> Plan:
+    fam = "swiglu"
+    exp_ops = [op for op in _ops(pf, ("ppl_exp",))]
+    if len(exp_ops) != 1:
+        _fail(fam, "expected one ppl_exp2")
+    ebuf = _buf(exp_ops[0].args[0])
+    # exp input = -gate: find mul_C(-1) producing ebuf
+    neg = [op for op in _ops(pf, ("ppl_mul_C",)) if _buf(op.args[0]) is ebuf]
+    if not neg or _const(neg[0].args[2]) != -1.0:
+        _fail(fam, "exp argument is not -gate")
+    gate = _source_param(pf, _buf(neg[0].args[1]))
+    writes = _written_params(pf)
+    reads = [p for p in pf.params if all(p is not w for w in writes)]
+    if gate is None or len(writes) != 1 or len(reads) != 2:
+        _fail(fam, "expected (gate, up) -> out")
+    up = reads[0] if reads[1] is gate else reads[1]
+    out = writes[0]
+    if not (_shape(gate) == _shape(up) == _shape(out)):
+        _fail(fam, "gate, up, out shapes differ")
+    if not (gate.dtype == up.dtype == out.dtype) or gate.dtype not in ("bfloat16", "float16"):
+        _fail(fam, "dtypes must all be bfloat16 or all float16")
+    return Plan(fam, pf.params, [_index(pf, out)], dict(
+        gate=_index(pf, gate), up=_index(pf, up), out=_index(pf, out),
+        n=math.prod(_shape(gate)), dtype=gate.dtype))
+
+
+def _rope(pf, names) -> Plan:
+    fam = "rope"
+    n = len(pf.params)
+    if n == 4:
+        x, c, s, o = pf.params
+        if not (_shape(x) == _shape(c) == _shape(s) == _shape(o)) or len(_shape(x)) != 2:
+            _fail(fam, "the 4-parameter form takes x, cos, sin, out of one [C, W] shape")
+        C, W = _shape(x)
+        attrs = dict(q=0, k=None, cos=1, sin=2, q_out=3, k_out=None, tokens=C, heads_q=1,
+                     heads_k=0, dim=W)
+        outs = [3]
+    elif n == 6:
+        q, k, c, s, qo, ko = pf.params
+        if _shape(c) != _shape(s) or len(_shape(c)) != 2:
+            _fail(fam, "cos/sin must be [tokens, dim]")
+        T, W = _shape(c)
+        if _shape(q)[0] != T or _shape(q)[-1] != W or _shape(k)[0] != T or _shape(k)[-1] != W:
+            _fail(fam, "q/k must be [tokens, heads, dim] matching the tables")
+        if _shape(qo) != _shape(q) or _shape(ko) != _shape(k):
+            _fail(fam, "outputs must match q and k")
+        hq = math.prod(_shape(q)[1:-1])
+        hk = math.prod(_shape(k)[1:-1])
+        attrs = dict(q=0, k=1, cos=2, sin=3, q_out=4, k_out=5, tokens=T, heads_q=hq, heads_k=hk,
+                     dim=W)
+        outs = [4, 5]
+    else:
+        _fail(fam, "expected (x, cos, sin, out) or (q, k, cos, sin, q_out, k_out)")
+    dts = {p.dtype for p in pf.params}
+    if len(dts) != 1 or next(iter(dts)) not in ("bfloat16", "float16"):
+        _fail(fam, f"all parameters must be bfloat16 or all float16, got {dts}")
+    if attrs["dim"] % 2:
+        _fail(fam, "dim must be even")
+    attrs["dtype"] = next(iter(dts))
+    return Plan(fam, pf.params, outs, attrs)
+
+
+def _gemm(pf, names) -> Plan:
+    fam = "gemm"
+    g = list(_ops(pf, _GEMM))
+    if len(g) != 1:
+        _fail(fam, "expected one gemm")
+    ta, tb = g[0].kwargs.get("transpose_A", False), g[0].kwargs.get("transpose_B", False)
+    if ta:
+        _fail(fam, "transpose_A is not supported")
+    A = _source_param(pf, _buf(g[0].args[0]))
+    B = _source_param(pf, _buf(g[0].args[1]))
+    C = _sink_param(pf, _buf(g[0].args[2]))
+    if A is None or B is None or C is None:
+        _fail(fam, "could not trace A, B and C through the tile copies")
+    M, K = _shape(A)
+    if tb:
+        N, Kb = _shape(B)
+    else:
+        Kb, N = _shape(B)
+    if Kb != K or _shape(C) != (M, N):
+        _fail(fam, f"shapes A{_shape(A)} B{_shape(B)} C{_shape(C)} do not chain")
+    if A.dtype != B.dtype or A.dtype not in ("float16", "bfloat16"):
+        _fail(fam, "A and B must both be float16 or both bfloat16")
+    if C.dtype not in ("float16", "bfloat16", "float32"):
+        _fail(fam, f"C dtype {C.dtype}")
+    return Plan(fam, pf.params, [_index(pf, C)], dict(
+        a=_index(pf, A), b=_index(pf, B), c=_index(pf, C), M=M, N=N, K=K, trans_b=bool(tb),
+        in_dtype=A.dtype, out_dtype=C.dtype))
+
+
+def _pipelined_extents(pf):
+    return [op.args[0].extents[0] for op in pf.ops
+            if op.name == "loop_begin" and op.args[0].kind == "pipelined"]
+
+
+def _flashattn(pf, names) -> Plan:
+    fam = "flashattn"
+    g = list(_ops(pf, _GEMM))
+    qk = [op for op in g if op.kwargs.get("transpose_B")]
+    pv = [op for op in g if not op.kwargs.get("transpose_B")]
+    if len(qk) != 1 or len(pv) != 1:
+        _fail(fam, "expected Q@K^T and P@V")
+    Q = _source_param(pf, _buf(qk[0].args[0]))
+    K = _source_param(pf, _buf(qk[0].args[1]))
+    V = _source_param(pf, _buf(pv[0].args[1]))
+    acc_o = _buf(pv[0].args[2])
+    O = _sink_param(pf, acc_o)
+    if None in (Q, K, V, O):
+        _fail(fam, "could not trace Q, K, V and Output")
+    shp = _shape(Q)
+    if len(shp) != 4 or not (shp == _shape(K) == _shape(V) == _shape(O)):
+        _fail(fam, "Q, K, V, Output must share a [batch, seq, heads, dim] shape")
+    if not (Q.dtype == K.dtype == V.dtype == O.dtype) or Q.dtype not in ("bfloat16", "float16"):
+        _fail(fam, "dtypes must all be bfloat16 or all float16")
+    B, S, H, D = shp
+    # causal: the KV loop is truncated at the diagonal (T.min(...) in the extent), or scores
+    # are masked by comparing query and key positions.
+    causal = any(isinstance(e, Expr) and e.has_op("min") for e in _pipelined_extents(pf))
+    for op in _ops(pf, ("store",)):
+        v = op.args[2]
+        if isinstance(v, Expr) and v.has_op("if_then_else"):
+            for e in v.walk():
+                if e.op == "if_then_else" and isinstance(e.args[0], Expr):
+                    fv = e.args[0].free_vars()
+                    if any(n.startswith("bx") for n in fv):
+                        causal = True
+    # softmax scale
+    acc_s = _buf(qk[0].args[2])
+    if "ppl_exp" in names:
+        cands = [op for op in _ops(pf, ("ppl_mul_C",)) if _buf(op.args[0]) is acc_s]
+        if not cands:
+            _fail(fam, "no ppl_mul_C scaling the scores")
+        sm_scale = _const(cands[0].args[2])
+    else:
+        sm_scale = None
+        for op in _ops(pf, ("store",)):
+            if op.args[0] is acc_s and isinstance(op.args[2], Expr) and op.args[2].has_op("exp2"):
+                cs = [c for c in op.args[2].consts() if isinstance(c, float) and c > 0]
+                if cs:
+                    sm_scale = cs[0] / LOG2E_REF
+        if sm_scale is None:
+            _fail(fam, "could not read the softmax scale")
+    return Plan(fam, pf.params, [_index(pf, O)], dict(
+        q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H, D=D,
+        causal=causal, sm_scale=sm_scale, dtype=Q.dtype))
+
+
+def _page_size_from_trace(pf, bt: Buffer) -> Optional[int]:
+    for op in pf.ops:
+        for a in op.args:
+            exprs = []
+            if isinstance(a, BufferAccess):
+                exprs = [ix.start for ix in a.indices if isinstance(ix, slice)]
+                exprs += [ix for ix in a.indices if isinstance(ix, Expr)]
+            for e in exprs:
+                if not isinstance(e, Expr):
+                    continue
+                for n in e.walk():
+                    if n.op == "mul" and isinstance(n.args[0], BufferAccess) and \
+                            n.args[0].buffer is bt and n.args[1].op == "const":
+                        return int(n.args[1].args[0])
+    return None
+
+
+def _mla(pf, names) -> Plan:
+    fam = "mla"
+    ints = [p for p in pf.params if p.dtype == "int32"]
+    bt = [p for p in ints if len(p.shape) == 2]
+    sl = [p for p in ints if len(p.shape) == 1]
+    if len(bt) != 1 or len(sl) != 1:
+        _fail(fam, "expected int32 BLOCK_TABLE [b, pages] and CACHE_SEQLENS [b]")
+    bt, sl = bt[0], sl[0]
+    kernels = {op.kernel for op in _ops(pf, _GEMM)}
+    g = [op for op in _ops(pf, _GEMM)]
+    qk = [op for op in g if op.kwargs.get("transpose_B")]
+    pv = [op for op in g if not op.kwargs.get("transpose_B")]
+    if len(qk) != 2 or len(pv) != 1 or len(kernels) != 1:
+        _fail(fam, "expected Q@KV^T + Q_pe@K_pe^T and P@KV in one kernel")
+    Q = _source_param(pf, _buf(qk[0].args[0]))
+    KV = _source_param(pf, _buf(qk[0].args[1]))
+    Qpe = _source_param(pf, _buf(qk[1].args[0]))
+    Kpe = _source_param(pf, _buf(qk[1].args[1]))
+    V = _source_param(pf, _buf(pv[0].args[1]))
+    if None in (Q, KV, Qpe, Kpe) or V is not KV:
+        _fail(fam, "could not trace Q, Q_pe, KV, K_pe (V must be the latent KV)")
+    out_params = _written_params(pf)
+    # Output = the [b, hq, dv] parameter written by the last kernel
+    O = None
+    glse = opart = None
+    b, hq, dv = _shape(Q)
+    dpe = _shape(Qpe)[-1]
+    for p in out_params:
+        s = _shape(p)
+        if s == (b, hq, dv):
+            O = p
+        elif len(s) == 3:
+            glse = p
+        elif len(s) == 4:
+            opart = p
+    if O is None:
+        _fail(fam, "no [batch, heads, dv] output")
+    for p in pf.params:  # glse / Output_partial may only be read (no-split form)
+        s = _shape(p)
+        if p in (Q, Qpe, KV, Kpe, bt, sl, O):
+            continue
+        if len(s) == 3 and glse is None and s[:2] == (b, hq):
+            glse = p
+        elif len(s) == 4 and opart is None and s[:2] == (b, hq):
+            opart = p
+    kv_shape = _shape(KV)
+    if len(kv_shape) != 3 or kv_shape[1] != 1 or kv_shape[2] != dv or _shape(Kpe)[-1] != dpe:
+        _fail(fam, "KV must be [rows, 1, dv] and K_pe [rows, 1, dpe] (one latent KV head)")
+    if _shape(Qpe)[:2] != (b, hq) or _shape(sl) != (b,) or _shape(bt)[0] != b:
+        _fail(fam, "batch/head dims disagree")
+    max_pages = _shape(bt)[1]
+    page = _page_size_from_trace(pf, bt)
+    if page is None:
+        page = kv_shape[0] // b // max_pages
+    num_split = _shape(glse)[-1] if glse is not None else 1
+    # scale: exp2(acc_s * c - max * c), c = sm_scale * log2(e)
+    sm_scale = None
+    for op in _ops(pf, ("store",)):
+        v = op.args[2]
+        if isinstance(v, Expr) and v.has_op("exp2") and len(op.args[0].shape) == 2:
+            cs = [c for c in v.consts() if isinstance(c, float) and c > 0]
+            if cs:
+                sm_scale = cs[0] / LOG2E_REF
+                break
+    if sm_scale is None:
+        _fail(fam, "could not read the softmax scale")
+    kv_scale = None
+    if KV.dtype == "float8_e4m3":
+        sc = [p for p in pf.params if p.dtype == "float32" and math.prod(_shape(p)) == 1]
+        if len(sc) != 1:
+            _fail(fam, "fp8 KV needs one float32 [1] scale parameter")
+        kv_scale = _index(pf, sc[0])
+    elif KV.dtype not in ("float16", "bfloat16"):
+        _fail(fam, f"KV dtype {KV.dtype}")
+    if Q.dtype not in ("float16", "bfloat16") or Qpe.dtype != Q.dtype:
+        _fail(fam, f"Q dtype {Q.dtype}")
+    if O.dtype not in ("float16", "bfloat16"):
+        _fail(fam, f"Output dtype {O.dtype}")
+    return Plan(fam, pf.params, [_index(pf, O)], dict(
+        q=_index(pf, Q), q_pe=_index(pf, Qpe), kv=_index(pf, KV), k_pe=_index(pf, Kpe),
+        block_table=_index(pf, bt), seqlens=_index(pf, sl), o=_index(pf, O),
+        glse=None if glse is None else _index(pf, glse),
+        o_partial=None if opart is None else _index(pf, opart), kv_scale=kv_scale, B=b, Hq=hq,
+        dv=dv, dpe=dpe, page=page, max_pages=max_pages, num_split=num_split, sm_scale=sm_scale,
+        q_dtype=Q.dtype, kv_dtype=KV.dtype, o_dtype=O.dtype))
+
+
+def recognize(pf) -> Plan:
+    """Return the :class:`Plan` for ``pf`` or raise :class:`UnsupportedProgram`."""
+    names = set(_op_names(pf))
+    ints = [p for p in pf.params if p.dtype == "int32"]
+    n_gemm = sum(1 for op in _ops(pf, _GEMM))
+    try:
+        if ints and n_gemm >= 3:
+            return _mla(pf, names)
+        if n_gemm == 2 and names & {"ppl_reduce_max", "reduce_max"}:
+            return _flashattn(pf, names)
+        if n_gemm == 1 and not names & {"ppl_exp", "ppl_reduce_max", "reduce_max"}:
+            return _gemm(pf, names)
+        if "ppl_rope_add" in names:
+            return _rope(pf, names)
+        if {"ppl_reduce_sum", "ppl_rsqrt"} <= names:
+            return _rmsnorm(pf, names)
+        if {"ppl_exp", "ppl_div"} <= names:
+            return _swiglu(pf, names)
+    except UnsupportedProgram:
+        raise
+    except (TypeError, ValueError, IndexError) as e:  # malformed trace
+        raise UnsupportedProgram(f"{pf.name}: could not analyse program: {e}") from e
+    raise UnsupportedProgram(
+        f"{pf.name}: no gfx950 kernel matches this program (ops: {sorted(names)}). Supported "
+        f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla")
