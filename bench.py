@@ -8,10 +8,13 @@ reported in "configs". A step is one pass of the config's kernel(s) over one bat
 input already resident in HBM. For working sets that fit the 256 MB Infinity Cache, steps rotate
 over enough input copies (> 512 MiB in total) that no step reads another step's data from cache.
 
-roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch duration, the duration
-measured with HIP events recorded on the stream the kernels run on (torch's current stream),
-each launch preceded by a 512 MiB cache flush. cpu_baseline = the oracle (restated reference
-torch path) on a bounded sample, timed on this host's cores.
+The timed steps are replayed from one HIP graph (captured from torch's current stream, which
+is the stream every kernel is launched on), between device synchronisations, and timed with HIP
+events on that stream. roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch
+duration, the mean taken over a graph of back-to-back launches (rotating input copies); each
+record also carries the median of single launches that each follow a 512 MiB cache flush.
+cpu_baseline = the oracle (restated reference torch path) on a bounded sample, timed on this
+host's cores.
 """
 import argparse
 import json
@@ -46,33 +49,80 @@ def _copies_for(nbytes):
     return max(1, math.ceil(CACHE_EVICT_BYTES / max(nbytes, 1)))
 
 
+def _capture(fns, n):
+    """A HIP graph of n launches cycling over fns (None if capture is not possible)."""
+    try:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fns[0]()  # warm any lazy state outside the capture
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                for i in range(n):
+                    fns[i % len(fns)]()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        return g
+    except Exception as e:  # pragma: no cover - reported in the JSON
+        log(f"[bench] graph capture failed ({e}); timing eager launches")
+        return None
+
+
 def time_steps(fns, steps, warmup):
-    """Run fns[i % len] warmup times then steps times; return ms per step (device-synchronised)."""
+    """ms per step over exactly `steps` steps after `warmup` untimed ones. The steps are
+    replayed from one HIP graph (launch-bound host loops would otherwise starve ~10 us
+    kernels); bracketed by device synchronisation, timed by HIP events on the replay stream."""
     for i in range(warmup):
         fns[i % len(fns)]()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    g = _capture(fns, steps)
+    if g is not None:
+        g.replay()  # warm replay
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        g.replay()
+        en.record()
+        torch.cuda.synchronize()
+        return st.elapsed_time(en) / steps, "hip-graph"
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
     for i in range(steps):
         fns[i % len(fns)]()
+    en.record()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    return st.elapsed_time(en) / steps, "eager"
 
 
-def time_launches(fn, reps, flush):
-    """Mean duration (ms) of single launches of fn, HIP events on the current stream, cache
-    flushed before each launch."""
-    st = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    en = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    fn()
-    torch.cuda.synchronize()
-    for i in range(reps):
+def time_launches(fns, reps, flush):
+    """Mean launch duration (ms): `reps` back-to-back launches replayed from a HIP graph, HIP
+    events on the stream they run on, divided by reps. Inputs rotate over copies sized to defeat
+    the Infinity Cache. Also returns the median of single launches each after a cache flush."""
+    g = _capture(fns, reps)
+    mean = None
+    if g is not None:
+        g.replay()
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        g.replay()
+        en.record()
+        torch.cuda.synchronize()
+        mean = st.elapsed_time(en) / reps
+    n1 = min(reps, 20)
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
+    for i in range(n1):
         flush.zero_()
         st[i].record()
-        fn()
+        fns[0]()
         en[i].record()
     torch.cuda.synchronize()
     ts = sorted(a.elapsed_time(b) for a, b in zip(st, en))
-    return sum(ts) / len(ts), ts[len(ts) // 2]
+    med = ts[len(ts) // 2]
+    return (mean if mean is not None else med), med
 
 
 def cpu_time(fn, reps=3):
@@ -109,12 +159,12 @@ def bench_rmsnorm(args, dev, flush, cpu):
         y = torch.empty_like(x)
         sets.append((x, wt, y))
     fns = [lambda s=s: k(*s) for s in sets]
-    ms = time_steps(fns, args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(fns[0], 50, flush)
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 200, flush)
     res = {"workload": "rmsnorm_fp16_4096x4096", "value": nbytes / (ms * 1e-3) / 1e9,
            "unit": "GB/s", "ms_per_step": ms, "dtype": "f16",
            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
-           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
         xs, ws = w.tensors["x"], w.tensors["w"]
@@ -135,12 +185,12 @@ def bench_swiglu(args, dev, flush, cpu):
     g, u = w.tensors["gate"].to(dev), w.tensors["up"].to(dev)
     o = torch.empty_like(g)
     fns = [lambda: k(g, u, o)]
-    ms = time_steps(fns, args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(fns[0], 30, flush)
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 50, flush)
     res = {"workload": "swiglu_bf16_8192x14336", "value": nbytes / (ms * 1e-3) / 1e9,
            "unit": "GB/s", "ms_per_step": ms, "dtype": "bf16",
            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
-           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
         gs, us = w.tensors["gate"][:1024], w.tensors["up"][:1024]
@@ -165,12 +215,12 @@ def bench_rope(args, dev, flush, cpu):
         sets.append((t["q"], t["k"], t["cos"], t["sin"], torch.empty_like(t["q"]),
                      torch.empty_like(t["k"])))
     fns = [lambda s=s: k(*s) for s in sets]
-    ms = time_steps(fns, args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(fns[0], 50, flush)
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 200, flush)
     res = {"workload": "rope_qk_bf16_8192x32x128", "value": nbytes / (ms * 1e-3) / 1e9,
            "unit": "GB/s", "ms_per_step": ms, "dtype": "bf16",
            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
-           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes}
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
         q, kk, c, s = (w.tensors[n][:1024] for n in ("q", "k", "cos", "sin"))
@@ -193,8 +243,8 @@ def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float1
     a, b = w.tensors["a"].to(dev), w.tensors["b"].to(dev)
     c = torch.empty(M, N, dtype=torch.float16, device=dev)
     fns = [lambda: k(a, b, c)]
-    ms = time_steps(fns, args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(fns[0], 30, flush)
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 50, flush)
     skinny = M <= 64
     if skinny:
         rl = roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS)
@@ -202,7 +252,7 @@ def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float1
         rl = roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s", MFMA_PEAK["fp16"])
     res = {"workload": f"gemm_{dn}_{M}x{N}x{K}", "value": flops / (ms * 1e-3) / 1e12,
            "unit": "TFLOP/s", "ms_per_step": ms, "dtype": "f16" if dn == "float16" else "bf16",
-           "roofline": rl, "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms,
+           "roofline": rl, "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
            "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
@@ -226,14 +276,14 @@ def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
     q, kk, v = (w.tensors[n].to(dev) for n in ("q", "k", "v"))
     o = torch.empty_like(q)
     fns = [lambda: k(q, kk, v, o)]
-    ms = time_steps(fns, args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(fns[0], 10, flush)
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 10, flush)
     res = {"workload": f"flashattn_bf16_b{B}h{H}s{S}d{D}_{'causal' if causal else 'full'}",
            "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
            "dtype": "bf16",
            "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
                                 MFMA_PEAK["bf16"]),
-           "kernel_ms_mean": mean_ms, "kernel_ms_median": med_ms, "algorithmic_flops": flops}
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_flops": flops}
     if cpu:
         from oracle import ref
         t = cpu_time(lambda: ref.flashattn_ref(w.tensors["q"], w.tensors["k"], w.tensors["v"],
@@ -266,8 +316,8 @@ def bench_mla(args, dev, flush, cpu):
         ops.mla_decode(q[..., :dv], q[..., dv:], kv[:, :dv], kv[:, dv:], t["block_table"],
                        t["seqlens"], out, ws, a["page"], num_split, a["sm_scale"], t["kv_scale"])
 
-    ms = time_steps([run], args.steps, args.warmup)
-    mean_ms, med_ms = time_launches(run, 50, flush)
+    ms, how = time_steps([run], args.steps, args.warmup)
+    mean_ms, med_ms = time_launches([run], 100, flush)
     res = {"workload": "mla_decode_fp8_b64_h128_d576", "value": nbytes / (ms * 1e-3) / 1e9,
            "unit": "GB/s", "ms_per_step": ms, "dtype": "fp8e4m3-kv/bf16-q",
            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),

@@ -59,9 +59,19 @@ struct h16 {
   static TLM_DEV float hi(uint32_t w) {
     return IS_BF16 ? __uint_as_float(w & 0xffff0000u) : f16_bits_to_f32(w >> 16);
   }
+  // Two floats -> two 16-bit values in one dword, round-to-nearest-even
+  // (one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).
   static TLM_DEV uint32_t pack(float a, float b) {
-    return IS_BF16 ? (f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16))
-                   : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    if constexpr (IS_BF16) {
+      typedef __bf16 o2 __attribute__((ext_vector_type(2)));
+      o2 v = __builtin_convertvector((f2){a, b}, o2);
+      return __builtin_bit_cast(uint32_t, v);
+    } else {
+      typedef _Float16 o2 __attribute__((ext_vector_type(2)));
+      o2 v = __builtin_convertvector((f2){a, b}, o2);
+      return __builtin_bit_cast(uint32_t, v);
+    }
   }
   static TLM_DEV float to_f32(uint32_t b16) {
     return IS_BF16 ? bf16_bits_to_f32(b16) : f16_bits_to_f32(b16);

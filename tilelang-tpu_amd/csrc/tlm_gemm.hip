@@ -1,5 +1,388 @@
-// GEMM C = A * B on MFMA (fp16 / bf16 in, fp32 accumulate).
+// GEMM C = A * B on gfx950 MFMA (fp16 / bf16 in, fp32 accumulate, one rounding on store).
+//
+// Reference semantics: ppl_gemm with transpose_B=False is C += A*B into an fp32 tile
+// (src/target/codegen_ppl.cc:1244-1279, tpu_bdc_fp_mm), the matmul demo fills C with 0, loops over
+// K and casts the fp32 tile to the output dtype once (tpu_demo/matmul/tpu_test_matmul_fp16.py:19-29).
+//
+// Main kernel (any M, N; K % 8 == 0, N % 8 == 0 for row-major B):
+//   * 256x256 output tile per workgroup, BK = 64, 512 threads = 8 waves of 128x64 sub-tiles;
+//   * v_mfma_f32_32x32x16_{f16,bf16}: per wave 4x2 accumulator tiles = 128 fp32 VGPRs;
+//   * A tile [256][64] and B tile [64][256] (row-major B kept row-major) double-buffered in LDS
+//     with padded pitches; global loads for tile k+1 are in flight while tile k is multiplied;
+//   * the B operand (8 consecutive k of one column per lane) is read with ds_read_b64_tr_b16,
+//     which transposes 4x16 blocks of 16-bit values across each 16-lane group, so B needs no
+//     transpose in registers or in a separate pass;
+//   * workgroup -> tile order is XCD-aware: consecutive workgroup ids land on different XCDs
+//     (round-robin dispatch), so ids are regrouped to give each XCD a compact block of tiles
+//     that shares A row-panels and B column-panels in that XCD's L2.
+// Skinny kernel (M <= 16): see gemm_skinny below.
 #include "tlm_common.h"
+
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int NTHREADS = 512;
+constexpr int A_PITCH = BK + 8;    // halves: 144-byte rows, conflict-free 16-byte column reads
+constexpr int BN_PITCH = BN + 16;  // halves: 544-byte rows, conflict-free transpose reads
+constexpr int BT_PITCH = BK + 8;   // halves: B^T tile [n][k]
+constexpr int A_STAGE = BM * A_PITCH;
+constexpr int B_STAGE_N = BK * BN_PITCH;
+constexpr int B_STAGE_T = BN * BT_PITCH;
+
+template <bool BF16>
+struct mfma_t;
+template <>
+struct mfma_t<false> {
+  typedef f16x8 v8;
+  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct mfma_t<true> {
+  typedef bf16x8 v8;
+  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Transposed LDS read: 4 k-rows starting at `p` (lane's own row/column chunk, see call site).
+TLM_DEV s16x4 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+template <typename V8>
+TLM_DEV V8 cat4(s16x4 lo, s16x4 hi) {
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(V8, v);
+}
+
+// Tile order: regroup workgroup ids so each XCD (id % 8) gets a contiguous range of the
+// grouped (GROUP_M rows of tiles at a time) tile sequence.
+TLM_DEV void tile_of(int wg, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int lin = wg;
+  if (total % 8 == 0) lin = (wg % 8) * (total / 8) + wg / 8;
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = lin / per_group;
+  const int first_m = g * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int r = lin % per_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
+template <int OUT>
+TLM_DEV void store_out(void* C, int64_t idx, float v) {
+  if constexpr (OUT == TLM_F32)
+    ((float*)C)[idx] = v;
+  else if constexpr (OUT == TLM_BF16)
+    ((uint16_t*)C)[idx] = (uint16_t)f32_to_bf16_bits(v);
+  else
+    ((uint16_t*)C)[idx] = (uint16_t)f32_to_f16_bits(v);
+}
+
+template <bool BF16, bool TRANS_B, int OUT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __restrict__ A,
+                                                           const uint16_t* __restrict__ B,
+                                                           void* __restrict__ C, int M, int N,
+                                                           int K) {
+  using MT = mfma_t<BF16>;
+  using v8 = typename MT::v8;
+  constexpr int B_STAGE = TRANS_B ? B_STAGE_T : B_STAGE_N;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (A_STAGE + B_STAGE)];
+  uint16_t* sA = smem;
+  uint16_t* sB = smem + 2 * A_STAGE;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;  // 0..1: 128-row half
+  const int wn = wave & 3;   // 0..3: 64-col quarter
+  int tm, tn;
+  tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = (K + BK - 1) / BK;
+
+  // global -> register staging (4 A vectors + 4 B vectors of 8 halves per thread)
+  u32x4 ra[4], rb[4];
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
+      const int gm = m0 + r, gk = k0 + c;
+      ra[p] = (gm < M && gk < K) ? *(const u32x4*)(A + (int64_t)gm * K + gk) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (TRANS_B) {
+        const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
+        const int gn = n0 + r, gk = k0 + c;
+        rb[p] = (gn < N && gk < K) ? *(const u32x4*)(B + (int64_t)gn * K + gk)
+                                   : u32x4{0, 0, 0, 0};
+      } else {
+        const int r = (tid >> 5) + 16 * p, c = (tid & 31) * 8;
+        const int gk = k0 + r, gn = n0 + c;
+        rb[p] = (gk < K && gn < N) ? *(const u32x4*)(B + (int64_t)gk * N + gn)
+                                   : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int stage) {
+    uint16_t* a = sA + stage * A_STAGE;
+    uint16_t* b = sB + stage * B_STAGE;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
+      *(u32x4*)(a + r * A_PITCH + c) = ra[p];
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (TRANS_B) {
+        const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
+        *(u32x4*)(b + r * BT_PITCH + c) = rb[p];
+      } else {
+        const int r = (tid >> 5) + 16 * p, c = (tid & 31) * 8;
+        *(u32x4*)(b + r * BN_PITCH + c) = rb[p];
+      }
+    }
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  // per-lane constant offsets of the MFMA operand reads
+  const int a_row = wm * 128 + (lane & 31);
+  const int a_col = 8 * (lane >> 5);
+  // transpose-read lane roles: group h of 16 lanes, row r = j/4 within the 4-row block, chunk q
+  const int h = lane >> 4, j = lane & 15;
+  const int tr_n = wn * 64 + 16 * (h & 1) + 4 * (j & 3);
+  const int tr_k = 8 * (h >> 1) + (j >> 2);
+  const int bt_row = wn * 64 + (lane & 31);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    const bool has_next = kt + 1 < KT;
+    if (has_next) load_tile(kt + 1);
+    const uint16_t* a = sA + cur * A_STAGE;
+    const uint16_t* b = sB + cur * B_STAGE;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      v8 av[4], bv[2];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        av[mi] = *(const v8*)(a + (a_row + mi * 32) * A_PITCH + ks * 16 + a_col);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        if constexpr (TRANS_B) {
+          bv[ni] = *(const v8*)(b + (bt_row + ni * 32) * BT_PITCH + ks * 16 + a_col);
+        } else {
+          const uint16_t* p = b + (ks * 16 + tr_k) * BN_PITCH + tr_n + ni * 32;
+          bv[ni] = cat4<v8>(lds_read_tr16(p), lds_read_tr16(p + 4 * BN_PITCH));
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = MT::mma(av[mi], bv[ni], acc[mi][ni]);
+    }
+    if (has_next) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8*(i/4) + 4*(lane/32) + i%4
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = m0 + wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mi][ni][i]);
+      }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Skinny GEMM (M <= 16): the whole of A fits one MFMA row block, so the kernel streams B.
+// Workgroup = 8 waves on a 64-column strip of C; the waves split K into interleaved 32-row
+// blocks, each block is one v_mfma_f32_16x16x32 per 16 columns. A operand (row m = lane%16,
+// k = 8*(lane/16)..+7) is a direct 16-byte global load. Row-major B goes through a wave-private
+// LDS buffer [32][64] and comes back through ds_read_b64_tr_b16; B^T ([N,K]) is loaded straight
+// into operand layout. The next block's loads are issued before the current block's MFMAs.
+// The 8 partial 16x64 tiles are summed through LDS at the end.
+constexpr int SK_WAVES = 8;
+constexpr int SK_NT = 64;
+constexpr int SK_BK = 32;
+constexpr int SK_BPITCH = SK_NT + 16;  // halves per LDS row of a B block (160 bytes)
+
+template <bool BF16>
+struct mfma16_t;
+template <>
+struct mfma16_t<false> {
+  typedef f16x8 v8;
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct mfma16_t<true> {
+  typedef bf16x8 v8;
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <bool BF16, bool TRANS_B, int OUT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __restrict__ A,
+                                                            const uint16_t* __restrict__ B,
+                                                            void* __restrict__ C, int M, int N,
+                                                            int K) {
+  using MT = mfma16_t<BF16>;
+  using v8 = typename MT::v8;
+  __shared__ __attribute__((aligned(16))) uint16_t sbuf[SK_WAVES][SK_BK * SK_BPITCH];
+  __shared__ float red[SK_WAVES][16][SK_NT + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * SK_NT;
+  const int KB = (K + SK_BK - 1) / SK_BK;
+  const int am = lane & 15, ak = 8 * (lane >> 4);
+  // row-major B block loads: 32 rows x 64 cols = 4 vectors per lane (rows lane/8 + 8p)
+  const int br = lane >> 3, bc = (lane & 7) * 8;
+  const int h = lane >> 4, j = lane & 15;
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{};
+
+  u32x4 ra, rb[4];
+  auto load = [&](int kb) {
+    const int k0 = kb * SK_BK;
+    ra = (am < M && k0 + ak < K) ? *(const u32x4*)(A + (int64_t)am * K + k0 + ak)
+                                 : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (TRANS_B) {
+        const int gn = n0 + 16 * p + am;
+        rb[p] = (gn < N && k0 + ak < K) ? *(const u32x4*)(B + (int64_t)gn * K + k0 + ak)
+                                        : u32x4{0, 0, 0, 0};
+      } else {
+        const int gk = k0 + br + 8 * p, gn = n0 + bc;
+        rb[p] = (gk < K && gn < N) ? *(const u32x4*)(B + (int64_t)gk * N + gn)
+                                   : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+
+  uint16_t* my = sbuf[wave];
+  int kb = wave;
+  if (kb < KB) load(kb);
+  for (; kb < KB; kb += SK_WAVES) {
+    const u32x4 ca = ra;
+    u32x4 cb[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) cb[p] = rb[p];
+    if (kb + SK_WAVES < KB) load(kb + SK_WAVES);
+    const v8 av = __builtin_bit_cast(v8, ca);
+    if constexpr (TRANS_B) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = MT::mma(av, __builtin_bit_cast(v8, cb[t]), acc[t]);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) *(u32x4*)(my + (br + 8 * p) * SK_BPITCH + bc) = cb[p];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        // 16-lane group h reads k rows 8h + (j/4) (+4), columns 16t + 4*(j%4)
+        const uint16_t* p = my + (8 * h + (j >> 2)) * SK_BPITCH + 16 * t + 4 * (j & 3);
+        const v8 bv = cat4<v8>(lds_read_tr16(p), lds_read_tr16(p + 4 * SK_BPITCH));
+        acc[t] = MT::mma(av, bv, acc[t]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+  // lane holds column 16t + lane%16, rows 4*(lane/16) + i
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][16 * t + (lane & 15)] = acc[t][i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < 16 * SK_NT; o += 64 * SK_WAVES) {
+    const int r = o / SK_NT, c = o % SK_NT;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < SK_WAVES; ++w) s += red[w][r][c];
+    if (r < M && n0 + c < N) store_out<OUT>(C, (int64_t)r * N + n0 + c, s);
+  }
+}
+
+// Generic fallback for shapes the vector kernels cannot take (K or N not a multiple of 8,
+// unaligned pointers): one thread per output, fp32 accumulation in k order.
+template <bool BF16, bool TRANS_B, int OUT>
+__global__ __launch_bounds__(256) void gemm_generic(const uint16_t* __restrict__ A,
+                                                    const uint16_t* __restrict__ B,
+                                                    void* __restrict__ C, int M, int N, int K) {
+  using H = h16<BF16>;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx % N);
+  float s = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float a = H::to_f32(A[(int64_t)m * K + k]);
+    const float b = TRANS_B ? H::to_f32(B[(int64_t)n * K + k]) : H::to_f32(B[(int64_t)k * N + n]);
+    s = fmaf(a, b, s);
+  }
+  store_out<OUT>(C, idx, s);
+}
+
+template <bool BF16, bool TRANS_B, int OUT>
+int launch(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t s) {
+  const bool vec = tlm_aligned(A, 16) && tlm_aligned(B, 16) && K % 8 == 0 &&
+                   (TRANS_B || N % 8 == 0);
+  if (vec && M <= 16) {
+    gemm_skinny<BF16, TRANS_B, OUT><<<(unsigned)((N + SK_NT - 1) / SK_NT), 64 * SK_WAVES, 0, s>>>(
+        (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
+  } else if (vec) {
+    const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    gemm_256x256<BF16, TRANS_B, OUT><<<(unsigned)tiles, NTHREADS, 0, s>>>(
+        (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
+  } else {
+    const int64_t n = (int64_t)M * N;
+    gemm_generic<BF16, TRANS_B, OUT><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
+  }
+  TLM_LAUNCH_CHECK("tlm_gemm");
+  return TLM_OK;
+}
+
+template <bool BF16, bool TRANS_B>
+int by_out(const void* A, const void* B, void* C, int M, int N, int K, int out, hipStream_t s) {
+  switch (out) {
+    case TLM_F16: return launch<BF16, TRANS_B, TLM_F16>(A, B, C, M, N, K, s);
+    case TLM_BF16: return launch<BF16, TRANS_B, TLM_BF16>(A, B, C, M, N, K, s);
+    default: return launch<BF16, TRANS_B, TLM_F32>(A, B, C, M, N, K, s);
+  }
+}
+
+}  // namespace
 
 extern "C" int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                         int in_dtype, int out_dtype, int trans_b, void* stream) {
@@ -7,7 +390,8 @@ extern "C" int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_
     tlm_set_error("tlm_gemm: null pointer argument");
     return TLM_EINVAL;
   }
-  if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+  if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX ||
+      M * N > ((int64_t)1 << 40)) {
     tlm_set_error("tlm_gemm: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                   (long long)K);
     return TLM_EINVAL;
@@ -24,8 +408,17 @@ extern "C" int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_
     tlm_set_error("tlm_gemm: out_dtype %d unsupported", out_dtype);
     return TLM_EUNSUPPORTED;
   }
+  if (!tlm_aligned(A, 2) || !tlm_aligned(B, 2) || !tlm_aligned(C, out_dtype == TLM_F32 ? 4 : 2)) {
+    tlm_set_error("tlm_gemm: misaligned pointer");
+    return TLM_EINVAL;
+  }
   if (M == 0 || N == 0) return TLM_OK;
-  (void)stream;
-  tlm_set_error("tlm_gemm: kernel not built yet");
-  return TLM_EUNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  const bool bf = in_dtype == TLM_BF16;
+  if (bf)
+    return trans_b ? by_out<true, true>(A, B, C, m, n, k, out_dtype, s)
+                   : by_out<true, false>(A, B, C, m, n, k, out_dtype, s);
+  return trans_b ? by_out<false, true>(A, B, C, m, n, k, out_dtype, s)
+                 : by_out<false, false>(A, B, C, m, n, k, out_dtype, s);
 }
