@@ -111,9 +111,11 @@ int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int
  *          separate Q / Q_pe tensors; pass q_pe = q + dv elements for a fused [.., 576] tensor.
  *   kv     token rows of the paged cache; row t at kv + t*kv_stride holds the dv latent values,
  *   k_pe   row t at k_pe + t*kpe_stride holds the dpe rope values (same convention as q_pe).
+ *   kv_rows number of token rows in the cache pool; a row index outside [0, kv_rows) produced by
+ *          a corrupt block table is read as zeros instead of faulting.
  *   block_table int32 [B, max_pages]: token j of sequence b lives in row
  *          block_table[b, j / page] * page + j % page   (example_mla_decode_paged.py:62-63).
- *   seqlens int32 [B], each in [1, max_pages*page].
+ *   seqlens int32 [B], each in [1, max_pages*page] (larger values are clamped to max_pages*page).
  *   o      [B, Hq, dv] out dtype (F16 | BF16).
  * kv_dtype: F8E4M3 (value = e4m3 decode of the byte times *kv_scale, a DEVICE fp32 scalar so
  *   that no host sync is needed; NULL means 1) | F16 | BF16 (kv_scale may be NULL).
@@ -122,7 +124,8 @@ int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int
  * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned). */
 int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
                    const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
-                   const int32_t* block_table, const int32_t* seqlens, void* o, void* ws,
+                   int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens, void* o,
+                   void* ws,
                    size_t ws_bytes, int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
                    int64_t max_pages, int num_split, float sm_scale, const float* kv_scale,
                    int q_dtype, int kv_dtype, int o_dtype, void* stream);
@@ -133,10 +136,11 @@ size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split)
 /* Integer-path check: out[i, :] = kv_bytes[row(i), :] for every token i of every sequence,
  * rows resolved through the block table exactly as tlm_mla_decode does; tokens of sequence b
  * are written at out + (cu_seqlens[b] + j) * row_bytes with cu_seqlens the exclusive prefix
- * sum of seqlens (computed on the host by the caller and passed in). Bit-exact by contract. */
-int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, const int32_t* block_table,
-                     const int32_t* seqlens, const int64_t* cu_seqlens, void* out, int64_t B,
-                     int64_t page, int64_t max_pages, void* stream);
+ * sum of seqlens (computed on the host by the caller and passed in). Rows outside [0, kv_rows)
+ * are written as zeros. Bit-exact by contract. */
+int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, int64_t kv_rows,
+                     const int32_t* block_table, const int32_t* seqlens, const int64_t* cu_seqlens,
+                     void* out, int64_t B, int64_t page, int64_t max_pages, void* stream);
 
 #ifdef __cplusplus
 }

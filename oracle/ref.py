@@ -127,18 +127,19 @@ def mla_decode_ref(q, q_pe, kv, k_pe, block_table, seqlens, page: int, sm_scale:
     """q [B,Hq,dv], q_pe [B,Hq,dpe], kv [rows,dv] / k_pe [rows,dpe] (any dtype incl. fp8),
     block_table int32 [B,P], seqlens int32 [B]. Returns [B,Hq,dv] (and lse [B,Hq], natural log)."""
     B, Hq, dv = q.shape
-    kvf = kv.reshape(kv.shape[0], -1).float() * kv_scale
-    kpf = k_pe.reshape(k_pe.shape[0], -1).float() * kv_scale
+    kv2 = kv.reshape(kv.shape[0], -1)
+    kp2 = k_pe.reshape(k_pe.shape[0], -1)
     out = torch.empty(B, Hq, dv, dtype=torch.float32)
     lse = torch.empty(B, Hq, dtype=torch.float32)
     for b in range(B):
         L = int(seqlens[b])
         rows = paged_rows(block_table, L, b, page)
-        kb = torch.cat([kvf[rows], kpf[rows]], dim=1)  # [L, dv+dpe]
+        vb = kv2[rows].float() * kv_scale  # gather, then dequantise
+        kb = torch.cat([vb, kp2[rows].float() * kv_scale], dim=1)  # [L, dv+dpe]
         qb = torch.cat([q[b].float(), q_pe[b].float()], dim=1)  # [Hq, dv+dpe]
         s = (qb @ kb.t()) * sm_scale
         lse[b] = torch.logsumexp(s, dim=-1)
-        out[b] = torch.softmax(s, dim=-1) @ kvf[rows]
+        out[b] = torch.softmax(s, dim=-1) @ vb
     o = out.to(out_dtype)
     return (o, lse) if return_lse else o
 
@@ -161,13 +162,16 @@ def mla_split_partition(seqlen: int, num_split: int, block_n: int):
 def mla_split_combine_ref(q, q_pe, kv, k_pe, block_table, seqlens, page, sm_scale, num_split,
                           block_n=64, kv_scale=1.0, out_dtype=torch.bfloat16):
     B, Hq, dv = q.shape
-    kvf = kv.reshape(kv.shape[0], -1).float() * kv_scale
-    kpf = k_pe.reshape(k_pe.shape[0], -1).float() * kv_scale
+    kv2 = kv.reshape(kv.shape[0], -1)
+    kp2 = k_pe.reshape(k_pe.shape[0], -1)
     out = torch.zeros(B, Hq, dv, dtype=torch.float32)
     log2e = 1.0 / math.log(2.0)
     for b in range(B):
         L = int(seqlens[b])
-        rows = paged_rows(block_table, L, b, page)
+        rows_all = paged_rows(block_table, L, b, page)
+        rows = torch.arange(L)
+        kvf = kv2[rows_all].float() * kv_scale
+        kpf = kp2[rows_all].float() * kv_scale
         qb = torch.cat([q[b].float(), q_pe[b].float()], dim=1)
         parts, lses = [], []
         for (st, en) in mla_split_partition(L, num_split, block_n):

@@ -102,17 +102,34 @@ def test_mla_validation_and_workspace():
     assert ws >= 64 * 128 * 4 * (512 + 1) * 4
     p = ctypes.c_void_p(0x1000)
     # workspace too small
-    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, p, p, p, p, 16, 2, 128, 512, 64, 64, 4,
-                          2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 16, 2, 128, 512, 64,
+                          64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
     assert rc == -4 and "workspace" in _err()
     # unsupported head dims
-    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, p, p, p, p, 1 << 30, 2, 128, 256, 64,
-                          64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 1 << 30, 2, 128, 256,
+                          64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
     assert rc == -2
     # null block table
-    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, None, p, p, p, 1 << 30, 2, 128, 512,
-                          64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, None, p, p, p, 1 << 30, 2, 128,
+                          512, 64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
     assert rc == -1
+    # fp16 KV with bf16 Q is not a kernel combination
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 1 << 30, 2, 128,
+                          512, 64, 64, 4, 2, 0.07, None, lib.BF16, lib.F16, lib.BF16, None)
+    assert rc == -2
+    # max_pages * page beyond the int32 token range
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 1 << 62, 2, 128,
+                          512, 64, 1 << 20, 1 << 20, 1, 0.07, None, lib.BF16, lib.F8E4M3,
+                          lib.BF16, None)
+    assert rc == -1
+
+
+def test_paged_gather_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_paged_gather(None, 576, 10, p, p, p, p, 1, 64, 4, None) == -1
+    assert L.tlm_paged_gather(p, 0, 10, p, p, p, p, 1, 64, 4, None) == -1
+    assert L.tlm_paged_gather(p, 576, 10, p, p, p, p, 0, 64, 4, None) == 0
 
 
 def test_init_without_gpu_reports_error():

@@ -1,24 +1,332 @@
 // MLA paged decode (FP8 / fp16 / bf16 latent KV) and the paged-gather integer-path check.
+//
+// Reference: examples/deepseek_mla/example_mla_decode_paged.py
+//   split kernel (:100-183): per (sequence, head block, split), loop over KV tiles of the split's
+//     token range, page address kv_start = BT[b, tok / page] * page + tok % page (:147-148),
+//     S = Q KV^T + Q_pe K_pe^T, tokens >= seqlen masked to -inf (:162-164), online softmax in the
+//     exp2 domain with scale = sm_scale * log2(e) (:12), P cast to the input dtype, O += P KV,
+//     glse = log2(l) + m * scale (:180-181);
+//   combine (:186-221): lse = log2(sum_s 2^(glse_s - max)) + max, O = sum_s O_s * 2^(glse_s - lse).
+//   Split partition (:140-144): the sequence's 64-token blocks are dealt out so the first
+//   (blocks % num_split) splits take one extra block.
+// The FP8 config stores the latent cache as OCP e4m3 with one fp32 scale: scores use
+// (Q . K_fp8) * kv_scale and the output is (P . V_fp8) * kv_scale.
+//
+// gfx950 mapping of the split kernel:
+//   * workgroup = (sequence, split, half of the query heads): 64 heads, 8 waves. The two halves of
+//     a (sequence, split) are adjacent workgroup ids, so they run concurrently and the second read
+//     of each KV tile is served by the Infinity Cache;
+//   * wave (hg, dq): 32 heads (hg) and one quarter (dq) of the contraction dims: it computes the
+//     partial S^T over d in [144*dq, 144*dq+144) and owns O^T rows d in [128*dq, 128*dq+128);
+//     the four partial S^T tiles of a head group are summed through LDS;
+//   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16 (bf16/fp16): lanes index heads, so the
+//     online softmax is lane-local; Q^T stays in VGPRs; P^T is the S^T accumulator rounded to the
+//     input dtype; V^T is read from the row-major KV tile with ds_read_b64_tr_b16;
+//   * 32-token KV tiles, gathered through the block table, fp8 decoded to bf16/fp16 (exact) while
+//     staging into a double-buffered LDS tile; the next tile's global loads overlap the MFMAs.
 #include "tlm_common.h"
 
 namespace {
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr int MLA_DV = 512, MLA_DPE = 64, MLA_D = MLA_DV + MLA_DPE;
+constexpr int MLA_WAVES = 8;
+constexpr int MLA_HEADS = 64;           // heads per workgroup
+constexpr int MLA_BN = 32;              // tokens per KV tile
+constexpr int MLA_PART_BLOCK = 64;      // split partition granularity (reference block_N)
+constexpr int KVP = MLA_D + 24;         // LDS pitch (halves): 1200 B rows
+constexpr int QK_SUB = MLA_D / 16 / 4;  // 9 k-substeps of S^T per wave
+constexpr int O_DT = MLA_DV / 4 / 32;   // 4 32-wide d tiles of O^T per wave
+
+TLM_DEV s16x4 lds_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+template <bool BF16>
+struct mla_mma;
+template <>
+struct mla_mma<false> {
+  typedef f16x8 v8;
+  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct mla_mma<true> {
+  typedef bf16x8 v8;
+  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16 OCP e4m3 bytes -> 16 values of the MFMA input type (exact: every e4m3 value is
+// representable in fp16 and bf16).
+template <bool BF16>
+TLM_DEV void fp8x16_to_h16(u32x4 in, u32x4& lo, u32x4& hi) {
+  using H = h16<BF16>;
+  u32x4 out[2];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], false);
+    const f2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)in[w], true);
+    out[w >> 1][(w & 1) * 2 + 0] = H::pack(a[0], a[1]);
+    out[w >> 1][(w & 1) * 2 + 1] = H::pack(b[0], b[1]);
+  }
+  lo = out[0];
+  hi = out[1];
+}
+
+// KV_KIND: 0 = fp8 e4m3, 1 = same 16-bit type as Q.
+template <bool BF16, int KV_KIND>
+__global__ __launch_bounds__(64 * MLA_WAVES, 1) void mla_split_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ q_pe, int64_t q_stride,
+    int64_t qpe_stride, const uint8_t* __restrict__ kv, const uint8_t* __restrict__ k_pe,
+    int64_t kv_stride_b, int64_t kpe_stride_b, int64_t kv_rows,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlens,
+    float* __restrict__ ws_o, float* __restrict__ ws_lse,
+    int Hq, int page, int max_pages, int num_split, float score_scale,
+    const float* __restrict__ kv_scale) {
+  using MT = mla_mma<BF16>;
+  using v8 = typename MT::v8;
+  __shared__ __attribute__((aligned(16))) uint16_t sKV[2][MLA_BN * KVP];
+  __shared__ float sRed[MLA_WAVES][16][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hg = wave >> 2, dq = wave & 3;
+  const int hhalves = Hq / MLA_HEADS;
+  const int lin = blockIdx.x;
+  const int hb = lin % hhalves;
+  const int split = (lin / hhalves) % num_split;
+  const int b = lin / (hhalves * num_split);
+  // clamp to what the block table can address (a larger seqlen would index past the table)
+  const int L = max(0, min(seqlens[b], max_pages * page));
+
+  // token range of this split (reference partition over 64-token blocks)
+  const int total = (L + MLA_PART_BLOCK - 1) / MLA_PART_BLOCK;
+  const int per = total / num_split, rem = total % num_split;
+  const int nb64 = per + (split < rem ? 1 : 0);
+  const int t_begin = (per * split + min(split, rem)) * MLA_PART_BLOCK;
+  const int t_end = min(t_begin + nb64 * MLA_PART_BLOCK, L);
+  const int nblk = t_end > t_begin ? (t_end - t_begin + MLA_BN - 1) / MLA_BN : 0;
+
+  const float kvs = (KV_KIND == 0 && kv_scale) ? kv_scale[0] : 1.0f;
+  const float c = score_scale * kvs;  // sm_scale * log2(e) * kv_scale
+
+  const int ql = lane & 31, g = lane >> 5;
+  const int head = hb * MLA_HEADS + hg * 32 + ql;
+  // Q^T operand for this wave's 144 contraction dims
+  v8 qreg[QK_SUB];
+#pragma unroll
+  for (int s = 0; s < QK_SUB; ++s) {
+    const int d = 16 * (QK_SUB * dq + s) + 8 * g;
+    const uint16_t* src = d < MLA_DV ? q + ((int64_t)b * Hq + head) * q_stride + d
+                                     : q_pe + ((int64_t)b * Hq + head) * qpe_stride + (d - MLA_DV);
+    qreg[s] = __builtin_bit_cast(v8, *(const u32x4*)src);
+  }
+
+  // staging: tile = 32 token rows; fp8 rows are 36 chunks of 16 bytes, 16-bit rows 72 chunks
+  constexpr int CH = KV_KIND == 0 ? MLA_D / 16 : MLA_D / 8;
+  constexpr int CH_DV = KV_KIND == 0 ? MLA_DV / 16 : MLA_DV / 8;
+  constexpr int NPASS = (MLA_BN * CH + 64 * MLA_WAVES - 1) / (64 * MLA_WAVES);
+  u32x4 rg[NPASS];
+  auto load_tile = [&](int blk) {
+    const int tok0 = t_begin + blk * MLA_BN;
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+      const int idx = tid + p * 64 * MLA_WAVES;
+      rg[p] = u32x4{0, 0, 0, 0};
+      if (idx < MLA_BN * CH) {
+        const int r = idx / CH, ch = idx % CH;
+        const int tok = tok0 + r;
+        const int64_t row =
+            tok < t_end
+                ? (int64_t)block_table[(int64_t)b * max_pages + tok / page] * page + tok % page
+                : -1;
+        if (row >= 0 && row < kv_rows) {  // rows outside the pool read as zeros
+          const uint8_t* src = ch < CH_DV ? kv + row * kv_stride_b + ch * 16
+                                          : k_pe + row * kpe_stride_b + (ch - CH_DV) * 16;
+          rg[p] = *(const u32x4*)src;
+        }
+      }
+    }
+  };
+  auto store_tile = [&](int stage) {
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+      const int idx = tid + p * 64 * MLA_WAVES;
+      if (idx < MLA_BN * CH) {
+        const int r = idx / CH, ch = idx % CH;
+        uint16_t* dst = &sKV[stage][r * KVP];
+        if constexpr (KV_KIND == 0) {
+          u32x4 lo, hi;
+          fp8x16_to_h16<BF16>(rg[p], lo, hi);
+          *(u32x4*)(dst + 16 * ch) = lo;
+          *(u32x4*)(dst + 16 * ch + 8) = hi;
+        } else {
+          *(u32x4*)(dst + 8 * ch) = rg[p];
+        }
+      }
+    }
+  };
+
+  f32x16 oacc[O_DT];
+#pragma unroll
+  for (int t = 0; t < O_DT; ++t) oacc[t] = f32x16{};
+  float m_run = -INFINITY, l_part = 0.f;
+  const int hh = lane >> 4, jj = lane & 15;
+
+  if (nblk > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int cur = blk & 1;
+    const bool has_next = blk + 1 < nblk;
+    if (has_next) load_tile(blk + 1);
+    const uint16_t* kt = sKV[cur];
+    // partial S^T[token][head] over this wave's 144 dims
+    f32x16 sacc = f32x16{};
+#pragma unroll
+    for (int s = 0; s < QK_SUB; ++s) {
+      const v8 a = *(const v8*)(kt + ql * KVP + 16 * (QK_SUB * dq + s) + 8 * g);
+      sacc = MT::mma(a, qreg[s], sacc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sRed[wave][i][lane] = sacc[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      sacc[i] = sRed[4 * hg + 0][i][lane] + sRed[4 * hg + 1][i][lane] +
+                sRed[4 * hg + 2][i][lane] + sRed[4 * hg + 3][i][lane];
+    // softmax over this tile's tokens: token = tok0 + 8(i/4) + 4g + i%4
+    const int tok0 = t_begin + blk * MLA_BN;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float x = sacc[i] * c;
+      if (tok0 + 8 * (i >> 2) + 4 * g + (i & 3) >= t_end) x = -INFINITY;
+      sacc[i] = x;
+      mloc = fmaxf(mloc, x);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.f;
+    v8 pb[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(sacc[8 * s2 + 2 * e] - m_use);
+        const float p1 = fast_exp2(sacc[8 * s2 + 2 * e + 1] - m_use);
+        psum += p0 + p1;
+        pk[e] = h16<BF16>::pack(p0, p1);
+      }
+      pb[s2] = __builtin_bit_cast(v8, pk);
+    }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < O_DT; ++dt) oacc[dt] *= alpha;
+    // O^T[d][head] += V^T[d][token] P^T[token][head]
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int base = 16 * s2 + 4 * (hh >> 1) + (jj >> 2);
+#pragma unroll
+      for (int dt = 0; dt < O_DT; ++dt) {
+        const uint16_t* p = kt + base * KVP + 128 * dq + 32 * dt + 16 * (hh & 1) + 4 * (jj & 3);
+        const s16x4 lo = lds_tr16(p), hi = lds_tr16(p + 8 * KVP);
+        const s16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        oacc[dt] = MT::mma(__builtin_bit_cast(v8, av), pb[s2], oacc[dt]);
+      }
+    }
+    if (has_next) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // partial results: O_s (normalised by this split's l) and lse_s = m + log2(l), log2 domain
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const int64_t slot = ((int64_t)b * Hq + head) * num_split + split;
+  float* o = ws_o + slot * MLA_DV;
+#pragma unroll
+  for (int dt = 0; dt < O_DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 128 * dq + 32 * dt + 8 * (i >> 2) + 4 * g + (i & 3);
+      o[d] = oacc[dt][i] * inv;
+    }
+  if (dq == 0 && g == 0) ws_lse[slot] = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
+}
+
+// LSE combine: one workgroup of 128 threads per (sequence, head), 4 output values per thread.
+template <bool OUT_BF16>
+__global__ __launch_bounds__(128) void mla_combine_kernel(const float* __restrict__ ws_o,
+                                                          const float* __restrict__ ws_lse,
+                                                          uint16_t* __restrict__ out,
+                                                          int num_split, const float* kv_scale,
+                                                          int kv_is_fp8) {
+  const int64_t bh = blockIdx.x;
+  const float* lse = ws_lse + bh * num_split;
+  float mx = -INFINITY;
+  for (int s = 0; s < num_split; ++s) mx = fmaxf(mx, lse[s]);
+  float sum = 0.f;
+  for (int s = 0; s < num_split; ++s) sum += fast_exp2(lse[s] - mx);
+  const float lse_tot = mx + __log2f(sum);
+  const int d = threadIdx.x * 4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < num_split; ++s) {
+    if (lse[s] == -INFINITY) continue;
+    const float w = fast_exp2(lse[s] - lse_tot);
+    const f32x4 v = *(const f32x4*)(ws_o + (bh * num_split + s) * MLA_DV + d);
+    acc += v * w;
+  }
+  const float kvs = (kv_is_fp8 && kv_scale) ? kv_scale[0] : 1.0f;
+  acc *= kvs;
+  using H = h16<OUT_BF16>;
+  u32x2 pk = {H::pack(acc[0], acc[1]), H::pack(acc[2], acc[3])};
+  *(u32x2*)(out + bh * MLA_DV + d) = pk;
+}
+
 // ------------------------------------------------------------------------------------------------
 // Paged gather: one 64-lane wave per token row; rows resolved through the block table exactly
-// as the decode kernel resolves them (examples/deepseek_mla/example_mla_decode_paged.py:62-63).
+// as the decode kernel resolves them (example_mla_decode_paged.py:62-63).
 __global__ __launch_bounds__(256) void paged_gather_kernel(
-    const uint8_t* __restrict__ kv, int64_t row_bytes, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seqlens, const int64_t* __restrict__ cu, uint8_t* __restrict__ out,
-    int64_t page, int64_t max_pages) {
+    const uint8_t* __restrict__ kv, int64_t row_bytes, int64_t kv_rows,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlens,
+    const int64_t* __restrict__ cu, uint8_t* __restrict__ out, int64_t page, int64_t max_pages) {
   const int b = blockIdx.y;
-  const int64_t L = seqlens[b];
+  const int64_t L = max((int64_t)0, min((int64_t)seqlens[b], max_pages * page));
   const int lane = threadIdx.x & 63;
   for (int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); j < L; j += (int64_t)gridDim.x * 4) {
     const int64_t row = (int64_t)block_table[b * max_pages + j / page] * page + j % page;
-    const uint8_t* src = kv + row * row_bytes;
+    const bool ok = row >= 0 && row < kv_rows;
+    const uint8_t* src = kv + (ok ? row : 0) * row_bytes;
     uint8_t* dst = out + (cu[b] + j) * row_bytes;
-    for (int64_t c = lane; c < row_bytes; c += 64) dst[c] = src[c];
+    for (int64_t c = lane; c < row_bytes; c += 64) dst[c] = ok ? src[c] : (uint8_t)0;
   }
+}
+
+template <bool BF16, int KV_KIND>
+int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, const void* kv,
+                 const void* k_pe, int64_t kvs_b, int64_t kpes_b, int64_t kv_rows, const int32_t* bt,
+                 const int32_t* sl, float* ws_o, float* ws_lse, int B, int Hq, int page,
+                 int max_pages, int ns, float sc, const float* kv_scale, hipStream_t st) {
+  const int64_t nwg = (int64_t)B * ns * (Hq / MLA_HEADS);
+  mla_split_kernel<BF16, KV_KIND><<<(unsigned)nwg, 64 * MLA_WAVES, 0, st>>>(
+      (const uint16_t*)q, (const uint16_t*)q_pe, qs, qpes, (const uint8_t*)kv,
+      (const uint8_t*)k_pe, kvs_b, kpes_b, kv_rows, bt, sl, ws_o, ws_lse, Hq, page, max_pages, ns, sc,
+      kv_scale);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (split)");
+  return TLM_OK;
 }
 
 }  // namespace
@@ -31,8 +339,9 @@ extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int
 
 extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
                               int64_t q_pe_stride, const void* kv, const void* k_pe,
-                              int64_t kv_stride, int64_t kpe_stride, const int32_t* block_table,
-                              const int32_t* seqlens, void* o, void* ws, size_t ws_bytes,
+                              int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                              const int32_t* block_table, const int32_t* seqlens, void* o,
+                              void* ws, size_t ws_bytes,
                               int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
                               int64_t max_pages, int num_split, float sm_scale,
                               const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
@@ -41,17 +350,22 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
     tlm_set_error("tlm_mla_decode: null pointer argument");
     return TLM_EINVAL;
   }
-  if (B < 0 || Hq <= 0 || page <= 0 || max_pages <= 0 || num_split <= 0 || num_split > 64) {
+  if (B < 0 || B > (1 << 20) || Hq <= 0 || page <= 0 || max_pages <= 0 || num_split <= 0 ||
+      num_split > 64 || page > (1 << 20) || max_pages > (1 << 20)) {
     tlm_set_error("tlm_mla_decode: bad sizes B=%lld Hq=%lld page=%lld max_pages=%lld splits=%d",
                   (long long)B, (long long)Hq, (long long)page, (long long)max_pages, num_split);
     return TLM_EINVAL;
   }
-  if (dv != 512 || dpe != 64 || Hq % 64 != 0) {
+  if (max_pages * page > INT32_MAX) {
+    tlm_set_error("tlm_mla_decode: max_pages * page exceeds the int32 token range");
+    return TLM_EINVAL;
+  }
+  if (dv != MLA_DV || dpe != MLA_DPE || Hq % MLA_HEADS != 0 || Hq > 4096) {
     tlm_set_error("tlm_mla_decode: kernels exist for dv=512, dpe=64, Hq a multiple of 64 "
                   "(got dv=%lld dpe=%lld Hq=%lld)", (long long)dv, (long long)dpe, (long long)Hq);
     return TLM_EUNSUPPORTED;
   }
-  if (q_stride < dv || q_pe_stride < dpe || kv_stride < dv || kpe_stride < dpe) {
+  if (q_stride < dv || q_pe_stride < dpe || kv_stride < dv || kpe_stride < dpe || kv_rows < 0) {
     tlm_set_error("tlm_mla_decode: row strides smaller than the row widths");
     return TLM_EINVAL;
   }
@@ -61,20 +375,54 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
     return TLM_EWORKSPACE;
   }
   if ((q_dtype != TLM_BF16 && q_dtype != TLM_F16) || (o_dtype != TLM_BF16 && o_dtype != TLM_F16) ||
-      (kv_dtype != TLM_F8E4M3 && kv_dtype != TLM_BF16 && kv_dtype != TLM_F16)) {
-    tlm_set_error("tlm_mla_decode: dtype combination q=%d kv=%d o=%d unsupported", q_dtype,
-                  kv_dtype, o_dtype);
+      (kv_dtype != TLM_F8E4M3 && kv_dtype != q_dtype)) {
+    tlm_set_error("tlm_mla_decode: dtype combination q=%d kv=%d o=%d unsupported (kv must be "
+                  "fp8 e4m3 or Q's dtype)", q_dtype, kv_dtype, o_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  const int64_t kv_elt = kv_dtype == TLM_F8E4M3 ? 1 : 2;
+  // every 16-byte chunk of Q and KV rows must be aligned
+  if (!tlm_aligned(q, 16) || !tlm_aligned(q_pe, 16) || !tlm_aligned(kv, 16) ||
+      !tlm_aligned(k_pe, 16) || q_stride % 8 || q_pe_stride % 8 || (kv_stride * kv_elt) % 16 ||
+      (kpe_stride * kv_elt) % 16 || !tlm_aligned(o, 8) || !tlm_aligned(ws, 16)) {
+    tlm_set_error("tlm_mla_decode: Q/KV rows must start on 16-byte boundaries");
     return TLM_EUNSUPPORTED;
   }
   if (B == 0) return TLM_OK;
-  (void)sm_scale;
-  (void)kv_scale;
-  (void)stream;
-  tlm_set_error("tlm_mla_decode: kernel not built yet");
-  return TLM_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  float* ws_o = (float*)ws;
+  float* ws_lse = ws_o + (size_t)B * Hq * num_split * dv;
+  const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  const bool bf = q_dtype == TLM_BF16;
+  const int b = (int)B, h = (int)Hq, pg = (int)page, mp = (int)max_pages;
+  int rc;
+  if (kv_dtype == TLM_F8E4M3)
+    rc = bf ? launch_split<true, 0>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                    kpe_stride, kv_rows, block_table, seqlens, ws_o, ws_lse, b, h, pg, mp,
+                                    num_split, sc, kv_scale, st)
+            : launch_split<false, 0>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                     kpe_stride, kv_rows, block_table, seqlens, ws_o, ws_lse, b, h, pg, mp,
+                                     num_split, sc, kv_scale, st);
+  else
+    rc = bf ? launch_split<true, 1>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride * 2,
+                                    kpe_stride * 2, kv_rows, block_table, seqlens, ws_o, ws_lse, b, h, pg,
+                                    mp, num_split, sc, kv_scale, st)
+            : launch_split<false, 1>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride * 2,
+                                     kpe_stride * 2, kv_rows, block_table, seqlens, ws_o, ws_lse, b, h, pg,
+                                     mp, num_split, sc, kv_scale, st);
+  if (rc) return rc;
+  const unsigned ncomb = (unsigned)(B * Hq);
+  if (o_dtype == TLM_BF16)
+    mla_combine_kernel<true><<<ncomb, 128, 0, st>>>(ws_o, ws_lse, (uint16_t*)o, num_split,
+                                                    kv_scale, kv_dtype == TLM_F8E4M3);
+  else
+    mla_combine_kernel<false><<<ncomb, 128, 0, st>>>(ws_o, ws_lse, (uint16_t*)o, num_split,
+                                                     kv_scale, kv_dtype == TLM_F8E4M3);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (combine)");
+  return TLM_OK;
 }
 
-extern "C" int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes,
+extern "C" int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, int64_t kv_rows,
                                 const int32_t* block_table, const int32_t* seqlens,
                                 const int64_t* cu_seqlens, void* out, int64_t B, int64_t page,
                                 int64_t max_pages, void* stream) {
@@ -82,14 +430,14 @@ extern "C" int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes,
     tlm_set_error("tlm_paged_gather: null pointer argument");
     return TLM_EINVAL;
   }
-  if (B < 0 || B > 65535 || row_bytes <= 0 || page <= 0 || max_pages <= 0) {
+  if (B < 0 || B > 65535 || row_bytes <= 0 || page <= 0 || max_pages <= 0 || kv_rows < 0) {
     tlm_set_error("tlm_paged_gather: bad sizes");
     return TLM_EINVAL;
   }
   if (B == 0) return TLM_OK;
   dim3 grid(256, (unsigned)B);
   paged_gather_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
-      (const uint8_t*)kv_bytes, row_bytes, block_table, seqlens, cu_seqlens, (uint8_t*)out, page,
+      (const uint8_t*)kv_bytes, row_bytes, kv_rows, block_table, seqlens, cu_seqlens, (uint8_t*)out, page,
       max_pages);
   TLM_LAUNCH_CHECK("tlm_paged_gather");
   return TLM_OK;

@@ -35,11 +35,11 @@ _SIGNATURES = {
     "tlm_flash_attn_fwd": ([c_void_p] * 4 + [c_int64] * 4 + [c_int, c_float, c_int, c_void_p],
                            c_int),
     "tlm_mla_decode": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
-                        c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
+                        c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
                        [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int, c_void_p], c_int),
     "tlm_mla_workspace_bytes": ([c_int64, c_int64, c_int64, c_int], c_size_t),
-    "tlm_paged_gather": ([c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
-                          c_int64, c_int64, c_void_p], c_int),
+    "tlm_paged_gather": ([c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                          c_int64, c_int64, c_int64, c_void_p], c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -163,6 +163,11 @@ def _rows(name, t, width):
     return t.data_ptr(), (rs if rs is not None else width)
 
 
+def _rows_count(kv, dv, k_pe, dpe) -> int:
+    """Token rows addressable in both the latent and the rope views of the cache."""
+    return min(kv.numel() // dv, k_pe.numel() // dpe)
+
+
 def mla_decode(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, page: int,
                num_split: int, sm_scale: float, kv_scale: Optional[torch.Tensor] = None):
     """Paged MLA decode. q [B,Hq,dv], q_pe [B,Hq,dpe], kv [rows,...,dv], k_pe [rows,...,dpe]
@@ -195,7 +200,7 @@ def mla_decode(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, page: in
         raise ValueError("kv_scale must be a one-element float32 tensor")
     ws_bytes = workspace.numel() * workspace.element_size()
     lib.call("tlm_mla_decode", q_ptr, qpe_ptr, q_rs, qpe_rs, kv_ptr, kpe_ptr, kv_rs, kpe_rs,
-             _ptr(block_table), _ptr(seqlens), _ptr(out), _ptr(workspace), ws_bytes, B, Hq, dv,
+             _rows_count(kv, dv, k_pe, dpe), _ptr(block_table), _ptr(seqlens), _ptr(out), _ptr(workspace), ws_bytes, B, Hq, dv,
              dpe, page, block_table.shape[1], num_split, float(sm_scale), _ptr(kv_scale),
              dtype_code(q.dtype), dtype_code(kv.dtype), dtype_code(out.dtype), _stream(dev))
     return out
@@ -205,7 +210,9 @@ def paged_gather(kv_bytes: torch.Tensor, block_table, seqlens, cu_seqlens, out, 
     """Bit-exact gather of every sequence's token rows through the block table."""
     dev = _dev(kv_bytes, block_table, seqlens, cu_seqlens, out)
     row_bytes = kv_bytes.shape[-1] * kv_bytes.element_size()
-    lib.call("tlm_paged_gather", _ptr(kv_bytes), row_bytes, _ptr(block_table), _ptr(seqlens),
+    kv_rows = kv_bytes.numel() * kv_bytes.element_size() // row_bytes
+    lib.call("tlm_paged_gather", _ptr(kv_bytes), row_bytes, kv_rows, _ptr(block_table),
+             _ptr(seqlens),
              _ptr(cu_seqlens), _ptr(out), block_table.shape[0], page, block_table.shape[1],
              _stream(dev))
     return out
