@@ -322,7 +322,7 @@ def bench_mla(args, dev, flush, cpu):
            "unit": "GB/s", "ms_per_step": ms, "dtype": "fp8e4m3-kv/bf16-q",
            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
            "tflops": flops / (mean_ms * 1e-3) / 1e12, "kernel_ms_mean": mean_ms,
-           "kernel_ms_median": med_ms, "algorithmic_bytes": nbytes, "sum_seqlens": sum_l,
+           "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_bytes": nbytes, "sum_seqlens": sum_l,
            "num_split": num_split}
     if cpu:
         from oracle import ref

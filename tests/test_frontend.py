@@ -1,0 +1,152 @@
+"""CPU tests of the drop-in boundary: tracing, recognition, JITKernel surface, argument
+validation (modelled on cython_wrapper.pyx:76-79, 130-150 and base.py:20-44 of the reference)."""
+import math
+
+import pytest
+import torch
+
+import tilelang
+import tilelang.language as T
+from tilelang.jit.adapter.base import legalize_result_idx
+from tilelang.jit.adapter.mi355x import UnsupportedProgram
+from tilelang.testing import programs
+
+
+def test_recognize_each_family():
+    cases = [
+        (programs.rms_norm(128, 128, 32), "rmsnorm", dict(eps=1e-12, cols=128, w=None)),
+        (programs.rms_norm(64, 4096, 1, eps=1e-6, with_weight=True), "rmsnorm",
+         dict(eps=1e-6, w=1, y=2)),
+        (programs.matmul(64, 96, 32, 32, 32, 32), "gemm", dict(M=64, N=96, K=32, trans_b=False)),
+        (programs.matmul(64, 96, 32, 32, 32, 32, trans_b=True), "gemm", dict(trans_b=True)),
+        (programs.rope(64, 16, 128, 64), "rope", dict(tokens=128, heads_q=1, dim=64)),
+        (programs.rope_qk(10, 4, 2, 128), "rope", dict(heads_q=4, heads_k=2, tokens=10)),
+        (programs.swi_glu(32, 32, 64, 64), "swiglu", dict(gate=0, up=1, out=2, n=4096)),
+        (programs.flashattn(1, 2, 256, 128, True), "flashattn", dict(causal=True, S=256)),
+        (programs.flashattn(1, 2, 256, 64, False), "flashattn", dict(causal=False, D=64)),
+        (programs.mla_decode(2, 128, 1, 256, 512, 64, 64, 64, 4, 64), "mla",
+         dict(num_split=4, page=64, max_pages=4, kv_dtype="float16")),
+        (programs.mla_decode(2, 128, 1, 256, 512, 64, 64, 64, 1, 32, dtype="bfloat16",
+                             kv_dtype="float8_e4m3"), "mla",
+         dict(num_split=1, page=32, kv_scale=9, kv_dtype="float8_e4m3")),
+    ]
+    for prog, fam, attrs in cases:
+        k = tilelang.compile(prog, out_idx=-1 if fam != "mla" else [8], target="mi355x")
+        assert k.plan.family == fam, (prog, k.plan)
+        for key, val in attrs.items():
+            assert k.plan.attrs[key] == val, (fam, key, k.plan.attrs[key], val)
+        assert fam in k.get_kernel_source()
+
+
+def test_softmax_scales_are_read_from_the_program():
+    fa = tilelang.compile(programs.flashattn(1, 2, 256, 128, True), out_idx=-1)
+    assert math.isclose(fa.plan.attrs["sm_scale"], 1 / math.sqrt(128), rel_tol=1e-12)
+    mla = tilelang.compile(programs.mla_decode(2, 128, 1, 256, 512, 64, 64, 64, 2, 64),
+                           out_idx=[8])
+    assert math.isclose(mla.plan.attrs["sm_scale"], 1 / math.sqrt(576), rel_tol=1e-9)
+
+
+def test_reference_fa_demo_style_copy_alias():
+    """tpu_test_flashattn_bf16.py:11 rebinds T.copy = T.ppl_copy before defining the program."""
+    saved = T.copy
+    try:
+        T.copy = T.ppl_copy
+        k = tilelang.compile(programs.flashattn(1, 2, 128, 128, False), out_idx=-1, target="tpu")
+        assert k.plan.family == "flashattn"
+    finally:
+        T.copy = saved
+
+
+def test_symbolic_branch_is_traced():
+    """`if kr == 0:` on a loop variable (example_mla_decode_paged.py:77) records a branch."""
+
+    @T.prim_func
+    def prog(A: T.Tensor((64, 64), "float16"), B: T.Tensor((64, 64), "float16")):
+        with T.Kernel(2, threads=64) as bx:
+            s = T.alloc_shared((32, 64), "float16")
+            for kr in T.Pipelined(4, num_stages=2):
+                if kr == 0:
+                    T.ppl_copy(A[bx * 32, 0], s)
+            T.ppl_copy(s, B[bx * 32, 0])
+
+    names = [op.name for op in prog.ops]
+    assert "branch" in names and names.count("ppl_copy") == 2
+    with pytest.raises(UnsupportedProgram):
+        tilelang.compile(prog, out_idx=-1)
+
+
+def test_unsupported_program_rejected():
+
+    @T.prim_func
+    def sig(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+        with T.Kernel(1, is_cpu=True) as (bx,):
+            a = T.alloc_shared((64, 64), "float32")
+            T.ppl_copy(A[0, 0], a)
+            T.ppl_sigmoid(a, a)
+            T.ppl_copy(a, B[0, 0])
+
+    with pytest.raises(UnsupportedProgram, match="no gfx950 kernel"):
+        tilelang.compile(sig, out_idx=-1)
+
+
+def test_unsupported_variants_have_clear_errors():
+    with pytest.raises(UnsupportedProgram, match="dtype"):
+        tilelang.compile(programs.rms_norm(64, 64, 32, dtype="float32"), out_idx=-1)
+    with pytest.raises(UnsupportedProgram, match="dtypes"):
+        tilelang.compile(programs.swi_glu(32, 32, 64, 64, dtype="float32"), out_idx=-1)
+
+
+def test_scalar_params_rejected():
+    with pytest.raises(TypeError, match="T.Tensor"):
+
+        @T.prim_func
+        def bad(A: T.Tensor((4,), "float16"), n: int):
+            pass
+
+
+def test_targets_and_modes():
+    prog = programs.swi_glu(32, 32, 64, 64)
+    for t in ("auto", "tpu", "mi355x", "hip"):
+        assert tilelang.compile(prog, out_idx=-1, target=t).target == "mi355x"
+    with pytest.raises(ValueError, match="not supported"):
+        tilelang.compile(prog, out_idx=-1, target="cuda")
+    with pytest.raises(AssertionError, match="mode"):
+        tilelang.compile(prog, out_idx=-1, mode="fpga")
+    with pytest.raises(AssertionError, match="backend"):
+        tilelang.compile(prog, out_idx=-1, execution_backend="tvm")
+    assert tilelang.compile(prog, out_idx=-1, mode="cmodel").mode == "cmodel"
+
+
+def test_out_idx_legalisation():
+    assert legalize_result_idx(-1, 4) == [3]
+    assert legalize_result_idx([0, -1], 4) == [0, 3]
+    assert legalize_result_idx(None, 4) == []
+    for bad in (4, -5, [4], "x"):
+        with pytest.raises(ValueError):
+            legalize_result_idx(bad, 4)
+    k = tilelang.compile(programs.rope_qk(4, 2, 2, 64), out_idx=None)
+    assert k.out_idx == [4, 5]  # the recogniser knows which parameters are written
+
+
+def test_kernel_surface():
+    k = tilelang.compile(programs.matmul(64, 64, 64, 32, 32, 32), out_idx=-1, target="tpu")
+    assert [p.dtype for p in k.params] == [torch.float16] * 3
+    assert [p.shape for p in k.params] == [[64, 64]] * 3
+    assert k.out_idx == [2]
+    assert callable(k.func) and k.func is k.adapter.func
+    prof = k.get_profiler()
+    assert prof.result_idx == [2]
+
+
+def test_argument_validation_before_device():
+    k = tilelang.compile(programs.swi_glu(32, 32, 64, 64), out_idx=-1)
+    a = torch.randn(64, 64).bfloat16()
+    with pytest.raises(ValueError, match="Expected 3 arguments"):
+        k(a)
+    with pytest.raises(ValueError, match="dtype mismatch"):
+        k(a.float(), a)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        k(torch.randn(32, 64).bfloat16(), a)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            k(a, a)

@@ -1,0 +1,259 @@
+"""Pin the CPU oracle (oracle/ref.py, oracle/oracle.c) before trusting it.
+
+The reference commits no golden vectors for this path (its demos only print allclose against
+torch), so each oracle function is checked against something that does not restate its own
+formula: an independent brute-force loop (pure Python / C fp64), a library routine that is a
+special case (torch SDPA, numpy complex rotation, torch's float8 decode), and invariants a
+plausible mistake would break (a dropped term, a transposed operand, a wrong sign or index).
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import ROOT
+from oracle import ref
+
+
+def _liboracle():
+    path = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
+    if not os.path.exists(path):
+        import subprocess
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    lib = ctypes.CDLL(path)
+    lib.oracle_fp8_e4m3fn_decode_one.restype = ctypes.c_float
+    lib.oracle_paged_gather.restype = ctypes.c_int64
+    return lib
+
+
+# ---------------------------------------------------------------------------------------- RMSNorm
+def test_rmsnorm_vs_c_fp64_brute_force():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, 37, generator=g).half()
+    w = (1 + 0.1 * torch.randn(37, generator=g)).half()
+    lib = _liboracle()
+    xf = np.ascontiguousarray(x.float().numpy())
+    wf = np.ascontiguousarray(w.float().numpy())
+    y = np.zeros((5, 37), dtype=np.float64)
+    lib.oracle_rmsnorm_f64(xf.ctypes.data_as(ctypes.c_void_p), wf.ctypes.data_as(ctypes.c_void_p),
+                           y.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(5),
+                           ctypes.c_int64(37), ctypes.c_double(1e-6))
+    got = ref.rmsnorm_ref(x, w, 1e-6).double().numpy()
+    # one fp16 rounding of the fp64 value (half-ulp, relative 2^-11)
+    assert np.all(np.abs(got - y) <= np.abs(y) * 2.0 ** -10 + 1e-7)
+
+
+def test_rmsnorm_invariants():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(8, 4096, generator=g).half()
+    y = ref.rmsnorm_ref(x, None, 1e-6).float()
+    # unit RMS per row (w = 1)
+    assert torch.allclose(y.pow(2).mean(-1).sqrt(), torch.ones(8), atol=2e-3)
+    # scale invariance: rmsnorm(4x) == rmsnorm(x) (power-of-two scale is exact in fp16)
+    assert torch.equal(ref.rmsnorm_ref((x.float() * 4).half(), None, 0.0),
+                       ref.rmsnorm_ref(x, None, 0.0))
+    # zero row stays zero with eps > 0
+    assert torch.equal(ref.rmsnorm_ref(torch.zeros(1, 16).half(), None, 1e-6),
+                       torch.zeros(1, 16).half())
+
+
+# ------------------------------------------------------------------------------------------- GEMM
+def test_matmul_vs_brute_force():
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(3, 5, generator=g).half()
+    b = torch.randn(5, 4, generator=g).half()
+    exp = [[sum(float(a[i, k]) * float(b[k, j]) for k in range(5)) for j in range(4)]
+           for i in range(3)]
+    got = ref.matmul_ref(a, b, out_dtype=torch.float32)
+    assert np.allclose(got.numpy(), np.array(exp), rtol=1e-6, atol=1e-6)
+    # trans_b takes B as [N, K]
+    got_t = ref.matmul_ref(a, b.t().contiguous(), out_dtype=torch.float32, trans_b=True)
+    assert torch.equal(got, got_t)
+    # non-square shapes catch a transposed operand
+    a2 = torch.randn(2, 7, generator=g).half()
+    b2 = torch.randn(7, 3, generator=g).half()
+    assert ref.matmul_ref(a2, b2).shape == (2, 3)
+    assert np.allclose(ref.matmul_ref(a2, b2, out_dtype=torch.float32).numpy(),
+                       a2.double().numpy() @ b2.double().numpy(), atol=1e-5)
+
+
+# ------------------------------------------------------------------------------------------- RoPE
+def test_rope_tables_closed_form():
+    cos, sin = ref.rope_cos_sin(300, 128, dtype=torch.float32)
+    for pos, i in ((0, 0), (7, 3), (299, 63), (256, 1), (100, 10)):
+        th = pos * 10000.0 ** (-2.0 * i / 128)
+        assert abs(float(cos[pos, 2 * i]) - math.cos(th)) < 1e-5
+        assert abs(float(sin[pos, 2 * i + 1]) - math.sin(th)) < 1e-5
+    assert torch.equal(cos[:, 0::2], cos[:, 1::2]) and torch.equal(sin[:, 0::2], sin[:, 1::2])
+
+
+def test_rope_vs_complex_rotation_and_invariants():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(50, 3, 64, generator=g)
+    cos, sin = ref.rope_cos_sin(50, 64, dtype=torch.float32)
+    out = ref.rope_ref(x, cos, sin).numpy()
+    z = x.numpy()[..., 0::2] + 1j * x.numpy()[..., 1::2]
+    th = np.arange(50)[:, None] * 10000.0 ** (-2.0 * np.arange(32) / 64)
+    rot = z * np.exp(1j * th)[:, None, :]
+    assert np.allclose(out[..., 0::2], rot.real, atol=1e-4)
+    assert np.allclose(out[..., 1::2], rot.imag, atol=1e-4)
+    # position 0 is the identity; pair norms are preserved
+    assert np.allclose(out[0], x.numpy()[0], atol=0)
+    assert np.allclose(np.abs(out[..., 0::2] + 1j * out[..., 1::2]), np.abs(z), atol=1e-4)
+
+
+# ----------------------------------------------------------------------------------------- SwiGLU
+def test_swiglu_vs_numpy_and_limits():
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(64, 33, generator=g).bfloat16()
+    b = torch.randn(64, 33, generator=g).bfloat16()
+    got = ref.swiglu_ref(a, b).double().numpy()
+    an, bn = a.double().numpy(), b.double().numpy()
+    exp = bn * an / (1.0 + np.exp(-an))
+    assert np.all(np.abs(got - exp) <= np.abs(exp) * 2.0 ** -8 + 1e-30)
+    z = torch.zeros(4).bfloat16()
+    assert torch.equal(ref.swiglu_ref(z, torch.ones(4).bfloat16()), z)
+    big = torch.full((2,), 30.0).bfloat16()
+    assert torch.equal(ref.swiglu_ref(big, torch.ones(2).bfloat16()), big)
+
+
+# --------------------------------------------------------------------------------- FlashAttention
+@pytest.mark.parametrize("causal", [False, True])
+def test_flashattn_vs_sdpa(causal):
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(2, 70, 3, 64, generator=g).bfloat16() for _ in range(3))
+    got = ref.flashattn_ref(q, k, v, causal).float()
+    exp = F.scaled_dot_product_attention(q.float().transpose(1, 2), k.float().transpose(1, 2),
+                                         v.float().transpose(1, 2),
+                                         is_causal=causal).transpose(1, 2)
+    assert (got - exp).abs().max() < 1e-2
+
+
+def test_flashattn_brute_force_and_invariants():
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(1, 3, 1, 2, generator=g) for _ in range(3))
+    got = ref.flashattn_ref(q, k, v, causal=True, sm_scale=0.5)
+    for i in range(3):
+        s = [0.5 * sum(float(q[0, i, 0, d]) * float(k[0, j, 0, d]) for d in range(2))
+             for j in range(i + 1)]
+        m = max(s)
+        p = [math.exp(x - m) for x in s]
+        o = [sum(p[j] * float(v[0, j, 0, d]) for j in range(i + 1)) / sum(p) for d in range(2)]
+        assert np.allclose(got[0, i, 0].numpy(), o, atol=1e-6)
+    # causal first query attends to key 0 only -> V[0]; softmax rows sum to 1 (V = 1 -> O = 1)
+    assert torch.allclose(got[0, 0], v[0, 0])
+    ones = torch.ones(1, 5, 2, 8)
+    assert torch.allclose(ref.flashattn_ref(torch.randn(1, 5, 2, 8), torch.randn(1, 5, 2, 8),
+                                            ones, False), ones)
+
+
+# -------------------------------------------------------------------------------------------- FP8
+def test_fp8_table_vs_torch_and_c():
+    t = ref.fp8_e4m3fn_table()
+    torch_dec = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    lib = _liboracle()
+    c_dec = np.array([lib.oracle_fp8_e4m3fn_decode_one(ctypes.c_uint8(b)) for b in range(256)],
+                     dtype=np.float32)
+    for arr in (torch_dec, c_dec):
+        nan = np.isnan(t)
+        assert np.array_equal(nan, np.isnan(arr))
+        assert np.array_equal(t[~nan], arr[~nan])
+    assert t[0x38] == 1.0 and t[0x7E] == 448.0 and t[0x01] == 2.0 ** -9 and t[0x08] == 2.0 ** -6
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF]) and t[0x80] == 0.0
+
+
+def test_fp8_quantize_round_trip():
+    x = torch.randn(1000, generator=torch.Generator().manual_seed(8))
+    q8, scale = ref.fp8_quantize(x)
+    assert abs(float(q8.float().abs().max()) - 448.0) < 1e-6
+    rel = ((q8.float() * scale - x).abs() / x.abs().clamp_min(1e-3)).median()
+    assert rel < 2 ** -4
+
+
+# -------------------------------------------------------------------------------------------- MLA
+def _mla_tiny(seed=9, B=2, Hq=3, dv=4, dpe=2, page=2, max_pages=3):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, dv, generator=g)
+    qp = torch.randn(B, Hq, dpe, generator=g)
+    n = B * max_pages * page
+    kv = torch.randn(n, dv, generator=g)
+    kp = torch.randn(n, dpe, generator=g)
+    bt = torch.randperm(B * max_pages, generator=g).view(B, max_pages).to(torch.int32)
+    sl = torch.tensor([5, 2], dtype=torch.int32)[:B]
+    return q, qp, kv, kp, bt, sl
+
+
+def test_mla_vs_token_loop():
+    q, qp, kv, kp, bt, sl = _mla_tiny()
+    got = ref.mla_decode_ref(q, qp, kv, kp, bt, sl, 2, 0.3, out_dtype=torch.float32)
+    for b in range(2):
+        for h in range(3):
+            rows = [int(bt[b, j // 2]) * 2 + j % 2 for j in range(int(sl[b]))]
+            s = [0.3 * (float(q[b, h] @ kv[r]) + float(qp[b, h] @ kp[r])) for r in rows]
+            m = max(s)
+            p = [math.exp(x - m) for x in s]
+            o = sum(p[i] * kv[r].double() for i, r in enumerate(rows)) / sum(p)
+            assert torch.allclose(got[b, h].double(), o, atol=1e-5)
+
+
+def test_mla_identity_table_matches_reference_slicing():
+    """With the reference's identity table (block_table = arange, begin = b * max_seqlen_pad),
+    the gather reads exactly the contiguous slice run_torch_mla reads (:292-299)."""
+    B, page, pages = 3, 4, 5
+    bt = torch.arange(B * pages, dtype=torch.int32).view(B, pages)
+    for b in range(B):
+        rows = ref.paged_rows(bt, 13, b, page)
+        assert torch.equal(rows, torch.arange(b * pages * page, b * pages * page + 13))
+
+
+def test_mla_page_permutation_and_split_invariance():
+    q, qp, kv, kp, bt, sl = _mla_tiny(seed=10)
+    base = ref.mla_decode_ref(q, qp, kv, kp, bt, sl, 2, 0.7, out_dtype=torch.float32)
+    perm = torch.randperm(6, generator=torch.Generator().manual_seed(11))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(6)
+    kv2 = kv.view(6, 2, -1)[perm].reshape(12, -1)
+    kp2 = kp.view(6, 2, -1)[perm].reshape(12, -1)
+    bt2 = inv[bt.long()].to(torch.int32)
+    assert torch.allclose(ref.mla_decode_ref(q, qp, kv2, kp2, bt2, sl, 2, 0.7,
+                                             out_dtype=torch.float32), base, atol=1e-6)
+    for ns in (1, 2, 3):
+        sc = ref.mla_split_combine_ref(q, qp, kv, kp, bt, sl, 2, 0.7, ns, block_n=2,
+                                       out_dtype=torch.float32)
+        assert torch.allclose(sc, base, atol=1e-5)
+
+
+def test_split_partition_rule():
+    """example_mla_decode_paged.py:140-144: blocks dealt out, first (total % ns) get one more."""
+    for L, ns, bn in ((4096, 4, 64), (65, 4, 64), (1, 8, 64), (1000, 3, 64)):
+        parts = ref.mla_split_partition(L, ns, bn)
+        covered = [t for st, en in parts for t in range(st, en)]
+        assert covered == list(range(L))
+        total = -(-L // bn)
+        sizes = [-(-(en - st) // bn) if en > st else 0 for st, en in parts]
+        assert sum(sizes) == total and max(sizes) - min(sizes) <= 1
+        assert sizes == sorted(sizes, reverse=True)
+
+
+def test_paged_gather_numpy_vs_c():
+    rng = np.random.default_rng(12)
+    B, page, pages = 4, 8, 6
+    kv = rng.integers(0, 256, (B * pages * page, 24), dtype=np.uint8)
+    bt = rng.permutation(B * pages).reshape(B, pages).astype(np.int32)
+    sl = np.array([1, 48, 17, 0], dtype=np.int32)
+    exp = ref.paged_gather_ref(kv, bt, sl, page)
+    lib = _liboracle()
+    out = np.zeros((int(sl.sum()), 24), dtype=np.uint8)
+    n = lib.oracle_paged_gather(kv.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(24),
+                                ctypes.c_int64(kv.shape[0]), bt.ctypes.data_as(ctypes.c_void_p),
+                                sl.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(B),
+                                ctypes.c_int64(pages), ctypes.c_int64(page),
+                                out.ctypes.data_as(ctypes.c_void_p))
+    assert n == sl.sum() and np.array_equal(out, exp)
+    # the second sequence's 9th token lives in page bt[1, 1], slot 0
+    off = 1 + 8
+    assert np.array_equal(exp[off], kv[bt[1, 1] * page])
