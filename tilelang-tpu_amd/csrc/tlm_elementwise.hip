@@ -29,17 +29,19 @@ TLM_DEV u32x4 swiglu8(u32x4 g, u32x4 u) {
   return o;
 }
 
+// Each block streams contiguous chunks of kSwiThreads*kSwiUnroll vectors (all loads of a chunk
+// issued before any math), grid-striding over chunks; this ordering measured faster than a
+// whole-grid stride on MI355X.
 template <bool IS_BF16>
 __global__ __launch_bounds__(kSwiThreads) void swiglu_vec(const u32x4* __restrict__ gate,
                                                           const u32x4* __restrict__ up,
                                                           u32x4* __restrict__ out, int64_t nvec) {
-  const int64_t stride = (int64_t)gridDim.x * kSwiThreads;
-  for (int64_t base = (int64_t)blockIdx.x * kSwiThreads + threadIdx.x; base < nvec;
-       base += stride * kSwiUnroll) {
+  constexpr int64_t chunk = (int64_t)kSwiThreads * kSwiUnroll;
+  for (int64_t c0 = (int64_t)blockIdx.x * chunk; c0 < nvec; c0 += (int64_t)gridDim.x * chunk) {
     u32x4 g[kSwiUnroll], u[kSwiUnroll];
 #pragma unroll
     for (int k = 0; k < kSwiUnroll; ++k) {
-      int64_t i = base + k * stride;
+      const int64_t i = c0 + k * kSwiThreads + threadIdx.x;
       if (i < nvec) {
         g[k] = ld_nt(gate + i);
         u[k] = ld_nt(up + i);
@@ -47,7 +49,7 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_vec(const u32x4* __restric
     }
 #pragma unroll
     for (int k = 0; k < kSwiUnroll; ++k) {
-      int64_t i = base + k * stride;
+      const int64_t i = c0 + k * kSwiThreads + threadIdx.x;
       if (i < nvec) st_nt(out + i, swiglu8<IS_BF16>(g[k], u[k]));
     }
   }
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_scalar(const uint16_t* __r
 // table vector only when its token changes, so tables cost ~1 read per token.
 
 constexpr int kRopeThreads = 256;
-constexpr int kRopeRowsPerThread = 4;
+constexpr int kRopeRowsPerThread = 2;
 
 template <bool IS_BF16, int LPR>
 __global__ __launch_bounds__(kRopeThreads) void rope_vec(
@@ -94,6 +96,16 @@ __global__ __launch_bounds__(kRopeThreads) void rope_vec(
   const int64_t row0 = (int64_t)blockIdx.x * RPP * kRopeRowsPerThread + threadIdx.x / LPR;
   int64_t cur_tok = -1;
   u32x4 c = {0, 0, 0, 0}, s = {0, 0, 0, 0};
+  u32x4 xs[kRopeRowsPerThread];
+#pragma unroll
+  for (int it = 0; it < kRopeRowsPerThread; ++it) {  // all row loads in flight first
+    const int64_t row = row0 + (int64_t)it * RPP;
+    if (row < nrows) {
+      const int64_t t = row / htot;
+      const int h = (int)(row - t * htot);
+      xs[it] = ld_nt(h < hq ? q + (t * hq + h) * LPR + sub : k + (t * hk + (h - hq)) * LPR + sub);
+    }
+  }
 #pragma unroll
   for (int it = 0; it < kRopeRowsPerThread; ++it) {
     const int64_t row = row0 + (int64_t)it * RPP;
@@ -105,16 +117,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_vec(
       s = sin_t[t * LPR + sub];
       cur_tok = t;
     }
-    const u32x4* src;
-    u32x4* dst;
-    if (h < hq) {
-      src = q + (t * hq + h) * LPR + sub;
-      dst = q_out + (t * hq + h) * LPR + sub;
-    } else {
-      src = k + (t * hk + (h - hq)) * LPR + sub;
-      dst = k_out + (t * hk + (h - hq)) * LPR + sub;
-    }
-    const u32x4 x = ld_nt(src);
+    u32x4* dst = h < hq ? q_out + (t * hq + h) * LPR + sub : k_out + (t * hk + (h - hq)) * LPR + sub;
+    const u32x4 x = xs[it];
     u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -216,9 +220,8 @@ extern "C" int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n
   const bool bf = dtype == TLM_BF16;
   if (n % 8 == 0 && tlm_aligned(gate, 16) && tlm_aligned(up, 16) && tlm_aligned(out, 16)) {
     const int64_t nvec = n / 8;
-    // Enough blocks for ~8 resident 256-thread blocks on each of 256 CUs, each thread keeping
-    // kSwiUnroll 16-byte load pairs in flight.
-    unsigned grid = grid_for(nvec, kSwiThreads * kSwiUnroll, 256 * 16);
+    // 1024 blocks (4 per CU) streaming 16 KiB chunks measured best at the 8192x14336 config.
+    unsigned grid = grid_for(nvec, kSwiThreads * kSwiUnroll, 1024);
     if (bf)
       swiglu_vec<true><<<grid, kSwiThreads, 0, s>>>((const u32x4*)gate, (const u32x4*)up,
                                                      (u32x4*)out, nvec);

@@ -333,8 +333,8 @@ int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, cons
 
 extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
   if (B <= 0 || Hq <= 0 || dv <= 0 || num_split <= 0) return 0;
-  // partial outputs fp32 [B, Hq, ns, dv] + log2-sum-exp fp32 [B, Hq, ns]
-  return (size_t)B * Hq * num_split * (dv + 1) * sizeof(float);
+  // partial outputs fp32 + log2-sum-exp fp32, one slot per (sequence, split, head)
+  return (size_t)B * num_split * Hq * (dv + 1) * sizeof(float);
 }
 
 extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
@@ -389,10 +389,14 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
     return TLM_EUNSUPPORTED;
   }
   if (B == 0) return TLM_OK;
+  if (kv_rows < 1) {
+    tlm_set_error("tlm_mla_decode: empty KV pool");
+    return TLM_EINVAL;
+  }
+  const float sc = (float)((double)sm_scale * 1.4426950408889634);
   hipStream_t st = (hipStream_t)stream;
   float* ws_o = (float*)ws;
   float* ws_lse = ws_o + (size_t)B * Hq * num_split * dv;
-  const float sc = (float)((double)sm_scale * 1.4426950408889634);
   const bool bf = q_dtype == TLM_BF16;
   const int b = (int)B, h = (int)Hq, pg = (int)page, mp = (int)max_pages;
   int rc;
