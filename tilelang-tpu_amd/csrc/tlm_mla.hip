@@ -26,6 +26,8 @@
 //     staging into a double-buffered LDS tile; the next tile's global loads overlap the MFMAs.
 #include "tlm_common.h"
 
+#include <algorithm>
+
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -331,10 +333,21 @@ int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, cons
 
 }  // namespace
 
+// FP8 path on the fp8 matrix cores (tlm_mla_fp8.hip); TLM_EUNSUPPORTED for shapes it does not take
+size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split);
+int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                       const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                       int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
+                       void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                       int num_split, float score_scale, const float* kv_scale, bool q_bf16,
+                       bool o_bf16, void* stream);
+
 extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
   if (B <= 0 || Hq <= 0 || dv <= 0 || num_split <= 0) return 0;
-  // partial outputs fp32 + log2-sum-exp fp32, one slot per (sequence, split, head)
-  return (size_t)B * num_split * Hq * (dv + 1) * sizeof(float);
+  // split path: partial outputs fp32 + log2-sum-exp fp32, one slot per (sequence, split, head);
+  // the fp8 path needs its own layout: the larger of the two serves both
+  const size_t split = (size_t)B * num_split * Hq * (dv + 1) * sizeof(float);
+  return std::max(split, tlm_mla_fp8_workspace_bytes(B, Hq, num_split));
 }
 
 extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
@@ -394,6 +407,13 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
     return TLM_EINVAL;
   }
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  if (kv_dtype == TLM_F8E4M3) {
+    const int rc = tlm_mla_fp8_launch(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                      kpe_stride, kv_rows, block_table, seqlens, o, ws, B, Hq,
+                                      page, max_pages, num_split, sc, kv_scale,
+                                      q_dtype == TLM_BF16, o_dtype == TLM_BF16, stream);
+    if (rc != TLM_EUNSUPPORTED) return rc;
+  }
   hipStream_t st = (hipStream_t)stream;
   float* ws_o = (float*)ws;
   float* ws_lse = ws_o + (size_t)B * Hq * num_split * dv;

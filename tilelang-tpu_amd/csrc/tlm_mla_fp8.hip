@@ -1,0 +1,699 @@
+// FP8 MLA paged decode, balanced over every CU, QK^T on fp8 MFMA.
+//
+// Reference: examples/deepseek_mla/example_mla_decode_paged.py — per (sequence, head):
+//   S = Q KV^T + Q_pe K_pe^T over the sequence's tokens (page address
+//   BT[b, tok / page] * page + tok % page, :147-148), scale = sm_scale * log2(e) (:12),
+//   softmax in the exp2 domain, O = P KV (:150-183), partial results merged by
+//   lse = log2(sum 2^(lse_s - max)) + max, O = sum O_s 2^(lse_s - lse) (:186-221).
+// FP8 config: KV is OCP e4m3 with one fp32 scale: scores use (Q . K_fp8) * kv_scale and the
+// output is (P . V_fp8) * kv_scale.
+//
+// At 128 heads the decode does ~480 flop per KV byte, above the MI355X bf16 ridge, so this kernel
+// is organised around the matrix cores:
+//   * work partition: the sequences' 64-token tiles are concatenated and cut into G equal ranges,
+//     so every CU gets the same number of tiles whatever the length mix. A range holds pieces of
+//     one or more sequences: a sequence entirely inside one range is written to the output
+//     directly; the pieces of a longer one go to fp32 partial slots (one for the range's first
+//     piece, one for its last) merged by the combine kernel;
+//   * workgroup = 64 heads x one range = 2 wave pairs x 32 heads. The two waves of a pair split a
+//     64-token tile by tokens for S^T = K Q^T (one 32-token block each, all 576 dims) and by V
+//     dims for O^T = V^T P^T (256 dims each, all 64 tokens), exchanging block maxima and the bf16
+//     P^T block through LDS: no work is duplicated and each wave holds only 128 O accumulators;
+//   * Q^T stays in VGPRs for the whole piece, split per head into two e4m3 terms
+//     q / s = hi + lo (s a power of two putting max|q| at <= 448), which keeps bf16-level accuracy
+//     while S^T runs on v_mfma_f32_32x32x64_f8f6f4 straight from the fp8 cache bytes (2 MFMAs per
+//     64 dims: the cost of one bf16 MFMA and no K conversion);
+//   * O^T on v_mfma_f32_32x32x16_bf16: V^T comes from the row-major fp8 tile through
+//     ds_read_b64_tr_b8 (8 tokens of one dim per lane), widened exactly to bf16; P^T is the S^T
+//     accumulator itself: K rows are fed to the MFMA in the order tau (bits 2 and 3 of the row
+//     index swapped) so accumulator element i of lane l is token 16(i/8) + 8(l/32) + i%8, the
+//     B-operand layout of the PV MFMA;
+//   * softmax without accumulator rescaling: a segment fixes its reference max m from its first
+//     tile and accumulates 2^(x - m); only when a tile's max exceeds m by more than 64 (log2
+//     units) does the segment end (its normalised partial is merged into a scratch slot) and a new
+//     one start at that tile. fp32 holds 2^64 * 448 * 2^31 without overflow, so the result equals
+//     the rescaling online softmax while the O accumulators are only ever touched by MFMAs;
+//   * KV tiles (64 tokens x 576 bytes) stream into a 3-stage LDS ring with buffer_load ... lds
+//     (16 bytes per lane, no VGPR round trip); each tile's buffer descriptor bounds the rows to
+//     the sequence's valid tokens and to the KV pool, so rows past either read as zeros (never
+//     stale NaN bytes); an explicit vmcnt wait plus s_barrier hands a stage over;
+//   * LDS layout per stage: latent rows of 512 B then rope rows of 64 B, 16-byte chunks XOR-
+//     swizzled so that the row reads of S^T (ds_read_b128) and the transposed reads of V^T
+//     (ds_read_b64_tr_b8) are both bank-conflict free.
+#include "tlm_common.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int F8_DV = 512, F8_DPE = 64;
+constexpr int F8_TILE = 64;                          // tokens per ring stage
+constexpr int F8_LAT = F8_TILE * F8_DV;              // latent bytes per stage
+constexpr int F8_STAGE = F8_LAT + F8_TILE * F8_DPE;  // + rope bytes
+constexpr int F8_NSTAGE = 3;
+constexpr int F8_HEADS = 64;                         // heads per workgroup (2 pairs x 32)
+constexpr int F8_LOADS = 9;                          // LDS-DMA loads per thread per stage
+constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
+constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
+constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
+constexpr int F8_WAVE_F4 = 8 * 4 * 64;               // float4 per wave in a partial slot
+constexpr int F8_QREG = 6;                           // Q k-steps held in VGPRs; the rest in LDS
+
+// swizzled 16-byte chunk index of latent row r / rope row r
+TLM_DEV int swz_lat(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+TLM_DEV int swz_rope(int r) { return (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+// K-row order fed to the S^T MFMA (bits 2 and 3 swapped)
+TLM_DEV int tau(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+TLM_DEV void wait_vm(int n) {  // s_waitcnt vmcnt(n), other counters untouched
+  if (n == 0)
+    __builtin_amdgcn_s_waitcnt(0x3f70);
+  else
+    __builtin_amdgcn_s_waitcnt(0x3f70 | F8_LOADS);
+}
+
+// Workgroup barrier that leaves the LDS-DMA loads of the ring in flight: waits for this wave's
+// LDS (and scalar) accesses only, so its LDS writes are visible to the other waves afterwards.
+TLM_DEV void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Read-only table entry through the constant address space: a uniform address then becomes a
+// scalar load (s_load), which neither uses VGPRs nor counts against the vmcnt ring accounting.
+template <class T>
+TLM_DEV T ldc(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+TLM_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// LDS reads of the ring issued as inline asm. Compiler-generated reads may be made to wait
+// (vmcnt(0)) for every outstanding LDS-DMA load, including the prefetch of the next stages, when
+// the compiler cannot prove they touch another stage. The caller waits with lds_wait() before
+// using the result.
+TLM_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+TLM_DEV i32x2 lds_tr8(const uint8_t* p) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+TLM_DEV i32x4 lds_b128(const void* p) {
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+TLM_DEV i32x8 lds_2xb128(const void* p0, const void* p1) {
+  const i32x4 a = lds_b128(p0), b = lds_b128(p1);
+  return i32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+// s_waitcnt lgkmcnt(0) that also orders the uses of the given asm-loaded operands after it
+TLM_DEV void lds_wait(i32x8& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a) : : "memory"); }
+TLM_DEV void lds_wait(i32x8& a, i32x8& b, i32x8& c) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c) : : "memory");
+}
+// s_waitcnt lgkmcnt(0) that also orders the uses of eight asm-loaded operands after it
+TLM_DEV void lds_wait(i32x2 (&r)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               :
+               : "memory");
+}
+
+TLM_DEV f32x16 mfma_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// 8 e4m3 bytes -> 8 bf16 (exact)
+TLM_DEV bf16x8 fp8x8_to_bf16(i32x2 v) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// four floats -> four e4m3 bytes (round to nearest even)
+TLM_DEV int pack_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+}
+
+struct F8Args {
+  const uint16_t* q;
+  const uint16_t* q_pe;
+  int64_t q_stride, qpe_stride;  // elements between (batch, head) rows
+  const uint8_t* kv;
+  const uint8_t* k_pe;
+  int64_t kv_stride, kpe_stride, kv_rows;  // bytes between token rows; rows in the pool
+  const int32_t* bt;
+  const int32_t* seqlens;
+  int32_t* cu;  // [B + 1] tile prefix over sequences (written by the plan kernel)
+  float* part_lse;
+  float* part_o;
+  uint16_t* out;
+  int B, Hq, page, max_pages, G;
+  int lmax;           // seqlens are clamped to [0, lmax = max_pages * page]
+  float score_scale;  // sm_scale * log2(e)
+  const float* kv_scale;
+};
+
+// Tile prefix over sequences: cu[b] = sum_{b' < b} ceil(L_b' / 64), cu[B] = total.
+__global__ __launch_bounds__(1024) void mla_fp8_plan(const F8Args a) {
+  __shared__ int32_t part[1024];
+  const int t = threadIdx.x;
+  const int per = (a.B + 1023) / 1024;
+  const int b0 = min(a.B, t * per), b1 = min(a.B, b0 + per);
+  auto tiles = [&](int b) {
+    const int L = max(0, min(a.seqlens[b], a.lmax));
+    return (L + F8_TILE - 1) / F8_TILE;
+  };
+  int32_t s = 0;
+  for (int b = b0; b < b1; ++b) s += tiles(b);
+  part[t] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int32_t run = part[t] - s;
+  for (int b = b0; b < b1; ++b) {
+    a.cu[b] = run;
+    run += tiles(b);
+  }
+  if (t == 1023) a.cu[a.B] = part[1023];
+}
+
+// Q^T operand of one head for S^T = K Q^T: k-step s (64 dims: 0..7 latent, 8 rope), lane half hf
+// holds dims 64 s + 32 hf + j at byte j. q / s_h = hi + lo, both e4m3; returns s_h.
+template <bool Q_BF16>
+TLM_DEV float prep_q(const uint16_t* qrow, const uint16_t* qperow, int hf, i32x8 (&qhi)[F8_QREG],
+                     i32x8 (&qlo)[F8_QREG], i32x8* qt, bool write_qt) {
+  using H = h16<Q_BF16>;
+  auto src = [&](int s, int v) -> const u32x4* {
+    return (const u32x4*)(s < 8 ? qrow + 64 * s + 32 * hf + 8 * v : qperow + 32 * hf + 8 * v);
+  };
+  float amax = 0.f;
+#pragma unroll
+  for (int s = 0; s < 9; ++s) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 w = *src(s, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fmaxf(fabsf(H::lo(w[e])), fabsf(H::hi(w[e]))));
+    }
+    sched_fence();
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  int ex = 0;
+  if (amax > 0.f) (void)frexpf(amax * (1.0f / 448.0f), &ex);  // amax / 2^ex <= 448
+  const float inv = ldexpf(1.0f, -ex);
+  i32x8 tail[2];
+#pragma unroll
+  for (int s = 0; s < 9; ++s)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 w = *src(s, v);
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = H::lo(w[e]) * inv;
+        x[2 * e + 1] = H::hi(w[e]) * inv;
+      }
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const float* y = x + 4 * h2;
+        const int hi = pack_fp8x4(y[0], y[1], y[2], y[3]);
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        const int lo = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
+        if (s < F8_QREG) {
+          qhi[s][2 * v + h2] = hi;
+          qlo[s][2 * v + h2] = lo;
+        } else {
+          tail[0][2 * v + h2] = hi;
+          tail[1][2 * v + h2] = lo;
+        }
+      }
+      if (v == 3) {
+        if (s >= F8_QREG && write_qt) {
+          qt[(2 * (s - F8_QREG)) * 64] = tail[0];
+          qt[(2 * (s - F8_QREG) + 1) * 64] = tail[1];
+        }
+        sched_fence();
+      }
+    }
+  return ldexpf(1.0f, ex);
+}
+
+// Workgroup index -> (range, 64-head group), keeping the head groups of one range on one XCD
+// (workgroup ids are dealt round-robin over the 8 XCDs) so the second read of each KV tile is an
+// L2 hit.
+struct F8Work {
+  int g, hgi;
+};
+TLM_DEV F8Work f8_work(int x, int HG) {
+  const int xcd = x & 7, k = x >> 3;
+  return F8Work{(k / HG) * 8 + xcd, k % HG};
+}
+
+template <bool Q_BF16, bool O_BF16>
+__global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[F8_NSTAGE * F8_STAGE];
+  __shared__ float xmax[2][2][32];  // [pair][token block][head]: block maxima
+  __shared__ float xsum[2][2][32];  // [pair][token block][head]: block sums of P
+  __shared__ __attribute__((aligned(16))) bf16x8 xp[2][2][2][64];  // [pair][block][kstep][lane]
+  // Q^T k-steps F8_QREG..8 of each pair: [pair][(k - F8_QREG) * 2 + hi/lo][lane]
+  __shared__ __attribute__((aligned(16))) i32x8 qt[2][(9 - F8_QREG) * 2][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
+  const int pr = wave >> 1, dh = wave & 1;  // pair (32 heads), token block / dim half
+  const int hh = lane & 31, hf = lane >> 5;
+  const int HG = a.Hq / F8_HEADS;
+  const F8Work wk = f8_work(blockIdx.x, HG);
+  if (wk.g >= a.G) return;
+  const int g = wk.g, hgi = wk.hgi;
+  const int head = hgi * F8_HEADS + pr * 32 + hh;
+  const int64_t T = ldc(a.cu + a.B);
+  const int64_t t_lo = (int64_t)g * T / a.G, t_hi = (int64_t)(g + 1) * T / a.G;
+  if (t_lo >= t_hi) return;
+  const float kvs = a.kv_scale ? ldc(a.kv_scale) : 1.0f;
+
+  // first sequence with a tile in [t_lo, t_hi): largest b with cu[b] <= t_lo
+  int b_first = 0;
+  {
+    int lo = 0, hi = a.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (ldc(a.cu + mid) <= t_lo) lo = mid; else hi = mid - 1;
+    }
+    b_first = lo;
+  }
+
+  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 3
+  int ib = b_first;
+  int64_t ib_lo = ldc(a.cu + ib), ib_hi = ldc(a.cu + ib + 1);
+  auto issue = [&](int64_t t) {
+    while (t >= ib_hi) {
+      ++ib;
+      ib_lo = ib_hi;
+      ib_hi = ldc(a.cu + ib + 1);
+    }
+    const int L = max(0, min(ldc(a.seqlens + ib), a.lmax));
+    const int tok0 = (int)(t - ib_lo) * F8_TILE;
+    const int valid = min(F8_TILE, L - tok0);
+    const int64_t row0 =
+        (int64_t)ldc(a.bt + (int64_t)ib * a.max_pages + tok0 / a.page) * a.page + tok0 % a.page;
+    int64_t nrow = min((int64_t)valid, a.kv_rows - row0);
+    if (row0 < 0 || nrow < 0) nrow = 0;
+    const uint8_t* bkv = nrow > 0 ? a.kv + row0 * a.kv_stride : a.kv;
+    const uint8_t* bpe = nrow > 0 ? a.k_pe + row0 * a.kpe_stride : a.k_pe;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)bkv, (short)0, (int)(nrow * a.kv_stride), F8_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)bpe, (short)0, (int)(nrow * a.kpe_stride), F8_RSRC_WORD3);
+    uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // latent: 2 rows x 32 chunks per wave-instruction
+      const int r = 2 * (8 * wave + k) + hf;
+      const int off = r * (int)a.kv_stride + 16 * ((lane & 31) ^ swz_lat(r));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(st + (8 * wave + k) * 1024), 16,
+                                               off, 0, 0, 0);
+    }
+    {  // rope: 16 rows x 4 chunks per wave-instruction
+      const int r = 16 * wave + (lane >> 2);
+      const int off = r * (int)a.kpe_stride + 16 * ((lane & 3) ^ swz_rope(r));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(st + F8_LAT + wave * 1024), 16,
+                                               off, 0, 0, 0);
+    }
+  };
+  issue(t_lo);
+  if (t_lo + 1 < t_hi) issue(t_lo + 1);
+
+  // ---- per-lane LDS read offsets
+  const int th = tau(hh);                  // K row of this lane within its 32-token block
+  const int fk = (2 * hf) ^ swz_lat(th);   // latent chunk of k-step s: (4 s) ^ fk
+  const int fr = (2 * hf) ^ swz_rope(th);  // rope chunks: fr, fr ^ 1
+  const int i16 = lane & 15, gq = lane >> 4;
+  const int vrow = 8 * (gq >> 1) + (i16 >> 1);  // V^T row (token) within a 16-token k-step
+  const int vu = (gq & 1) ^ swz_lat(vrow);
+  const int vbase = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1) + 256 * dh;
+  const int vx = vu >> 1;
+
+  i32x8 qhi[F8_QREG], qlo[F8_QREG];
+  int64_t t = t_lo;
+  int cb = b_first;
+  int64_t cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
+  while (t < t_hi) {  // one iteration per sequence piece
+    while (t >= cb_hi) {
+      ++cb;
+      cb_lo = cb_hi;
+      cb_hi = ldc(a.cu + cb + 1);
+    }
+    const int L = max(0, min(ldc(a.seqlens + cb), a.lmax));
+    const int64_t qr = (int64_t)cb * a.Hq + head;
+    const float ch = a.score_scale * kvs *
+                     prep_q<Q_BF16>(a.q + qr * a.q_stride, a.q_pe + qr * a.qpe_stride, hf, qhi, qlo,
+                                    &qt[pr][0][lane], dh == 0);
+    const int64_t p_lo = t, p_hi = min(t_hi, cb_hi);
+    const bool complete = p_lo == cb_lo && p_hi == cb_hi;
+    const int slot = p_lo == t_lo ? 0 : 1;
+    bool have_scr = false, carry = false;
+    float lse_scr = 0.f, mt = 0.f;
+    f32x16 s;  // scores of this wave's 32-token block (log2 units, masked)
+    for (;;) {  // one iteration per softmax segment (normally one per piece)
+      f32x16 oacc[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
+      float mref = 0.f, lsum = 0.f;
+      bool first = true, cut = false;
+      while (t < p_hi) {
+        const uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
+        const int valid = L - (int)(t - cb_lo) * F8_TILE;  // tokens of the tile, >= 1
+        if (!carry) {
+          // hand over tile t, refill the stage freed by tile t - 1
+          wait_vm(t + 1 < t_hi ? F8_LOADS : 0);
+          wg_barrier();
+          if (t + 2 < t_hi) issue(t + 2);
+          // S^T = K Q^T for this wave's 32 tokens x 32 heads
+          const int own = valid - 32 * dh;
+          float mb = -INFINITY;
+          if (own > 0) {
+            const uint8_t* krow = st + (32 * dh + th) * F8_DV;
+            const uint8_t* prow = st + F8_LAT + (32 * dh + th) * F8_DPE;
+            // operands of k-step k: K (32 bytes of this lane's row) and, past F8_QREG, Q^T hi/lo
+            i32x8 kop[2], qop[2][2];
+            auto kread = [&](int k) {
+              kop[k & 1] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk),
+                                              krow + 16 * (((4 * k) ^ fk) ^ 1))
+                                 : lds_2xb128(prow + 16 * fr, prow + 16 * (fr ^ 1));
+              if (k >= F8_QREG) {
+                const i32x8* q = &qt[pr][2 * (k - F8_QREG)][lane];
+                qop[k & 1][0] = lds_2xb128(q, (const i32x4*)q + 1);
+                qop[k & 1][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
+              }
+            };
+            kread(0);
+            s = f32x16{};
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+              if (k < F8_QREG)
+                lds_wait(kop[k & 1]);
+              else
+                lds_wait(kop[k & 1], qop[k & 1][0], qop[k & 1][1]);
+              if (k + 1 < 9) kread(k + 1);
+              s = mfma_fp8(kop[k & 1], k < F8_QREG ? qhi[k] : qop[k & 1][0], s);
+              s = mfma_fp8(kop[k & 1], k < F8_QREG ? qlo[k] : qop[k & 1][1], s);
+              sched_fence();
+            }
+            // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
+            if (own >= 32) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                s[i] *= ch;
+                mb = fmaxf(mb, s[i]);
+              }
+            } else {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                const int tok = 16 * (i >> 3) + 8 * hf + (i & 7);
+                s[i] = tok < own ? s[i] * ch : -INFINITY;
+                mb = fmaxf(mb, s[i]);
+              }
+            }
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = -INFINITY;
+          }
+          if (hf == 0) xmax[pr][dh][hh] = mb;
+          wg_barrier();
+          mt = fmaxf(mb, xmax[pr][dh ^ 1][hh]);  // tile max of the head
+          if (first) {
+            mref = mt;
+            first = false;
+          } else if (__ballot(mt > mref + F8_RESET)) {
+            cut = true;
+            break;
+          }
+        } else {
+          carry = false;
+          mref = mt;
+          first = false;
+        }
+        // P^T of this wave's block, shared with the partner wave
+        bf16x8 pown[2];
+        float ps = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          float p[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(s[8 * ks + e] - mref);
+            ps += p[e];
+          }
+          typedef float f8v __attribute__((ext_vector_type(8)));
+          pown[ks] = __builtin_convertvector(f8v{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]},
+                                             bf16x8);
+          xp[pr][dh][ks][lane] = pown[ks];
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        if (hf == 0) xsum[pr][dh][hh] = ps;
+        wg_barrier();
+        const bf16x8 po0 = xp[pr][dh ^ 1][0][lane], po1 = xp[pr][dh ^ 1][1][lane];
+        const bf16x8 pb[4] = {dh ? po0 : pown[0], dh ? po1 : pown[1], dh ? pown[0] : po0,
+                              dh ? pown[1] : po1};
+        lsum += dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
+        // O^T (this wave's 256 dims) += V^T P^T over the tile's tokens
+        const uint8_t* vt = st + vbase;
+        auto pv = [&](auto nks) {
+          constexpr int NKS = decltype(nks)::value;
+          // V^T operands of token k-step ks, one per 32-dim block (8 tokens of one dim per lane)
+          auto vread = [&](int ks, i32x2 (&r)[8]) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) r[dt] = lds_tr8(vt + 16 * ks * F8_DV + 32 * (dt ^ vx));
+          };
+          i32x2 raw[2][8];
+          vread(0, raw[0]);
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) {
+            lds_wait(raw[ks & 1]);
+            if (ks + 1 < NKS) vread(ks + 1, raw[(ks + 1) & 1]);
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+              oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp8x8_to_bf16(raw[ks & 1][dt]),
+                                                                pb[ks], oacc[dt], 0, 0, 0);
+            }
+            sched_fence();
+          }
+        };
+        if (valid > 32)
+          pv(std::integral_constant<int, 4>{});
+        else
+          pv(std::integral_constant<int, 2>{});  // second block fully masked: P = 0
+        ++t;
+      }
+
+      // ---- segment end: normalise, merge with an earlier segment, store this wave's 256 dims
+      const float lse_seg = mref + __log2f(lsum);
+      float w_seg = kvs / lsum, w_old = 0.f, lse_out = lse_seg;
+      if (have_scr) {
+        const float mx = fmaxf(lse_scr, lse_seg);
+        const float e_old = __builtin_amdgcn_exp2f(lse_scr - mx);
+        const float e_seg = __builtin_amdgcn_exp2f(lse_seg - mx);
+        const float tot = e_old + e_seg;
+        lse_out = mx + __log2f(tot);
+        w_old = e_old / tot;
+        w_seg *= e_seg / tot;
+      }
+      const int64_t scr_slot = (int64_t)g * F8_SLOTS + 2;
+      const f32x4* scr =
+          (const f32x4*)a.part_o + ((scr_slot * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
+      // value of output float4 (dt, q4) of this wave
+      auto val = [&](int dt, int q4, auto merge) {
+        f32x4 v = {oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+                   oacc[dt][4 * q4 + 3]};
+        v *= w_seg;
+        if constexpr (decltype(merge)::value) v += scr[(dt * 4 + q4) * 64] * w_old;
+        return v;
+      };
+      auto store = [&](auto merge) {
+        if (cut || !complete) {
+          const int64_t sb = (int64_t)g * F8_SLOTS + (cut ? 2 : slot);
+          f32x4* dst = (f32x4*)a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) dst[(dt * 4 + q4) * 64] = val(dt, q4, merge);
+            sched_fence();
+          }
+          if (dh == 0 && hf == 0) a.part_lse[sb * a.Hq + head] = lse_out;
+        } else {
+          using H = h16<O_BF16>;
+          uint16_t* o = a.out + qr * F8_DV + 256 * dh + 4 * hf;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const f32x4 v = val(dt, q4, merge);
+              *(u32x2*)(o + 32 * dt + 8 * q4) = u32x2{H::pack(v[0], v[1]), H::pack(v[2], v[3])};
+            }
+            sched_fence();
+          }
+        }
+      };
+      if (have_scr)
+        store(std::true_type{});
+      else
+        store(std::false_type{});
+      wait_vm(0);  // stores retire before the ring's vmcnt accounting resumes
+      if (!cut) break;
+      have_scr = true;
+      lse_scr = lse_out;
+      carry = true;  // tile t's scores are kept; the next segment starts from them
+    }
+  }
+}
+
+// Merge the partial slots of every sequence that spans more than one range; zero-length
+// sequences produce zeros. Workgroup = (sequence, 64-head group, 32-dim block of each half);
+// wave w reads what decode wave w stored, in the same lane layout.
+template <bool O_BF16>
+__global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
+  const int HG = a.Hq / F8_HEADS;
+  const int dt = blockIdx.x & 7;
+  const int bh = blockIdx.x >> 3;
+  const int hgi = bh % HG, b = bh / HG;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pr = wave >> 1, dh = wave & 1;
+  const int hh = lane & 31, hf = lane >> 5;
+  const int head = hgi * F8_HEADS + pr * 32 + hh;
+  using H = h16<O_BF16>;
+  uint16_t* o = a.out + ((int64_t)b * a.Hq + head) * F8_DV + 256 * dh + 32 * dt + 4 * hf;
+  const int64_t T = a.cu[a.B], c0 = a.cu[b], c1 = a.cu[b + 1];
+  if (c0 == c1) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) *(u32x2*)(o + 8 * q4) = u32x2{0u, 0u};
+    return;
+  }
+  const int64_t G = a.G;
+  const int64_t g0 = ((c0 + 1) * G - 1) / T, g1 = (c1 * G - 1) / T;
+  if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
+  auto start = [&](int64_t g) { return g * T / G; };
+  auto slot_of = [&](int64_t g) { return g * F8_SLOTS + ((g == g0 && c0 != start(g0)) ? 1 : 0); };
+  float mx = -INFINITY;
+  for (int64_t g = g0; g <= g1; ++g) {
+    if (start(g) == start(g + 1)) continue;
+    mx = fmaxf(mx, a.part_lse[slot_of(g) * a.Hq + head]);
+  }
+  float sum = 0.f;
+  for (int64_t g = g0; g <= g1; ++g) {
+    if (start(g) == start(g + 1)) continue;
+    sum += __builtin_amdgcn_exp2f(a.part_lse[slot_of(g) * a.Hq + head] - mx);
+  }
+  const float lse = mx + __log2f(sum);
+  f32x4 acc[4] = {};
+  for (int64_t g = g0; g <= g1; ++g) {
+    if (start(g) == start(g + 1)) continue;
+    const int64_t sb = slot_of(g);
+    const float w = __builtin_amdgcn_exp2f(a.part_lse[sb * a.Hq + head] - lse);
+    const f32x4* src =
+        (const f32x4*)a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) acc[q4] += src[q4 * 64] * w;
+  }
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    *(u32x2*)(o + 8 * q4) = u32x2{H::pack(acc[q4][0], acc[q4][1]), H::pack(acc[q4][2], acc[q4][3])};
+}
+
+size_t f8_cu_bytes(int64_t B) { return ((size_t)(B + 1) * 4 + 255) & ~(size_t)255; }
+
+// ranges per call: B * num_split workgroups shared by the Hq / 64 head groups
+int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
+  return std::max<int64_t>(1, B * num_split / (Hq / F8_HEADS));
+}
+
+}  // namespace
+
+// Workspace of the fp8 path: tile prefix, then lse and O partial slots (three 64-head x 512 slots
+// per range and head group).
+size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split) {
+  if (Hq % F8_HEADS) return 0;
+  const size_t G = (size_t)f8_ranges(B, Hq, num_split);
+  return f8_cu_bytes(B) + G * F8_SLOTS * (size_t)Hq * (F8_DV + 1) * sizeof(float);
+}
+
+// Returns TLM_EUNSUPPORTED (launching nothing) when the shape is outside this kernel's domain.
+int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                       const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                       int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
+                       void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                       int num_split, float score_scale, const float* kv_scale, bool q_bf16,
+                       bool o_bf16, void* stream) {
+  const int64_t tiles_per_seq = (max_pages * page + F8_TILE - 1) / F8_TILE;
+  if (Hq % F8_HEADS != 0 || page % F8_TILE != 0 || kv_stride > (1 << 24) ||
+      kpe_stride > (1 << 24) || B * tiles_per_seq > INT32_MAX)
+    return TLM_EUNSUPPORTED;
+  F8Args a;
+  a.q = (const uint16_t*)q;
+  a.q_pe = (const uint16_t*)q_pe;
+  a.q_stride = q_stride;
+  a.qpe_stride = q_pe_stride;
+  a.kv = (const uint8_t*)kv;
+  a.k_pe = (const uint8_t*)k_pe;
+  a.kv_stride = kv_stride;
+  a.kpe_stride = kpe_stride;
+  a.kv_rows = kv_rows;
+  a.bt = block_table;
+  a.seqlens = seqlens;
+  a.cu = (int32_t*)ws;
+  const int64_t G = f8_ranges(B, Hq, num_split);
+  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B));
+  a.part_o = a.part_lse + G * F8_SLOTS * Hq;
+  a.out = (uint16_t*)o;
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.page = (int)page;
+  a.max_pages = (int)max_pages;
+  a.G = (int)G;
+  a.lmax = (int)(max_pages * page);
+  a.score_scale = score_scale;
+  a.kv_scale = kv_scale;
+  hipStream_t st = (hipStream_t)stream;
+  const int HG = (int)(Hq / F8_HEADS);
+  mla_fp8_plan<<<1, 1024, 0, st>>>(a);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 plan)");
+  const dim3 grid((unsigned)(((G + 7) / 8) * 8 * HG));
+  if (q_bf16) {
+    if (o_bf16) mla_fp8_decode<true, true><<<grid, 256, 0, st>>>(a);
+    else mla_fp8_decode<true, false><<<grid, 256, 0, st>>>(a);
+  } else {
+    if (o_bf16) mla_fp8_decode<false, true><<<grid, 256, 0, st>>>(a);
+    else mla_fp8_decode<false, false><<<grid, 256, 0, st>>>(a);
+  }
+  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
+  const dim3 cgrid((unsigned)(B * HG * 8));
+  if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
+  else mla_fp8_combine<false><<<cgrid, 256, 0, st>>>(a);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 combine)");
+  return TLM_OK;
+}
