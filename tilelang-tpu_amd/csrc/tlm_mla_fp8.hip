@@ -118,8 +118,29 @@ TLM_DEV i32x8 lds_2xb128(const void* p0, const void* p1) {
   const i32x4 a = lds_b128(p0), b = lds_b128(p1);
   return i32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
+// LDS write issued as inline asm, for the same reason (a compiler-generated write may be made to
+// wait for the ring's LDS-DMA loads); wg_barrier() waits for it (lgkmcnt(0)) before publishing.
+TLM_DEV void lds_write_b64(void* p, u32x2 v) {
+  asm volatile("ds_write_b64 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
 // s_waitcnt lgkmcnt(0) that also orders the uses of the given asm-loaded operands after it
 TLM_DEV void lds_wait(i32x8& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a) : : "memory"); }
+// s_waitcnt lgkmcnt(n): all but the n most recent LDS accesses of this wave have completed (LDS
+// accesses complete in order; no scalar loads may be outstanding). n is a compile-time constant
+// after unrolling.
+TLM_DEV void lgkm_wait(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0xc27f); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0xc47f); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0xc67f); break;
+    default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+  }
+}
+TLM_DEV void order_after(i32x8& a) { asm volatile("" : "+v"(a) : : "memory"); }
+TLM_DEV void lds_wait(i32x8& a, i32x8& b) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b) : : "memory");
+}
 TLM_DEV void lds_wait(i32x8& a, i32x8& b, i32x8& c) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c) : : "memory");
 }
@@ -134,6 +155,12 @@ TLM_DEV void lds_wait(i32x2 (&r)[8]) {
 
 TLM_DEV f32x16 mfma_fp8(i32x8 a, i32x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// A unscaled (E8M0 127 = 1), B scaled by 2^(sb - 127). Operand k order: byte j of lane half h is
+// k = 32 (j / 16) + 16 h + j % 16; the scale of B's k-block kb (32 values) for column n comes
+// from lane 32 kb + n.
+TLM_DEV f32x16 mfma_fp8_bscaled(i32x8 a, i32x8 b, f32x16 c, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
 }
 
 // 8 e4m3 bytes -> 8 bf16 (exact)
@@ -208,17 +235,20 @@ TLM_DEV float prep_q(const uint16_t* qrow, const uint16_t* qperow, int hf, i32x8
   auto src = [&](int s, int v) -> const u32x4* {
     return (const u32x4*)(s < 8 ? qrow + 64 * s + 32 * hf + 8 * v : qperow + 32 * hf + 8 * v);
   };
+  u32x4 raw[9][4];
+#pragma unroll
+  for (int s = 0; s < 9; ++s)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) raw[s][v] = *src(s, v);
   float amax = 0.f;
 #pragma unroll
-  for (int s = 0; s < 9; ++s) {
+  for (int s = 0; s < 9; ++s)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const u32x4 w = *src(s, v);
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fmaxf(fabsf(H::lo(w[e])), fabsf(H::hi(w[e]))));
-    }
-    sched_fence();
-  }
+      for (int e = 0; e < 4; ++e)
+        amax = fmaxf(amax, fmaxf(fabsf(H::lo(raw[s][v][e])), fabsf(H::hi(raw[s][v][e]))));
+  sched_fence();
   amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
   int ex = 0;
   if (amax > 0.f) (void)frexpf(amax * (1.0f / 448.0f), &ex);  // amax / 2^ex <= 448
@@ -228,7 +258,7 @@ TLM_DEV float prep_q(const uint16_t* qrow, const uint16_t* qperow, int hf, i32x8
   for (int s = 0; s < 9; ++s)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const u32x4 w = *src(s, v);
+      const u32x4 w = raw[s][v];
       float x[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -278,7 +308,10 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[F8_NSTAGE * F8_STAGE];
   __shared__ float xmax[2][2][32];  // [pair][token block][head]: block maxima
   __shared__ float xsum[2][2][32];  // [pair][token block][head]: block sums of P
-  __shared__ __attribute__((aligned(16))) bf16x8 xp[2][2][2][64];  // [pair][block][kstep][lane]
+  // P^T blocks as e4m3 hi / lo terms: [pair][token block][hi, lo][head][32 tokens], and the
+  // E8M0 scale of each (block, head)
+  __shared__ __attribute__((aligned(16))) uint8_t xq[2][2][2][32][32];
+  __shared__ int xsc[2][2][32];
   // Q^T k-steps F8_QREG..8 of each pair: [pair][(k - F8_QREG) * 2 + hi/lo][lane]
   __shared__ __attribute__((aligned(16))) i32x8 qt[2][(9 - F8_QREG) * 2][64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -306,43 +339,76 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     b_first = lo;
   }
 
-  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 3
-  int ib = b_first;
-  int64_t ib_lo = ldc(a.cu + ib), ib_hi = ldc(a.cu + ib + 1);
-  auto issue = [&](int64_t t) {
-    while (t >= ib_hi) {
-      ++ib;
-      ib_lo = ib_hi;
-      ib_hi = ldc(a.cu + ib + 1);
+  // ---- per-tile page table: lane j holds the first KV row of tile tb + j and the number of its
+  // rows to load (the sequence's valid tokens that lie inside the pool; the rest read as zeros)
+  int64_t tb = INT64_MIN / 2;
+  uint32_t tab_lo = 0, tab_hi = 0;
+  int tab_n = 0;
+  auto build_table = [&](int64_t base) {
+    tb = base;
+    const int64_t tj = base + lane;
+    tab_lo = tab_hi = 0;
+    tab_n = 0;
+    if (tj < t_hi) {
+      int blo = 0, bhi = a.B - 1;  // largest b with cu[b] <= tj
+      while (blo < bhi) {
+        const int mid = (blo + bhi + 1) >> 1;
+        if (a.cu[mid] <= tj) blo = mid; else bhi = mid - 1;
+      }
+      const int L = max(0, min(a.seqlens[blo], a.lmax));
+      const int tok0 = (int)(tj - a.cu[blo]) * F8_TILE;
+      const int valid = min(F8_TILE, L - tok0);
+      const int64_t row0 =
+          (int64_t)a.bt[(int64_t)blo * a.max_pages + tok0 / a.page] * a.page + tok0 % a.page;
+      int64_t nrow = min((int64_t)valid, a.kv_rows - row0);
+      if (row0 < 0 || nrow < 0) nrow = 0;
+      tab_lo = (uint32_t)row0;
+      tab_hi = (uint32_t)((uint64_t)row0 >> 32);
+      tab_n = (int)nrow;
     }
-    const int L = max(0, min(ldc(a.seqlens + ib), a.lmax));
-    const int tok0 = (int)(t - ib_lo) * F8_TILE;
-    const int valid = min(F8_TILE, L - tok0);
-    const int64_t row0 =
-        (int64_t)ldc(a.bt + (int64_t)ib * a.max_pages + tok0 / a.page) * a.page + tok0 % a.page;
-    int64_t nrow = min((int64_t)valid, a.kv_rows - row0);
-    if (row0 < 0 || nrow < 0) nrow = 0;
+  };
+  build_table(t_lo);
+
+  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 3
+  struct Dma {  // one tile's source rows (base, byte count) and ring stage
+    const uint8_t* bkv;
+    const uint8_t* bpe;
+    int nkv, npe;
+    uint8_t* st;
+  };
+  auto issue_setup = [&](int64_t t) {
+    if (t >= tb + 64) build_table(t);
+    const int j = (int)(t - tb);
+    const int64_t row0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)tab_hi, j) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)tab_lo, j));
+    const int64_t nrow = __builtin_amdgcn_readlane(tab_n, j);
     const uint8_t* bkv = nrow > 0 ? a.kv + row0 * a.kv_stride : a.kv;
     const uint8_t* bpe = nrow > 0 ? a.k_pe + row0 * a.kpe_stride : a.k_pe;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)bkv, (short)0, (int)(nrow * a.kv_stride), F8_RSRC_WORD3);
-    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)bpe, (short)0, (int)(nrow * a.kpe_stride), F8_RSRC_WORD3);
-    uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      // latent: 2 rows x 32 chunks per wave-instruction
+    return Dma{bkv, bpe, (int)(nrow * a.kv_stride), (int)(nrow * a.kpe_stride),
+               ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE};
+  };
+  // LDS-DMA instruction k (0..8) of this thread for a tile: 0..7 latent, 8 rope
+  auto issue_dma = [&](const Dma& d, int k) {
+    if (k < 8) {  // latent: 2 rows x 32 chunks per wave-instruction
       const int r = 2 * (8 * wave + k) + hf;
       const int off = r * (int)a.kv_stride + 16 * ((lane & 31) ^ swz_lat(r));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(st + (8 * wave + k) * 1024), 16,
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + (8 * wave + k) * 1024), 16,
                                                off, 0, 0, 0);
-    }
-    {  // rope: 16 rows x 4 chunks per wave-instruction
+    } else {  // rope: 16 rows x 4 chunks per wave-instruction
       const int r = 16 * wave + (lane >> 2);
       const int off = r * (int)a.kpe_stride + 16 * ((lane & 3) ^ swz_rope(r));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(st + F8_LAT + wave * 1024), 16,
+      const __amdgpu_buffer_rsrc_t rp =
+          __builtin_amdgcn_make_buffer_rsrc((void*)d.bpe, (short)0, d.npe, F8_RSRC_WORD3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(d.st + F8_LAT + wave * 1024), 16,
                                                off, 0, 0, 0);
     }
+  };
+  auto issue = [&](int64_t t) {
+    const Dma d = issue_setup(t);
+#pragma unroll
+    for (int k = 0; k < F8_LOADS; ++k) issue_dma(d, k);
   };
   issue(t_lo);
   if (t_lo + 1 < t_hi) issue(t_lo + 1);
@@ -351,11 +417,18 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   const int th = tau(hh);                  // K row of this lane within its 32-token block
   const int fk = (2 * hf) ^ swz_lat(th);   // latent chunk of k-step s: (4 s) ^ fk
   const int fr = (2 * hf) ^ swz_rope(th);  // rope chunks: fr, fr ^ 1
+  // V^T operand of a 32-dim block: lane (dim l % 32, half h) holds tokens 16 h + 0..15 and
+  // 32 + 16 h + 0..15, read as four 8-token transposes r = 0..3 at rows
+  // 16 h + 8 (r & 1) + 32 (r >> 1) + (lane % 16) / 2; the swizzle depends on r & 1 only
   const int i16 = lane & 15, gq = lane >> 4;
-  const int vrow = 8 * (gq >> 1) + (i16 >> 1);  // V^T row (token) within a 16-token k-step
-  const int vu = (gq & 1) ^ swz_lat(vrow);
-  const int vbase = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1) + 256 * dh;
-  const int vx = vu >> 1;
+  int vbase[2], vx[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int vrow = 16 * (gq >> 1) + 8 * par + (i16 >> 1);
+    const int vu = (gq & 1) ^ swz_lat(vrow);
+    vbase[par] = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1) + 256 * dh;
+    vx[par] = vu >> 1;
+  }
 
   i32x8 qhi[F8_QREG], qlo[F8_QREG];
   int64_t t = t_lo;
@@ -376,8 +449,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
     const int slot = p_lo == t_lo ? 0 : 1;
     bool have_scr = false, carry = false;
-    float lse_scr = 0.f, mt = 0.f;
-    f32x16 s;  // scores of this wave's 32-token block (log2 units, masked)
+    float lse_scr = 0.f, mt = 0.f, mbo = -INFINITY;
+    f32x16 s;  // raw scores of this wave's 32-token block (masked to -inf past the sequence)
     for (;;) {  // one iteration per softmax segment (normally one per piece)
       f32x16 oacc[8];
 #pragma unroll
@@ -391,58 +464,63 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
           // hand over tile t, refill the stage freed by tile t - 1
           wait_vm(t + 1 < t_hi ? F8_LOADS : 0);
           wg_barrier();
-          if (t + 2 < t_hi) issue(t + 2);
+          const bool refill = t + 2 < t_hi;
+          const Dma dma = refill ? issue_setup(t + 2) : Dma{};
           // S^T = K Q^T for this wave's 32 tokens x 32 heads
           const int own = valid - 32 * dh;
           float mb = -INFINITY;
+          if (own <= 0 && refill) issue(t + 2);
           if (own > 0) {
             const uint8_t* krow = st + (32 * dh + th) * F8_DV;
             const uint8_t* prow = st + F8_LAT + (32 * dh + th) * F8_DPE;
             // operands of k-step k: K (32 bytes of this lane's row) and, past F8_QREG, Q^T hi/lo
-            i32x8 kop[2], qop[2][2];
+            i32x8 kop[3], qop[3][2];
+            auto nreads = [](int k) { return k < F8_QREG ? 2 : 6; };  // LDS reads of k-step k
             auto kread = [&](int k) {
-              kop[k & 1] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk),
+              kop[k % 3] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk),
                                               krow + 16 * (((4 * k) ^ fk) ^ 1))
                                  : lds_2xb128(prow + 16 * fr, prow + 16 * (fr ^ 1));
               if (k >= F8_QREG) {
                 const i32x8* q = &qt[pr][2 * (k - F8_QREG)][lane];
-                qop[k & 1][0] = lds_2xb128(q, (const i32x4*)q + 1);
-                qop[k & 1][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
+                qop[k % 3][0] = lds_2xb128(q, (const i32x4*)q + 1);
+                qop[k % 3][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
               }
             };
             kread(0);
+            kread(1);
             s = f32x16{};
 #pragma unroll
             for (int k = 0; k < 9; ++k) {
-              if (k < F8_QREG)
-                lds_wait(kop[k & 1]);
-              else
-                lds_wait(kop[k & 1], qop[k & 1][0], qop[k & 1][1]);
-              if (k + 1 < 9) kread(k + 1);
-              s = mfma_fp8(kop[k & 1], k < F8_QREG ? qhi[k] : qop[k & 1][0], s);
-              s = mfma_fp8(kop[k & 1], k < F8_QREG ? qlo[k] : qop[k & 1][1], s);
+              // reads of k-step k done; those of k + 1 may still be in flight
+              lgkm_wait(k + 1 < 9 ? nreads(k + 1) : 0);
+              order_after(kop[k % 3]);
+              if (k >= F8_QREG) {
+                order_after(qop[k % 3][0]);
+                order_after(qop[k % 3][1]);
+              }
+              if (k + 2 < 9) kread(k + 2);
+              if (refill) issue_dma(dma, k);
+              s = mfma_fp8(kop[k % 3], k < F8_QREG ? qhi[k] : qop[k % 3][0], s);
+              s = mfma_fp8(kop[k % 3], k < F8_QREG ? qlo[k] : qop[k % 3][1], s);
               sched_fence();
             }
-            // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
-            if (own >= 32) {
-#pragma unroll
-              for (int i = 0; i < 16; ++i) {
-                s[i] *= ch;
-                mb = fmaxf(mb, s[i]);
-              }
-            } else {
+            // raw scores (the log2-domain scale ch > 0 is applied inside exp2); element i is token
+            // 16 (i / 8) + 8 hf + i % 8 of the block
+            if (own < 32) {
 #pragma unroll
               for (int i = 0; i < 16; ++i) {
                 const int tok = 16 * (i >> 3) + 8 * hf + (i & 7);
-                s[i] = tok < own ? s[i] * ch : -INFINITY;
-                mb = fmaxf(mb, s[i]);
+                if (tok >= own) s[i] = -INFINITY;
               }
             }
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[i]);
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * ch;
           } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[i] = -INFINITY;
           }
+          mbo = mb;
           if (hf == 0) xmax[pr][dh][hh] = mb;
           wg_barrier();
           mt = fmaxf(mb, xmax[pr][dh ^ 1][hh]);  // tile max of the head
@@ -458,56 +536,81 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
           mref = mt;
           first = false;
         }
-        // P^T of this wave's block, shared with the partner wave
-        bf16x8 pown[2];
-        float ps = 0.f;
+        // P^T of this wave's block as two e4m3 terms on a per-head power-of-two scale 2^es (es =
+        // exponent of the block's largest P minus 8, so scaled values are below 256), folded into
+        // the exp2 argument; exchanged with the partner wave through LDS
+        int es = 0;
+        if (mbo != -INFINITY) {
+          (void)frexpf(__builtin_amdgcn_exp2f(mbo - mref), &es);
+          es = max(-127, min(127, es - 8));
+        }
+        float x[16], ps = 0.f;
+        const float sh = -(mref + (float)es);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          float p[8];
+        for (int i = 0; i < 16; ++i) {
+          x[i] = __builtin_amdgcn_exp2f(fmaf(s[i], ch, sh));
+          ps += x[i];
+        }
+        ps = ldexpf(ps, es);
+        {
+          int phi4[4], plo4[4];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(s[8 * ks + e] - mref);
-            ps += p[e];
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const float* y = x + 4 * q4;
+            phi4[q4] = pack_fp8x4(y[0], y[1], y[2], y[3]);
+            typedef float f2 __attribute__((ext_vector_type(2)));
+            const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], false);
+            const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], true);
+            plo4[q4] = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
           }
-          typedef float f8v __attribute__((ext_vector_type(8)));
-          pown[ks] = __builtin_convertvector(f8v{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]},
-                                             bf16x8);
-          xp[pr][dh][ks][lane] = pown[ks];
+          // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
+          uint8_t* rh = &xq[pr][dh][0][hh][8 * hf];
+          uint8_t* rl = &xq[pr][dh][1][hh][8 * hf];
+          lds_write_b64(rh, u32x2{(uint32_t)phi4[0], (uint32_t)phi4[1]});
+          lds_write_b64(rh + 16, u32x2{(uint32_t)phi4[2], (uint32_t)phi4[3]});
+          lds_write_b64(rl, u32x2{(uint32_t)plo4[0], (uint32_t)plo4[1]});
+          lds_write_b64(rl + 16, u32x2{(uint32_t)plo4[2], (uint32_t)plo4[3]});
         }
         ps += __shfl_xor(ps, 32, 64);
-        if (hf == 0) xsum[pr][dh][hh] = ps;
+        if (hf == 0) {
+          xsum[pr][dh][hh] = ps;
+          xsc[pr][dh][hh] = es + 127;
+        }
         wg_barrier();
-        const bf16x8 po0 = xp[pr][dh ^ 1][0][lane], po1 = xp[pr][dh ^ 1][1][lane];
-        const bf16x8 pb[4] = {dh ? po0 : pown[0], dh ? po1 : pown[1], dh ? pown[0] : po0,
-                              dh ? pown[1] : po1};
         lsum += dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
-        // O^T (this wave's 256 dims) += V^T P^T over the tile's tokens
-        const uint8_t* vt = st + vbase;
-        auto pv = [&](auto nks) {
-          constexpr int NKS = decltype(nks)::value;
-          // V^T operands of token k-step ks, one per 32-dim block (8 tokens of one dim per lane)
-          auto vread = [&](int ks, i32x2 (&r)[8]) {
+        // B operand: lane (head hh, half hf) holds tokens 16 hf + 0..15 of both blocks; its scale
+        // is that of block hf
+        i32x8 pbh = lds_2xb128(&xq[pr][0][0][hh][16 * hf], &xq[pr][1][0][hh][16 * hf]);
+        i32x8 pbl = lds_2xb128(&xq[pr][0][1][hh][16 * hf], &xq[pr][1][1][hh][16 * hf]);
+        const int psc = xsc[pr][hf][hh];
+        // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks x hi/lo
+        auto vread = [&](int dt) {
+          i32x2 r[4];
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) r[dt] = lds_tr8(vt + 16 * ks * F8_DV + 32 * (dt ^ vx));
-          };
-          i32x2 raw[2][8];
-          vread(0, raw[0]);
-#pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) {
-            lds_wait(raw[ks & 1]);
-            if (ks + 1 < NKS) vread(ks + 1, raw[(ks + 1) & 1]);
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-              oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp8x8_to_bf16(raw[ks & 1][dt]),
-                                                                pb[ks], oacc[dt], 0, 0, 0);
-            }
-            sched_fence();
-          }
+          for (int rr = 0; rr < 4; ++rr)
+            r[rr] = lds_tr8(st + vbase[rr & 1] + 32 * F8_DV * (rr >> 1) +
+                            32 * (dt ^ vx[rr & 1]));
+          return i32x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
         };
-        if (valid > 32)
-          pv(std::integral_constant<int, 4>{});
-        else
-          pv(std::integral_constant<int, 2>{});  // second block fully masked: P = 0
+        i32x8 vop[2][2];
+        vop[0][0] = vread(0);
+        vop[0][1] = vread(1);
+        lds_wait(pbh, pbl);
+#pragma unroll
+        for (int g2 = 0; g2 < 4; ++g2) {
+          lds_wait(vop[g2 & 1][0], vop[g2 & 1][1]);
+          if (g2 + 1 < 4) {
+            vop[(g2 + 1) & 1][0] = vread(2 * g2 + 2);
+            vop[(g2 + 1) & 1][1] = vread(2 * g2 + 3);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int dt = 2 * g2 + u;
+            oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbh, oacc[dt], psc);
+            oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbl, oacc[dt], psc);
+          }
+          sched_fence();
+        }
         ++t;
       }
 
