@@ -188,7 +188,9 @@ struct F8Args {
   int64_t kv_stride, kpe_stride, kv_rows;  // bytes between token rows; rows in the pool
   const int32_t* bt;
   const int32_t* seqlens;
-  int32_t* cu;  // [B + 1] tile prefix over sequences (written by the plan kernel)
+  int32_t* cu;  // [B + 1] tile prefix over sequences (written by the prep kernel)
+  uint8_t* qsplit;  // [B * Hq][2][576] e4m3 hi and lo terms of q / 2^qexp (written by prep)
+  int32_t* qexp;    // [B * Hq] power-of-two exponent of each head's Q scale
   float* part_lse;
   float* part_o;
   uint16_t* out;
@@ -198,98 +200,111 @@ struct F8Args {
   const float* kv_scale;
 };
 
-// Tile prefix over sequences: cu[b] = sum_{b' < b} ceil(L_b' / 64), cu[B] = total.
-__global__ __launch_bounds__(1024) void mla_fp8_plan(const F8Args a) {
-  __shared__ int32_t part[1024];
-  const int t = threadIdx.x;
-  const int per = (a.B + 1023) / 1024;
-  const int b0 = min(a.B, t * per), b1 = min(a.B, b0 + per);
-  auto tiles = [&](int b) {
-    const int L = max(0, min(a.seqlens[b], a.lmax));
-    return (L + F8_TILE - 1) / F8_TILE;
-  };
-  int32_t s = 0;
-  for (int b = b0; b < b1; ++b) s += tiles(b);
-  part[t] = s;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t v = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int32_t run = part[t] - s;
-  for (int b = b0; b < b1; ++b) {
-    a.cu[b] = run;
-    run += tiles(b);
-  }
-  if (t == 1023) a.cu[a.B] = part[1023];
-}
+constexpr int F8_QROW = 2 * (F8_DV + F8_DPE);  // bytes per (sequence, head) in qsplit
 
-// Q^T operand of one head for S^T = K Q^T: k-step s (64 dims: 0..7 latent, 8 rope), lane half hf
-// holds dims 64 s + 32 hf + j at byte j. q / s_h = hi + lo, both e4m3; returns s_h.
+// Prep kernel, one launch ahead of the decode kernel:
+//   * workgroups 0 .. nq-1: one wave per (sequence, head) splits that Q row into two e4m3 terms,
+//     q / 2^e = hi + lo, with 2^e the power of two that puts max|q| at <= 448; hi + lo is exact
+//     for every element within 2^10 of the row maximum (a bf16/fp16 value has at most 8/11
+//     significant bits and the residual of the first rounding fits e4m3's 4);
+//   * workgroup nq: tile prefix over sequences, cu[b] = sum_{b' < b} ceil(L_b' / 64).
 template <bool Q_BF16>
-TLM_DEV float prep_q(const uint16_t* qrow, const uint16_t* qperow, int hf, i32x8 (&qhi)[F8_QREG],
-                     i32x8 (&qlo)[F8_QREG], i32x8* qt, bool write_qt) {
+__global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
+  if ((int)blockIdx.x == nq) {
+    __shared__ int32_t part[256];
+    const int t = threadIdx.x;
+    const int per = (a.B + 255) / 256;
+    const int b0 = min(a.B, t * per), b1 = min(a.B, b0 + per);
+    auto tiles = [&](int b) {
+      const int L = max(0, min(a.seqlens[b], a.lmax));
+      return (L + F8_TILE - 1) / F8_TILE;
+    };
+    int32_t sum = 0;
+    for (int b = b0; b < b1; ++b) sum += tiles(b);
+    part[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int32_t v = t >= off ? part[t - off] : 0;
+      __syncthreads();
+      part[t] += v;
+      __syncthreads();
+    }
+    int32_t run = part[t] - sum;
+    for (int b = b0; b < b1; ++b) {
+      a.cu[b] = run;
+      run += tiles(b);
+    }
+    if (t == 255) a.cu[a.B] = part[255];
+    return;
+  }
   using H = h16<Q_BF16>;
-  auto src = [&](int s, int v) -> const u32x4* {
-    return (const u32x4*)(s < 8 ? qrow + 64 * s + 32 * hf + 8 * v : qperow + 32 * hf + 8 * v);
-  };
-  u32x4 raw[9][4];
-#pragma unroll
-  for (int s = 0; s < 9; ++s)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) raw[s][v] = *src(s, v);
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.Hq) return;
+  // lane: latent dims 8 lane .. +7; lanes 0..7 also rope dims 8 lane .. +7
+  const u32x4 wl = *(const u32x4*)(a.q + row * a.q_stride + 8 * lane);
+  const bool has_pe = lane < 8;
+  const u32x4 wp = has_pe ? *(const u32x4*)(a.q_pe + row * a.qpe_stride + 8 * lane)
+                          : u32x4{0u, 0u, 0u, 0u};
   float amax = 0.f;
 #pragma unroll
-  for (int s = 0; s < 9; ++s)
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        amax = fmaxf(amax, fmaxf(fabsf(H::lo(raw[s][v][e])), fabsf(H::hi(raw[s][v][e]))));
-  sched_fence();
-  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  for (int e = 0; e < 4; ++e)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(H::lo(wl[e])), fabsf(H::hi(wl[e]))),
+                             fmaxf(fabsf(H::lo(wp[e])), fabsf(H::hi(wp[e])))));
+  amax = wave_max(amax);
   int ex = 0;
   if (amax > 0.f) (void)frexpf(amax * (1.0f / 448.0f), &ex);  // amax / 2^ex <= 448
   const float inv = ldexpf(1.0f, -ex);
-  i32x8 tail[2];
+  auto split8 = [&](u32x4 w, u32x2& hi, u32x2& lo) {
+    float x[8];
 #pragma unroll
-  for (int s = 0; s < 9; ++s)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const u32x4 w = raw[s][v];
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[2 * e] = H::lo(w[e]) * inv;
-        x[2 * e + 1] = H::hi(w[e]) * inv;
-      }
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const float* y = x + 4 * h2;
-        const int hi = pack_fp8x4(y[0], y[1], y[2], y[3]);
-        typedef float f2 __attribute__((ext_vector_type(2)));
-        const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-        const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-        const int lo = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
-        if (s < F8_QREG) {
-          qhi[s][2 * v + h2] = hi;
-          qlo[s][2 * v + h2] = lo;
-        } else {
-          tail[0][2 * v + h2] = hi;
-          tail[1][2 * v + h2] = lo;
-        }
-      }
-      if (v == 3) {
-        if (s >= F8_QREG && write_qt) {
-          qt[(2 * (s - F8_QREG)) * 64] = tail[0];
-          qt[(2 * (s - F8_QREG) + 1) * 64] = tail[1];
-        }
-        sched_fence();
-      }
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = H::lo(w[e]) * inv;
+      x[2 * e + 1] = H::hi(w[e]) * inv;
     }
-  return ldexpf(1.0f, ex);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const float* y = x + 4 * h2;
+      const int h = pack_fp8x4(y[0], y[1], y[2], y[3]);
+      typedef float f2 __attribute__((ext_vector_type(2)));
+      const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(h, false);
+      const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(h, true);
+      hi[h2] = (uint32_t)h;
+      lo[h2] = (uint32_t)pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
+    }
+  };
+  uint8_t* qs = a.qsplit + row * F8_QROW;
+  u32x2 hi, lo;
+  split8(wl, hi, lo);
+  *(u32x2*)(qs + 8 * lane) = hi;
+  *(u32x2*)(qs + F8_DV + F8_DPE + 8 * lane) = lo;
+  if (has_pe) {
+    split8(wp, hi, lo);
+    *(u32x2*)(qs + F8_DV + 8 * lane) = hi;
+    *(u32x2*)(qs + 2 * F8_DV + F8_DPE + 8 * lane) = lo;
+  }
+  if (lane == 0) a.qexp[row] = ex;
+}
+
+// Q^T operand of one head for S^T = K Q^T, from the prep kernel's split: k-step s (64 dims: 0..7
+// latent, 8 rope), lane half hf holds dims 64 s + 32 hf + j at byte j. k-steps >= F8_QREG go to
+// the pair's LDS copy (written by one wave of the pair). Returns the scale 2^e of the head.
+TLM_DEV float load_q(const F8Args& a, int64_t row, int hf, i32x8 (&qhi)[F8_QREG],
+                     i32x8 (&qlo)[F8_QREG], i32x8* qt, bool write_qt) {
+  const uint8_t* qs = a.qsplit + row * F8_QROW;
+#pragma unroll
+  for (int k = 0; k < F8_QREG; ++k) {
+    qhi[k] = *(const i32x8*)(qs + 64 * k + 32 * hf);
+    qlo[k] = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * k + 32 * hf);
+  }
+  if (write_qt) {
+#pragma unroll
+    for (int k = F8_QREG; k < 9; ++k) {
+      qt[(2 * (k - F8_QREG)) * 64] = *(const i32x8*)(qs + 64 * k + 32 * hf);
+      qt[(2 * (k - F8_QREG) + 1) * 64] = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * k + 32 * hf);
+    }
+  }
+  return ldexpf(1.0f, a.qexp[row]);
 }
 
 // Workgroup index -> (range, 64-head group), keeping the head groups of one range on one XCD
@@ -303,7 +318,7 @@ TLM_DEV F8Work f8_work(int x, int HG) {
   return F8Work{(k / HG) * 8 + xcd, k % HG};
 }
 
-template <bool Q_BF16, bool O_BF16>
+template <bool O_BF16>
 __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[F8_NSTAGE * F8_STAGE];
   __shared__ float xmax[2][2][32];  // [pair][token block][head]: block maxima
@@ -442,9 +457,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     }
     const int L = max(0, min(ldc(a.seqlens + cb), a.lmax));
     const int64_t qr = (int64_t)cb * a.Hq + head;
-    const float ch = a.score_scale * kvs *
-                     prep_q<Q_BF16>(a.q + qr * a.q_stride, a.q_pe + qr * a.qpe_stride, hf, qhi, qlo,
-                                    &qt[pr][0][lane], dh == 0);
+    const float ch = a.score_scale * kvs * load_q(a, qr, hf, qhi, qlo, &qt[pr][0][lane], dh == 0);
     const int64_t p_lo = t, p_hi = min(t_hi, cb_hi);
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
     const int slot = p_lo == t_lo ? 0 : 1;
@@ -728,7 +741,11 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
     *(u32x2*)(o + 8 * q4) = u32x2{H::pack(acc[q4][0], acc[q4][1]), H::pack(acc[q4][2], acc[q4][3])};
 }
 
-size_t f8_cu_bytes(int64_t B) { return ((size_t)(B + 1) * 4 + 255) & ~(size_t)255; }
+size_t f8_align(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t f8_cu_bytes(int64_t B) { return f8_align((size_t)(B + 1) * 4); }
+size_t f8_q_bytes(int64_t B, int64_t Hq) {
+  return f8_align((size_t)B * Hq * F8_QROW) + f8_align((size_t)B * Hq * 4);
+}
 
 // ranges per call: B * num_split workgroups shared by the Hq / 64 head groups
 int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
@@ -742,7 +759,7 @@ int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
 size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split) {
   if (Hq % F8_HEADS) return 0;
   const size_t G = (size_t)f8_ranges(B, Hq, num_split);
-  return f8_cu_bytes(B) + G * F8_SLOTS * (size_t)Hq * (F8_DV + 1) * sizeof(float);
+  return f8_cu_bytes(B) + f8_q_bytes(B, Hq) + G * F8_SLOTS * (size_t)Hq * (F8_DV + 1) * sizeof(float);
 }
 
 // Returns TLM_EUNSUPPORTED (launching nothing) when the shape is outside this kernel's domain.
@@ -770,7 +787,9 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.seqlens = seqlens;
   a.cu = (int32_t*)ws;
   const int64_t G = f8_ranges(B, Hq, num_split);
-  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B));
+  a.qsplit = (uint8_t*)ws + f8_cu_bytes(B);
+  a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
+  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B) + f8_q_bytes(B, Hq));
   a.part_o = a.part_lse + G * F8_SLOTS * Hq;
   a.out = (uint16_t*)o;
   a.B = (int)B;
@@ -783,16 +802,17 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.kv_scale = kv_scale;
   hipStream_t st = (hipStream_t)stream;
   const int HG = (int)(Hq / F8_HEADS);
-  mla_fp8_plan<<<1, 1024, 0, st>>>(a);
-  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 plan)");
+  const int nq = (int)((B * Hq + 3) / 4);
+  if (q_bf16)
+    mla_fp8_prep<true><<<nq + 1, 256, 0, st>>>(a, nq);
+  else
+    mla_fp8_prep<false><<<nq + 1, 256, 0, st>>>(a, nq);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 prep)");
   const dim3 grid((unsigned)(((G + 7) / 8) * 8 * HG));
-  if (q_bf16) {
-    if (o_bf16) mla_fp8_decode<true, true><<<grid, 256, 0, st>>>(a);
-    else mla_fp8_decode<true, false><<<grid, 256, 0, st>>>(a);
-  } else {
-    if (o_bf16) mla_fp8_decode<false, true><<<grid, 256, 0, st>>>(a);
-    else mla_fp8_decode<false, false><<<grid, 256, 0, st>>>(a);
-  }
+  if (o_bf16)
+    mla_fp8_decode<true><<<grid, 256, 0, st>>>(a);
+  else
+    mla_fp8_decode<false><<<grid, 256, 0, st>>>(a);
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
   const dim3 cgrid((unsigned)(B * HG * 8));
   if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
