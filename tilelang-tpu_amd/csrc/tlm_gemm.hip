@@ -87,6 +87,54 @@ TLM_DEV void store_out(void* C, int64_t idx, float v) {
     ((uint16_t*)C)[idx] = (uint16_t)f32_to_f16_bits(v);
 }
 
+// LDS access as inline asm: compiler-generated LDS reads may be made to wait for every
+// outstanding LDS-DMA load (including the prefetch of the next k-tile) when the compiler cannot
+// prove that they touch the other stage. Waits are explicit (lgkm_wait + order_after).
+TLM_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+TLM_DEV u32x4 lds_b128(const void* p) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+TLM_DEV u32x2 lds_tr16(const void* p) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+TLM_DEV void lgkm_wait(int n) {  // lgkmcnt(n); n a compile-time constant after unrolling
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0xc87f); break;
+    default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+  }
+}
+TLM_DEV void order_after(u32x4& a) { asm volatile("" : "+v"(a) : : "memory"); }
+TLM_DEV void barrier_lds() {  // workgroup barrier; LDS-DMA loads stay in flight
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+TLM_DEV void wait_dma() {  // this thread's LDS-DMA loads have landed
+  __builtin_amdgcn_s_waitcnt(0x3f70);
+}
+
+constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr uint32_t OOB = 0xfffffff0u;   // offset past num_records: the load returns zeros
+// LDS tiles (16-bit elements, no padding), 16-byte chunks XOR-swizzled so that the MFMA operand
+// reads are bank-conflict free and every LDS-DMA instruction fills 1 KB of contiguous LDS:
+//   * [rows][64 k] tiles (A, and B^T): chunk c of row r at c ^ ((r >> 1) & 7);
+//     a 16-lane ds_read_b128 phase covers rows r0..r0+15 of one chunk column;
+//   * [64 k][256 n] row-major B: chunk c of row k at c ^ (4 (k & 3)); a 32-lane
+//     ds_read_b64_tr_b16 phase covers 4 k-rows x 64 bytes.
+TLM_DEV int swz_rows(int r) { return (r >> 1) & 7; }
+TLM_DEV int swz_k(int k) { return 4 * (k & 3); }
+constexpr int ST_A = BM * BK * 2;                 // bytes per stage of A
+constexpr int ST_B = BK * BN * 2;                 // bytes per stage of B (either layout)
+constexpr int STAGE = ST_A + ST_B;
+
 template <bool BF16, bool TRANS_B, int OUT>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __restrict__ A,
                                                            const uint16_t* __restrict__ B,
@@ -94,14 +142,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
                                                            int K) {
   using MT = mfma_t<BF16>;
   using v8 = typename MT::v8;
-  constexpr int B_STAGE = TRANS_B ? B_STAGE_T : B_STAGE_N;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (A_STAGE + B_STAGE)];
-  uint16_t* sA = smem;
-  uint16_t* sB = smem + 2 * A_STAGE;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2;  // 0..1: 128-row half
   const int wn = wave & 3;   // 0..3: 64-col quarter
   int tm, tn;
@@ -109,47 +154,48 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = (K + BK - 1) / BK;
 
-  // global -> register staging (4 A vectors + 4 B vectors of 8 halves per thread)
-  u32x4 ra[4], rb[4];
-  auto load_tile = [&](int kt) {
+  // ---- LDS-DMA fill: 8 wave-instructions of 1 KB per thread per k-tile (4 for A, 4 for B)
+  auto issue = [&](int kt, int stage) {
     const int k0 = kt * BK;
+    uint8_t* sa = smem + stage * STAGE;
+    uint8_t* sb = sa + ST_A;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + ((int64_t)m0 * K + k0)), (short)0, 0x7ffffff0, RSRC_WORD3);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
-      const int gm = m0 + r, gk = k0 + c;
-      ra[p] = (gm < M && gk < K) ? *(const u32x4*)(A + (int64_t)gm * K + gk) : u32x4{0, 0, 0, 0};
+      const int ins = wave * 4 + p;             // 8 rows of 128 bytes
+      const int r = 8 * ins + (lane >> 3);
+      const int c = (lane & 7) ^ swz_rows(r);   // global chunk landing in slot lane & 7
+      const bool ok = m0 + r < M && k0 + 8 * c < K;
+      const uint32_t off = ok ? (uint32_t)(r * K + 8 * c) * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sa + ins * 1024),
+                                               16, off, 0, 0, 0);
     }
+    if constexpr (TRANS_B) {
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(B + ((int64_t)n0 * K + k0)), (short)0, 0x7ffffff0, RSRC_WORD3);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      if constexpr (TRANS_B) {
-        const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
-        const int gn = n0 + r, gk = k0 + c;
-        rb[p] = (gn < N && gk < K) ? *(const u32x4*)(B + (int64_t)gn * K + gk)
-                                   : u32x4{0, 0, 0, 0};
-      } else {
-        const int r = (tid >> 5) + 16 * p, c = (tid & 31) * 8;
-        const int gk = k0 + r, gn = n0 + c;
-        rb[p] = (gk < K && gn < N) ? *(const u32x4*)(B + (int64_t)gk * N + gn)
-                                   : u32x4{0, 0, 0, 0};
+      for (int p = 0; p < 4; ++p) {
+        const int ins = wave * 4 + p;
+        const int r = 8 * ins + (lane >> 3);
+        const int c = (lane & 7) ^ swz_rows(r);
+        const bool ok = n0 + r < N && k0 + 8 * c < K;
+        const uint32_t off = ok ? (uint32_t)(r * K + 8 * c) * 2u : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (__attribute__((address_space(3))) void*)(sb + ins * 1024), 16, off, 0, 0, 0);
       }
-    }
-  };
-  auto store_tile = [&](int stage) {
-    uint16_t* a = sA + stage * A_STAGE;
-    uint16_t* b = sB + stage * B_STAGE;
+    } else {
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(B + ((int64_t)k0 * N + n0)), (short)0, 0x7ffffff0, RSRC_WORD3);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
-      *(u32x4*)(a + r * A_PITCH + c) = ra[p];
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      if constexpr (TRANS_B) {
-        const int r = (tid >> 3) + 64 * p, c = (tid & 7) * 8;
-        *(u32x4*)(b + r * BT_PITCH + c) = rb[p];
-      } else {
-        const int r = (tid >> 5) + 16 * p, c = (tid & 31) * 8;
-        *(u32x4*)(b + r * BN_PITCH + c) = rb[p];
+      for (int p = 0; p < 4; ++p) {
+        const int ins = wave * 4 + p;             // 2 k-rows of 512 bytes
+        const int k = 2 * ins + (lane >> 5);
+        const int c = (lane & 31) ^ swz_k(k);
+        const bool ok = k0 + k < K && n0 + 8 * c < N;
+        const uint32_t off = ok ? (uint32_t)(k * N + 8 * c) * 2u : OOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (__attribute__((address_space(3))) void*)(sb + ins * 1024), 16, off, 0, 0, 0);
       }
     }
   };
@@ -160,47 +206,80 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  // per-lane constant offsets of the MFMA operand reads
-  const int a_row = wm * 128 + (lane & 31);
-  const int a_col = 8 * (lane >> 5);
-  // transpose-read lane roles: group h of 16 lanes, row r = j/4 within the 4-row block, chunk q
+  // ---- per-lane operand read offsets (bytes within a stage)
+  const int hf = lane >> 5;
+  const int sw = (lane >> 1) & 7;                              // swz_rows of this lane's rows
+  const int a_row = (wm * 128 + (lane & 31)) * (BK * 2);       // + mi * 32 rows
+  const int bt_row = (wn * 64 + (lane & 31)) * (BK * 2);       // + ni * 32 rows (B^T)
+  // row-major B through ds_read_b64_tr_b16: group h of 16 lanes, lane j in it
   const int h = lane >> 4, j = lane & 15;
-  const int tr_n = wn * 64 + 16 * (h & 1) + 4 * (j & 3);
-  const int tr_k = 8 * (h >> 1) + (j >> 2);
-  const int bt_row = wn * 64 + (lane & 31);
+  const int tr_k = 8 * (h >> 1) + (j >> 2);                    // + 16 ks, + 4 for the 2nd read
+  const int tr_c = 8 * wn + 2 * (h & 1) + ((j & 3) >> 1);      // + 4 ni
+  const int tr_off = tr_k * (BN * 2) + 8 * (j & 1);
 
+  struct Ops {
+    u32x4 a[4], b[2][2];
+  };
+  auto reads = [&](int stage, int ks, Ops& o) {
+    const uint8_t* sa = smem + stage * STAGE;
+    const uint8_t* sb = sa + ST_A;
+    const int ca = 16 * ((2 * ks + hf) ^ sw);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) o.a[mi] = lds_b128(sa + a_row + mi * 32 * BK * 2 + ca);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      if constexpr (TRANS_B) {
+        o.b[ni][0] = lds_b128(sb + bt_row + ni * 32 * BK * 2 + ca);
+      } else {
+        const uint8_t* p = sb + (16 * ks) * (BN * 2) + tr_off;
+        const int c = tr_c + 4 * ni;
+        const u32x2 lo = lds_tr16(p + 16 * (c ^ swz_k(j >> 2)));
+        const u32x2 hi = lds_tr16(p + 4 * (BN * 2) + 16 * (c ^ swz_k(j >> 2)));
+        o.b[ni][0] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    }
+  };
+  auto order = [&](Ops& o) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) order_after(o.a[mi]);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) order_after(o.b[ni][0]);
+  };
+  // LDS instructions issued by reads(): 4 for A, 2 (B^T) or 4 (transposed B reads) for B
+  constexpr int NREAD = TRANS_B ? 6 : 8;
+  static_assert(NREAD == 8 || TRANS_B, "lgkm_wait covers 8 outstanding reads");
+
+  issue(0, 0);
+  wait_dma();
+  barrier_lds();
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool has_next = kt + 1 < KT;
-    if (has_next) load_tile(kt + 1);
-    const uint16_t* a = sA + cur * A_STAGE;
-    const uint16_t* b = sB + cur * B_STAGE;
+    const int st = kt & 1;
+    if (kt + 1 < KT) issue(kt + 1, st ^ 1);
+    Ops op[2];
+    reads(st, 0, op[0]);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      v8 av[4], bv[2];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        av[mi] = *(const v8*)(a + (a_row + mi * 32) * A_PITCH + ks * 16 + a_col);
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
+      if (ks + 1 < BK / 16) {
+        reads(st, ks + 1, op[(ks + 1) & 1]);
         if constexpr (TRANS_B) {
-          bv[ni] = *(const v8*)(b + (bt_row + ni * 32) * BT_PITCH + ks * 16 + a_col);
+          __builtin_amdgcn_s_waitcnt(0xc07f | (NREAD << 8));
         } else {
-          const uint16_t* p = b + (ks * 16 + tr_k) * BN_PITCH + tr_n + ni * 32;
-          bv[ni] = cat4<v8>(lds_read_tr16(p), lds_read_tr16(p + 4 * BN_PITCH));
+          lgkm_wait(NREAD);
         }
+      } else {
+        lgkm_wait(0);
       }
+      order(op[ks & 1]);
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = MT::mma(av[mi], bv[ni], acc[mi][ni]);
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = MT::mma(__builtin_bit_cast(v8, op[ks & 1].a[mi]),
+                                __builtin_bit_cast(v8, op[ks & 1].b[ni][0]), acc[mi][ni]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (has_next) store_tile(cur ^ 1);
-    __syncthreads();
+    wait_dma();
+    barrier_lds();
   }
 
   // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8*(i/4) + 4*(lane/32) + i%4
