@@ -25,12 +25,6 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int NTHREADS = 512;
-constexpr int A_PITCH = BK + 8;    // halves: 144-byte rows, conflict-free 16-byte column reads
-constexpr int BN_PITCH = BN + 16;  // halves: 544-byte rows, conflict-free transpose reads
-constexpr int BT_PITCH = BK + 8;   // halves: B^T tile [n][k]
-constexpr int A_STAGE = BM * A_PITCH;
-constexpr int B_STAGE_N = BK * BN_PITCH;
-constexpr int B_STAGE_T = BN * BT_PITCH;
 
 template <bool BF16>
 struct mfma_t;
@@ -106,19 +100,27 @@ TLM_DEV u32x2 lds_tr16(const void* p) {
 TLM_DEV void lgkm_wait(int n) {  // lgkmcnt(n); n a compile-time constant after unrolling
   switch (n) {
     case 0: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0xc27f); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0xc47f); break;
     case 8: __builtin_amdgcn_s_waitcnt(0xc87f); break;
     default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
   }
 }
-TLM_DEV void order_after(u32x4& a) { asm volatile("" : "+v"(a) : : "memory"); }
+TLM_DEV void order_after(u32x4& a) { asm volatile("" : "+v"(a)); }
+// Phase boundaries: sched_barrier keeps the scheduler from moving instructions (MFMAs only touch
+// registers) across the wait or the barrier.
 TLM_DEV void barrier_lds() {  // workgroup barrier; LDS-DMA loads stay in flight
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 TLM_DEV void wait_dma() {  // this thread's LDS-DMA loads have landed
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(0x3f70);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 constexpr int RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data format
@@ -131,9 +133,10 @@ constexpr uint32_t OOB = 0xfffffff0u;   // offset past num_records: the load ret
 //     ds_read_b64_tr_b16 phase covers 4 k-rows x 64 bytes.
 TLM_DEV int swz_rows(int r) { return (r >> 1) & 7; }
 TLM_DEV int swz_k(int k) { return 4 * (k & 3); }
-constexpr int ST_A = BM * BK * 2;                 // bytes per stage of A
-constexpr int ST_B = BK * BN * 2;                 // bytes per stage of B (either layout)
-constexpr int STAGE = ST_A + ST_B;
+constexpr int ST_A = BM * BK * 2;  // bytes per stage of A
+constexpr int ST_B = BK * BN * 2;  // bytes per stage of B (either layout)
+constexpr int NST_A = 2, NST_B = 3;
+constexpr int SMEM = NST_A * ST_A + NST_B * ST_B;  // 160 KB
 
 template <bool BF16, bool TRANS_B, int OUT>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __restrict__ A,
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
                                                            int K) {
   using MT = mfma_t<BF16>;
   using v8 = typename MT::v8;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -154,50 +157,48 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = (K + BK - 1) / BK;
 
-  // ---- LDS-DMA fill: 8 wave-instructions of 1 KB per thread per k-tile (4 for A, 4 for B)
-  auto issue = [&](int kt, int stage) {
+  // ---- LDS-DMA fill: 8 wave-instructions of 1 KB per thread per k-tile (4 for A, 4 for B).
+  // Instruction d covers LDS slots [64 ins, 64 ins + 64) of its operand (ins = 4 wave + d % 4);
+  // lanes whose chunk lies outside A, B (rows against M / N, columns against K) read zeros.
+  struct Dma {  // the k-tile's A and B base addresses and LDS destinations
+    const uint16_t* base[2];
+    uint8_t* st[2];
+  };
+  auto sa_of = [&](int kt) { return smem + (kt % NST_A) * ST_A; };
+  auto sb_of = [&](int kt) { return smem + NST_A * ST_A + (kt % NST_B) * ST_B; };
+  auto dma_setup = [&](int kt) {
     const int k0 = kt * BK;
-    uint8_t* sa = smem + stage * STAGE;
-    uint8_t* sb = sa + ST_A;
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(A + ((int64_t)m0 * K + k0)), (short)0, 0x7ffffff0, RSRC_WORD3);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int ins = wave * 4 + p;             // 8 rows of 128 bytes
+    return Dma{{A + ((int64_t)m0 * K + k0),
+                TRANS_B ? B + ((int64_t)n0 * K + k0) : B + ((int64_t)k0 * N + n0)},
+               {sa_of(kt), sb_of(kt)}};
+  };
+  // kmax: number of valid k (columns for A / B^T, rows for row-major B) in this k-tile
+  auto dma = [&](const Dma& dd, int d, int kmax) {
+    const int ins = wave * 4 + (d & 3);
+    uint32_t off;
+    bool ok;
+    if (d < 4 || TRANS_B) {  // [rows][64 k]: 8 rows of 128 bytes
       const int r = 8 * ins + (lane >> 3);
-      const int c = (lane & 7) ^ swz_rows(r);   // global chunk landing in slot lane & 7
-      const bool ok = m0 + r < M && k0 + 8 * c < K;
-      const uint32_t off = ok ? (uint32_t)(r * K + 8 * c) * 2u : OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sa + ins * 1024),
-                                               16, off, 0, 0, 0);
+      const int c = (lane & 7) ^ swz_rows(r);
+      ok = (d < 4 ? m0 + r < M : n0 + r < N) && 8 * c < kmax;
+      off = (uint32_t)(r * K + 8 * c) * 2u;
+    } else {  // row-major B [64 k][256 n]: 2 k-rows of 512 bytes
+      const int k = 2 * ins + (lane >> 5);
+      const int c = (lane & 31) ^ swz_k(k);
+      ok = n0 + 8 * c < N && k < kmax;
+      off = (uint32_t)(k * N + 8 * c) * 2u;
     }
-    if constexpr (TRANS_B) {
-      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(B + ((int64_t)n0 * K + k0)), (short)0, 0x7ffffff0, RSRC_WORD3);
+    uint8_t* dst = dd.st[d >> 2] + ins * 1024;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)dd.base[d >> 2], (short)0, 0x7ffffff0, RSRC_WORD3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
+                                             ok ? off : OOB, 0, 0, 0);
+  };
+  auto issue = [&](int kt) {
+    const Dma dd = dma_setup(kt);
+    const int kmax = min(BK, K - kt * BK);
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int ins = wave * 4 + p;
-        const int r = 8 * ins + (lane >> 3);
-        const int c = (lane & 7) ^ swz_rows(r);
-        const bool ok = n0 + r < N && k0 + 8 * c < K;
-        const uint32_t off = ok ? (uint32_t)(r * K + 8 * c) * 2u : OOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (__attribute__((address_space(3))) void*)(sb + ins * 1024), 16, off, 0, 0, 0);
-      }
-    } else {
-      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(B + ((int64_t)k0 * N + n0)), (short)0, 0x7ffffff0, RSRC_WORD3);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int ins = wave * 4 + p;             // 2 k-rows of 512 bytes
-        const int k = 2 * ins + (lane >> 5);
-        const int c = (lane & 31) ^ swz_k(k);
-        const bool ok = k0 + k < K && n0 + 8 * c < N;
-        const uint32_t off = ok ? (uint32_t)(k * N + 8 * c) * 2u : OOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (__attribute__((address_space(3))) void*)(sb + ins * 1024), 16, off, 0, 0, 0);
-      }
-    }
+    for (int d = 0; d < 8; ++d) dma(dd, d, kmax);
   };
 
   f32x16 acc[4][2];
@@ -217,69 +218,111 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   const int tr_c = 8 * wn + 2 * (h & 1) + ((j & 3) >> 1);      // + 4 ni
   const int tr_off = tr_k * (BN * 2) + 8 * (j & 1);
 
-  struct Ops {
-    u32x4 a[4], b[2][2];
-  };
-  auto reads = [&](int stage, int ks, Ops& o) {
-    const uint8_t* sa = smem + stage * STAGE;
-    const uint8_t* sb = sa + ST_A;
-    const int ca = 16 * ((2 * ks + hf) ^ sw);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) o.a[mi] = lds_b128(sa + a_row + mi * 32 * BK * 2 + ca);
+  // Ping-pong schedule. The two waves on a SIMD (w and w + 4, groups grp = w / 4) run half a
+  // k-tile apart: in each phase one of them issues MFMAs while the other reads the next k-tile's
+  // A operands (all four k-steps) and first B operand from LDS into registers; the computing
+  // wave reads B one k-step ahead. Group 0 loads k-tile kt in phase 2 kt and computes it in
+  // phase 2 kt + 1; group 1 is one phase later. Every phase ends with a workgroup barrier. Each
+  // thread's LDS-DMA of k-tile kt + 1 is issued at the start of phase 2 kt and has landed by the
+  // end of phase 2 kt + 1. A k-tile's A stage is read in phases 2 kt, 2 kt + 1 and its B stage
+  // through phase 2 kt + 2, hence 2 A stages and 3 B stages.
+  const int grp = wave >> 2;
+  u32x4 aop[BK / 16][4];  // A operands of a whole k-tile
+  u32x4 bop[2][2];        // B operands of one k-step
+  auto readb = [&](int kt, int ks, u32x4 (&o)[2]) {
+    const uint8_t* sb = sb_of(kt);
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
       if constexpr (TRANS_B) {
-        o.b[ni][0] = lds_b128(sb + bt_row + ni * 32 * BK * 2 + ca);
+        o[ni] = lds_b128(sb + bt_row + ni * 32 * BK * 2 + 16 * ((2 * ks + hf) ^ sw));
       } else {
-        const uint8_t* p = sb + (16 * ks) * (BN * 2) + tr_off;
+        const uint8_t* q = sb + (16 * ks) * (BN * 2) + tr_off;
         const int c = tr_c + 4 * ni;
-        const u32x2 lo = lds_tr16(p + 16 * (c ^ swz_k(j >> 2)));
-        const u32x2 hi = lds_tr16(p + 4 * (BN * 2) + 16 * (c ^ swz_k(j >> 2)));
-        o.b[ni][0] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        const u32x2 lo = lds_tr16(q + 16 * (c ^ swz_k(j >> 2)));
+        const u32x2 hi = lds_tr16(q + 4 * (BN * 2) + 16 * (c ^ swz_k(j >> 2)));
+        o[ni] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     }
   };
-  auto order = [&](Ops& o) {
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) order_after(o.a[mi]);
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) order_after(o.b[ni][0]);
+  constexpr int BREADS = TRANS_B ? 2 : 4;  // LDS instructions of readb()
+  // The CU's vector memory path takes ~1 KB per 16 cycles, so the 64 LDS-DMA instructions of a
+  // k-tile are interleaved with other work (two per k-step) instead of stalling a wave in a burst.
+  // dma_kt < 0: nothing to issue.
+  auto dma_pair = [&](const Dma& dd, int dma_kt, int ks) {
+    if (dma_kt >= 0) {
+      const int kmax = min(BK, K - dma_kt * BK);
+      dma(dd, 2 * ks, kmax);
+      dma(dd, 2 * ks + 1, kmax);
+    }
   };
-  // LDS instructions issued by reads(): 4 for A, 2 (B^T) or 4 (transposed B reads) for B
-  constexpr int NREAD = TRANS_B ? 6 : 8;
-  static_assert(NREAD == 8 || TRANS_B, "lgkm_wait covers 8 outstanding reads");
-
-  issue(0, 0);
-  wait_dma();
-  barrier_lds();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < KT) issue(kt + 1, st ^ 1);
-    Ops op[2];
-    reads(st, 0, op[0]);
+  auto load_phase = [&](int kt, int dma_kt) {
+    const uint8_t* sa = sa_of(kt);
+    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        aop[ks][mi] = lds_b128(sa + a_row + mi * 32 * BK * 2 + 16 * ((2 * ks + hf) ^ sw));
+      dma_pair(dd, dma_kt, ks);
+    }
+    readb(kt, 0, bop[0]);
+    lgkm_wait(0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) order_after(aop[ks][mi]);
+    order_after(bop[0][0]);
+    order_after(bop[0][1]);
+  };
+  auto compute_phase = [&](int kt, int dma_kt) {
+    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      // B of k-step ks has landed; the reads of k-step ks + 1 stay in flight
       if (ks + 1 < BK / 16) {
-        reads(st, ks + 1, op[(ks + 1) & 1]);
-        if constexpr (TRANS_B) {
-          __builtin_amdgcn_s_waitcnt(0xc07f | (NREAD << 8));
-        } else {
-          lgkm_wait(NREAD);
-        }
+        readb(kt, ks + 1, bop[(ks + 1) & 1]);
+        lgkm_wait(BREADS);
       } else {
         lgkm_wait(0);
       }
-      order(op[ks & 1]);
+      order_after(bop[ks & 1][0]);
+      order_after(bop[ks & 1][1]);
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
-          acc[mi][ni] = MT::mma(__builtin_bit_cast(v8, op[ks & 1].a[mi]),
-                                __builtin_bit_cast(v8, op[ks & 1].b[ni][0]), acc[mi][ni]);
-      __builtin_amdgcn_sched_barrier(0);
+          acc[mi][ni] = MT::mma(__builtin_bit_cast(v8, aop[ks][mi]),
+                                __builtin_bit_cast(v8, bop[ks & 1][ni]), acc[mi][ni]);
+        if (mi == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          dma_pair(dd, dma_kt, ks);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
     }
-    wait_dma();
+  };
+  issue(0);
+  wait_dma();
+  barrier_lds();
+  if (grp == 0) {
+    for (int kt = 0; kt < KT; ++kt) {
+      load_phase(kt, kt + 1 < KT ? kt + 1 : -1);  // phase 2 kt (+ this thread's DMA of kt + 1)
+      barrier_lds();
+      compute_phase(kt, -1);  // phase 2 kt + 1
+      wait_dma();
+      barrier_lds();
+    }
+    barrier_lds();  // phase 2 KT: group 1 computes the last k-tile
+  } else {
+    if (1 < KT) issue(1);  // phase 0
     barrier_lds();
+    for (int kt = 0; kt < KT; ++kt) {
+      load_phase(kt, -1);  // phase 2 kt + 1
+      wait_dma();
+      barrier_lds();
+      compute_phase(kt, kt + 2 < KT ? kt + 2 : -1);  // phase 2 kt + 2 (+ DMA of kt + 2)
+      barrier_lds();
+    }
   }
 
   // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8*(i/4) + 4*(lane/32) + i%4
