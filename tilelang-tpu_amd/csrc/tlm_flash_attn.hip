@@ -21,6 +21,9 @@
 //     workgroups are issued heaviest query tile first.
 #include "tlm_common.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -246,6 +249,402 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Head dim 128: ping-pong kernel.
+//
+//   * workgroup = 8 waves = 256 queries of one (batch, head); a wave owns one 32-query block and
+//     computes S^T = K Q^T and O^T = V^T P^T as above (Q^T in VGPRs, P^T straight from the S^T
+//     accumulator);
+//   * the waves form two groups of four (one wave of each group per SIMD) that run one phase
+//     apart: while one group issues MFMAs (QK of tile j and PV of tile j-1: 32 MFMAs per wave) the
+//     other runs the softmax of its tile on the VALU, so each SIMD's matrix core and VALU are busy
+//     at the same time. Each half-step ends with a workgroup barrier;
+//   * K and V tiles (64 keys x 128 dims, 16 KB each) stream into 4-stage LDS rings through
+//     buffer_load ... lds (16 bytes per lane, no VGPR staging). Tile j + 2 is loaded during step j;
+//     the buffer descriptor of a tile ends at its last valid key, so keys >= S read as zeros;
+//   * LDS layout: rows of 256 bytes, 16-byte chunk c of key row r stored at chunk c ^ (r & 15) for
+//     K (the ds_read_b128 row reads of 16 lanes hit 16 distinct chunks) and c ^ 4 (r & 3) for V
+//     (the ds_read_b64_tr_b16 reads of 32 lanes cover 4 rows x 4 chunks);
+//   * online softmax with a lazy running max: m is raised only when a tile's max exceeds it by
+//     more than 8 (log2 units), so P = 2^(s - m) <= 256 and the O/l rescale (64 VALU multiplies
+//     per lane) happens on a handful of tiles per row instead of every tile; the result is the
+//     same softmax (the common factor cancels in O / l). Row sums of P take the bf16/fp16 values
+//     that enter the PV MFMA two at a time (v_dot2 with ones);
+//   * query blocks are assigned so that the two waves sharing a SIMD hold blocks b and 7 - b
+//     (equal causal work per SIMD), and workgroup ids are regrouped so that one XCD runs all query
+//     tiles of a (batch, head) together, heaviest first: its K/V tiles are then read from that
+//     XCD's L2 by up to 16 workgroups at about the same time.
+constexpr int PP_D = 128;
+constexpr int PP_BQ = 256;                        // queries per workgroup
+constexpr int PP_KV = 64;                         // keys per tile
+constexpr int PP_TILE = PP_KV * PP_D * 2;         // bytes of one K or V tile
+constexpr int PP_NST = 4;                         // ring stages (tiles j-1 .. j+2 live in step j)
+constexpr int PP_VRING = PP_NST * PP_TILE;        // V ring follows the K ring
+constexpr int PP_SMEM = 2 * PP_NST * PP_TILE;     // 128 KB
+constexpr int PP_OP = PP_D + 8;                   // epilogue staging pitch (halves)
+constexpr float PP_HEADROOM = 8.0f;               // log2 units m may trail the running max
+constexpr int PP_RSRC_WORD3 = 0x00020000;         // raw buffer, 32-bit data format
+static_assert(8 * 32 * PP_OP * 2 <= PP_SMEM, "epilogue staging must fit in the rings");
+
+#define TLM_INLINE __attribute__((always_inline))
+
+template <typename F, int... I>
+TLM_DEV void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+TLM_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS reads as inline asm with an immediate offset: compiler-generated LDS reads may be made to
+// wait for all outstanding LDS-DMA loads (including prefetches of later tiles). Their completion
+// is awaited explicitly with lgkm_wait.
+template <int OFF>
+TLM_DEV u32x4 ds_b128(uint32_t a) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF) : "memory");
+  return r;
+}
+template <int OFF>
+TLM_DEV u32x2 ds_tr16(uint32_t a) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF) : "memory");
+  return r;
+}
+template <int N>
+TLM_DEV void lgkm_wait() {  // s_waitcnt lgkmcnt(N)
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  __builtin_amdgcn_s_waitcnt(0xc07f | (N << 8));
+}
+template <int N>
+TLM_DEV void vm_wait() {  // s_waitcnt vmcnt(N)
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (N & 15) | ((N >> 4) << 14));
+}
+TLM_DEV void order_after(u32x4& a) { asm volatile("" : "+v"(a)); }
+TLM_DEV uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// Workgroup barrier at a phase boundary: this wave's LDS reads have completed; sched_barrier
+// keeps the scheduler from moving MFMAs (register-only instructions) across it.
+TLM_DEV void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool BF16>
+TLM_DEV float dot2_ones(uint32_t pk, float acc) {  // acc + the two 16-bit values in pk
+  if constexpr (BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, pk), one, acc, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk), one, acc, false);
+  }
+}
+
+template <bool BF16, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__ Q,
+                                                   const uint16_t* __restrict__ K,
+                                                   const uint16_t* __restrict__ V,
+                                                   uint16_t* __restrict__ O, int B, int S, int H,
+                                                   float sc) {
+  using MT = fa_mma<BF16>;
+  using v8 = typename MT::v8;
+  using HH = h16<BF16>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[PP_SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wl = wave & 3;
+  const int blk = grp == 0 ? 2 * wl : 7 - 2 * wl;  // waves w and w + 4 share a SIMD
+
+  // workgroup -> (batch, head, query tile)
+  const int nqt = (S + PP_BQ - 1) / PP_BQ;
+  const int lin = blockIdx.x;
+  int bh, qt;
+  if ((B * H) % 8 == 0) {
+    const int xcd = lin & 7, s = lin >> 3;
+    bh = (s / nqt) * 8 + xcd;
+    qt = nqt - 1 - s % nqt;
+  } else {
+    bh = lin / nqt;
+    qt = nqt - 1 - lin % nqt;
+  }
+  const int b = bh / H, h = bh % H;
+  const int q0 = qt * PP_BQ;
+  const int64_t rs = (int64_t)H * PP_D;  // elements between consecutive tokens
+  const int64_t head = ((int64_t)b * S * H + h) * PP_D;
+  const uint16_t* Qb = Q + head;
+
+  const int n_all = (S + PP_KV - 1) / PP_KV;
+  const int n = CAUSAL ? min(n_all, (q0 + PP_BQ) / PP_KV) : n_all;  // key tiles of the workgroup
+  const int qb0 = q0 + 32 * blk;                                     // first query of the wave
+  const int nw = qb0 >= S ? 0 : (CAUSAL ? min(n, (qb0 + 31) / PP_KV + 1) : n);
+
+  const int ql = lane & 31, g = lane >> 5;
+  const int my_q = qb0 + ql;
+
+  // Q^T operand: lane holds query my_q, d = 16 ds + 8 g .. + 7
+  v8 qreg[PP_D / 16];
+#pragma unroll
+  for (int ds = 0; ds < PP_D / 16; ++ds) {
+    u32x4 v = {0, 0, 0, 0};
+    if (my_q < S) v = *(const u32x4*)(Qb + (int64_t)my_q * rs + 16 * ds + 8 * g);
+    qreg[ds] = __builtin_bit_cast(v8, v);
+  }
+
+  // ---- LDS-DMA: group 0 fills K tiles, group 1 V tiles; wave wl writes rows 16 wl .. 16 wl + 15
+  // (4 instructions of 4 rows x 16 chunks). Lane -> (row, stored chunk p) fetches chunk p ^ swz.
+  const bool dma_v = grp == 1;
+  const uint16_t* dsrc = (dma_v ? V : K) + head;
+  const uint32_t rs2 = (uint32_t)(rs * 2);
+  uint32_t doff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 16 * wl + 4 * r + (lane >> 4), p = lane & 15;
+    const int c = dma_v ? (p ^ (4 * (row & 3))) : (p ^ (row & 15));
+    doff[r] = (uint32_t)row * rs2 + 16u * (uint32_t)c;
+  }
+  uint8_t* const dlds = smem + (dma_v ? PP_VRING : 0) + wl * 4096;
+  auto issue = [&](int tile, int slot) TLM_INLINE {
+    const int valid = min(PP_KV, S - PP_KV * tile);
+    const uint32_t nrec = (uint32_t)(valid - 1) * rs2 + PP_D * 2;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(dsrc + (int64_t)tile * PP_KV * rs), (short)0, (int)nrec, PP_RSRC_WORD3);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (__attribute__((address_space(3))) void*)(dlds + slot * PP_TILE + r * 1024), 16,
+          doff[r], 0, 0, 0);
+  };
+
+  // ---- operand read addresses (LDS byte addresses of the current K / V stage; row-block offsets
+  // within a stage are immediates)
+  const uint32_t sbase = lds_u32(smem);
+  uint32_t kaddr[PP_D / 16];  // K row (lane & 31) of the 32-key block, d chunk 2 ds + g
+#pragma unroll
+  for (int ds = 0; ds < PP_D / 16; ++ds)
+    kaddr[ds] = sbase + (uint32_t)(ql * 256 + 16 * ((2 * ds + g) ^ (lane & 15)));
+  // V^T through ds_read_b64_tr_b16: 16-lane group hh, lane jj reads 4 dims of key row
+  // 4 (hh >> 1) + (jj >> 2) (+ 8 for the second half of the k-step)
+  const int hh = lane >> 4, jj = lane & 15;
+  uint32_t vaddr[PP_D / 32];
+#pragma unroll
+  for (int dt = 0; dt < PP_D / 32; ++dt) {
+    const int row = 4 * (hh >> 1) + (jj >> 2);
+    const int c = (4 * dt + 2 * (hh & 1) + ((jj & 3) >> 1)) ^ (4 * (row & 3));
+    vaddr[dt] = sbase + PP_VRING + (uint32_t)(row * 256 + 16 * c + 8 * (jj & 1));
+  }
+
+  f32x16 oacc[PP_D / 32];
+#pragma unroll
+  for (int t = 0; t < PP_D / 32; ++t) oacc[t] = f32x16{};
+  f32x16 sacc[2];
+  u32x4 pb[2][2];  // P^T operands of the last softmax: [32-key block t][16-key half s2]
+  float m_run = -INFINITY, l_part = 0.f;
+
+  // ---- MFMA phase: QK of the tile in the current K stage (16 MFMAs), then PV of the tile in the
+  // current V stage (16 MFMAs). Operand reads run DEPTH MFMAs ahead.
+  constexpr int DEPTH = 4;
+  auto x_phase = [&](auto QKc, auto PVc) TLM_INLINE {
+    constexpr bool DO_QK = decltype(QKc)::value, DO_PV = decltype(PVc)::value;
+    constexpr int NQK = DO_QK ? 16 : 0;
+    constexpr int NOPS = NQK + (DO_PV ? 16 : 0);
+    u32x4 op[DEPTH + 1];
+    auto read = [&](auto Mc) TLM_INLINE {
+      constexpr int m = decltype(Mc)::value;
+      if constexpr (m < NOPS) {
+        if constexpr (m < NQK) {  // K rows 32 t .. 32 t + 31, d chunk 2 ds + g
+          constexpr int ds = m / 2, t = m % 2;
+          op[m % (DEPTH + 1)] = ds_b128<t * 32 * 256>(kaddr[ds]);
+        } else {  // V^T: keys 32 t + 16 s2 + .., dims 32 dt + ..
+          constexpr int mm = m - NQK, ts = mm / 4, dt = mm % 4;
+          constexpr int off = 16 * ts * 256;
+          const u32x2 lo = ds_tr16<off>(vaddr[dt]);
+          const u32x2 hi = ds_tr16<off + 8 * 256>(vaddr[dt]);
+          op[m % (DEPTH + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      }
+    };
+    constexpr auto nreads = [](int m) { return m < NQK ? 1 : 2; };
+    static_for<DEPTH>([&](auto Mc) TLM_INLINE { read(Mc); });
+    static_for<NOPS>([&](auto Mc) TLM_INLINE {
+      constexpr int m = decltype(Mc)::value;
+      read(std::integral_constant<int, m + DEPTH>{});
+      constexpr int pending = [&] {
+        int c = 0;
+        for (int i = m + 1; i <= m + DEPTH && i < NOPS; ++i) c += nreads(i);
+        return c;
+      }();
+      lgkm_wait<pending>();
+      order_after(op[m % (DEPTH + 1)]);
+      const v8 a = __builtin_bit_cast(v8, op[m % (DEPTH + 1)]);
+      if constexpr (m < NQK) {
+        constexpr int ds = m / 2, t = m % 2;
+        sacc[t] = MT::mma(a, qreg[ds], ds == 0 ? f32x16{} : sacc[t]);
+      } else {
+        constexpr int mm = m - NQK, ts = mm / 4, dt = mm % 4;
+        oacc[dt] = MT::mma(a, __builtin_bit_cast(v8, pb[ts >> 1][ts & 1]), oacc[dt]);
+      }
+    });
+  };
+
+  // ---- softmax of tile j (scores in sacc): keys of this lane 64 j + 32 t + 8 (i / 4) + 4 g + i % 4
+  auto y_phase = [&](int j) TLM_INLINE {
+    const int k0 = PP_KV * j;
+    const bool need_mask = (CAUSAL && k0 + PP_KV - 1 > qb0) || (k0 + PP_KV > S);
+    if (need_mask) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
+          if (key >= S || (CAUSAL && key > my_q)) sacc[t][i] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) mx = fmaxf(fmaxf(mx, sacc[t][i]), sacc[t][i + 1]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float ms = mx * sc;
+    if (__builtin_amdgcn_ballot_w64(ms > m_run + PP_HEADROOM)) {  // wave-uniform
+      const float m_new = fmaxf(m_run, ms);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < PP_D / 32; ++dt) oacc[dt] *= alpha;
+    }
+    const float nb = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e], sc, nb));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e + 1], sc, nb));
+          const uint32_t pk = HH::pack(p0, p1);
+          l_part = dot2_ones<BF16>(pk, l_part);
+          pb[t][s2][e] = pk;
+        }
+  };
+
+  // ---- schedule. Step j: group 0 runs X(j) = QK(j) + PV(j-1), then Y(j) = softmax(j); group 1
+  // runs Y(j-1), then X(j). Both issue their half of tile j + 2 at the start of their Y half.
+  // Tile j lives in stage j % 4: its K stage is read in step j and its V stage in step j + 1, so
+  // the stage of tile j + 2 (that of tile j - 2) is free in step j. A wave runs the full X phase
+  // in every step 1 .. nw: in step nw its QK reads a stage that holds finished data and the scores
+  // are not used. Step 0 (no PV yet) is peeled.
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (n > 0) issue(0, 0);
+  if (n > 1) issue(1, 1);
+  if (n > 1)
+    vm_wait<4>();
+  else
+    vm_wait<0>();
+  phase_barrier();
+  // stage offsets of step j: K stage j % 4, V stage (j - 1) % 4
+  auto advance = [&](int j) TLM_INLINE {
+    const int dk = (j & 3) == 0 ? -3 * PP_TILE : PP_TILE;
+#pragma unroll
+    for (int ds = 0; ds < PP_D / 16; ++ds) kaddr[ds] += dk;
+    if (j >= 2) {
+      const int dv = ((j - 1) & 3) == 0 ? -3 * PP_TILE : PP_TILE;
+#pragma unroll
+      for (int dt = 0; dt < PP_D / 32; ++dt) vaddr[dt] += dv;
+    }
+  };
+  auto end_step = [&](bool dma) TLM_INLINE {
+    if (dma)
+      vm_wait<4>();
+    else
+      vm_wait<0>();
+    phase_barrier();
+  };
+  if (n > 0) {
+    if (grp == 0) {
+      if (nw > 0) x_phase(T_{}, F_{});
+      phase_barrier();
+      if (2 < n) issue(2, 2);
+      if (nw > 0) y_phase(0);
+      end_step(2 < n);
+      for (int j = 1; j <= n; ++j) {
+        advance(j);
+        if (j <= nw) x_phase(T_{}, T_{});
+        phase_barrier();
+        if (j + 2 < n) issue(j + 2, (j + 2) & 3);
+        if (j < nw) y_phase(j);
+        end_step(j + 2 < n);
+      }
+    } else {
+      if (2 < n) issue(2, 2);
+      phase_barrier();
+      if (nw > 0) x_phase(T_{}, F_{});
+      end_step(2 < n);
+      for (int j = 1; j <= n; ++j) {
+        advance(j);
+        if (j + 2 < n) issue(j + 2, (j + 2) & 3);
+        if (j <= nw) y_phase(j - 1);
+        phase_barrier();
+        if (j <= nw) x_phase(T_{}, T_{});
+        end_step(j + 2 < n);
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds O^T[d = 32 dt + 8 (i / 4) + 4 g + i % 4][query my_q]
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  uint16_t* stage = (uint16_t*)smem + wave * 32 * PP_OP;  // [32 queries][PP_OP]
+#pragma unroll
+  for (int dt = 0; dt < PP_D / 32; ++dt)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const uint32_t lo = HH::pack(oacc[dt][4 * r4] * inv, oacc[dt][4 * r4 + 1] * inv);
+      const uint32_t hi = HH::pack(oacc[dt][4 * r4 + 2] * inv, oacc[dt][4 * r4 + 3] * inv);
+      *(u32x2*)(stage + ql * PP_OP + 32 * dt + 8 * r4 + 4 * g) = u32x2{lo, hi};
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint16_t* Ob = O + head;
+#pragma unroll
+  for (int it = 0; it < 32 * (PP_D / 8) / 64; ++it) {
+    const int idx = lane + 64 * it;
+    const int r = idx / (PP_D / 8), c = (idx % (PP_D / 8)) * 8;
+    const int q = qb0 + r;
+    if (q < S) *(u32x4*)(Ob + (int64_t)q * rs + c) = *(const u32x4*)(stage + r * PP_OP + c);
+  }
+}
+
+template <bool BF16, bool CAUSAL>
+int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
+              float sc, hipStream_t st) {
+  const int64_t nwg = (int64_t)((S + PP_BQ - 1) / PP_BQ) * B * H;
+  if (nwg > INT32_MAX) {
+    tlm_set_error("tlm_flash_attn_fwd: problem too large");
+    return TLM_EINVAL;
+  }
+  fa_fwd_pp<BF16, CAUSAL><<<(unsigned)nwg, 512, 0, st>>>(
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, sc);
+  TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
+  return TLM_OK;
+}
+
 template <bool BF16, bool CAUSAL, int D>
 int launch(const void* q, const void* k, const void* v, void* o, int B, int S, int H, float sc,
            hipStream_t st) {
@@ -264,8 +663,8 @@ template <bool BF16>
 int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int D,
              bool causal, float sc, hipStream_t st) {
   if (D == 128)
-    return causal ? launch<BF16, true, 128>(q, k, v, o, B, S, H, sc, st)
-                  : launch<BF16, false, 128>(q, k, v, o, B, S, H, sc, st);
+    return causal ? launch_pp<BF16, true>(q, k, v, o, B, S, H, sc, st)
+                  : launch_pp<BF16, false>(q, k, v, o, B, S, H, sc, st);
   return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, sc, st)
                 : launch<BF16, false, 64>(q, k, v, o, B, S, H, sc, st);
 }
