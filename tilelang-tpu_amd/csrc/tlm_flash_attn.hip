@@ -256,20 +256,23 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
 //     computes S^T = K Q^T and O^T = V^T P^T as above (Q^T in VGPRs, P^T straight from the S^T
 //     accumulator);
 //   * the waves form two groups of four (one wave of each group per SIMD) that run one phase
-//     apart: while one group issues MFMAs (QK of tile j and PV of tile j-1: 32 MFMAs per wave) the
-//     other runs the softmax of its tile on the VALU, so each SIMD's matrix core and VALU are busy
-//     at the same time. Each half-step ends with a workgroup barrier;
+//     apart: while one group issues MFMAs (QK of tile j and PV of tile j-1: 32 MFMAs per wave, at
+//     raised wave priority) the other runs the softmax of its tile on the VALU, so each SIMD's
+//     matrix core and VALU are busy at the same time. Each half-step ends with a workgroup
+//     barrier. (Interleaving each wave's own softmax into its MFMA stream instead measured ~10%
+//     slower: the softmax of both waves then competes for the SIMD's VALU inside the MFMA phase);
 //   * K and V tiles (64 keys x 128 dims, 16 KB each) stream into 4-stage LDS rings through
 //     buffer_load ... lds (16 bytes per lane, no VGPR staging). Tile j + 2 is loaded during step j;
 //     the buffer descriptor of a tile ends at its last valid key, so keys >= S read as zeros;
 //   * LDS layout: rows of 256 bytes, 16-byte chunk c of key row r stored at chunk c ^ (r & 15) for
 //     K (the ds_read_b128 row reads of 16 lanes hit 16 distinct chunks) and c ^ 4 (r & 3) for V
 //     (the ds_read_b64_tr_b16 reads of 32 lanes cover 4 rows x 4 chunks);
-//   * online softmax with a lazy running max: m is raised only when a tile's max exceeds it by
-//     more than 8 (log2 units), so P = 2^(s - m) <= 256 and the O/l rescale (64 VALU multiplies
-//     per lane) happens on a handful of tiles per row instead of every tile; the result is the
-//     same softmax (the common factor cancels in O / l). Row sums of P take the bf16/fp16 values
-//     that enter the PV MFMA two at a time (v_dot2 with ones);
+//   * online softmax with a lazy running max: a tile is exponentiated against the current m
+//     without computing its max; only when its P sum leaves the safe range (bf16 2^64, fp16 2^15;
+//     also the first tile, where m = -inf) is it redone with m raised to the tile max and O, l
+//     rescaled. The result is the same softmax (the common factor cancels in O / l) at about 3.5
+//     VALU operations per score (fma, exp2, add into the fp32 row sum, half a pack). v_dot2 is
+//     avoided on purpose: it does not overlap with the MFMAs of the other wave on the SIMD;
 //   * query blocks are assigned so that the two waves sharing a SIMD hold blocks b and 7 - b
 //     (equal causal work per SIMD), and workgroup ids are regrouped so that one XCD runs all query
 //     tiles of a (batch, head) together, heaviest first: its K/V tiles are then read from that
@@ -282,7 +285,6 @@ constexpr int PP_NST = 4;                         // ring stages (tiles j-1 .. j
 constexpr int PP_VRING = PP_NST * PP_TILE;        // V ring follows the K ring
 constexpr int PP_SMEM = 2 * PP_NST * PP_TILE;     // 128 KB
 constexpr int PP_OP = PP_D + 8;                   // epilogue staging pitch (halves)
-constexpr float PP_HEADROOM = 8.0f;               // log2 units m may trail the running max
 constexpr int PP_RSRC_WORD3 = 0x00020000;         // raw buffer, 32-bit data format
 static_assert(8 * 32 * PP_OP * 2 <= PP_SMEM, "epilogue staging must fit in the rings");
 
@@ -337,19 +339,6 @@ TLM_DEV void phase_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-}
-
-template <bool BF16>
-TLM_DEV float dot2_ones(uint32_t pk, float acc) {  // acc + the two 16-bit values in pk
-  if constexpr (BF16) {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, pk), one, acc, false);
-  } else {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk), one, acc, false);
-  }
 }
 
 template <bool BF16, bool CAUSAL>
@@ -477,6 +466,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
       }
     };
     constexpr auto nreads = [](int m) { return m < NQK ? 1 : 2; };
+    __builtin_amdgcn_s_setprio(1);
     static_for<DEPTH>([&](auto Mc) TLM_INLINE { read(Mc); });
     static_for<NOPS>([&](auto Mc) TLM_INLINE {
       constexpr int m = decltype(Mc)::value;
@@ -496,10 +486,31 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
         constexpr int mm = m - NQK, ts = mm / 4, dt = mm % 4;
         oacc[dt] = MT::mma(a, __builtin_bit_cast(v8, pb[ts >> 1][ts & 1]), oacc[dt]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     });
+    __builtin_amdgcn_s_setprio(0);
   };
 
-  // ---- softmax of tile j (scores in sacc): keys of this lane 64 j + 32 t + 8 (i / 4) + 4 g + i % 4
+  // ---- softmax of tile j (scores in sacc): keys of this lane 64 j + 32 t + 8 (i / 4) + 4 g + i % 4.
+  // P = 2^(s sc - m) with the current m; the tile's P sum bounds every P, so a sum above P_LIMIT
+  // (or not finite) sends the tile through the rescaling path. P_LIMIT keeps P in range of the
+  // 16-bit type (fp16: every P <= 2^15) and O, l far from fp32 overflow (bf16: P <= 2^64).
+  constexpr float P_LIMIT = BF16 ? 18446744073709551616.0f : 32768.0f;
+  auto exp_tile = [&](float nb) TLM_INLINE {  // fills pb, returns the tile's row-sum part
+    float ts0 = 0.f, ts1 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e], sc, nb));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e + 1], sc, nb));
+          if (e & 1) ts1 += p0 + p1; else ts0 += p0 + p1;
+          pb[t][s2][e] = HH::pack(p0, p1);
+        }
+    return ts0 + ts1;
+  };
   auto y_phase = [&](int j) TLM_INLINE {
     const int k0 = PP_KV * j;
     const bool need_mask = (CAUSAL && k0 + PP_KV - 1 > qb0) || (k0 + PP_KV > S);
@@ -512,34 +523,23 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
           if (key >= S || (CAUSAL && key > my_q)) sacc[t][i] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    float ts = exp_tile(-m_run);
+    if (__builtin_amdgcn_ballot_w64(!(ts <= P_LIMIT))) {  // wave-uniform, rare
+      float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) mx = fmaxf(fmaxf(mx, sacc[t][i]), sacc[t][i + 1]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float ms = mx * sc;
-    if (__builtin_amdgcn_ballot_w64(ms > m_run + PP_HEADROOM)) {  // wave-uniform
-      const float m_new = fmaxf(m_run, ms);
+        for (int i = 0; i < 16; i += 2) mx = fmaxf(fmaxf(mx, sacc[t][i]), sacc[t][i + 1]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx * sc);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
       m_run = m_new;
       l_part *= alpha;
 #pragma unroll
       for (int dt = 0; dt < PP_D / 32; ++dt) oacc[dt] *= alpha;
+      ts = exp_tile(m_new == -INFINITY ? 0.f : -m_new);
     }
-    const float nb = m_run == -INFINITY ? 0.f : -m_run;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e], sc, nb));
-          const float p1 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e + 1], sc, nb));
-          const uint32_t pk = HH::pack(p0, p1);
-          l_part = dot2_ones<BF16>(pk, l_part);
-          pb[t][s2][e] = pk;
-        }
+    l_part += ts;
   };
 
   // ---- schedule. Step j: group 0 runs X(j) = QK(j) + PV(j-1), then Y(j) = softmax(j); group 1
