@@ -10,7 +10,8 @@ over enough input copies (> 512 MiB in total) that no step reads another step's 
 
 The timed steps are replayed from one HIP graph (captured from torch's current stream, which
 is the stream every kernel is launched on), between device synchronisations, and timed with HIP
-events on that stream. roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch
+events on that stream. Before the timed replay the graph is replayed untimed for >= 50 ms: the
+clocks dip at the start of a burst of matrix work and need ~20 ms to reach their sustained level. roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch
 duration, the mean taken over a graph of back-to-back launches (rotating input copies); each
 record also carries the median of single launches that each follow a 512 MiB cache flush.
 cpu_baseline = the oracle (restated reference torch path) on a bounded sample, timed on this
@@ -69,6 +70,23 @@ def _capture(fns, n):
         return None
 
 
+SETTLE_MS = 50.0
+
+
+def _settle(g):
+    """Replay g untimed until >= SETTLE_MS of GPU time has passed: the clocks dip at the start
+    of a burst of matrix work and take ~20 ms to reach their sustained level."""
+    spent, n = 0.0, 0
+    while spent < SETTLE_MS and n < 1000:
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        g.replay()
+        en.record()
+        torch.cuda.synchronize()
+        spent += st.elapsed_time(en)
+        n += 1
+
+
 def time_steps(fns, steps, warmup):
     """ms per step over exactly `steps` steps after `warmup` untimed ones. The steps are
     replayed from one HIP graph (launch-bound host loops would otherwise starve ~10 us
@@ -78,8 +96,7 @@ def time_steps(fns, steps, warmup):
     torch.cuda.synchronize()
     g = _capture(fns, steps)
     if g is not None:
-        g.replay()  # warm replay
-        torch.cuda.synchronize()
+        _settle(g)
         st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         st.record()
         g.replay()
@@ -103,8 +120,7 @@ def time_launches(fns, reps, flush):
     g = _capture(fns, reps)
     mean = None
     if g is not None:
-        g.replay()
-        torch.cuda.synchronize()
+        _settle(g)
         st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         st.record()
         g.replay()
@@ -141,6 +157,36 @@ def roofline(bound, achieved, unit, peak, traffic=None):
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
+class PmcOnly(Exception):
+    """Raised by a config in --pmc-launches mode once its kernel has run the requested times."""
+
+
+def pmc_launches(args, fns, workload):
+    """--pmc-launches N: N plain launches for hardware-counter collection (rocprofv3 --pmc),
+    no graphs, no timing, no cache flush."""
+    if not args.pmc_launches:
+        return
+    torch.cuda.synchronize()
+    for i in range(args.pmc_launches):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    raise PmcOnly(workload)
+
+
+def load_traffic():
+    """HBM bytes per launch by workload from profiles/pmc_traffic.md (rocprofv3 --pmc
+    FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration recorded there)."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.md")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[0].startswith("`") and cells[5].replace(".", "").isdigit():
+            out[cells[0].strip("`")] = float(cells[5])
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # configs
 
@@ -159,6 +205,7 @@ def bench_rmsnorm(args, dev, flush, cpu):
         y = torch.empty_like(x)
         sets.append((x, wt, y))
     fns = [lambda s=s: k(*s) for s in sets]
+    pmc_launches(args, fns, "rmsnorm")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 200, flush)
     res = {"workload": "rmsnorm_fp16_4096x4096", "value": nbytes / (ms * 1e-3) / 1e9,
@@ -185,6 +232,7 @@ def bench_swiglu(args, dev, flush, cpu):
     g, u = w.tensors["gate"].to(dev), w.tensors["up"].to(dev)
     o = torch.empty_like(g)
     fns = [lambda: k(g, u, o)]
+    pmc_launches(args, fns, "swiglu")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 50, flush)
     res = {"workload": "swiglu_bf16_8192x14336", "value": nbytes / (ms * 1e-3) / 1e9,
@@ -215,6 +263,7 @@ def bench_rope(args, dev, flush, cpu):
         sets.append((t["q"], t["k"], t["cos"], t["sin"], torch.empty_like(t["q"]),
                      torch.empty_like(t["k"])))
     fns = [lambda s=s: k(*s) for s in sets]
+    pmc_launches(args, fns, "rope")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 200, flush)
     res = {"workload": "rope_qk_bf16_8192x32x128", "value": nbytes / (ms * 1e-3) / 1e9,
@@ -243,6 +292,7 @@ def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float1
     a, b = w.tensors["a"].to(dev), w.tensors["b"].to(dev)
     c = torch.empty(M, N, dtype=torch.float16, device=dev)
     fns = [lambda: k(a, b, c)]
+    pmc_launches(args, fns, "gemm")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 50, flush)
     skinny = M <= 64
@@ -273,9 +323,11 @@ def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
     w = workloads.flashattn(B, S, H, D, causal=causal)
     k = tilelang.compile(programs.flashattn(B, H, S, D, causal), out_idx=-1)
     flops = 4 * B * H * S * S * D * (0.5 if causal else 1.0)
+    nbytes = 4 * B * S * H * D * 2  # Q, K, V read once, O written once
     q, kk, v = (w.tensors[n].to(dev) for n in ("q", "k", "v"))
     o = torch.empty_like(q)
     fns = [lambda: k(q, kk, v, o)]
+    pmc_launches(args, fns, "flashattn")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 10, flush)
     res = {"workload": f"flashattn_bf16_b{B}h{H}s{S}d{D}_{'causal' if causal else 'full'}",
@@ -283,7 +335,8 @@ def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
            "dtype": "bf16",
            "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
                                 MFMA_PEAK["bf16"]),
-           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how, "algorithmic_flops": flops}
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
         t = cpu_time(lambda: ref.flashattn_ref(w.tensors["q"], w.tensors["k"], w.tensors["v"],
@@ -316,6 +369,7 @@ def bench_mla(args, dev, flush, cpu):
         ops.mla_decode(q[..., :dv], q[..., dv:], kv[:, :dv], kv[:, dv:], t["block_table"],
                        t["seqlens"], out, ws, a["page"], num_split, a["sm_scale"], t["kv_scale"])
 
+    pmc_launches(args, [run], "mla")
     ms, how = time_steps([run], args.steps, args.warmup)
     mean_ms, med_ms = time_launches([run], 100, flush)
     # 128 heads share each KV row: ~480 flop per KV byte, above the bf16 ridge, so the decode is
@@ -348,7 +402,22 @@ def bench_mla(args, dev, flush, cpu):
     return res
 
 
+def bench_copy(args, dev, flush, cpu):
+    """Calibration kernel for the HBM counters: a 1 GiB device-to-device copy (torch's copy
+    kernel) reads 1 GiB and writes 1 GiB."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    fns = [lambda: dst.copy_(src)]
+    pmc_launches(args, fns, "copy")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    return {"workload": "copy_1GiB", "value": 2 * src.numel() / (ms * 1e-3) / 1e9, "unit": "GB/s",
+            "ms_per_step": ms, "dtype": "u8", "timing": how,
+            "roofline": roofline("hbm", 2 * src.numel() / (ms * 1e-3) / 1e9, "GB/s",
+                                 HBM_PEAK_GBS)}
+
+
 BENCHES = {
+    "copy": bench_copy,
     "gemm": bench_gemm,
     "gemm_skinny": lambda a, d, f, c: bench_gemm(a, d, f, c, M=16, N=14336, K=4096),
     "rmsnorm": bench_rmsnorm,
@@ -367,7 +436,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["all"] + ORDER)
+    ap.add_argument("--workload", default="all", choices=["all", "copy"] + ORDER)
+    ap.add_argument("--pmc-launches", type=int, default=0,
+                    help="only launch the workload's kernel N times (for rocprofv3 --pmc)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--mla-splits", type=int, default=4)
     args = ap.parse_args()
@@ -383,13 +454,20 @@ def main():
     torch.set_num_threads(os.cpu_count() or 1)
     flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
     names = ORDER if args.workload == "all" else [args.workload]
+    traffic = load_traffic()
     results = {}
     for n in names:
         log(f"[bench] {n} ...")
         try:
             results[n] = BENCHES[n](args, dev, flush, not args.no_cpu)
+            tb = traffic.get(results[n].get("workload"))
+            if tb is not None and results[n].get("roofline"):
+                results[n]["roofline"]["traffic"] = tb
             log(f"[bench] {n}: {results[n]['value']:.1f} {results[n]['unit']} "
                 f"(roofline {results[n]['roofline']['frac'] * 100:.1f}%)")
+        except PmcOnly:
+            print(json.dumps({"pmc_launches": args.pmc_launches, "workload": n}))
+            return
         except Exception as e:  # a family without a kernel yet is reported, not fatal
             results[n] = {"workload": n, "error": f"{type(e).__name__}: {e}"}
             log(f"[bench] {n}: ERROR {e}")
