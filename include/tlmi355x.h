@@ -115,13 +115,18 @@ int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int
  *          a corrupt block table is read as zeros instead of faulting.
  *   block_table int32 [B, max_pages]: token j of sequence b lives in row
  *          block_table[b, j / page] * page + j % page   (example_mla_decode_paged.py:62-63).
- *   seqlens int32 [B], each in [1, max_pages*page] (larger values are clamped to max_pages*page).
+ *   seqlens int32 [B], each in [0, max_pages*page] (larger values are clamped to
+ *          max_pages*page; a zero-length sequence gets a zero output row).
  *   o      [B, Hq, dv] out dtype (F16 | BF16).
  * kv_dtype: F8E4M3 (value = e4m3 decode of the byte times *kv_scale, a DEVICE fp32 scalar so
  *   that no host sync is needed; NULL means 1) | F16 | BF16 (kv_scale may be NULL).
  * q_dtype: BF16 | F16. The softmax uses sm_scale (natural-log domain).
- * num_split >= 1 KV splits per sequence, combined by an LSE pass through `ws`;
- * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned). */
+ * num_split >= 1 KV splits per sequence, combined by an LSE pass through `ws`. With fp8 KV, page
+ *   a multiple of 64 and Hq a multiple of 64 the decode runs on the fp8 matrix cores with the
+ *   sequences' tiles balanced over B*num_split/(Hq/64) ranges (num_split then only sets the
+ *   parallelism); other cases use one workgroup per (sequence, split, 64 heads).
+ * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned; the larger of
+ *   the two paths' layouts). */
 int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
                    const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
                    int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens, void* o,
