@@ -7,8 +7,13 @@
 // Main kernel (any M, N; K % 8 == 0, N % 8 == 0 for row-major B):
 //   * 256x256 output tile per workgroup, BK = 64, 512 threads = 8 waves of 128x64 sub-tiles;
 //   * v_mfma_f32_32x32x16_{f16,bf16}: per wave 4x2 accumulator tiles = 128 fp32 VGPRs;
-//   * A tile [256][64] and B tile [64][256] (row-major B kept row-major) double-buffered in LDS
-//     with padded pitches; global loads for tile k+1 are in flight while tile k is multiplied;
+//   * A tiles [256][64] and B tiles [64][256] (row-major B kept row-major; [256][64] for B^T)
+//     are filled by buffer_load ... lds (16 bytes per lane straight into LDS, no VGPR staging)
+//     into unpadded, XOR-swizzled stages (2 for A, 3 for B: 160 KB); lanes whose chunk lies
+//     outside the matrix read zeros through the buffer descriptor's bounds;
+//   * the two waves on each SIMD (groups of 4) run half a k-tile apart: one reads the next
+//     k-tile's operands from LDS while the other issues MFMAs; each LDS-DMA instruction is
+//     issued between operand reads or MFMAs rather than in a burst;
 //   * the B operand (8 consecutive k of one column per lane) is read with ds_read_b64_tr_b16,
 //     which transposes 4x16 blocks of 16-bit values across each 16-lane group, so B needs no
 //     transpose in registers or in a separate pass;
