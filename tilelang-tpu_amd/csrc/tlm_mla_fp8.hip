@@ -64,7 +64,7 @@ constexpr int F8_SLOTS = 3;                          // first piece, last piece,
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
 constexpr int F8_WAVE_F4 = 8 * 4 * 64;               // float4 per wave in a partial slot
-constexpr int F8_QREG = 6;                           // Q k-steps held in VGPRs; the rest in LDS
+constexpr int F8_QREG = 4;                           // Q k-steps held in VGPRs; the rest in LDS
 
 // swizzled 16-byte chunk index of latent row r / rope row r
 TLM_DEV int swz_lat(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
@@ -96,6 +96,19 @@ TLM_DEV T ldc(const T* p) {
 }
 
 TLM_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// max / sum of x over lanes l and l ^ 32 through v_permlane32_swap (a VALU op; __shfl_xor would
+// be an LDS round trip). Both results are symmetric in the two lane halves.
+TLM_DEV float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+TLM_DEV float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // LDS reads of the ring issued as inline asm. Compiler-generated reads may be made to wait
 // (vmcnt(0)) for every outstanding LDS-DMA load, including the prefetch of the next stages, when
@@ -404,16 +417,18 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   };
   // LDS-DMA instruction k (0..8) of this thread for a tile: 0..7 latent, 8 rope
   auto issue_dma = [&](const Dma& d, int k) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // offsets recomputed per use, not hoisted into live registers
     if (k < 8) {  // latent: 2 rows x 32 chunks per wave-instruction
-      const int r = 2 * (8 * wave + k) + hf;
-      const int off = r * (int)a.kv_stride + 16 * ((lane & 31) ^ swz_lat(r));
+      const int r = 2 * (8 * wave + k) + (ln >> 5);
+      const int off = r * (int)a.kv_stride + 16 * ((ln & 31) ^ swz_lat(r));
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + (8 * wave + k) * 1024), 16,
                                                off, 0, 0, 0);
     } else {  // rope: 16 rows x 4 chunks per wave-instruction
-      const int r = 16 * wave + (lane >> 2);
-      const int off = r * (int)a.kpe_stride + 16 * ((lane & 3) ^ swz_rope(r));
+      const int r = 16 * wave + (ln >> 2);
+      const int off = r * (int)a.kpe_stride + 16 * ((ln & 3) ^ swz_rope(r));
       const __amdgpu_buffer_rsrc_t rp =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bpe, (short)0, d.npe, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(d.st + F8_LAT + wave * 1024), 16,
@@ -445,10 +460,76 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     vx[par] = vu >> 1;
   }
 
+  // ---- software pipeline over the tiles of a piece: the S^T MFMAs of tile t + 1 run with the
+  // softmax of tile t (and its two block exchanges) interleaved between their k-steps, then the
+  // O^T MFMAs of tile t. Every wave executes the same barriers per tile (A: tile t + 1 landed,
+  // B: block maxima, C: P^T blocks), whatever its own tokens or segment state.
   i32x8 qhi[F8_QREG], qlo[F8_QREG];
   int64_t t = t_lo;
+  int64_t issued = t_lo + 1 < t_hi ? t_lo + 2 : t_lo + 1;  // tiles [t_lo, issued) requested
   int cb = b_first;
   int64_t cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
+
+  // Tile x becomes visible: this thread's loads of it have landed (only tile x + 1's may still
+  // be in flight), then the workgroup barrier, after which every wave is also done with the
+  // stage of tile x - 2. Returns whether tile x + 1 is to be loaded now (into that stage).
+  auto visible = [&](int64_t x, Dma& dma) {
+    wait_vm(issued > x + 1 ? F8_LOADS : 0);
+    wg_barrier();
+    if (issued == x + 1 && issued < t_hi) {
+      dma = issue_setup(issued);
+      ++issued;
+      return true;
+    }
+    return false;
+  };
+  // S^T = K Q^T of tile x for this wave's 32 tokens (rows past the sequence read as zeros and
+  // are masked later), one LDS-DMA instruction of the refill per k-step (REFILL) and the work
+  // hook(k) after the k-step k MFMAs. No branches inside: the k-steps form one block.
+  auto qk_body = [&](int64_t x, f32x16& so, const Dma& dma, auto REFILLc, auto&& hook) {
+    constexpr bool REFILL = decltype(REFILLc)::value;
+    const uint8_t* st = ring + (int)((x - t_lo) % F8_NSTAGE) * F8_STAGE;
+    const uint8_t* krow = st + (32 * dh + th) * F8_DV;
+    const uint8_t* prow = st + F8_LAT + (32 * dh + th) * F8_DPE;
+    // operands of k-step k: K (32 bytes of this lane's row) and, past F8_QREG, Q^T hi/lo
+    i32x8 kop[3], qop[3][2];
+    auto nreads = [](int k) { return k < F8_QREG ? 2 : 6; };  // LDS reads of k-step k
+    auto kread = [&](int k) {
+      kop[k % 3] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk), krow + 16 * (((4 * k) ^ fk) ^ 1))
+                         : lds_2xb128(prow + 16 * fr, prow + 16 * (fr ^ 1));
+      if (k >= F8_QREG) {
+        const i32x8* q = &qt[pr][2 * (k - F8_QREG)][lane];
+        qop[k % 3][0] = lds_2xb128(q, (const i32x4*)q + 1);
+        qop[k % 3][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
+      }
+    };
+    kread(0);
+    kread(1);
+    so = f32x16{};
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      // reads of k-step k done (later LDS accesses only make the wait stricter)
+      lgkm_wait(k + 1 < 9 ? nreads(k + 1) : 0);
+      order_after(kop[k % 3]);
+      if (k >= F8_QREG) {
+        order_after(qop[k % 3][0]);
+        order_after(qop[k % 3][1]);
+      }
+      if (k + 2 < 9) kread(k + 2);
+      if constexpr (REFILL) issue_dma(dma, k);
+      so = mfma_fp8(kop[k % 3], k < F8_QREG ? qhi[k] : qop[k % 3][0], so);
+      so = mfma_fp8(kop[k % 3], k < F8_QREG ? qlo[k] : qop[k % 3][1], so);
+      hook(k);
+      sched_fence();
+    }
+  };
+  auto qk = [&](int64_t x, f32x16& so, bool refill, const Dma& dma, auto&& hook) {
+    if (refill)
+      qk_body(x, so, dma, std::true_type{}, hook);
+    else
+      qk_body(x, so, dma, std::false_type{}, hook);
+  };
+
   while (t < t_hi) {  // one iteration per sequence piece
     while (t >= cb_hi) {
       ++cb;
@@ -461,174 +542,17 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     const int64_t p_lo = t, p_hi = min(t_hi, cb_hi);
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
     const int slot = p_lo == t_lo ? 0 : 1;
-    bool have_scr = false, carry = false;
-    float lse_scr = 0.f, mt = 0.f, mbo = -INFINITY;
-    f32x16 s;  // raw scores of this wave's 32-token block (masked to -inf past the sequence)
-    for (;;) {  // one iteration per softmax segment (normally one per piece)
-      f32x16 oacc[8];
+    bool have_scr = false, first = true;
+    float lse_scr = 0.f, mref = 0.f, lsum = 0.f;
+    f32x16 oacc[8];
 #pragma unroll
-      for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
-      float mref = 0.f, lsum = 0.f;
-      bool first = true, cut = false;
-      while (t < p_hi) {
-        const uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
-        const int valid = L - (int)(t - cb_lo) * F8_TILE;  // tokens of the tile, >= 1
-        if (!carry) {
-          // hand over tile t, refill the stage freed by tile t - 1
-          wait_vm(t + 1 < t_hi ? F8_LOADS : 0);
-          wg_barrier();
-          const bool refill = t + 2 < t_hi;
-          const Dma dma = refill ? issue_setup(t + 2) : Dma{};
-          // S^T = K Q^T for this wave's 32 tokens x 32 heads
-          const int own = valid - 32 * dh;
-          float mb = -INFINITY;
-          if (own <= 0 && refill) issue(t + 2);
-          if (own > 0) {
-            const uint8_t* krow = st + (32 * dh + th) * F8_DV;
-            const uint8_t* prow = st + F8_LAT + (32 * dh + th) * F8_DPE;
-            // operands of k-step k: K (32 bytes of this lane's row) and, past F8_QREG, Q^T hi/lo
-            i32x8 kop[3], qop[3][2];
-            auto nreads = [](int k) { return k < F8_QREG ? 2 : 6; };  // LDS reads of k-step k
-            auto kread = [&](int k) {
-              kop[k % 3] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk),
-                                              krow + 16 * (((4 * k) ^ fk) ^ 1))
-                                 : lds_2xb128(prow + 16 * fr, prow + 16 * (fr ^ 1));
-              if (k >= F8_QREG) {
-                const i32x8* q = &qt[pr][2 * (k - F8_QREG)][lane];
-                qop[k % 3][0] = lds_2xb128(q, (const i32x4*)q + 1);
-                qop[k % 3][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
-              }
-            };
-            kread(0);
-            kread(1);
-            s = f32x16{};
-#pragma unroll
-            for (int k = 0; k < 9; ++k) {
-              // reads of k-step k done; those of k + 1 may still be in flight
-              lgkm_wait(k + 1 < 9 ? nreads(k + 1) : 0);
-              order_after(kop[k % 3]);
-              if (k >= F8_QREG) {
-                order_after(qop[k % 3][0]);
-                order_after(qop[k % 3][1]);
-              }
-              if (k + 2 < 9) kread(k + 2);
-              if (refill) issue_dma(dma, k);
-              s = mfma_fp8(kop[k % 3], k < F8_QREG ? qhi[k] : qop[k % 3][0], s);
-              s = mfma_fp8(kop[k % 3], k < F8_QREG ? qlo[k] : qop[k % 3][1], s);
-              sched_fence();
-            }
-            // raw scores (the log2-domain scale ch > 0 is applied inside exp2); element i is token
-            // 16 (i / 8) + 8 hf + i % 8 of the block
-            if (own < 32) {
-#pragma unroll
-              for (int i = 0; i < 16; ++i) {
-                const int tok = 16 * (i >> 3) + 8 * hf + (i & 7);
-                if (tok >= own) s[i] = -INFINITY;
-              }
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[i]);
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * ch;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = -INFINITY;
-          }
-          mbo = mb;
-          if (hf == 0) xmax[pr][dh][hh] = mb;
-          wg_barrier();
-          mt = fmaxf(mb, xmax[pr][dh ^ 1][hh]);  // tile max of the head
-          if (first) {
-            mref = mt;
-            first = false;
-          } else if (__ballot(mt > mref + F8_RESET)) {
-            cut = true;
-            break;
-          }
-        } else {
-          carry = false;
-          mref = mt;
-          first = false;
-        }
-        // P^T of this wave's block as two e4m3 terms on a per-head power-of-two scale 2^es (es =
-        // exponent of the block's largest P minus 8, so scaled values are below 256), folded into
-        // the exp2 argument; exchanged with the partner wave through LDS
-        int es = 0;
-        if (mbo != -INFINITY) {
-          (void)frexpf(__builtin_amdgcn_exp2f(mbo - mref), &es);
-          es = max(-127, min(127, es - 8));
-        }
-        float x[16], ps = 0.f;
-        const float sh = -(mref + (float)es);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          x[i] = __builtin_amdgcn_exp2f(fmaf(s[i], ch, sh));
-          ps += x[i];
-        }
-        ps = ldexpf(ps, es);
-        {
-          int phi4[4], plo4[4];
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const float* y = x + 4 * q4;
-            phi4[q4] = pack_fp8x4(y[0], y[1], y[2], y[3]);
-            typedef float f2 __attribute__((ext_vector_type(2)));
-            const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], false);
-            const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], true);
-            plo4[q4] = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
-          }
-          // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
-          uint8_t* rh = &xq[pr][dh][0][hh][8 * hf];
-          uint8_t* rl = &xq[pr][dh][1][hh][8 * hf];
-          lds_write_b64(rh, u32x2{(uint32_t)phi4[0], (uint32_t)phi4[1]});
-          lds_write_b64(rh + 16, u32x2{(uint32_t)phi4[2], (uint32_t)phi4[3]});
-          lds_write_b64(rl, u32x2{(uint32_t)plo4[0], (uint32_t)plo4[1]});
-          lds_write_b64(rl + 16, u32x2{(uint32_t)plo4[2], (uint32_t)plo4[3]});
-        }
-        ps += __shfl_xor(ps, 32, 64);
-        if (hf == 0) {
-          xsum[pr][dh][hh] = ps;
-          xsc[pr][dh][hh] = es + 127;
-        }
-        wg_barrier();
-        lsum += dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
-        // B operand: lane (head hh, half hf) holds tokens 16 hf + 0..15 of both blocks; its scale
-        // is that of block hf
-        i32x8 pbh = lds_2xb128(&xq[pr][0][0][hh][16 * hf], &xq[pr][1][0][hh][16 * hf]);
-        i32x8 pbl = lds_2xb128(&xq[pr][0][1][hh][16 * hf], &xq[pr][1][1][hh][16 * hf]);
-        const int psc = xsc[pr][hf][hh];
-        // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks x hi/lo
-        auto vread = [&](int dt) {
-          i32x2 r[4];
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            r[rr] = lds_tr8(st + vbase[rr & 1] + 32 * F8_DV * (rr >> 1) +
-                            32 * (dt ^ vx[rr & 1]));
-          return i32x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
-        };
-        i32x8 vop[2][2];
-        vop[0][0] = vread(0);
-        vop[0][1] = vread(1);
-        lds_wait(pbh, pbl);
-#pragma unroll
-        for (int g2 = 0; g2 < 4; ++g2) {
-          lds_wait(vop[g2 & 1][0], vop[g2 & 1][1]);
-          if (g2 + 1 < 4) {
-            vop[(g2 + 1) & 1][0] = vread(2 * g2 + 2);
-            vop[(g2 + 1) & 1][1] = vread(2 * g2 + 3);
-          }
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int dt = 2 * g2 + u;
-            oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbh, oacc[dt], psc);
-            oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbl, oacc[dt], psc);
-          }
-          sched_fence();
-        }
-        ++t;
-      }
+    for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
 
-      // ---- segment end: normalise, merge with an earlier segment, store this wave's 256 dims
-      const float lse_seg = mref + __log2f(lsum);
+    // Segment end: normalise, merge with an earlier segment (scratch slot), store this wave's
+    // 256 dims: to the output for a complete sequence, else to the piece's partial slot (a cut
+    // segment goes to the scratch slot)
+    auto flush = [&](bool cut, float m_seg) {
+      const float lse_seg = m_seg + __log2f(lsum);
       float w_seg = kvs / lsum, w_old = 0.f, lse_out = lse_seg;
       if (have_scr) {
         const float mx = fmaxf(lse_scr, lse_seg);
@@ -680,11 +604,151 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
       else
         store(std::false_type{});
       wait_vm(0);  // stores retire before the ring's vmcnt accounting resumes
-      if (!cut) break;
-      have_scr = true;
-      lse_scr = lse_out;
-      carry = true;  // tile t's scores are kept; the next segment starts from them
+      if (cut) {
+        have_scr = true;
+        lse_scr = lse_out;
+      }
+    };
+
+    // prologue: S^T of the piece's first tile
+    f32x16 s;
+    {
+      Dma dma{};
+      const bool refill = visible(t, dma);
+      qk(t, s, refill, dma, [](int) {});
     }
+    for (; t < p_hi; ++t) {
+      const uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
+      const int own = L - (int)(t - cb_lo) * F8_TILE - 32 * dh;  // this wave's valid tokens
+      const bool nxt = t + 1 < p_hi;
+      // softmax of tile t, in pieces placed after the k-steps of the next tile's S^T:
+      //   0: block max -> LDS; 2: barrier; 3: tile max, segment check, block scale; 3..6: P^T
+      //   as two e4m3 terms, 4 elements per step; 6: P^T blocks -> LDS; 7: block sums and
+      //   scales -> LDS, barrier; 8: row sums, B operands
+      float mb = -INFINITY, ps = 0.f, sh = 0.f, m_old = 0.f, tsum = 0.f;
+      int es = 0;
+      bool cut = false;  // a new segment starts at this tile (flushed before its O^T update)
+      int phi4[4], plo4[4];
+      i32x8 pbh, pbl;
+      int psc = 0;
+      auto hook = [&](int k) {
+        if (k == 0) {
+          // raw scores (the log2-domain scale ch > 0 is applied inside exp2); element i is token
+          // 16 (i / 8) + 8 hf + i % 8 of the block
+          if (own < 32) {  // wave-uniform: the sequence ends inside this wave's block
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int tok = 16 * (i >> 3) + 8 * hf + (i & 7);
+              s[i] = tok >= own ? -INFINITY : s[i];
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[i]);
+          mb = xhalf_max(mb) * ch;
+          xmax[pr][dh][hh] = mb;  // both lane halves write the same value
+        }
+        if (k == 2) wg_barrier();
+        if (k == 3) {
+          const float mt = fmaxf(mb, xmax[pr][dh ^ 1][hh]);  // tile max of the head
+          // a tile whose max exceeds the reference by more than the headroom ends the segment;
+          // P of this tile then uses the new reference and the old segment is flushed after the
+          // S^T k-steps (wave-uniform decision, no branch here)
+          cut = !first && __ballot(mt > mref + F8_RESET) != 0;
+          m_old = mref;
+          mref = (first || cut) ? mt : mref;
+          first = false;
+          // P^T of this wave's block as two e4m3 terms on a per-head power-of-two scale 2^es
+          // (es = exponent of the block's largest P minus 8, so scaled values are below 256),
+          // folded into the exp2 argument
+          int e2 = 0;
+          (void)frexpf(__builtin_amdgcn_exp2f(mb - mref), &e2);
+          es = mb == -INFINITY ? 0 : max(-127, min(127, e2 - 8));
+          sh = -(mref + (float)es);
+        }
+        if (k >= 3 && k <= 6) {
+          const int q4 = k - 3;
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = __builtin_amdgcn_exp2f(fmaf(s[4 * q4 + e], ch, sh));
+            ps += y[e];
+          }
+          phi4[q4] = pack_fp8x4(y[0], y[1], y[2], y[3]);
+          typedef float f2 __attribute__((ext_vector_type(2)));
+          const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], false);
+          const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], true);
+          plo4[q4] = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
+        }
+        if (k == 6) {
+          // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
+          uint8_t* rh = &xq[pr][dh][0][hh][8 * hf];
+          uint8_t* rl = &xq[pr][dh][1][hh][8 * hf];
+          lds_write_b64(rh, u32x2{(uint32_t)phi4[0], (uint32_t)phi4[1]});
+          lds_write_b64(rh + 16, u32x2{(uint32_t)phi4[2], (uint32_t)phi4[3]});
+          lds_write_b64(rl, u32x2{(uint32_t)plo4[0], (uint32_t)plo4[1]});
+          lds_write_b64(rl + 16, u32x2{(uint32_t)plo4[2], (uint32_t)plo4[3]});
+        }
+        if (k == 7) {
+          ps = xhalf_sum(ldexpf(ps, es));
+          xsum[pr][dh][hh] = ps;  // both lane halves write the same values
+          xsc[pr][dh][hh] = es + 127;
+          wg_barrier();
+        }
+        if (k == 8) {
+          tsum = dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
+          // B operand: lane (head hh, half hf) holds tokens 16 hf + 0..15 of both blocks; its
+          // scale is that of block hf
+          pbh = lds_2xb128(&xq[pr][0][0][hh][16 * hf], &xq[pr][1][0][hh][16 * hf]);
+          pbl = lds_2xb128(&xq[pr][0][1][hh][16 * hf], &xq[pr][1][1][hh][16 * hf]);
+          psc = xsc[pr][hf][hh];
+        }
+      };
+      f32x16 sn;
+      if (nxt) {
+        Dma dma{};
+        const bool refill = visible(t + 1, dma);
+        qk(t + 1, sn, refill, dma, hook);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) hook(k);
+      }
+      if (cut) {  // wave-uniform; rare
+        flush(true, m_old);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
+        lsum = 0.f;
+      }
+      lsum += tsum;
+      // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks x hi/lo
+      auto vread = [&](int dt) {
+        i32x2 r[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          r[rr] = lds_tr8(st + vbase[rr & 1] + 32 * F8_DV * (rr >> 1) + 32 * (dt ^ vx[rr & 1]));
+        return i32x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
+      };
+      i32x8 vop[2][2];
+      vop[0][0] = vread(0);
+      vop[0][1] = vread(1);
+      lds_wait(pbh, pbl);
+#pragma unroll
+      for (int g2 = 0; g2 < 4; ++g2) {
+        lds_wait(vop[g2 & 1][0], vop[g2 & 1][1]);
+        if (g2 + 1 < 4) {
+          vop[(g2 + 1) & 1][0] = vread(2 * g2 + 2);
+          vop[(g2 + 1) & 1][1] = vread(2 * g2 + 3);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int dt = 2 * g2 + u;
+          oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbh, oacc[dt], psc);
+          oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbl, oacc[dt], psc);
+        }
+        sched_fence();
+      }
+      if (nxt) s = sn;
+    }
+    flush(false, mref);
   }
 }
 
