@@ -416,6 +416,43 @@ def bench_copy(args, dev, flush, cpu):
                                  HBM_PEAK_GBS)}
 
 
+def bench_kv_append(args, dev, flush, cpu):
+    """Paged KV append + e4m3 quantisation (the step before the MLA decode) at a prefill-sized
+    chunk: 64 sequences x 512 new latent tokens x 576 dims, bf16 in, fp8 pages out."""
+    from tilelang.jit.adapter.mi355x import ops
+    B, T, D, page = 64, 512, 576, 64
+    pages = 128
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(B * pages, generator=g).view(B, pages).to(torch.int32)
+    start = torch.randint(0, pages * page - T, (B,), generator=g, dtype=torch.int32)
+    count = torch.full((B,), T, dtype=torch.int32)
+    scale = torch.tensor([float(x.float().abs().max()) / 448.0], dtype=torch.float32)
+    nbytes = B * T * D * (2 + 1) + B * pages * 4 + 2 * B * 4
+    xs, bts, sts, cns, scs = (t.to(dev) for t in (x, bt, start, count, scale))
+    kv = torch.zeros(B * pages * page, D, dtype=torch.float8_e4m3fn, device=dev)
+    fns = [lambda: ops.kv_append_fp8(xs, sts, cns, bts, kv, page, scs)]
+    pmc_launches(args, fns, "kv_append")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 200, flush)
+    res = {"workload": "kv_append_fp8_b64_t512_d576", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms, "dtype": "bf16 in, fp8e4m3 out",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        nb = 4
+        pool = torch.zeros(B * pages * page, D, dtype=torch.uint8).numpy()
+        t = cpu_time(lambda: ref.kv_append_fp8_ref(x[:nb], start[:nb].numpy(), count[:nb].numpy(),
+                                                   bt[:nb].numpy(), pool, page, float(scale)),
+                     reps=1)
+        res["cpu_baseline"] = {"value": nbytes * nb / B / t / 1e9, "unit": "GB/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"first {nb} of {B} sequences, oracle.ref.kv_append_fp8_ref"}
+    return res
+
+
 BENCHES = {
     "copy": bench_copy,
     "gemm": bench_gemm,
@@ -426,9 +463,10 @@ BENCHES = {
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
     "mla": bench_mla,
+    "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "mla"]
+         "mla", "kv_append"]
 
 
 def main():

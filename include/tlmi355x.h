@@ -147,6 +147,25 @@ int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, int64_t kv_rows,
                      const int32_t* block_table, const int32_t* seqlens, const int64_t* cu_seqlens,
                      void* out, int64_t B, int64_t page, int64_t max_pages, void* stream);
 
+/* Paged KV-cache append with FP8 (OCP e4m3) quantisation, the step that fills the cache
+ * tlm_mla_decode reads. For every sequence b and each of its count[b] new tokens j
+ * (0 <= j < min(count[b], T)), at position p = start[b] + j:
+ *   kv[row(p)] = e4m3(clamp(x[b, j, :] / *scale, -448, 448))   (NaN stays NaN)
+ * with row(p) = block_table[b, p / page] * page + p % page, the decode's page addressing
+ * (examples/deepseek_mla/example_mla_decode_paged.py:62-63; table layout :26). No reference
+ * program implements this step; the quantisation equals the MLA config's cache construction
+ * (x / scale).to(float8_e4m3fn) for in-range values and saturates beyond +-448.
+ *   x      [B, T, D] rows of D elements (x_dtype BF16 | F16) at x + b*x_batch_stride +
+ *          j*x_row_stride (elements; strides and D multiples of 8, x 16-byte aligned)
+ *   kv     fp8 pool rows of kv_stride bytes, kv_rows rows (8-byte aligned)
+ *   scale  device pointer to the fp32 dequantisation scale (value = code * scale)
+ * Positions beyond the table and rows outside [0, kv_rows) are skipped (nothing written). */
+int tlm_kv_append_fp8(const void* x, int64_t x_batch_stride, int64_t x_row_stride, int x_dtype,
+                      const int32_t* start, const int32_t* count, const int32_t* block_table,
+                      int64_t max_pages, int64_t page, void* kv, int64_t kv_stride,
+                      int64_t kv_rows, int64_t B, int64_t T, int64_t D, const float* scale,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -219,6 +219,33 @@ def fp8_quantize(x: torch.Tensor):
     return q, scale
 
 
+def fp8_saturate_quantize(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """e4m3 codes of clamp(x / scale, -448, 448): fp32 division, then torch's RNE cast (the MLA
+    config's cache construction, fp8_quantize above, for in-range values); NaN stays NaN."""
+    return (x.float() / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+
+
+def kv_append_fp8_ref(x: torch.Tensor, start, count, block_table, kv_bytes: np.ndarray,
+                      page: int, scale: float) -> np.ndarray:
+    """Paged KV append (the step before the MLA decode): token j < count[b] of sequence b goes to
+    position p = start[b] + j, row block_table[b, p // page] * page + p % page
+    (example_mla_decode_paged.py:62-63); positions beyond the table and rows outside the pool
+    are skipped. Returns an updated copy of kv_bytes (uint8 [rows, D])."""
+    out = kv_bytes.copy()
+    codes = fp8_saturate_quantize(x, scale).view(torch.uint8).numpy()
+    B, T = x.shape[0], x.shape[1]
+    pages = block_table.shape[1]
+    for b in range(B):
+        for j in range(min(int(count[b]), T)):
+            p = int(start[b]) + j
+            if p < 0 or p >= pages * page:
+                continue
+            row = int(block_table[b, p // page]) * page + p % page
+            if 0 <= row < out.shape[0]:
+                out[row] = codes[b, j]
+    return out
+
+
 def paged_gather_ref(kv_bytes: np.ndarray, block_table: np.ndarray, seqlens: np.ndarray,
                      page: int) -> np.ndarray:
     """Concatenate every sequence's rows in token order (uint8 rows), numpy."""

@@ -25,7 +25,7 @@ def test_header_declares_entry_points():
     syms = declared_symbols()
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
-              "tlm_paged_gather"):
+              "tlm_paged_gather", "tlm_kv_append_fp8"):
         assert s in syms
 
 
@@ -140,3 +140,15 @@ def test_init_without_gpu_reports_error():
     assert L.tlm_init(0) != 0
     assert _err()
     assert L.tlm_init(-1) == -1
+
+
+def test_kv_append_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    args = lambda x=p, dt=lib.BF16, D=576, B=2, T=3, ks=576: (
+        x, 576 * 3, 576, dt, p, p, p, 4, 64, p, ks, 100, B, T, D, p, None)
+    assert L.tlm_kv_append_fp8(*args(x=None)) == -1
+    assert L.tlm_kv_append_fp8(*args(dt=lib.F32)) == -2
+    assert L.tlm_kv_append_fp8(*args(D=570, ks=576)) == -2
+    assert L.tlm_kv_append_fp8(*args(ks=100)) == -1  # kv row stride smaller than D
+    assert L.tlm_kv_append_fp8(*args(B=0)) == 0

@@ -257,3 +257,78 @@ def test_paged_gather_numpy_vs_c():
     # the second sequence's 9th token lives in page bt[1, 1], slot 0
     off = 1 + 8
     assert np.array_equal(exp[off], kv[bt[1, 1] * page])
+
+
+# ------------------------------------------------------------------------------- KV append (FP8)
+def _e4m3_nearest_even(v: float, table: np.ndarray) -> int:
+    """Brute force over the 256 codes: nearest finite e4m3 value to v, ties to the even
+    mantissa (code with bit 0 clear), +0 for 0."""
+    best, best_d = None, None
+    for code in range(256):
+        t = table[code]
+        if np.isnan(t):
+            continue
+        d = abs(float(t) - v)
+        if best is None or d < best_d or (d == best_d and (code & 1) == 0 and (best & 1) == 1):
+            best, best_d = code, d
+    if float(table[best]) == 0.0:
+        best = 0x80 if math.copysign(1.0, v) < 0 and v != 0.0 else 0x00
+    return best
+
+
+def test_fp8_saturate_quantize_vs_brute_force_rne():
+    """The quantiser (torch's RNE cast after clamping) picks the nearest e4m3 value with ties to
+    even for every sample, including subnormals, exact ties and the +-448 saturation."""
+    table = ref.fp8_e4m3fn_table()
+    g = torch.Generator().manual_seed(31)
+    finite = table[~np.isnan(table)].astype(np.float64)
+    pos = np.unique(finite[finite > 0])
+    mids = (pos[:-1] + pos[1:]) / 2.0  # exact ties between neighbours
+    vals = torch.cat([torch.randn(400, generator=g) * 30, torch.rand(200, generator=g) * 0.004,
+                      torch.tensor(mids, dtype=torch.float32), -torch.tensor(mids[:20], dtype=torch.float32),
+                      torch.tensor([0.0, 447.9, 448.0, 460.0, 470.0, 1e6, -1e6, 2.0 ** -10,
+                                    2.0 ** -10 + 2.0 ** -20])])
+    codes = ref.fp8_saturate_quantize(vals, 1.0).view(torch.uint8).numpy()
+    for v, c in zip(vals.tolist(), codes.tolist()):
+        vs = min(max(v, -448.0), 448.0)
+        assert c == _e4m3_nearest_even(vs, table), (v, hex(c))
+    nan = ref.fp8_saturate_quantize(torch.tensor([float("nan")]), 1.0).float()
+    assert torch.isnan(nan).all()
+
+
+def test_kv_append_round_trip_through_gather():
+    """Appending whole sequences into an empty pool and gathering them back through the block
+    table (C-pinned gather) returns the quantised rows in token order."""
+    g = torch.Generator().manual_seed(32)
+    B, T, D, page, pages = 3, 20, 16, 4, 6
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(B * pages, generator=g).view(B, pages).to(torch.int32).numpy()
+    count = np.array([20, 7, 0], dtype=np.int32)
+    start = np.zeros(B, dtype=np.int32)
+    pool = np.zeros((B * pages * page, D), dtype=np.uint8)
+    scale = 0.01
+    out = ref.kv_append_fp8_ref(x, start, count, bt, pool, page, scale)
+    got = ref.paged_gather_ref(out, bt, count, page)
+    q = ref.fp8_saturate_quantize(x, scale).view(torch.uint8).numpy()
+    exp = np.concatenate([q[b, :count[b]] for b in range(B)])
+    assert np.array_equal(got, exp)
+    assert np.count_nonzero(out.any(axis=1)) <= int(count.sum())
+
+
+def test_kv_append_incremental_equals_bulk_and_skips_out_of_range():
+    g = torch.Generator().manual_seed(33)
+    B, T, D, page, pages = 2, 9, 8, 4, 3
+    x = torch.randn(B, T, D, generator=g).to(torch.float16)
+    bt = np.array([[5, 0, 3], [1, 4, 2]], dtype=np.int32)
+    pool = np.zeros((6 * page, D), dtype=np.uint8)
+    bulk = ref.kv_append_fp8_ref(x, np.array([0, 2]), np.array([9, 7]), bt, pool, page, 0.05)
+    step = pool
+    for j in range(T):  # one token per call, decode-style
+        xj = x[:, j:j + 1]
+        cnt = np.array([1 if j < 9 else 0, 1 if j < 7 else 0])
+        step = ref.kv_append_fp8_ref(xj, np.array([j, 2 + j]), cnt, bt, step, page, 0.05)
+    assert np.array_equal(bulk, step)
+    # positions past the table (3 pages * 4 = 12) and rows outside the pool are skipped
+    out = ref.kv_append_fp8_ref(x, np.array([10, 0]), np.array([9, 1]), np.array(
+        [[5, 0, 3], [99, 4, 2]], dtype=np.int32), pool, page, 0.05)
+    assert np.count_nonzero(out.any(axis=1)) == 2  # positions 10, 11 of sequence 0 only

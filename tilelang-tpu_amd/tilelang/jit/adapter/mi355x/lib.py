@@ -40,6 +40,9 @@ _SIGNATURES = {
     "tlm_mla_workspace_bytes": ([c_int64, c_int64, c_int64, c_int], c_size_t),
     "tlm_paged_gather": ([c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int64, c_int64, c_int64, c_void_p], c_int),
+    "tlm_kv_append_fp8": ([c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p,
+                           c_int64, c_int64, c_void_p] + [c_int64] * 5 + [c_void_p, c_void_p],
+                          c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -216,3 +216,29 @@ def paged_gather(kv_bytes: torch.Tensor, block_table, seqlens, cu_seqlens, out, 
              _ptr(cu_seqlens), _ptr(out), block_table.shape[0], page, block_table.shape[1],
              _stream(dev))
     return out
+
+
+def kv_append_fp8(x: torch.Tensor, start: torch.Tensor, count: torch.Tensor,
+                  block_table: torch.Tensor, kv: torch.Tensor, page: int, scale: torch.Tensor):
+    """Quantise new latent rows x [B, T, D] (bf16/fp16) to e4m3 with the cache scale and write
+    them into the paged fp8 pool kv [rows, D] at positions start[b] .. start[b] + count[b] - 1
+    of each sequence (saturating at +-448). Returns kv."""
+    dev = _dev(x, start, count, block_table, kv, scale)
+    if x.dim() != 3:
+        raise ValueError("x must be [B, T, D]")
+    B, T, D = x.shape
+    if x.stride(2) != 1:
+        raise ValueError("x rows must be contiguous")
+    if kv.dtype != torch.float8_e4m3fn or kv.dim() != 2 or kv.shape[1] != D or kv.stride(1) != 1:
+        raise ValueError("kv must be a float8_e4m3fn [rows, D] tensor with contiguous rows")
+    for n, t in (("start", start), ("count", count), ("block_table", block_table)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous int32 tensor")
+    if start.numel() != B or count.numel() != B or block_table.dim() != 2 or block_table.shape[0] != B:
+        raise ValueError("start/count must have B entries and block_table B rows")
+    if scale.dtype != torch.float32 or scale.numel() != 1:
+        raise ValueError("scale must be a one-element float32 tensor")
+    lib.call("tlm_kv_append_fp8", _ptr(x), x.stride(0), x.stride(1), dtype_code(x.dtype),
+             _ptr(start), _ptr(count), _ptr(block_table), block_table.shape[1], page, _ptr(kv),
+             kv.stride(0), kv.shape[0], B, T, D, _ptr(scale), _stream(dev))
+    return kv
