@@ -115,3 +115,45 @@ def test_random_scales_bit_exact():
         gn, en = np.isnan(table[got]), np.isnan(table[exp])
         assert np.array_equal(gn, en), trial
         assert np.array_equal(got[~gn], exp[~en]), trial
+
+
+@pytest.mark.parametrize("D,width", [(72, 72), (64, 72), (512, 576)])
+def test_column_slices_and_8_wide_rows(D, width):
+    """kv given as the first D columns of a wider pool (the latent part of a fused [rows, 576]
+    cache) and row strides that are not multiples of 16 bytes (8-element kernel variant); the
+    columns beyond D stay untouched."""
+    g = torch.Generator().manual_seed(45)
+    B, T, page, pages = 3, 50, 16, 4
+    x = (torch.randn(B, T, D, generator=g) * 2).to(torch.bfloat16)
+    bt = torch.randperm(B * pages, generator=g).view(B, pages).to(torch.int32).numpy()
+    start = np.array([0, 13, 30], dtype=np.int32)
+    count = np.array([50, 20, 34], dtype=np.int32)
+    pool = np.full((B * pages * page, width), 0x5A, dtype=np.uint8)
+    full = torch.from_numpy(pool.copy()).to(DEV).view(torch.float8_e4m3fn)
+    ops.kv_append_fp8(x.to(DEV), torch.as_tensor(start).to(DEV), torch.as_tensor(count).to(DEV),
+                      torch.as_tensor(bt).to(DEV), full[:, :D], page,
+                      torch.tensor([0.01], dtype=torch.float32, device=DEV))
+    torch.cuda.synchronize()
+    got = full.view(torch.uint8).cpu().numpy()
+    exp = pool.copy()
+    exp[:, :D] = ref.kv_append_fp8_ref(x, start, count, bt, pool[:, :D], page, 0.01)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("scale", [2.0 ** -126, 2.0 ** -100, 2.0 ** -90, 2.0 ** -89.5,
+                                   2.0 ** 89.5, 2.0 ** 90, 2.0 ** 100, 3e38])
+def test_extreme_scales_every_bf16_value(scale):
+    """Every bf16 bit pattern at scales on both sides of the kernel's fast-path window
+    [2^-90, 2^90] (outside it the kernel divides per element): bf16 subnormals against the
+    smallest normal scale, quotients that overflow fp32, exact signed zeros."""
+    allbits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = allbits.view(1, 65536 // 64, 64)
+    page, T = 64, x.shape[1]
+    bt = np.arange(16, dtype=np.int32).reshape(1, 16)
+    pool = np.zeros((16 * page, 64), dtype=np.uint8)
+    got = _run(x, np.array([0]), np.array([T]), bt, pool, page, scale)
+    exp = ref.kv_append_fp8_ref(x, np.array([0]), np.array([T]), bt, pool, page, scale)
+    table = ref.fp8_e4m3fn_table()
+    gnan, enan = np.isnan(table[got]), np.isnan(table[exp])
+    assert np.array_equal(gnan, enan)
+    assert np.array_equal(got[~gnan], exp[~enan])

@@ -10,14 +10,16 @@
 // this is exactly torch's (x.float() / scale).to(torch.float8_e4m3fn), which is how the MLA
 // config's cache is built; out-of-range values saturate instead of becoming NaN.
 //
-// HBM-bound streaming kernel: one thread per 8 elements (one 16-byte load, one 8-byte store),
-// grid-stride over all (sequence, token, chunk) triples. (One wave per token row, or four rows
-// per wave with their loads issued together, measured 10-15% slower at the bench size.)
+// HBM-bound streaming kernel: one thread per VEC elements (VEC = 16: two 16-byte loads, one
+// 16-byte store; VEC = 8 when D or the cache's row stride is not a multiple of 16), grid-stride
+// over all (sequence, token, chunk) triples, at most 4096 workgroups. (One wave per token row,
+// or four rows per wave with their loads issued together, measured 10-20% slower; non-temporal
+// loads and stores 15% slower.)
 #include "tlm_common.h"
 
 namespace {
 
-template <bool BF16>
+template <bool BF16, int VEC>
 __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_bstride, int64_t x_rstride,
     const int32_t* __restrict__ start, const int32_t* __restrict__ count,
@@ -26,11 +28,16 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     const float* __restrict__ scale) {
   using H = h16<BF16>;
   const float s = *scale;
-  // x / s correctly rounded without a division per element (Markstein): y = RN(1 / s),
-  // q = RN(x y), q' = RN(q + RN(x - q s) y) is RN(x / s) when the residual does not underflow
-  // (|x| >= 2^-100; checked against exact quotients over 1.5e8 random pairs); zeros keep their
-  // sign through q, quotients beyond 1e30 saturate anyway, tiny x takes the division.
+  // x / s correctly rounded without a division per element (Markstein): with y = RN(1 / s),
+  // q0 = RN(x y) and r = x - q0 s (exact in an fma), RN(q0 + r y) = RN(x / s) whenever the
+  // residual does not underflow, which holds for |x| >= 2^-100 (checked against exact quotients
+  // over 1.5e8 random pairs). For 2^-90 <= s <= 2^90 every smaller |x| gives |x / s| < 2^-10,
+  // which rounds to a signed e4m3 zero whatever the last fp32 bit, so the uniform fast path
+  // needs no per-element guard: q0 is clamped to +-1024 before the refinement so an overflowing
+  // x y cannot turn into inf - inf, the sign is taken from q0 (an fma of a zero residual drops
+  // the sign of -0), and NaN inputs are passed through. Other scales divide per element.
   const float y = __fdiv_rn(1.0f, s);
+  const bool fast = s >= 0x1p-90f && s <= 0x1p90f;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
     const int c = i % chunks;
     const int bt = i / chunks;
@@ -40,32 +47,62 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     if (p < 0 || p >= max_pages * page) continue;  // beyond the block table
     const int64_t row = (int64_t)block_table[b * max_pages + p / page] * page + p % page;
     if (row < 0 || row >= kv_rows) continue;  // a corrupt table entry never writes out of the pool
-    const u32x4 w = *(const u32x4*)(x + b * x_bstride + j * x_rstride + 8 * c);
-    float v[8];
+    const u32x4* src = (const u32x4*)(x + b * x_bstride + j * x_rstride + VEC * c);
+    u32x4 w[VEC / 8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = H::lo(w[e]);
-      v[2 * e + 1] = H::hi(w[e]);
+    for (int u = 0; u < VEC / 8; ++u) w[u] = src[u];
+    float v[VEC];
+#pragma unroll
+    for (int u = 0; u < VEC / 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[8 * u + 2 * e] = H::lo(w[u][e]);
+        v[8 * u + 2 * e + 1] = H::hi(w[u][e]);
+      }
+    if (fast) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float q0 = v[e] * y;
+        const float qc = __builtin_amdgcn_fmed3f(q0, -1024.f, 1024.f);
+        const float q1 = copysignf(fmaf(fmaf(-qc, s, v[e]), y, qc), q0);
+        const float o = __builtin_amdgcn_fmed3f(q1, -448.f, 448.f);  // saturate
+        v[e] = v[e] != v[e] ? v[e] : o;                                // NaN stays NaN
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float q = __fdiv_rn(v[e], s);
+        v[e] = q != q ? q : fminf(fmaxf(q, -448.f), 448.f);
+      }
     }
+    // v_cvt_pk_fp8_f32 rounds to nearest even (448 is the largest finite e4m3; a 464 tie rounds
+    // to it, larger magnitudes would give the NaN code, hence the clamp above).
+    uint32_t o[VEC / 4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float ax = fabsf(v[e]);
-      float q = v[e] * y;
-      if (ax >= 0x1p-100f && fabsf(q) <= 1e30f)
-        q = fmaf(fmaf(-q, s, v[e]), y, q);
-      else if (ax != 0.f && ax < 0x1p-100f)
-        q = __fdiv_rn(v[e], s);
-      v[e] = q != q ? q : fminf(fmaxf(q, -448.f), 448.f);  // saturate, keep NaN
-    }
-    u32x2 o;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < VEC / 4; ++h) {
       int word = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h], v[4 * h + 1], 0, false);
       word = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h + 2], v[4 * h + 3], word, true);
       o[h] = (uint32_t)word;
     }
-    *(u32x2*)(kv + row * kv_stride + 8 * c) = o;
+    uint8_t* dst = kv + row * kv_stride + VEC * c;
+    if constexpr (VEC == 16) {
+      *(u32x4*)dst = u32x4{o[0], o[1], o[2], o[3]};
+    } else {
+      *(u32x2*)dst = u32x2{o[0], o[1]};
+    }
   }
+}
+
+template <bool BF16, int VEC>
+void launch(const void* x, int64_t xb, int64_t xr, const int32_t* start, const int32_t* count,
+            const int32_t* bt, int64_t max_pages, int64_t page, void* kv, int64_t kv_stride,
+            int64_t kv_rows, int64_t B, int64_t T, int64_t D, const float* scale, hipStream_t st) {
+  const int chunks = (int)(D / VEC);
+  const int total = (int)(B * T * chunks);
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+  kv_append_fp8_kernel<BF16, VEC><<<grid, 256, 0, st>>>(
+      (const uint16_t*)x, xb, xr, start, count, bt, max_pages, page, (uint8_t*)kv, kv_stride,
+      kv_rows, (int)T, chunks, total, scale);
 }
 
 }  // namespace
@@ -97,22 +134,27 @@ extern "C" int tlm_kv_append_fp8(const void* x, int64_t x_batch_stride, int64_t 
     return TLM_EINVAL;
   }
   if (B == 0 || T == 0) return TLM_OK;
-  const int64_t chunks = D / 8;
-  if (B * T * chunks > INT32_MAX || B * max_pages > INT32_MAX) {
+  if (B * T * (D / 8) > INT32_MAX || B * max_pages > INT32_MAX) {
     tlm_set_error("tlm_kv_append_fp8: problem too large for one launch");
     return TLM_EINVAL;
   }
-  const int total = (int)(B * T * chunks);
-  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 256 * 16);
   hipStream_t st = (hipStream_t)stream;
-  if (x_dtype == TLM_BF16)
-    kv_append_fp8_kernel<true><<<grid, 256, 0, st>>>(
-        (const uint16_t*)x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
-        page, (uint8_t*)kv, kv_stride, kv_rows, (int)T, (int)chunks, total, scale);
-  else
-    kv_append_fp8_kernel<false><<<grid, 256, 0, st>>>(
-        (const uint16_t*)x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
-        page, (uint8_t*)kv, kv_stride, kv_rows, (int)T, (int)chunks, total, scale);
+  const bool v16 = D % 16 == 0 && kv_stride % 16 == 0 && tlm_aligned(kv, 16);
+  if (x_dtype == TLM_BF16) {
+    if (v16)
+      launch<true, 16>(x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
+                       page, kv, kv_stride, kv_rows, B, T, D, scale, st);
+    else
+      launch<true, 8>(x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
+                      page, kv, kv_stride, kv_rows, B, T, D, scale, st);
+  } else {
+    if (v16)
+      launch<false, 16>(x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
+                        page, kv, kv_stride, kv_rows, B, T, D, scale, st);
+    else
+      launch<false, 8>(x, x_batch_stride, x_row_stride, start, count, block_table, max_pages,
+                       page, kv, kv_stride, kv_rows, B, T, D, scale, st);
+  }
   TLM_LAUNCH_CHECK("tlm_kv_append_fp8");
   return TLM_OK;
 }
