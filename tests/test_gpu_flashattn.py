@@ -75,3 +75,17 @@ def test_flashattn_fp16_and_consistency():
     assert torch.equal(o1, o2)
     exp = ref.flashattn_ref(w.tensors["q"], w.tensors["k"], w.tensors["v"], True)
     torch_assert_close(o1.cpu(), exp, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flashattn_score_jumps_rescale(causal):
+    """Keys of later 64-key tiles scaled up (x1, x9, x17, ...): row maxima jump by far more than
+    the lazy-max headroom, so tiles after the first are redone with O and l rescaled."""
+    w = workloads.flashattn(1, 640, 2, 128, causal=causal, seed=25)
+    q, kk, v = (w.tensors[n] for n in ("q", "k", "v"))
+    f = (1 + 8 * (torch.arange(640) // 64)).to(torch.float32).view(1, 640, 1, 1)
+    kk = (kk.float() * f).to(torch.bfloat16)
+    o = torch.empty_like(q, device=DEV)
+    ops.flash_attn_fwd(q.to(DEV), kk.to(DEV), v.to(DEV), o, causal, 1 / math.sqrt(128))
+    exp = ref.flashattn_ref(q, kk, v, causal)
+    torch_assert_close(o.cpu(), exp, atol=2e-2, rtol=2e-2)

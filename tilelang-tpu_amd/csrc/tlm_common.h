@@ -98,6 +98,19 @@ TLM_DEV float wave_max(float v) {
 TLM_DEV float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 TLM_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum of x over lanes l and l ^ 32 through v_permlane32_swap (a VALU op; __shfl_xor would
+// be an LDS round trip). Both results are symmetric in the two lane halves.
+TLM_DEV float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+TLM_DEV float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Non-temporal (streaming) 16-byte global accesses for single-use data.
 TLM_DEV u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
 TLM_DEV void st_nt(u32x4* p, u32x4 v) { __builtin_nontemporal_store(v, p); }

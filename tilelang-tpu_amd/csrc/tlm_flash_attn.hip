@@ -259,8 +259,10 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
 //     apart: while one group issues MFMAs (QK of tile j and PV of tile j-1: 32 MFMAs per wave, at
 //     raised wave priority) the other runs the softmax of its tile on the VALU, so each SIMD's
 //     matrix core and VALU are busy at the same time. Each half-step ends with a workgroup
-//     barrier. (Interleaving each wave's own softmax into its MFMA stream instead measured ~10%
-//     slower: the softmax of both waves then competes for the SIMD's VALU inside the MFMA phase);
+//     barrier. (Interleaving each wave's own softmax into its MFMA stream instead, one piece of
+//     the next tile's softmax after each PV MFMA, measured 7% slower with 8 waves of 32 queries
+//     and 25-33% slower with 4 waves of 64 queries, where one wave per SIMD cannot cover its own
+//     LDS and VALU latencies);
 //   * K and V tiles (64 keys x 128 dims, 16 KB each) stream into 4-stage LDS rings through
 //     buffer_load ... lds (16 bytes per lane, no VGPR staging). Tile j + 2 is loaded during step j;
 //     the buffer descriptor of a tile ends at its last valid key, so keys >= S read as zeros;

@@ -97,19 +97,6 @@ TLM_DEV T ldc(const T* p) {
 
 TLM_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// max / sum of x over lanes l and l ^ 32 through v_permlane32_swap (a VALU op; __shfl_xor would
-// be an LDS round trip). Both results are symmetric in the two lane halves.
-TLM_DEV float xhalf_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-TLM_DEV float xhalf_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // LDS reads of the ring issued as inline asm. Compiler-generated reads may be made to wait
 // (vmcnt(0)) for every outstanding LDS-DMA load, including the prefetch of the next stages, when
 // the compiler cannot prove they touch another stage. The caller waits with lds_wait() before
