@@ -68,13 +68,16 @@ int tlm_num_cus(void);
 
 /* RMSNorm over the last dim: y[r,:] = cast(x[r,:] * rsqrt(mean_fp32(x[r,:]^2) + eps) * w).
  * Reference program: tpu_demo/rms_norm/rms_norm_fp16.py:9-35 (no weight, eps 1e-12);
- * oracle rms_norm_fp16.py:51-54. `w` may be NULL (reference behaviour). dtype: F16 | BF16. */
+ * oracle rms_norm_fp16.py:51-54. `w` may be NULL (reference behaviour). dtype: F16 | BF16 |
+ * F32 (rmsnorm_fp32.py: the same expression on fp32 tiles, stored without rounding). The
+ * split-K programs (rmsnorm_splitk_{fp16,bf16,fp32}.py:9-47) compute the same result. */
 int tlm_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
                 int dtype, void* stream);
 
 /* SwiGLU: out = cast(up * gate / (1 + exp(-gate))) in fp32.
  * Reference program tpu_demo/tpu_test_swiglu_bf16.py:5-54 (param order gate, up, out),
- * oracle :68 (b * F.silu(a)). dtype: BF16 | F16. n = number of elements. */
+ * oracle :68 (b * F.silu(a)). dtype: BF16 | F16 | F32 (tpu_test_swiglu_fp32.py: fp32 out, no
+ * rounding). n = number of elements. */
 int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
 
 /* Interleaved RoPE on x[tokens, heads, dim] with tables cos/sin[tokens, dim] shared by all
@@ -82,7 +85,8 @@ int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype
  *   out[2i]   = x[2i]*c - x[2i+1]*s,   out[2i+1] = x[2i+1]*c + x[2i]*s   (fp32, one rounding).
  * Reference program tpu_demo/tpu_test_rope_bf16.py:5-51 (ppl_rope_add), oracle :76-92.
  * The reference's [C, W] program is the case heads == 1. `k`/`k_out` may be NULL; when
- * given, k[tokens, heads_k, dim] is rotated in the same launch. dtype: BF16 | F16. */
+ * given, k[tokens, heads_k, dim] is rotated in the same launch. dtype: BF16 | F16 | F32
+ * (tpu_test_rope_fp16.py, tpu_test_rope_fp32.py, tpu_test_rope.py). */
 int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t, void* q_out,
              void* k_out, int64_t tokens, int64_t heads_q, int64_t heads_k, int64_t dim, int dtype,
              void* stream);
@@ -91,17 +95,34 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * trans_b == 0: B is [K,N] row-major (reference ppl_gemm transpose_B=False,
  *   tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31, src/target/codegen_ppl.cc:1244-1279).
  * trans_b == 1: B is [N,K] row-major (ppl_gemm transpose_B=True).
- * in_dtype: F16 | BF16; out_dtype: F16 | BF16 | F32. */
+ * in_dtype: F16 | BF16; out_dtype: F16 | BF16 | F32. The fp32 program
+ * (tpu_demo/matmul/tpu_test_matmul_fp32.py:9-31) copies its fp32 A/B tiles to fp16 before
+ * ppl_gemm: tlm_cast to F16, then this with out_dtype F32. */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
              int out_dtype, int trans_b, void* stream);
+
+/* Element-type conversion of n contiguous values, the cast of a ppl_copy between tiles of
+ * different dtypes (src/target/codegen_ppl.cc:1138-1152): F32 -> F16 | BF16 rounds to nearest
+ * even, F16 | BF16 -> F32 is exact. Used for the fp32 demo programs whose matrix operands are
+ * fp16 tiles (tpu_test_matmul_fp32.py:22-28, flashattn/tpu_test_flashattn_fp32.py:28-55). */
+int tlm_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n, void* stream);
 
 /* FlashAttention forward, BSHD layout: q,k,v,o [B, S, H, D]; softmax in fp32 with scale
  * sm_scale; P rounded to the input dtype before P*V; causal masks key j > query i.
  * Reference: tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (oracle :171-182),
  * element mask per examples/flash_attention/example_mha_fwd_bshd.py:50-53.
- * dtype: BF16 | F16; D == 128 (64 also accepted). */
+ * dtype: BF16 | F16 (q, k, v and o). D: any multiple of 8 up to 256 (tiled MFMA kernels for
+ * 128 and 64; other head dims, such as the demo programs' dim 8, run a per-query kernel). */
 int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t S,
                        int64_t H, int64_t D, int causal, float sm_scale, int dtype, void* stream);
+
+/* tlm_flash_attn_fwd with o in out_dtype (in_dtype or F32): the fp32 demo program
+ * (tpu_demo/flashattn/tpu_test_flashattn_fp32.py:14-135) multiplies fp16 copies of its fp32
+ * Q/K/V tiles and of P but keeps acc_o and the output in fp32: tlm_cast Q, K, V to F16, then
+ * this with in_dtype F16, out_dtype F32. */
+int tlm_flash_attn_fwd_mixed(const void* q, const void* k, const void* v, void* o, int64_t B,
+                             int64_t S, int64_t H, int64_t D, int causal, float sm_scale,
+                             int in_dtype, int out_dtype, void* stream);
 
 /* MLA paged decode (one query token per sequence, one shared latent KV head).
  * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,

@@ -25,7 +25,7 @@ def test_header_declares_entry_points():
     syms = declared_symbols()
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
-              "tlm_paged_gather", "tlm_kv_append_fp8"):
+              "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_mixed"):
         assert s in syms
 
 
@@ -50,8 +50,10 @@ def test_rmsnorm_rejects_null_and_dtype():
     assert L.tlm_rmsnorm(None, None, None, 4, 4, 1e-6, lib.F16, None) == -1
     assert "null" in _err()
     p = ctypes.c_void_p(0x1000)
-    assert L.tlm_rmsnorm(p, None, p, 4, 4, 1e-6, lib.F32, None) == -2
+    assert L.tlm_rmsnorm(p, None, p, 4, 4, 1e-6, lib.F8E4M3, None) == -2
     assert "dtype" in _err()
+    # fp32 rows need 4-byte alignment
+    assert L.tlm_rmsnorm(ctypes.c_void_p(0x1002), None, p, 4, 4, 1e-6, lib.F32, None) == -1
     assert L.tlm_rmsnorm(p, None, p, -1, 4, 1e-6, lib.F16, None) == -1
     assert L.tlm_rmsnorm(ctypes.c_void_p(0x1001), None, p, 4, 4, 1e-6, lib.F16, None) == -1
     assert "aligned" in _err()
@@ -66,15 +68,30 @@ def test_swiglu_rope_validation():
     assert L.tlm_swiglu(p, p, p, 8, lib.F8E4M3, None) == -2
     # zero-size is a successful no-op that never reaches HIP
     assert L.tlm_swiglu(p, p, p, 0, lib.BF16, None) == 0
+    assert L.tlm_swiglu(p, p, p, 0, lib.F32, None) == 0
+    assert L.tlm_swiglu(ctypes.c_void_p(0x1002), p, p, 8, lib.F32, None) == -1
     assert L.tlm_rope(p, p, p, p, p, None, 4, 2, 2, 128, lib.BF16, None) == -1  # k_out missing
     assert L.tlm_rope(p, None, p, p, p, None, 4, 2, 0, 127, lib.BF16, None) == -1  # odd dim
     assert L.tlm_rope(p, None, p, p, p, None, 0, 2, 0, 128, lib.BF16, None) == 0
+    assert L.tlm_rope(p, None, p, p, p, None, 0, 2, 0, 128, lib.F32, None) == 0
+    assert L.tlm_rope(p, None, p, p, p, None, 4, 2, 0, 128, lib.F8E4M3, None) == -2
+
+
+def test_cast_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_cast(None, lib.F32, p, lib.F16, 8, None) == -1
+    assert L.tlm_cast(p, lib.F32, p, lib.F16, -1, None) == -1
+    assert L.tlm_cast(p, lib.F16, p, lib.BF16, 8, None) == -2  # 16-bit <-> 16-bit
+    assert L.tlm_cast(p, lib.F32, p, lib.F32, 8, None) == -2
+    assert L.tlm_cast(ctypes.c_void_p(0x1002), lib.F32, p, lib.F16, 8, None) == -1
+    assert L.tlm_cast(p, lib.BF16, p, lib.F32, 0, None) == 0
 
 
 @pytest.mark.parametrize("args,code", [
     # null pointers
     ((None, None, None, 16, 16, 16, lib.F16, lib.F16, 0), -1),
-    # bad in dtype
+    # bad in dtype (fp32 operands are cast to 16-bit tiles by the caller, tlm_cast)
     ((0x1000, 0x1000, 0x1000, 16, 16, 16, lib.F32, lib.F16, 0), -2),
     # bad trans flag
     ((0x1000, 0x1000, 0x1000, 16, 16, 16, lib.F16, lib.F16, 2), -1),
@@ -91,9 +108,15 @@ def test_flash_attn_validation():
     L = lib.load()
     p = ctypes.c_void_p(0x1000)
     assert L.tlm_flash_attn_fwd(None, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.BF16, None) == -1
-    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 96, 0, 0.1, lib.BF16, None) == -2
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 100, 0, 0.1, lib.BF16, None) == -2  # D % 8
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 264, 0, 0.1, lib.BF16, None) == -2  # > 256
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.F32, None) == -2
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 128, 0, 0.1, lib.BF16, None) == 0
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 8, 0, 0.1, lib.BF16, None) == 0
+    mixed = L.tlm_flash_attn_fwd_mixed
+    assert mixed(p, p, p, p, 1, 0, 1, 8, 0, 0.1, lib.F16, lib.F32, None) == 0
+    assert mixed(p, p, p, p, 1, 16, 1, 8, 0, 0.1, lib.F16, lib.BF16, None) == -2
+    assert mixed(p, p, p, p, 1, 16, 1, 8, 0, 0.1, lib.F32, lib.F32, None) == -2
 
 
 def test_mla_validation_and_workspace():

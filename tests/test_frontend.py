@@ -9,6 +9,7 @@ import tilelang
 import tilelang.language as T
 from tilelang.jit.adapter.base import legalize_result_idx
 from tilelang.jit.adapter.mi355x import UnsupportedProgram
+from tilelang.jit.adapter.mi355x.recognize import recognize
 from tilelang.testing import programs
 
 
@@ -90,10 +91,46 @@ def test_unsupported_program_rejected():
 
 
 def test_unsupported_variants_have_clear_errors():
-    with pytest.raises(UnsupportedProgram, match="dtype"):
-        tilelang.compile(programs.rms_norm(64, 64, 32, dtype="float32"), out_idx=-1)
-    with pytest.raises(UnsupportedProgram, match="dtypes"):
-        tilelang.compile(programs.swi_glu(32, 32, 64, 64, dtype="float32"), out_idx=-1)
+    # fp32 matrix tiles (no cast to 16-bit tiles before ppl_gemm): no fp32-operand kernel
+    with pytest.raises(UnsupportedProgram, match="tiles"):
+        tilelang.compile(programs.matmul(64, 64, 64, 32, 32, 32, dtype="float32",
+                                         out_dtype="float32"), out_idx=-1)
+    with pytest.raises(UnsupportedProgram, match="tiles"):
+        tilelang.compile(programs.flashattn(1, 2, 4, 8, False, 2, 2, dtype="float32"),
+                         out_idx=-1)
+
+
+@pytest.mark.parametrize("name,prog,attrs", [
+    ("rmsnorm_fp32.py", lambda: programs.rms_norm(128, 512, 32, dtype="float32"),
+     dict(dtype="float32", cols=512, eps=1e-12)),
+    ("rmsnorm_splitk_fp16.py", lambda: programs.rms_norm_splitk(512, 512, 32, 32),
+     dict(dtype="float16", rows=512, cols=512)),
+    ("rmsnorm_splitk_bf16.py", lambda: programs.rms_norm_splitk(512, 512, 32, 32, "bfloat16"),
+     dict(dtype="bfloat16")),
+    ("rmsnorm_splitk_fp32.py", lambda: programs.rms_norm_splitk(512, 512, 32, 32, "float32"),
+     dict(dtype="float32")),
+    ("tpu_test_matmul_fp32.py", lambda: programs.matmul(64, 64, 64, 32, 32, 32, "float32",
+                                                        "float32", operand_dtype="float16"),
+     dict(in_dtype="float32", out_dtype="float32", operand_dtype="float16")),
+    ("tpu_test_rope_fp32.py", lambda: programs.rope(64, 16, 128, 64, dtype="float32"),
+     dict(dtype="float32", dim=64, tokens=128)),
+    ("tpu_test_rope_fp16.py", lambda: programs.rope(64, 16, 128, 64, dtype="float16"),
+     dict(dtype="float16")),
+    ("tpu_test_swiglu_fp32.py", lambda: programs.swi_glu(32, 32, 1024, 1024, dtype="float32"),
+     dict(dtype="float32", n=1024 * 1024)),
+    ("tpu_test_flashattn_fp16.py", lambda: programs.flashattn(1, 2, 4, 8, False, 2, 2,
+                                                              dtype="float16"),
+     dict(dtype="float16", D=8, S=4, operand_dtype=None)),
+    ("tpu_test_flashattn_fp32.py", lambda: programs.flashattn(1, 2, 4, 8, False, 2, 2,
+                                                              dtype="float32",
+                                                              gemm_dtype="float16"),
+     dict(dtype="float32", D=8, operand_dtype="float16")),
+])
+def test_demo_variants_recognised(name, prog, attrs):
+    """The remaining tpu_demo programs (fp32 / fp16 twins, split-K RMSNorm) map to a family."""
+    plan = recognize(prog())
+    for k, v in attrs.items():
+        assert plan.attrs[k] == v, (name, k, plan.attrs[k])
 
 
 def test_scalar_params_rejected():

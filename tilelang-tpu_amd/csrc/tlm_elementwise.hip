@@ -157,6 +157,147 @@ __global__ __launch_bounds__(kRopeThreads) void rope_scalar(
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// fp32 programs (tpu_demo/tpu_test_swiglu_fp32.py, tpu_test_rope_fp32.py, tpu_test_rope.py): the
+// same expressions on fp32 tiles, stored as fp32 (no rounding step).
+
+TLM_DEV float swiglu1(float g, float u) {
+  return u * (g * __builtin_amdgcn_rcpf(fast_exp(-g) + 1.0f));
+}
+
+__global__ __launch_bounds__(kSwiThreads) void swiglu_f32_vec(const f32x4* __restrict__ gate,
+                                                              const f32x4* __restrict__ up,
+                                                              f32x4* __restrict__ out,
+                                                              int64_t nvec) {
+  constexpr int64_t chunk = (int64_t)kSwiThreads * kSwiUnroll;
+  for (int64_t c0 = (int64_t)blockIdx.x * chunk; c0 < nvec; c0 += (int64_t)gridDim.x * chunk) {
+    f32x4 g[kSwiUnroll], u[kSwiUnroll];
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const int64_t i = c0 + k * kSwiThreads + threadIdx.x;
+      if (i < nvec) {
+        g[k] = __builtin_nontemporal_load(gate + i);
+        u[k] = __builtin_nontemporal_load(up + i);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSwiUnroll; ++k) {
+      const int64_t i = c0 + k * kSwiThreads + threadIdx.x;
+      if (i < nvec) {
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = swiglu1(g[k][j], u[k][j]);
+        __builtin_nontemporal_store(o, out + i);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSwiThreads) void swiglu_f32_scalar(const float* __restrict__ gate,
+                                                                 const float* __restrict__ up,
+                                                                 float* __restrict__ out,
+                                                                 int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kSwiThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kSwiThreads)
+    out[i] = swiglu1(gate[i], up[i]);
+}
+
+// fp32 RoPE, dim % 4 == 0: one thread per 16-byte chunk (two pairs) of a (token, head) row.
+__global__ __launch_bounds__(kRopeThreads) void rope_f32_vec(
+    const f32x4* __restrict__ q, const f32x4* __restrict__ k, const f32x4* __restrict__ cos_t,
+    const f32x4* __restrict__ sin_t, f32x4* __restrict__ q_out, f32x4* __restrict__ k_out,
+    int64_t tokens, int hq, int hk, int cpr) {
+  const int htot = hq + hk;
+  const int64_t total = tokens * htot * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * kRopeThreads + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kRopeThreads) {
+    const int c = (int)(i % cpr);
+    const int64_t row = i / cpr;
+    const int64_t t = row / htot;
+    const int h = (int)(row - t * htot);
+    const int64_t off = (h < hq ? t * hq + h : t * hk + (h - hq)) * cpr + c;
+    const f32x4 x = h < hq ? q[off] : k[off];
+    const f32x4 cv = cos_t[t * cpr + c], sv = sin_t[t * cpr + c];
+    f32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j += 2) {
+      o[j] = fmaf(x[j], cv[j], -(x[j + 1] * sv[j + 1]));
+      o[j + 1] = fmaf(x[j + 1], cv[j + 1], x[j] * sv[j]);
+    }
+    if (h < hq)
+      q_out[off] = o;
+    else
+      k_out[off] = o;
+  }
+}
+
+// fp32 RoPE, any even dim: one thread per pair.
+__global__ __launch_bounds__(kRopeThreads) void rope_f32_scalar(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float* __restrict__ q_out, float* __restrict__ k_out,
+    int64_t tokens, int hq, int hk, int dim) {
+  const int htot = hq + hk, half = dim / 2;
+  const int64_t total = tokens * htot * half;
+  for (int64_t i = (int64_t)blockIdx.x * kRopeThreads + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kRopeThreads) {
+    const int p = (int)(i % half);
+    const int64_t row = i / half;
+    const int64_t t = row / htot;
+    const int h = (int)(row - t * htot);
+    const float* src = h < hq ? q + (t * hq + h) * dim : k + (t * hk + (h - hq)) * dim;
+    float* dst = h < hq ? q_out + (t * hq + h) * dim : k_out + (t * hk + (h - hq)) * dim;
+    const float* ct = cos_t + t * dim;
+    const float* st = sin_t + t * dim;
+    const float xe = src[2 * p], xo = src[2 * p + 1];
+    dst[2 * p] = fmaf(xe, ct[2 * p], -(xo * st[2 * p + 1]));
+    dst[2 * p + 1] = fmaf(xo, ct[2 * p + 1], xe * st[2 * p]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// dtype conversion of a tile copy between global tensors (ppl_copy with differing dtypes,
+// codegen_ppl.cc:1138-1152): fp32 -> fp16 / bf16 rounds to nearest even, 16-bit -> fp32 is exact.
+
+template <int SRC, int DST>
+TLM_DEV float cast_load(const void* p, int64_t i) {
+  if constexpr (SRC == TLM_F32) return ((const float*)p)[i];
+  else return h16<SRC == TLM_BF16>::to_f32(((const uint16_t*)p)[i]);
+}
+
+template <int SRC, int DST>
+__global__ __launch_bounds__(256) void cast_scalar(const void* __restrict__ src,
+                                                   void* __restrict__ dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const float v = cast_load<SRC, DST>(src, i);
+    if constexpr (DST == TLM_F32) ((float*)dst)[i] = v;
+    else ((uint16_t*)dst)[i] = (uint16_t)h16<DST == TLM_BF16>::from_f32(v);
+  }
+}
+
+// 8 elements per thread and iteration: 2 x 16 bytes of fp32 <-> 16 bytes of 16-bit values.
+template <int SRC, int DST>
+__global__ __launch_bounds__(256) void cast_vec8(const void* __restrict__ src,
+                                                 void* __restrict__ dst, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * 256) {
+    if constexpr (SRC == TLM_F32) {
+      const f32x4 a = ((const f32x4*)src)[2 * i], b = ((const f32x4*)src)[2 * i + 1];
+      using H = h16<DST == TLM_BF16>;
+      ((u32x4*)dst)[i] = u32x4{H::pack(a[0], a[1]), H::pack(a[2], a[3]), H::pack(b[0], b[1]),
+                               H::pack(b[2], b[3])};
+    } else {
+      using H = h16<SRC == TLM_BF16>;
+      const u32x4 w = ((const u32x4*)src)[i];
+      ((f32x4*)dst)[2 * i] = f32x4{H::lo(w[0]), H::hi(w[0]), H::lo(w[1]), H::hi(w[1])};
+      ((f32x4*)dst)[2 * i + 1] = f32x4{H::lo(w[2]), H::hi(w[2]), H::lo(w[3]), H::hi(w[3])};
+    }
+  }
+}
+
+template <int SRC, int DST>
+void launch_cast(const void* src, void* dst, int64_t n, hipStream_t st);
+
 unsigned grid_for(int64_t work, int per_block, int64_t cap) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g > cap) g = cap;
@@ -195,7 +336,49 @@ int rope_dispatch(const void* q, const void* k, const void* c, const void* s, vo
   return TLM_OK;
 }
 
+template <int SRC, int DST>
+void launch_cast(const void* src, void* dst, int64_t n, hipStream_t st) {
+  if (n % 8 == 0 && tlm_aligned(src, 16) && tlm_aligned(dst, 16))
+    cast_vec8<SRC, DST><<<grid_for(n / 8, 256, 256 * 16), 256, 0, st>>>(src, dst, n / 8);
+  else
+    cast_scalar<SRC, DST><<<grid_for(n, 256, 256 * 16), 256, 0, st>>>(src, dst, n);
+}
+
 }  // namespace
+
+extern "C" int tlm_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+                        void* stream) {
+  if (!src || !dst) {
+    tlm_set_error("tlm_cast: null pointer");
+    return TLM_EINVAL;
+  }
+  if (n < 0) {
+    tlm_set_error("tlm_cast: negative size");
+    return TLM_EINVAL;
+  }
+  const bool f32_to_16 = src_dtype == TLM_F32 && (dst_dtype == TLM_F16 || dst_dtype == TLM_BF16);
+  const bool h16_to_f32 = dst_dtype == TLM_F32 && (src_dtype == TLM_F16 || src_dtype == TLM_BF16);
+  if (!f32_to_16 && !h16_to_f32) {
+    tlm_set_error("tlm_cast: %d -> %d unsupported (F32 <-> F16 / BF16)", src_dtype, dst_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  if (!tlm_aligned(src, src_dtype == TLM_F32 ? 4 : 2) ||
+      !tlm_aligned(dst, dst_dtype == TLM_F32 ? 4 : 2)) {
+    tlm_set_error("tlm_cast: pointers must be aligned to their element size");
+    return TLM_EINVAL;
+  }
+  if (n == 0) return TLM_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (f32_to_16) {
+    if (dst_dtype == TLM_F16) launch_cast<TLM_F32, TLM_F16>(src, dst, n, st);
+    else launch_cast<TLM_F32, TLM_BF16>(src, dst, n, st);
+  } else {
+    if (src_dtype == TLM_F16) launch_cast<TLM_F16, TLM_F32>(src, dst, n, st);
+    else launch_cast<TLM_BF16, TLM_F32>(src, dst, n, st);
+  }
+  TLM_LAUNCH_CHECK("tlm_cast");
+  return TLM_OK;
+}
 
 extern "C" int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                           void* stream) {
@@ -207,16 +390,27 @@ extern "C" int tlm_swiglu(const void* gate, const void* up, void* out, int64_t n
     tlm_set_error("tlm_swiglu: negative size");
     return TLM_EINVAL;
   }
-  if (!tlm_aligned(gate, 2) || !tlm_aligned(up, 2) || !tlm_aligned(out, 2)) {
-    tlm_set_error("tlm_swiglu: pointers must be 2-byte aligned");
-    return TLM_EINVAL;
-  }
-  if (dtype != TLM_F16 && dtype != TLM_BF16) {
-    tlm_set_error("tlm_swiglu: dtype %d unsupported (F16 or BF16)", dtype);
+  if (dtype != TLM_F16 && dtype != TLM_BF16 && dtype != TLM_F32) {
+    tlm_set_error("tlm_swiglu: dtype %d unsupported (F16, BF16 or F32)", dtype);
     return TLM_EUNSUPPORTED;
+  }
+  const int esz = dtype == TLM_F32 ? 4 : 2;
+  if (!tlm_aligned(gate, esz) || !tlm_aligned(up, esz) || !tlm_aligned(out, esz)) {
+    tlm_set_error("tlm_swiglu: pointers must be aligned to the element size");
+    return TLM_EINVAL;
   }
   if (n == 0) return TLM_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == TLM_F32) {
+    if (n % 4 == 0 && tlm_aligned(gate, 16) && tlm_aligned(up, 16) && tlm_aligned(out, 16))
+      swiglu_f32_vec<<<grid_for(n / 4, kSwiThreads * kSwiUnroll, 1024), kSwiThreads, 0, s>>>(
+          (const f32x4*)gate, (const f32x4*)up, (f32x4*)out, n / 4);
+    else
+      swiglu_f32_scalar<<<grid_for(n, kSwiThreads, 256 * 16), kSwiThreads, 0, s>>>(
+          (const float*)gate, (const float*)up, (float*)out, n);
+    TLM_LAUNCH_CHECK("tlm_swiglu");
+    return TLM_OK;
+  }
   const bool bf = dtype == TLM_BF16;
   if (n % 8 == 0 && tlm_aligned(gate, 16) && tlm_aligned(up, 16) && tlm_aligned(out, 16)) {
     const int64_t nvec = n / 8;
@@ -259,17 +453,36 @@ extern "C" int tlm_rope(const void* q, const void* k, const void* cos_t, const v
                   (long long)tokens, (long long)heads_q, (long long)heads_k, (long long)dim);
     return TLM_EINVAL;
   }
-  if (!tlm_aligned(q, 2) || !tlm_aligned(cos_t, 2) || !tlm_aligned(sin_t, 2) ||
-      !tlm_aligned(q_out, 2) || (k && (!tlm_aligned(k, 2) || !tlm_aligned(k_out, 2)))) {
-    tlm_set_error("tlm_rope: pointers must be 2-byte aligned");
-    return TLM_EINVAL;
-  }
-  if (dtype != TLM_F16 && dtype != TLM_BF16) {
-    tlm_set_error("tlm_rope: dtype %d unsupported (F16 or BF16)", dtype);
+  if (dtype != TLM_F16 && dtype != TLM_BF16 && dtype != TLM_F32) {
+    tlm_set_error("tlm_rope: dtype %d unsupported (F16, BF16 or F32)", dtype);
     return TLM_EUNSUPPORTED;
+  }
+  const int esz = dtype == TLM_F32 ? 4 : 2;
+  if (!tlm_aligned(q, esz) || !tlm_aligned(cos_t, esz) || !tlm_aligned(sin_t, esz) ||
+      !tlm_aligned(q_out, esz) || (k && (!tlm_aligned(k, esz) || !tlm_aligned(k_out, esz)))) {
+    tlm_set_error("tlm_rope: pointers must be aligned to the element size");
+    return TLM_EINVAL;
   }
   if (tokens == 0) return TLM_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == TLM_F32) {
+    const bool vec = dim % 4 == 0 && tlm_aligned(q, 16) && tlm_aligned(q_out, 16) &&
+                     tlm_aligned(cos_t, 16) && tlm_aligned(sin_t, 16) &&
+                     (!k || (tlm_aligned(k, 16) && tlm_aligned(k_out, 16)));
+    if (vec) {
+      const int64_t total = tokens * (heads_q + heads_k) * (dim / 4);
+      rope_f32_vec<<<grid_for(total, kRopeThreads, 1 << 20), kRopeThreads, 0, s>>>(
+          (const f32x4*)q, (const f32x4*)k, (const f32x4*)cos_t, (const f32x4*)sin_t,
+          (f32x4*)q_out, (f32x4*)k_out, tokens, (int)heads_q, (int)heads_k, (int)(dim / 4));
+    } else {
+      const int64_t total = tokens * (heads_q + heads_k) * (dim / 2);
+      rope_f32_scalar<<<grid_for(total, kRopeThreads, 1 << 20), kRopeThreads, 0, s>>>(
+          (const float*)q, (const float*)k, (const float*)cos_t, (const float*)sin_t,
+          (float*)q_out, (float*)k_out, tokens, (int)heads_q, (int)heads_k, (int)dim);
+    }
+    TLM_LAUNCH_CHECK("tlm_rope");
+    return TLM_OK;
+  }
   return dtype == TLM_BF16
              ? rope_dispatch<true>(q, k, cos_t, sin_t, q_out, k_out, tokens, (int)heads_q,
                                    (int)heads_k, (int)dim, s)

@@ -343,11 +343,11 @@ TLM_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool OUT32>
 __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__ Q,
                                                    const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ V,
-                                                   uint16_t* __restrict__ O, int B, int S, int H,
+                                                   void* __restrict__ O, int B, int S, int H,
                                                    float sc) {
   using MT = fa_mma<BF16>;
   using v8 = typename MT::v8;
@@ -611,6 +611,19 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   // ---- epilogue: lane holds O^T[d = 32 dt + 8 (i / 4) + 4 g + i % 4][query my_q]
   const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  if constexpr (OUT32) {  // fp32 output (fp32 programs): 16-byte stores straight from registers
+    float* Of = (float*)O + head;
+    if (my_q < S) {
+#pragma unroll
+      for (int dt = 0; dt < PP_D / 32; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *(f32x4*)(Of + (int64_t)my_q * rs + 32 * dt + 8 * r4 + 4 * g) =
+              f32x4{oacc[dt][4 * r4] * inv, oacc[dt][4 * r4 + 1] * inv,
+                    oacc[dt][4 * r4 + 2] * inv, oacc[dt][4 * r4 + 3] * inv};
+    }
+    return;
+  }
   uint16_t* stage = (uint16_t*)smem + wave * 32 * PP_OP;  // [32 queries][PP_OP]
 #pragma unroll
   for (int dt = 0; dt < PP_D / 32; ++dt)
@@ -623,7 +636,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  uint16_t* Ob = O + head;
+  uint16_t* Ob = (uint16_t*)O + head;
 #pragma unroll
   for (int it = 0; it < 32 * (PP_D / 8) / 64; ++it) {
     const int idx = lane + 64 * it;
@@ -633,7 +646,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   }
 }
 
-template <bool BF16, bool CAUSAL>
+template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
               float sc, hipStream_t st) {
   const int64_t nwg = (int64_t)((S + PP_BQ - 1) / PP_BQ) * B * H;
@@ -641,8 +654,8 @@ int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
-  fa_fwd_pp<BF16, CAUSAL><<<(unsigned)nwg, 512, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, sc);
+  fa_fwd_pp<BF16, CAUSAL, OUT32><<<(unsigned)nwg, 512, 0, st>>>(
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, sc);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
@@ -661,21 +674,133 @@ int launch(const void* q, const void* k, const void* v, void* o, int B, int S, i
   return TLM_OK;
 }
 
-template <bool BF16>
+// ---- any head dim (multiple of 8, <= 256): the demo programs' own shapes (dim 8) and head dims
+// without a tiled kernel. One query per lane with q and O in registers; key and value rows are
+// read with wave-uniform addresses; per key the online softmax of the reference (m = running
+// max, alpha = 2^(m_prev - m), P = 2^(s sc - m) rounded to the input type before P V, l from
+// the fp32 P). No MFMA: for shapes far too small to fill matrix tiles.
+template <bool BF16, bool CAUSAL, bool OUT32, int DC>  // DC = capacity in 8-element chunks
+__global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict__ Q,
+                                                      const uint16_t* __restrict__ K,
+                                                      const uint16_t* __restrict__ V,
+                                                      void* __restrict__ O, int S, int H, int D,
+                                                      float sc) {
+  using HH = h16<BF16>;
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  const int nc = D / 8;
+  const int64_t rs = (int64_t)H * D;
+  const int64_t head = ((int64_t)b * S * H + h) * D;
+  u32x4 qv[DC];
+  float o[DC][8];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    qv[c] = u32x4{0, 0, 0, 0};
+    if (c < nc && q < S) qv[c] = *(const u32x4*)(Q + head + (int64_t)q * rs + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  // keys of the wave: causal stops after the wave's last query (wave-uniform bound)
+  const int wq_last = min(S - 1, (int)(blockIdx.x * 256 + (threadIdx.x & ~63) + 63));
+  const int kend = CAUSAL ? wq_last + 1 : S;
+  for (int j = 0; j < kend; ++j) {
+    const uint16_t* kr = K + head + (int64_t)j * rs;
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c < nc) {
+        const u32x4 kc = *(const u32x4*)(kr + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = fmaf(HH::lo(qv[c][e]), HH::lo(kc[e]), s);
+          s = fmaf(HH::hi(qv[c][e]), HH::hi(kc[e]), s);
+        }
+      }
+    }
+    s *= sc;
+    if (CAUSAL && j > q) s = -INFINITY;
+    const float m_new = fmaxf(m, s);
+    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+    const float p = m_new == -INFINITY ? 0.f : fast_exp2(s - m_new);
+    const float pr = HH::to_f32(HH::from_f32(p));
+    l = fmaf(l, alpha, p);
+    m = m_new;
+    const uint16_t* vr = V + head + (int64_t)j * rs;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c < nc) {
+        const u32x4 vc = *(const u32x4*)(vr + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[c][2 * e] = fmaf(o[c][2 * e], alpha, pr * HH::lo(vc[e]));
+          o[c][2 * e + 1] = fmaf(o[c][2 * e + 1], alpha, pr * HH::hi(vc[e]));
+        }
+      }
+    }
+  }
+  if (q >= S) return;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    if (c < nc) {
+      const int64_t off = head + (int64_t)q * rs + 8 * c;
+      if constexpr (OUT32) {
+        float* Of = (float*)O + off;
+        *(f32x4*)Of = f32x4{o[c][0] * inv, o[c][1] * inv, o[c][2] * inv, o[c][3] * inv};
+        *(f32x4*)(Of + 4) = f32x4{o[c][4] * inv, o[c][5] * inv, o[c][6] * inv, o[c][7] * inv};
+      } else {
+        *(u32x4*)((uint16_t*)O + off) =
+            u32x4{HH::pack(o[c][0] * inv, o[c][1] * inv), HH::pack(o[c][2] * inv, o[c][3] * inv),
+                  HH::pack(o[c][4] * inv, o[c][5] * inv), HH::pack(o[c][6] * inv, o[c][7] * inv)};
+      }
+    }
+  }
+}
+
+template <bool BF16, bool CAUSAL, bool OUT32>
+int launch_generic(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
+                   int D, float sc, hipStream_t st) {
+  if ((int64_t)B * H > 65535) {
+    tlm_set_error("tlm_flash_attn_fwd: head dim %d needs batch * heads <= 65535", D);
+    return TLM_EUNSUPPORTED;
+  }
+  const dim3 grid((unsigned)((S + 255) / 256), (unsigned)(B * H));
+  auto go = [&](auto kern) {
+    kern<<<grid, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, S,
+                               H, D, sc);
+  };
+  if (D <= 16)
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 2>);
+  else if (D <= 64)
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 8>);
+  else if (D <= 128)
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 16>);
+  else
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 32>);
+  TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
+  return TLM_OK;
+}
+
+template <bool BF16, bool OUT32>
 int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int D,
              bool causal, float sc, hipStream_t st) {
   if (D == 128)
-    return causal ? launch_pp<BF16, true>(q, k, v, o, B, S, H, sc, st)
-                  : launch_pp<BF16, false>(q, k, v, o, B, S, H, sc, st);
-  return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, sc, st)
-                : launch<BF16, false, 64>(q, k, v, o, B, S, H, sc, st);
+    return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, sc, st)
+                  : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, sc, st);
+  if (D == 64 && !OUT32)
+    return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, sc, st)
+                  : launch<BF16, false, 64>(q, k, v, o, B, S, H, sc, st);
+  return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, D, sc, st)
+                : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, D, sc, st);
 }
 
 }  // namespace
 
-extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
-                                  int64_t B, int64_t S, int64_t H, int64_t D, int causal,
-                                  float sm_scale, int dtype, void* stream) {
+extern "C" int tlm_flash_attn_fwd_mixed(const void* q, const void* k, const void* v, void* o,
+                                        int64_t B, int64_t S, int64_t H, int64_t D, int causal,
+                                        float sm_scale, int in_dtype, int out_dtype,
+                                        void* stream) {
   if (!q || !k || !v || !o) {
     tlm_set_error("tlm_flash_attn_fwd: null pointer argument");
     return TLM_EINVAL;
@@ -684,12 +809,18 @@ extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, v
     tlm_set_error("tlm_flash_attn_fwd: bad shape");
     return TLM_EINVAL;
   }
-  if (D != 128 && D != 64) {
-    tlm_set_error("tlm_flash_attn_fwd: head dim %lld unsupported (64 or 128)", (long long)D);
+  if (D <= 0 || D > 256 || D % 8 != 0) {
+    tlm_set_error("tlm_flash_attn_fwd: head dim %lld unsupported (a multiple of 8, at most 256)",
+                  (long long)D);
     return TLM_EUNSUPPORTED;
   }
-  if (dtype != TLM_BF16 && dtype != TLM_F16) {
-    tlm_set_error("tlm_flash_attn_fwd: dtype %d unsupported (BF16 or F16)", dtype);
+  if (in_dtype != TLM_BF16 && in_dtype != TLM_F16) {
+    tlm_set_error("tlm_flash_attn_fwd: dtype %d unsupported (BF16 or F16)", in_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  if (out_dtype != in_dtype && out_dtype != TLM_F32) {
+    tlm_set_error("tlm_flash_attn_fwd: output dtype %d unsupported (the input dtype or F32)",
+                  out_dtype);
     return TLM_EUNSUPPORTED;
   }
   if (!(sm_scale > 0.f) || !__builtin_isfinite(sm_scale)) {
@@ -703,8 +834,18 @@ extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, v
   if (B == 0 || S == 0 || H == 0) return TLM_OK;
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
   hipStream_t st = (hipStream_t)stream;
-  return dtype == TLM_BF16 ? by_shape<true>(q, k, v, o, (int)B, (int)S, (int)H, (int)D,
-                                            causal != 0, sc, st)
-                           : by_shape<false>(q, k, v, o, (int)B, (int)S, (int)H, (int)D,
-                                             causal != 0, sc, st);
+  const bool bf = in_dtype == TLM_BF16, f32o = out_dtype == TLM_F32;
+  const int b = (int)B, s = (int)S, h = (int)H, d = (int)D;
+  const bool c = causal != 0;
+  if (bf)
+    return f32o ? by_shape<true, true>(q, k, v, o, b, s, h, d, c, sc, st)
+                : by_shape<true, false>(q, k, v, o, b, s, h, d, c, sc, st);
+  return f32o ? by_shape<false, true>(q, k, v, o, b, s, h, d, c, sc, st)
+              : by_shape<false, false>(q, k, v, o, b, s, h, d, c, sc, st);
+}
+
+extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                                  int64_t B, int64_t S, int64_t H, int64_t D, int causal,
+                                  float sm_scale, int dtype, void* stream) {
+  return tlm_flash_attn_fwd_mixed(q, k, v, o, B, S, H, D, causal, sm_scale, dtype, dtype, stream);
 }

@@ -5,9 +5,14 @@
 //   s = s * (1/N) + eps; r = rsqrt(s) (ppl_rsqrt); y = cast(x32 * r)   (ppl_copy with cast, RNE).
 // The optional weight w (fp16/bf16 [cols]) is applied in fp32 before the single rounding.
 //
-// Layout: x, y [rows, cols] row-major 16-bit. Each lane keeps its slice of the row in VGPRs
-// (cols/512 16-byte vectors per lane), so x is read exactly once and y written once:
-// algorithmic traffic = 2*rows*cols*2 + cols*2 bytes. No MFMA: the sum of squares reduces with
+// fp32 programs (tpu_demo/rms_norm/rmsnorm_fp32.py, rmsnorm_splitk_fp32.py) compute the same
+// expression on fp32 tiles and store fp32 (no rounding step); the split-K programs
+// (rmsnorm_splitk_fp16.py:9-47) accumulate the same row sum over column blocks, so they map to
+// the same kernels.
+//
+// Layout: x, y [rows, cols] row-major 16-bit or fp32. Each lane keeps its slice of the row in
+// VGPRs (cols/512 or cols/256 16-byte vectors per lane), so x is read exactly once and y written
+// once: algorithmic traffic = 2*rows*cols*esize + cols*esize bytes. No MFMA: the sum of squares reduces with
 // xor-shuffles across the wavefront.
 #include "tlm_common.h"
 
@@ -85,6 +90,90 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void rmsnorm_row_generic(
   }
 }
 
+// fp32 rows: VPL 16-byte vectors (4 floats) per lane, cols == 256*VPL; row kept in VGPRs.
+template <int VPL, bool HAS_W>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void rmsnorm_f32_regs(
+    const f32x4* __restrict__ x, const f32x4* __restrict__ w, f32x4* __restrict__ y,
+    int64_t rows, float inv_cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const f32x4* xr = x + row * (64 * VPL);
+  f32x4* yr = y + row * (64 * VPL);
+  f32x4 v[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) v[i] = xr[i * 64 + lane];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+  ss = wave_sum(ss);
+  const float r = __frsqrt_rn(ss * inv_cols + eps);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    f32x4 o;
+    if constexpr (HAS_W) {
+      const f32x4 wv = w[i * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = v[i][j] * r * wv[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = v[i][j] * r;
+    }
+    __builtin_nontemporal_store(o, yr + i * 64 + lane);
+  }
+}
+
+__global__ __launch_bounds__(64 * kWavesPerBlock) void rmsnorm_f32_generic(
+    const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y, int64_t rows,
+    int64_t cols, float inv_cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * cols;
+  float* yr = y + row * cols;
+  float ss = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) ss = fmaf(xr[c], xr[c], ss);
+  ss = wave_sum(ss);
+  const float r = __frsqrt_rn(ss * inv_cols + eps);
+  for (int64_t c = lane; c < cols; c += 64) yr[c] = w ? xr[c] * r * w[c] : xr[c] * r;
+}
+
+template <int VPL>
+void launch_f32_regs(const void* x, const void* w, void* y, int64_t rows, float inv, float eps,
+                     hipStream_t s, dim3 grid, dim3 block) {
+  if (w)
+    rmsnorm_f32_regs<VPL, true><<<grid, block, 0, s>>>((const f32x4*)x, (const f32x4*)w,
+                                                       (f32x4*)y, rows, inv, eps);
+  else
+    rmsnorm_f32_regs<VPL, false><<<grid, block, 0, s>>>((const f32x4*)x, nullptr, (f32x4*)y,
+                                                        rows, inv, eps);
+}
+
+int dispatch_f32(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
+                 hipStream_t s) {
+  const float inv = 1.0f / (float)cols;
+  dim3 block(64 * kWavesPerBlock);
+  dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock));
+  const bool vec_ok = tlm_aligned(x, 16) && tlm_aligned(y, 16) && (!w || tlm_aligned(w, 16));
+  const int64_t vpl = cols / 256;
+  if (vec_ok && cols % 256 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8 || vpl == 16)) {
+    switch (vpl) {
+      case 1: launch_f32_regs<1>(x, w, y, rows, inv, eps, s, grid, block); break;
+      case 2: launch_f32_regs<2>(x, w, y, rows, inv, eps, s, grid, block); break;
+      case 4: launch_f32_regs<4>(x, w, y, rows, inv, eps, s, grid, block); break;
+      case 8: launch_f32_regs<8>(x, w, y, rows, inv, eps, s, grid, block); break;
+      default: launch_f32_regs<16>(x, w, y, rows, inv, eps, s, grid, block); break;
+    }
+  } else {
+    rmsnorm_f32_generic<<<grid, block, 0, s>>>((const float*)x, (const float*)w, (float*)y, rows,
+                                               cols, inv, eps);
+  }
+  TLM_LAUNCH_CHECK("tlm_rmsnorm");
+  return TLM_OK;
+}
+
 template <bool IS_BF16, int VPL>
 void launch_regs(const void* x, const void* w, void* y, int64_t rows, float inv, float eps,
                  hipStream_t s, dim3 grid, dim3 block) {
@@ -134,20 +223,22 @@ extern "C" int tlm_rmsnorm(const void* x, const void* w, void* y, int64_t rows, 
     tlm_set_error("tlm_rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
     return TLM_EINVAL;
   }
-  if (!tlm_aligned(x, 2) || !tlm_aligned(y, 2) || (w && !tlm_aligned(w, 2))) {
-    tlm_set_error("tlm_rmsnorm: pointers must be 2-byte aligned");
+  const int esz = dtype == TLM_F32 ? 4 : 2;
+  if (!tlm_aligned(x, esz) || !tlm_aligned(y, esz) || (w && !tlm_aligned(w, esz))) {
+    tlm_set_error("tlm_rmsnorm: pointers must be aligned to the element size");
     return TLM_EINVAL;
   }
   if (!(eps >= 0.f)) {
     tlm_set_error("tlm_rmsnorm: eps must be >= 0");
     return TLM_EINVAL;
   }
-  if (dtype != TLM_F16 && dtype != TLM_BF16) {
-    tlm_set_error("tlm_rmsnorm: dtype %d unsupported (F16 or BF16)", dtype);
+  if (dtype != TLM_F16 && dtype != TLM_BF16 && dtype != TLM_F32) {
+    tlm_set_error("tlm_rmsnorm: dtype %d unsupported (F16, BF16 or F32)", dtype);
     return TLM_EUNSUPPORTED;
   }
   if (rows == 0) return TLM_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == TLM_F32) return dispatch_f32(x, w, y, rows, cols, eps, s);
   return dtype == TLM_BF16 ? dispatch<true>(x, w, y, rows, cols, eps, s)
                            : dispatch<false>(x, w, y, rows, cols, eps, s);
 }

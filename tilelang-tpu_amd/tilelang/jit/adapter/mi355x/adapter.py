@@ -18,9 +18,13 @@ from ..base import BaseKernelAdapter
 from . import ops
 
 
+_TORCH_DT = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+
+
 def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     a = plan.attrs
     f = plan.family
+    odt = _TORCH_DT.get(a.get("operand_dtype"))  # fp32 programs with 16-bit matrix tiles
     if f == "rmsnorm":
         w = None if a["w"] is None else t[a["w"]]
         ops.rmsnorm(t[a["x"]], w, t[a["y"]], a["eps"])
@@ -31,9 +35,10 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
         ko = None if a["k_out"] is None else t[a["k_out"]]
         ops.rope(t[a["q"]], t[a["cos"]], t[a["sin"]], t[a["q_out"]], k, ko)
     elif f == "gemm":
-        ops.gemm(t[a["a"]], t[a["b"]], t[a["c"]], a["trans_b"])
+        ops.gemm(t[a["a"]], t[a["b"]], t[a["c"]], a["trans_b"], operand_dtype=odt)
     elif f == "flashattn":
-        ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"])
+        ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"],
+                           operand_dtype=odt)
     elif f == "mla":
         q = t[a["q"]]
         dev = q.device

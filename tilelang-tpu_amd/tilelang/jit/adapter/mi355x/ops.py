@@ -105,9 +105,35 @@ def rope(q: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, q_out: torch.Ten
     return q_out
 
 
-def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = False):
-    """c = a @ b (trans_b=False, b [K,N]) or a @ b.T (trans_b=True, b [N,K]); fp32 accumulate."""
+def cast(src: torch.Tensor, dst: torch.Tensor):
+    """dst = src converted elementwise (fp32 -> fp16/bf16 round-to-nearest-even, 16-bit -> fp32
+    exact): the cast of a ppl_copy between tiles of different dtypes."""
+    dev = _dev(src, dst)
+    _contig("src", src)
+    _contig("dst", dst)
+    if src.numel() != dst.numel():
+        raise ValueError("src and dst must have the same number of elements")
+    lib.call("tlm_cast", _ptr(src), dtype_code(src.dtype), _ptr(dst), dtype_code(dst.dtype),
+             src.numel(), _stream(dev))
+    return dst
+
+
+def _as_operand(t: torch.Tensor, dt: Optional[torch.dtype]) -> torch.Tensor:
+    """t itself, or a device copy rounded to the matrix-operand dtype dt (fp32 programs that copy
+    their tiles to fp16 before ppl_gemm); the copy is made by the tlm_cast kernel."""
+    if dt is None or t.dtype == dt:
+        return t
+    out = torch.empty(t.shape, dtype=dt, device=t.device)
+    return cast(t, out)
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = False,
+         operand_dtype: Optional[torch.dtype] = None):
+    """c = a @ b (trans_b=False, b [K,N]) or a @ b.T (trans_b=True, b [N,K]); fp32 accumulate.
+    operand_dtype: fp32 a/b are first rounded to this 16-bit type."""
     dev = _dev(a, b, c)
+    a = _as_operand(a, operand_dtype)
+    b = _as_operand(b, operand_dtype)
     for n, t in (("A", a), ("B", b), ("C", c)):
         _contig(n, t)
     M, K = a.shape
@@ -122,18 +148,24 @@ def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = Fals
     return c
 
 
-def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float):
-    """BSHD attention forward: q,k,v,o [B, S, H, D]."""
+def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float,
+                   operand_dtype: Optional[torch.dtype] = None):
+    """BSHD attention forward: q,k,v,o [B, S, H, D]. o may be fp32 with 16-bit q/k/v;
+    operand_dtype: fp32 q/k/v are first rounded to this 16-bit type (the fp32 program)."""
     dev = _dev(q, k, v, o)
     for n, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
         _contig(n, t)
     if not (q.shape == k.shape == v.shape == o.shape):
         raise ValueError("Q, K, V and O must share the [B, S, H, D] shape")
-    if not (q.dtype == k.dtype == v.dtype == o.dtype):
-        raise ValueError("Q, K, V and O must share a dtype")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("Q, K and V must share a dtype")
+    q, k, v = (_as_operand(t, operand_dtype) for t in (q, k, v))
+    if o.dtype not in (q.dtype, torch.float32):
+        raise ValueError(f"O must be {q.dtype} or float32")
     B, S, H, D = q.shape
-    lib.call("tlm_flash_attn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, S, H, D,
-             1 if causal else 0, float(sm_scale), dtype_code(q.dtype), _stream(dev))
+    lib.call("tlm_flash_attn_fwd_mixed", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, S, H, D,
+             1 if causal else 0, float(sm_scale), dtype_code(q.dtype), dtype_code(o.dtype),
+             _stream(dev))
     return o
 
 

@@ -8,12 +8,17 @@ of the program, and anything that does not fit a family is rejected with a clear
 no generic code generation and no fallback.
 
 Families and the reference programs they accept:
-  rmsnorm  tpu_demo/rms_norm/rms_norm_fp16.py:9-35 (+ bf16 twin; optional weight parameter)
-  gemm     tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31 (+ bf16 / fp32-out variants)
-  rope     tpu_demo/tpu_test_rope_bf16.py:5-51 (4 params) and a fused q+k form (6 params)
-  swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54
-  flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 and the upstream
-           examples/flash_attention/example_mha_fwd_bshd.py:30-151 structure
+  rmsnorm  tpu_demo/rms_norm/rms_norm_fp16.py:9-35 (+ bf16 and fp32 twins, rmsnorm_fp32.py;
+           optional weight parameter) and the split-K programs rmsnorm_splitk_{fp16,bf16,
+           fp32}.py:9-47 (row sum accumulated over column blocks)
+  gemm     tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31 (+ bf16 / fp32-out variants, and
+           tpu_test_matmul_fp32.py: fp32 A/B copied to fp16 tiles before ppl_gemm)
+  rope     tpu_demo/tpu_test_rope_bf16.py:5-51 (4 params; fp16 / fp32 twins and tpu_test_rope.py)
+           and a fused q+k form (6 params)
+  swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54 (+ tpu_test_swiglu_fp32.py)
+  flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, and fp32 with fp16
+           matrix tiles) and the upstream examples/flash_attention/example_mha_fwd_bshd.py:30-151
+           structure
   mla      examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split and no-split forms),
            with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV
 """
@@ -148,6 +153,13 @@ def _rmsnorm(pf, names) -> Plan:
         _fail(fam, "expected one row reduce_sum over the last dim")
     acc = _buf(red[0].args[1])
     sq = _buf(red[0].args[0])
+    # split-K programs add each block's row sum into a running sum: follow that accumulation
+    for op in _ops(pf, ("ppl_add",)):
+        srcs = (_buf(op.args[1]), _buf(op.args[2]))
+        dst = _buf(op.args[0])
+        if acc in srcs and dst is not acc and dst in srcs:
+            acc = dst
+            break
     # eps and 1/N applied to the reduced buffer
     eps = None
     inv = None
@@ -173,8 +185,8 @@ def _rmsnorm(pf, names) -> Plan:
     N = _shape(x)[-1]
     if abs(inv * N - 1.0) > 1e-6:
         _fail(fam, f"mean scale {inv} is not 1/{N}")
-    if x.dtype not in ("float16", "bfloat16"):
-        _fail(fam, f"dtype {x.dtype} (float16/bfloat16 kernels only)")
+    if x.dtype not in ("float16", "bfloat16", "float32"):
+        _fail(fam, f"dtype {x.dtype} (float16 / bfloat16 / float32 kernels only)")
     w = None
     for p in pf.params:
         if p is x or p is y:
@@ -208,8 +220,9 @@ def _swiglu(pf, names) -> Plan:
     out = writes[0]
     if not (_shape(gate) == _shape(up) == _shape(out)):
         _fail(fam, "gate, up, out shapes differ")
-    if not (gate.dtype == up.dtype == out.dtype) or gate.dtype not in ("bfloat16", "float16"):
-        _fail(fam, "dtypes must all be bfloat16 or all float16")
+    if not (gate.dtype == up.dtype == out.dtype) or gate.dtype not in ("bfloat16", "float16",
+                                                                       "float32"):
+        _fail(fam, "dtypes must all be bfloat16, all float16 or all float32")
     return Plan(fam, pf.params, [_index(pf, out)], dict(
         gate=_index(pf, gate), up=_index(pf, up), out=_index(pf, out),
         n=math.prod(_shape(gate)), dtype=gate.dtype))
@@ -243,8 +256,8 @@ def _rope(pf, names) -> Plan:
     else:
         _fail(fam, "expected (x, cos, sin, out) or (q, k, cos, sin, q_out, k_out)")
     dts = {p.dtype for p in pf.params}
-    if len(dts) != 1 or next(iter(dts)) not in ("bfloat16", "float16"):
-        _fail(fam, f"all parameters must be bfloat16 or all float16, got {dts}")
+    if len(dts) != 1 or next(iter(dts)) not in ("bfloat16", "float16", "float32"):
+        _fail(fam, f"all parameters must share one of bfloat16 / float16 / float32, got {dts}")
     if attrs["dim"] % 2:
         _fail(fam, "dim must be even")
     attrs["dtype"] = next(iter(dts))
@@ -271,13 +284,20 @@ def _gemm(pf, names) -> Plan:
         Kb, N = _shape(B)
     if Kb != K or _shape(C) != (M, N):
         _fail(fam, f"shapes A{_shape(A)} B{_shape(B)} C{_shape(C)} do not chain")
-    if A.dtype != B.dtype or A.dtype not in ("float16", "bfloat16"):
-        _fail(fam, "A and B must both be float16 or both bfloat16")
+    # dtype of the tiles the gemm multiplies (fp32 programs copy their tiles to fp16 first)
+    ta_dt, tb_dt = _buf(g[0].args[0]).dtype, _buf(g[0].args[1]).dtype
+    if ta_dt != tb_dt or ta_dt not in ("float16", "bfloat16"):
+        _fail(fam, f"matrix tiles must both be float16 or both bfloat16 (got {ta_dt}, {tb_dt})")
+    if A.dtype != B.dtype or A.dtype not in ("float16", "bfloat16", "float32"):
+        _fail(fam, "A and B must share a dtype: float16, bfloat16, or float32 cast to the tiles")
+    if A.dtype != "float32" and A.dtype != ta_dt:
+        _fail(fam, f"A is {A.dtype} but the gemm multiplies {ta_dt} tiles")
     if C.dtype not in ("float16", "bfloat16", "float32"):
         _fail(fam, f"C dtype {C.dtype}")
     return Plan(fam, pf.params, [_index(pf, C)], dict(
         a=_index(pf, A), b=_index(pf, B), c=_index(pf, C), M=M, N=N, K=K, trans_b=bool(tb),
-        in_dtype=A.dtype, out_dtype=C.dtype))
+        in_dtype=A.dtype, out_dtype=C.dtype,
+        operand_dtype=ta_dt if A.dtype == "float32" else None))
 
 
 def _pipelined_extents(pf):
@@ -302,8 +322,16 @@ def _flashattn(pf, names) -> Plan:
     shp = _shape(Q)
     if len(shp) != 4 or not (shp == _shape(K) == _shape(V) == _shape(O)):
         _fail(fam, "Q, K, V, Output must share a [batch, seq, heads, dim] shape")
-    if not (Q.dtype == K.dtype == V.dtype == O.dtype) or Q.dtype not in ("bfloat16", "float16"):
-        _fail(fam, "dtypes must all be bfloat16 or all float16")
+    # tiles the two gemms multiply: the fp32 program copies Q, K, V and P to fp16 tiles first
+    tile_dts = {_buf(qk[0].args[0]).dtype, _buf(qk[0].args[1]).dtype, _buf(pv[0].args[0]).dtype,
+                _buf(pv[0].args[1]).dtype}
+    if len(tile_dts) != 1 or next(iter(tile_dts)) not in ("bfloat16", "float16"):
+        _fail(fam, f"the gemm tiles must all be bfloat16 or all float16, got {tile_dts}")
+    tile_dt = next(iter(tile_dts))
+    if not (Q.dtype == K.dtype == V.dtype == O.dtype):
+        _fail(fam, "Q, K, V and Output must share a dtype")
+    if Q.dtype not in (tile_dt, "float32"):
+        _fail(fam, f"parameters are {Q.dtype} but the gemms multiply {tile_dt} tiles")
     B, S, H, D = shp
     # causal: the KV loop is truncated at the diagonal (T.min(...) in the extent), or scores
     # are masked by comparing query and key positions.
@@ -334,7 +362,8 @@ def _flashattn(pf, names) -> Plan:
             _fail(fam, "could not read the softmax scale")
     return Plan(fam, pf.params, [_index(pf, O)], dict(
         q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H, D=D,
-        causal=causal, sm_scale=sm_scale, dtype=Q.dtype))
+        causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
+        operand_dtype=tile_dt if Q.dtype == "float32" else None))
 
 
 def _page_size_from_trace(pf, bt: Buffer) -> Optional[int]:

@@ -13,16 +13,20 @@ import tilelang.language as T
 
 
 def rms_norm(M, N, blk_m, dtype="float16", eps=1e-12, with_weight=False):
+    """rms_norm_fp16.py:9-35 (bf16 twin); dtype float32 gives rmsnorm_fp32.py, which squares and
+    scales the fp32 tile directly (no cast copies)."""
     rN = 1.0 / N
+    f32 = dtype == "float32"
 
     def body(A, W, B):
         with T.Kernel(T.ceildiv(M, blk_m), is_cpu=True) as (bx,):
             x_tile = T.alloc_shared((blk_m, N), dtype)
-            x32 = T.alloc_shared((blk_m, N), "float32")
+            x32 = x_tile if f32 else T.alloc_shared((blk_m, N), "float32")
             sq = T.alloc_shared((blk_m, N), "float32")
             ssum = T.alloc_shared((blk_m, 1), "float32")
             T.ppl_copy(A[bx * blk_m, 0], x_tile)
-            T.ppl_copy(x_tile, x32)
+            if not f32:
+                T.ppl_copy(x_tile, x32)
             T.ppl_mul(sq, x32, x32)
             T.ppl_reduce_sum(sq, ssum, dim=1)
             T.ppl_mul_C(ssum, ssum, T.float32(rN))
@@ -31,11 +35,13 @@ def rms_norm(M, N, blk_m, dtype="float16", eps=1e-12, with_weight=False):
             T.ppl_mul(x32, x32, ssum)
             if W is not None:
                 w_tile = T.alloc_shared((1, N), dtype)
-                w32 = T.alloc_shared((1, N), "float32")
+                w32 = w_tile if f32 else T.alloc_shared((1, N), "float32")
                 T.ppl_copy(W[0], w_tile)
-                T.ppl_copy(w_tile, w32)
+                if not f32:
+                    T.ppl_copy(w_tile, w32)
                 T.ppl_mul(x32, x32, w32)
-            T.ppl_copy(x32, x_tile)
+            if not f32:
+                T.ppl_copy(x32, x_tile)
             T.ppl_copy(x_tile, B[bx * blk_m, 0])
 
     if with_weight:
@@ -54,10 +60,52 @@ def rms_norm(M, N, blk_m, dtype="float16", eps=1e-12, with_weight=False):
     return rmsnorm
 
 
+def rms_norm_splitk(M, N, blk_m, blk_k, dtype="float16", eps=1e-12):
+    """rmsnorm_splitk_fp16.py:9-47 (bf16 / fp32 twins): the row sum of squares accumulated over
+    column blocks of blk_k, then a second pass over the blocks scales them."""
+    rN = 1.0 / N
+    f32 = dtype == "float32"
+
+    @T.prim_func
+    def rmsnorm_splitk(A: T.Tensor((M, N), dtype), B: T.Tensor((M, N), dtype)):
+        with T.Kernel(T.ceildiv(M, blk_m), is_cpu=True) as (bx,):
+            a_s = T.alloc_shared((blk_m, blk_k), dtype)
+            a32 = a_s if f32 else T.alloc_shared((blk_m, blk_k), "float32")
+            sq = T.alloc_shared((blk_m, blk_k), "float32")
+            powsum = T.alloc_shared((blk_m, 1), "float32")
+            tmp = T.alloc_shared((blk_m, 1), "float32")
+            T.ppl_fill(powsum, T.float32(0.0))
+            nk = T.ceildiv(N, blk_k)
+            for k in T.Pipelined(nk, num_stages=0):
+                T.ppl_copy(A[bx * blk_m, k * blk_k], a_s)
+                if not f32:
+                    T.ppl_copy(a_s, a32)
+                T.ppl_mul(sq, a32, a32)
+                T.ppl_reduce_sum(sq, tmp, dim=1)
+                T.ppl_add(powsum, powsum, tmp)
+            T.ppl_mul_C(powsum, powsum, T.float32(rN))
+            T.ppl_add_C(powsum, powsum, T.float32(eps))
+            T.ppl_rsqrt(powsum, powsum)
+            for k in T.Pipelined(nk, num_stages=0):
+                kb = nk - 1 - k
+                T.ppl_copy(A[bx * blk_m, kb * blk_k], a_s)
+                if not f32:
+                    T.ppl_copy(a_s, a32)
+                T.ppl_mul(a32, a32, powsum)
+                if not f32:
+                    T.ppl_copy(a32, a_s)
+                T.ppl_copy(a_s, B[bx * blk_m, kb * blk_k])
+
+    return rmsnorm_splitk
+
+
 def matmul(M, N, K, block_M, block_N, block_K, dtype="float16", out_dtype="float16",
-           trans_b=False):
+           trans_b=False, operand_dtype=None):
+    """tpu_test_matmul_fp16.py:9-31 (bf16 / fp32-out twins); dtype float32 with operand_dtype
+    float16 gives tpu_test_matmul_fp32.py (fp32 tiles copied to fp16 tiles before ppl_gemm)."""
     b_shape = (N, K) if trans_b else (K, N)
     b_tile = (block_N, block_K) if trans_b else (block_K, block_N)
+    op_dt = operand_dtype or dtype
 
     @T.prim_func
     def gemm(A: T.Tensor((M, K), dtype), B: T.Tensor(b_shape, dtype),
@@ -65,6 +113,8 @@ def matmul(M, N, K, block_M, block_N, block_K, dtype="float16", out_dtype="float
         with T.Kernel(T.ceildiv(N, block_N), T.ceildiv(M, block_M), is_cpu=True) as (bx, by):
             a_s = T.alloc_shared((block_M, block_K), dtype)
             b_s = T.alloc_shared(b_tile, dtype)
+            a_op = a_s if op_dt == dtype else T.alloc_shared((block_M, block_K), op_dt)
+            b_op = b_s if op_dt == dtype else T.alloc_shared(b_tile, op_dt)
             acc = T.alloc_shared((block_M, block_N), "float32")
             c_s = T.alloc_shared((block_M, block_N), out_dtype)
             T.ppl_fill(acc, T.float32(0))
@@ -74,7 +124,10 @@ def matmul(M, N, K, block_M, block_N, block_K, dtype="float16", out_dtype="float
                     T.ppl_copy(B[bx * block_N, k * block_K], b_s)
                 else:
                     T.ppl_copy(B[k * block_K, bx * block_N], b_s)
-                T.ppl_gemm(a_s, b_s, acc, transpose_B=trans_b)
+                if op_dt != dtype:
+                    T.ppl_copy(a_s, a_op)
+                    T.ppl_copy(b_s, b_op)
+                T.ppl_gemm(a_op, b_op, acc, transpose_B=trans_b)
             T.ppl_copy(acc, c_s)
             T.ppl_copy(c_s, C[by * block_M, bx * block_N])
 
@@ -133,8 +186,11 @@ def rope_qk(tokens, heads_q, heads_k, W, Block_t=64, dtype="bfloat16"):
 
 
 def swi_glu(Block_w, Block_c, C, W, dtype="bfloat16"):
+    """tpu_test_swiglu_bf16.py:5-54; dtype float32 gives tpu_test_swiglu_fp32.py (tiles loaded
+    and stored as fp32 directly)."""
     shape = (C, W)
     acc = "float32"
+    f32 = dtype == "float32"
 
     @T.prim_func
     def swiglu(G_in: T.Tensor(shape, dtype), G_right: T.Tensor(shape, dtype),
@@ -143,35 +199,41 @@ def swi_glu(Block_w, Block_c, C, W, dtype="bfloat16"):
             tile = (Block_c, Block_w)
             g16 = T.alloc_shared(tile, dtype)
             u16 = T.alloc_shared(tile, dtype)
-            g = T.alloc_shared(tile, acc)
-            u = T.alloc_shared(tile, acc)
+            g = g16 if f32 else T.alloc_shared(tile, acc)
+            u = u16 if f32 else T.alloc_shared(tile, acc)
             e = T.alloc_shared(tile, acc)
             ones = T.alloc_shared(tile, acc)
             den = T.alloc_shared(tile, acc)
             sig = T.alloc_shared(tile, acc)
             out = T.alloc_shared(tile, acc)
-            o16 = T.alloc_shared(tile, dtype)
+            o16 = out if f32 else T.alloc_shared(tile, dtype)
             T.ppl_fill(ones, T.float32(1.0))
             T.ppl_copy(G_in[bx * Block_c, by * Block_w], g16)
             T.ppl_copy(G_right[bx * Block_c, by * Block_w], u16)
-            T.ppl_copy(g16, g)
-            T.ppl_copy(u16, u)
+            if not f32:
+                T.ppl_copy(g16, g)
+                T.ppl_copy(u16, u)
             T.ppl_mul_C(e, g, T.float32(-1.0))
             T.ppl_exp2(e)  # natural exp on BM1690 (customize.py:328-329)
             T.ppl_add(den, e, ones)
             T.ppl_div(sig, g, den)
             T.ppl_mul(out, u, sig)
-            T.ppl_copy(out, o16)
+            if not f32:
+                T.ppl_copy(out, o16)
             T.ppl_copy(o16, G_out[bx * Block_c, by * Block_w])
 
     return swiglu
 
 
 def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
-              dtype="bfloat16"):
+              dtype="bfloat16", gemm_dtype=None):
+    """tpu_test_flashattn_bf16.py:14-135 (fp16 twin); dtype float32 with gemm_dtype float16
+    gives tpu_test_flashattn_fp32.py: Q, K, V tiles and P copied to fp16 tiles for the two
+    ppl_gemm, softmax state, acc_o and the output in fp32."""
     scale = (1.0 / dim) ** 0.5
     shape = [batch, seq_len, heads, dim]
     acc = "float32"
+    gdt = gemm_dtype or dtype
 
     @T.prim_func
     def fa(Q: T.Tensor(shape, dtype), K: T.Tensor(shape, dtype), V: T.Tensor(shape, dtype),
@@ -180,9 +242,12 @@ def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
             q_s = T.alloc_shared([block_M, dim], dtype)
             k_s = T.alloc_shared([block_N, dim], dtype)
             v_s = T.alloc_shared([block_N, dim], dtype)
+            q_g = q_s if gdt == dtype else T.alloc_shared([block_M, dim], gdt)
+            k_g = k_s if gdt == dtype else T.alloc_shared([block_N, dim], gdt)
+            v_g = v_s if gdt == dtype else T.alloc_shared([block_N, dim], gdt)
             o_s = T.alloc_shared([block_M, dim], dtype)
             s = T.alloc_shared([block_M, block_N], acc)
-            p = T.alloc_shared([block_M, block_N], dtype)
+            p = T.alloc_shared([block_M, block_N], gdt)
             o = T.alloc_shared([block_M, dim], acc)
             m = T.alloc_shared([block_M, 1], acc)
             m_prev = T.alloc_shared([block_M, 1], acc)
@@ -198,7 +263,10 @@ def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
             for k in T.Pipelined(n_kv, num_stages=2):
                 T.ppl_copy(K[bz, k * block_N:(k + 1) * block_N, by, :], k_s)
                 T.ppl_fill(s, T.float32(0))
-                T.ppl_gemm(q_s, k_s, s, transpose_B=True)
+                if gdt != dtype:
+                    T.ppl_copy(q_s, q_g)
+                    T.ppl_copy(k_s, k_g)
+                T.ppl_gemm(q_g, k_g, s, transpose_B=True)
                 T.ppl_copy(m, m_prev)
                 T.ppl_fill(m, -T.infinity(acc))
                 T.ppl_reduce_max(s, m, dim=1, clear=False)
@@ -214,7 +282,9 @@ def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
                 T.ppl_copy(s, p)
                 T.ppl_mul(o, o, alpha)
                 T.ppl_copy(V[bz, k * block_N:(k + 1) * block_N, by, :], v_s)
-                T.ppl_gemm(p, v_s, o)
+                if gdt != dtype:
+                    T.ppl_copy(v_s, v_g)
+                T.ppl_gemm(p, v_g, o)
             T.ppl_div(o, o, l)
             T.ppl_copy(o, o_s)
             T.ppl_copy(o_s, Output[bz, bx * block_M:(bx + 1) * block_M, by, :])
