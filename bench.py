@@ -348,6 +348,41 @@ def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
     return res
 
 
+def bench_flashattn_gqa(args, dev, flush, cpu):
+    """examples/flash_attention/example_gqa_fwd_bshd.py defaults: batch 1, 64 heads, 16 groups
+    (4 K/V heads), seq 8192, dim 128, fp16, non-causal; the upstream program structure."""
+    import tilelang
+    from tilelang.testing import programs
+    B, H, G, S, D = 1, 64, 16, 8192, 128
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, S, H, D, generator=g).half()
+    kk = torch.randn(B, S, H // G, D, generator=g).half()
+    v = torch.randn(B, S, H // G, D, generator=g).half()
+    k = tilelang.compile(programs.flashattn_gqa(B, H, S, D, False, G), out_idx=[3])
+    flops = 4 * B * H * S * S * D
+    nbytes = (2 * B * S * H * D + 2 * B * S * (H // G) * D) * 2
+    qd, kd, vd = q.to(dev), kk.to(dev), v.to(dev)
+    o = torch.empty_like(qd)
+    fns = [lambda: k(qd, kd, vd, o)]
+    pmc_launches(args, fns, "flashattn_gqa")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 10, flush)
+    res = {"workload": f"flashattn_gqa_fp16_b{B}h{H}g{G}s{S}d{D}_full",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "dtype": "f16",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["fp16"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        t = cpu_time(lambda: ref.flashattn_ref(q, kk, v, False, heads=[0]), reps=1)
+        res["cpu_baseline"] = {"value": flops / H / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "head 0, oracle.ref.flashattn_ref"}
+    return res
+
+
 def bench_mla(args, dev, flush, cpu):
     from tilelang.jit.adapter.mi355x import ops
     from tilelang.testing import workloads
@@ -462,11 +497,12 @@ BENCHES = {
     "swiglu": bench_swiglu,
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
+    "flashattn_gqa": bench_flashattn_gqa,
     "mla": bench_mla,
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "mla", "kv_append"]
+         "flashattn_gqa", "mla", "kv_append"]
 
 
 def main():

@@ -116,13 +116,17 @@ int tlm_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n
 int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int64_t B, int64_t S,
                        int64_t H, int64_t D, int causal, float sm_scale, int dtype, void* stream);
 
-/* tlm_flash_attn_fwd with o in out_dtype (in_dtype or F32): the fp32 demo program
- * (tpu_demo/flashattn/tpu_test_flashattn_fp32.py:14-135) multiplies fp16 copies of its fp32
- * Q/K/V tiles and of P but keeps acc_o and the output in fp32: tlm_cast Q, K, V to F16, then
- * this with in_dtype F16, out_dtype F32. */
-int tlm_flash_attn_fwd_mixed(const void* q, const void* k, const void* v, void* o, int64_t B,
-                             int64_t S, int64_t H, int64_t D, int causal, float sm_scale,
-                             int in_dtype, int out_dtype, void* stream);
+/* General form of tlm_flash_attn_fwd.
+ *   H_kv: K and V are [B, S, H_kv, D] and query head h attends with K/V head h / (H / H_kv)
+ *         (grouped-query attention, examples/flash_attention/example_gqa_fwd_bshd.py:92-100:
+ *         K[bz, .., by // groups, :]); H_kv == H is multi-head attention. H % H_kv == 0.
+ *   out_dtype: in_dtype or F32. The fp32 demo program
+ *         (tpu_demo/flashattn/tpu_test_flashattn_fp32.py:14-135) multiplies fp16 copies of its
+ *         fp32 Q/K/V tiles and of P but keeps acc_o and the output in fp32: tlm_cast Q, K, V to
+ *         F16, then this with in_dtype F16, out_dtype F32. */
+int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, int64_t B,
+                          int64_t S, int64_t H, int64_t H_kv, int64_t D, int causal,
+                          float sm_scale, int in_dtype, int out_dtype, void* stream);
 
 /* MLA paged decode (one query token per sequence, one shared latent KV head).
  * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,

@@ -91,7 +91,11 @@ def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 # Evaluated one (batch, head) at a time so the [S, S] scores fit in host memory.
 def flashattn_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None,
                   heads: Optional[list] = None, batches: Optional[list] = None):
+    """K, V may have fewer heads than Q (grouped-query attention): query head h reads K/V head
+    h // (H // H_kv), as examples/flash_attention/example_gqa_fwd_bshd.py:181-205 (ref_program:
+    K.repeat_interleave(groups, dim=2))."""
     B, S, H, D = Q.shape
+    G = H // K.shape[2]
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else sm_scale
     out = torch.empty(B, S, H, D, dtype=torch.float32)
     mask = None
@@ -102,8 +106,8 @@ def flashattn_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None,
     for b in bs:
         for h in hs:
             q = Q[b, :, h, :].float()
-            k = K[b, :, h, :].float()
-            v = V[b, :, h, :].float()
+            k = K[b, :, h // G, :].float()
+            v = V[b, :, h // G, :].float()
             s = (q @ k.t()) * scale
             if mask is not None:
                 s = s.masked_fill(~mask, float("-inf"))

@@ -25,7 +25,7 @@ def test_header_declares_entry_points():
     syms = declared_symbols()
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
-              "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_mixed"):
+              "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex"):
         assert s in syms
 
 
@@ -113,10 +113,13 @@ def test_flash_attn_validation():
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.F32, None) == -2
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 128, 0, 0.1, lib.BF16, None) == 0
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 8, 0, 0.1, lib.BF16, None) == 0
-    mixed = L.tlm_flash_attn_fwd_mixed
-    assert mixed(p, p, p, p, 1, 0, 1, 8, 0, 0.1, lib.F16, lib.F32, None) == 0
-    assert mixed(p, p, p, p, 1, 16, 1, 8, 0, 0.1, lib.F16, lib.BF16, None) == -2
-    assert mixed(p, p, p, p, 1, 16, 1, 8, 0, 0.1, lib.F32, lib.F32, None) == -2
+    ex = L.tlm_flash_attn_fwd_ex
+    assert ex(p, p, p, p, 1, 0, 1, 1, 8, 0, 0.1, lib.F16, lib.F32, None) == 0
+    assert ex(p, p, p, p, 1, 16, 1, 1, 8, 0, 0.1, lib.F16, lib.BF16, None) == -2
+    assert ex(p, p, p, p, 1, 16, 1, 1, 8, 0, 0.1, lib.F32, lib.F32, None) == -2
+    assert ex(p, p, p, p, 1, 16, 8, 3, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1  # 8 % 3
+    assert ex(p, p, p, p, 1, 16, 8, 0, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1
+    assert ex(p, p, p, p, 1, 0, 8, 2, 128, 0, 0.1, lib.BF16, lib.BF16, None) == 0
 
 
 def test_mla_validation_and_workspace():

@@ -332,3 +332,20 @@ def test_kv_append_incremental_equals_bulk_and_skips_out_of_range():
     out = ref.kv_append_fp8_ref(x, np.array([10, 0]), np.array([9, 1]), np.array(
         [[5, 0, 3], [99, 4, 2]], dtype=np.int32), pool, page, 0.05)
     assert np.count_nonzero(out.any(axis=1)) == 2  # positions 10, 11 of sequence 0 only
+
+
+def test_flashattn_gqa_equals_mha_on_repeated_kv():
+    """Grouped K/V heads: the oracle equals the MHA oracle on K/V repeated per group
+    (example_gqa_fwd_bshd.py:195-196, repeat_interleave), for causal and full attention."""
+    g = torch.Generator().manual_seed(31)
+    B, S, H, Hkv, D = 2, 20, 6, 2, 8
+    q = torch.randn(B, S, H, D, generator=g)
+    k = torch.randn(B, S, Hkv, D, generator=g)
+    v = torch.randn(B, S, Hkv, D, generator=g)
+    for causal in (False, True):
+        got = ref.flashattn_ref(q, k, v, causal)
+        exp = ref.flashattn_ref(q, k.repeat_interleave(H // Hkv, dim=2),
+                                v.repeat_interleave(H // Hkv, dim=2), causal)
+        assert torch.equal(got, exp)
+        # and heads of one group differ from the next group's (the mapping is h // G, not h % H_kv)
+        assert not torch.allclose(got[:, :, 0], got[:, :, H // Hkv])

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
                                                           const uint16_t* __restrict__ K,
                                                           const uint16_t* __restrict__ V,
                                                           uint16_t* __restrict__ O, int B, int S,
-                                                          int H, float scale_log2) {
+                                                          int H, int Hkv, float scale_log2) {
   using MT = fa_mma<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
@@ -84,10 +84,12 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   const int bh = lin % (B * H);
   const int b = bh / H, h = bh % H;
   const int q0 = qt * BQ;
-  const int64_t row_stride = (int64_t)H * D;  // elements between consecutive tokens
+  const int64_t row_stride = (int64_t)H * D;  // elements between consecutive tokens (Q, O)
+  const int64_t kv_stride = (int64_t)Hkv * D;  // K, V: Hkv heads, query head h reads h / (H/Hkv)
+  const int hk = h / (H / Hkv);
   const uint16_t* Qb = Q + ((int64_t)b * S * H + h) * D;
-  const uint16_t* Kb = K + ((int64_t)b * S * H + h) * D;
-  const uint16_t* Vb = V + ((int64_t)b * S * H + h) * D;
+  const uint16_t* Kb = K + ((int64_t)b * S * Hkv + hk) * D;
+  const uint16_t* Vb = V + ((int64_t)b * S * Hkv + hk) * D;
 
   const int ql = lane & 31, g = lane >> 5;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
@@ -114,8 +116,8 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
       const int r = idx / CH, c = (idx % CH) * 8;
       const int key = j * BKV + r;
       if (key < S) {
-        rk[p] = *(const u32x4*)(Kb + (int64_t)key * row_stride + c);
-        rv[p] = *(const u32x4*)(Vb + (int64_t)key * row_stride + c);
+        rk[p] = *(const u32x4*)(Kb + (int64_t)key * kv_stride + c);
+        rv[p] = *(const u32x4*)(Vb + (int64_t)key * kv_stride + c);
       } else {
         rk[p] = u32x4{0, 0, 0, 0};
         rv[p] = u32x4{0, 0, 0, 0};
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
                                                    const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ V,
                                                    void* __restrict__ O, int B, int S, int H,
-                                                   float sc) {
+                                                   int Hkv, float sc) {
   using MT = fa_mma<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
@@ -359,22 +361,31 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int grp = wave >> 2, wl = wave & 3;
   const int blk = grp == 0 ? 2 * wl : 7 - 2 * wl;  // waves w and w + 4 share a SIMD
 
-  // workgroup -> (batch, head, query tile)
+  // workgroup -> (batch, head, query tile). Workgroup ids go round-robin over the 8 XCDs; each
+  // XCD takes whole K/V heads: all query tiles of the G = H / Hkv query heads that read one K/V
+  // head run there together (heaviest tiles first), so their K/V tiles come from that XCD's L2.
   const int nqt = (S + PP_BQ - 1) / PP_BQ;
+  const int G = H / Hkv;
   const int lin = blockIdx.x;
-  int bh, qt;
-  if ((B * H) % 8 == 0) {
+  int b, h, qt;
+  if ((B * Hkv) % 8 == 0) {
     const int xcd = lin & 7, s = lin >> 3;
-    bh = (s / nqt) * 8 + xcd;
-    qt = nqt - 1 - s % nqt;
+    const int per = nqt * G;  // workgroups per K/V head
+    const int kvh = (s / per) * 8 + xcd, rem = s % per;
+    qt = nqt - 1 - rem % nqt;
+    b = kvh / Hkv;
+    h = (kvh % Hkv) * G + rem / nqt;
   } else {
-    bh = lin / nqt;
+    const int bh = lin / nqt;
     qt = nqt - 1 - lin % nqt;
+    b = bh / H;
+    h = bh % H;
   }
-  const int b = bh / H, h = bh % H;
   const int q0 = qt * PP_BQ;
-  const int64_t rs = (int64_t)H * PP_D;  // elements between consecutive tokens
+  const int64_t rs = (int64_t)H * PP_D;      // elements between consecutive tokens of Q, O
+  const int64_t rs_kv = (int64_t)Hkv * PP_D;  // ... of K, V
   const int64_t head = ((int64_t)b * S * H + h) * PP_D;
+  const int64_t head_kv = ((int64_t)b * S * Hkv + h / G) * PP_D;
   const uint16_t* Qb = Q + head;
 
   const int n_all = (S + PP_KV - 1) / PP_KV;
@@ -397,8 +408,8 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   // ---- LDS-DMA: group 0 fills K tiles, group 1 V tiles; wave wl writes rows 16 wl .. 16 wl + 15
   // (4 instructions of 4 rows x 16 chunks). Lane -> (row, stored chunk p) fetches chunk p ^ swz.
   const bool dma_v = grp == 1;
-  const uint16_t* dsrc = (dma_v ? V : K) + head;
-  const uint32_t rs2 = (uint32_t)(rs * 2);
+  const uint16_t* dsrc = (dma_v ? V : K) + head_kv;
+  const uint32_t rs2 = (uint32_t)(rs_kv * 2);
   uint32_t doff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -411,7 +422,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     const int valid = min(PP_KV, S - PP_KV * tile);
     const uint32_t nrec = (uint32_t)(valid - 1) * rs2 + PP_D * 2;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(dsrc + (int64_t)tile * PP_KV * rs), (short)0, (int)nrec, PP_RSRC_WORD3);
+        (void*)(dsrc + (int64_t)tile * PP_KV * rs_kv), (short)0, (int)nrec, PP_RSRC_WORD3);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -647,7 +658,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
 }
 
 template <bool BF16, bool CAUSAL, bool OUT32>
-int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
+int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
               float sc, hipStream_t st) {
   const int64_t nwg = (int64_t)((S + PP_BQ - 1) / PP_BQ) * B * H;
   if (nwg > INT32_MAX) {
@@ -655,21 +666,21 @@ int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S
     return TLM_EINVAL;
   }
   fa_fwd_pp<BF16, CAUSAL, OUT32><<<(unsigned)nwg, 512, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, sc);
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
 
 template <bool BF16, bool CAUSAL, int D>
-int launch(const void* q, const void* k, const void* v, void* o, int B, int S, int H, float sc,
-           hipStream_t st) {
+int launch(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
+           float sc, hipStream_t st) {
   const int64_t nwg = (int64_t)((S + BQ - 1) / BQ) * B * H;
   if (nwg > INT32_MAX) {
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
   fa_fwd<BF16, CAUSAL, D><<<(unsigned)nwg, 64 * FA_WAVES, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, sc);
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, Hkv, sc);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
@@ -683,14 +694,15 @@ template <bool BF16, bool CAUSAL, bool OUT32, int DC>  // DC = capacity in 8-ele
 __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict__ Q,
                                                       const uint16_t* __restrict__ K,
                                                       const uint16_t* __restrict__ V,
-                                                      void* __restrict__ O, int S, int H, int D,
-                                                      float sc) {
+                                                      void* __restrict__ O, int S, int H, int Hkv,
+                                                      int D, float sc) {
   using HH = h16<BF16>;
   const int bh = blockIdx.y, b = bh / H, h = bh % H;
   const int q = blockIdx.x * 256 + threadIdx.x;
   const int nc = D / 8;
-  const int64_t rs = (int64_t)H * D;
+  const int64_t rs = (int64_t)H * D, rs_kv = (int64_t)Hkv * D;
   const int64_t head = ((int64_t)b * S * H + h) * D;
+  const int64_t head_kv = ((int64_t)b * S * Hkv + h / (H / Hkv)) * D;
   u32x4 qv[DC];
   float o[DC][8];
 #pragma unroll
@@ -705,7 +717,7 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
   const int wq_last = min(S - 1, (int)(blockIdx.x * 256 + (threadIdx.x & ~63) + 63));
   const int kend = CAUSAL ? wq_last + 1 : S;
   for (int j = 0; j < kend; ++j) {
-    const uint16_t* kr = K + head + (int64_t)j * rs;
+    const uint16_t* kr = K + head_kv + (int64_t)j * rs_kv;
     float s = 0.f;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
@@ -726,7 +738,7 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
     const float pr = HH::to_f32(HH::from_f32(p));
     l = fmaf(l, alpha, p);
     m = m_new;
-    const uint16_t* vr = V + head + (int64_t)j * rs;
+    const uint16_t* vr = V + head_kv + (int64_t)j * rs_kv;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       if (c < nc) {
@@ -760,7 +772,7 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
 
 template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_generic(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
-                   int D, float sc, hipStream_t st) {
+                   int Hkv, int D, float sc, hipStream_t st) {
   if ((int64_t)B * H > 65535) {
     tlm_set_error("tlm_flash_attn_fwd: head dim %d needs batch * heads <= 65535", D);
     return TLM_EUNSUPPORTED;
@@ -768,7 +780,7 @@ int launch_generic(const void* q, const void* k, const void* v, void* o, int B, 
   const dim3 grid((unsigned)((S + 255) / 256), (unsigned)(B * H));
   auto go = [&](auto kern) {
     kern<<<grid, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, S,
-                               H, D, sc);
+                               H, Hkv, D, sc);
   };
   if (D <= 16)
     go(fa_fwd_generic<BF16, CAUSAL, OUT32, 2>);
@@ -783,30 +795,35 @@ int launch_generic(const void* q, const void* k, const void* v, void* o, int B, 
 }
 
 template <bool BF16, bool OUT32>
-int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int D,
-             bool causal, float sc, hipStream_t st) {
+int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
+             int D, bool causal, float sc, hipStream_t st) {
   if (D == 128)
-    return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, sc, st)
-                  : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, sc, st);
+    return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, sc, st)
+                  : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, sc, st);
   if (D == 64 && !OUT32)
-    return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, sc, st)
-                  : launch<BF16, false, 64>(q, k, v, o, B, S, H, sc, st);
-  return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, D, sc, st)
-                : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, D, sc, st);
+    return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, Hkv, sc, st)
+                  : launch<BF16, false, 64>(q, k, v, o, B, S, H, Hkv, sc, st);
+  return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, st)
+                : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, st);
 }
 
 }  // namespace
 
-extern "C" int tlm_flash_attn_fwd_mixed(const void* q, const void* k, const void* v, void* o,
-                                        int64_t B, int64_t S, int64_t H, int64_t D, int causal,
-                                        float sm_scale, int in_dtype, int out_dtype,
-                                        void* stream) {
+extern "C" int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v, void* o,
+                                     int64_t B, int64_t S, int64_t H, int64_t H_kv, int64_t D,
+                                     int causal, float sm_scale, int in_dtype, int out_dtype,
+                                     void* stream) {
   if (!q || !k || !v || !o) {
     tlm_set_error("tlm_flash_attn_fwd: null pointer argument");
     return TLM_EINVAL;
   }
   if (B < 0 || S < 0 || H < 0 || B > 65535 || H > 65535 || S > (1 << 24)) {
     tlm_set_error("tlm_flash_attn_fwd: bad shape");
+    return TLM_EINVAL;
+  }
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) {
+    tlm_set_error("tlm_flash_attn_fwd: %lld query heads do not split into groups of %lld K/V "
+                  "heads", (long long)H, (long long)H_kv);
     return TLM_EINVAL;
   }
   if (D <= 0 || D > 256 || D % 8 != 0) {
@@ -835,17 +852,17 @@ extern "C" int tlm_flash_attn_fwd_mixed(const void* q, const void* k, const void
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = in_dtype == TLM_BF16, f32o = out_dtype == TLM_F32;
-  const int b = (int)B, s = (int)S, h = (int)H, d = (int)D;
+  const int b = (int)B, s = (int)S, h = (int)H, hk = (int)H_kv, d = (int)D;
   const bool c = causal != 0;
   if (bf)
-    return f32o ? by_shape<true, true>(q, k, v, o, b, s, h, d, c, sc, st)
-                : by_shape<true, false>(q, k, v, o, b, s, h, d, c, sc, st);
-  return f32o ? by_shape<false, true>(q, k, v, o, b, s, h, d, c, sc, st)
-              : by_shape<false, false>(q, k, v, o, b, s, h, d, c, sc, st);
+    return f32o ? by_shape<true, true>(q, k, v, o, b, s, h, hk, d, c, sc, st)
+                : by_shape<true, false>(q, k, v, o, b, s, h, hk, d, c, sc, st);
+  return f32o ? by_shape<false, true>(q, k, v, o, b, s, h, hk, d, c, sc, st)
+              : by_shape<false, false>(q, k, v, o, b, s, h, hk, d, c, sc, st);
 }
 
 extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,
                                   int64_t B, int64_t S, int64_t H, int64_t D, int causal,
                                   float sm_scale, int dtype, void* stream) {
-  return tlm_flash_attn_fwd_mixed(q, k, v, o, B, S, H, D, causal, sm_scale, dtype, dtype, stream);
+  return tlm_flash_attn_fwd_ex(q, k, v, o, B, S, H, H, D, causal, sm_scale, dtype, dtype, stream);
 }

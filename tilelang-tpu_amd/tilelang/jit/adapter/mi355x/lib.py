@@ -34,8 +34,8 @@ _SIGNATURES = {
     "tlm_gemm": ([c_void_p] * 3 + [c_int64] * 3 + [c_int] * 3 + [c_void_p], c_int),
     "tlm_flash_attn_fwd": ([c_void_p] * 4 + [c_int64] * 4 + [c_int, c_float, c_int, c_void_p],
                            c_int),
-    "tlm_flash_attn_fwd_mixed": ([c_void_p] * 4 + [c_int64] * 4 +
-                                 [c_int, c_float, c_int, c_int, c_void_p], c_int),
+    "tlm_flash_attn_fwd_ex": ([c_void_p] * 4 + [c_int64] * 5 +
+                              [c_int, c_float, c_int, c_int, c_void_p], c_int),
     "tlm_cast": ([c_void_p, c_int, c_void_p, c_int, c_int64, c_void_p], c_int),
     "tlm_mla_decode": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                         c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +

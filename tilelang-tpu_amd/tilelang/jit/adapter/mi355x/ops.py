@@ -150,20 +150,25 @@ def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = Fals
 
 def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float,
                    operand_dtype: Optional[torch.dtype] = None):
-    """BSHD attention forward: q,k,v,o [B, S, H, D]. o may be fp32 with 16-bit q/k/v;
-    operand_dtype: fp32 q/k/v are first rounded to this 16-bit type (the fp32 program)."""
+    """BSHD attention forward: q, o [B, S, H, D]; k, v [B, S, H_kv, D] with H % H_kv == 0
+    (grouped-query attention when H_kv < H). o may be fp32 with 16-bit q/k/v; operand_dtype:
+    fp32 q/k/v are first rounded to this 16-bit type (the fp32 program)."""
     dev = _dev(q, k, v, o)
     for n, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
         _contig(n, t)
-    if not (q.shape == k.shape == v.shape == o.shape):
-        raise ValueError("Q, K, V and O must share the [B, S, H, D] shape")
+    if q.dim() != 4 or q.shape != o.shape or k.shape != v.shape or k.dim() != 4:
+        raise ValueError("Q, O must be [B, S, H, D] and K, V [B, S, H_kv, D]")
+    B, S, H, D = q.shape
+    Hkv = k.shape[2]
+    if (k.shape[0], k.shape[1], k.shape[3]) != (B, S, D) or Hkv == 0 or H % Hkv:
+        raise ValueError(f"K/V {tuple(k.shape)} do not match Q {tuple(q.shape)} "
+                         "(same B, S, D; H a multiple of H_kv)")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("Q, K and V must share a dtype")
     q, k, v = (_as_operand(t, operand_dtype) for t in (q, k, v))
     if o.dtype not in (q.dtype, torch.float32):
         raise ValueError(f"O must be {q.dtype} or float32")
-    B, S, H, D = q.shape
-    lib.call("tlm_flash_attn_fwd_mixed", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, S, H, D,
+    lib.call("tlm_flash_attn_fwd_ex", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, S, H, Hkv, D,
              1 if causal else 0, float(sm_scale), dtype_code(q.dtype), dtype_code(o.dtype),
              _stream(dev))
     return o

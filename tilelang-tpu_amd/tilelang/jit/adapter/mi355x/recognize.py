@@ -18,7 +18,7 @@ Families and the reference programs they accept:
   swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54 (+ tpu_test_swiglu_fp32.py)
   flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, and fp32 with fp16
            matrix tiles) and the upstream examples/flash_attention/example_mha_fwd_bshd.py:30-151
-           structure
+           structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178)
   mla      examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split and no-split forms),
            with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV
 """
@@ -320,8 +320,11 @@ def _flashattn(pf, names) -> Plan:
     if None in (Q, K, V, O):
         _fail(fam, "could not trace Q, K, V and Output")
     shp = _shape(Q)
-    if len(shp) != 4 or not (shp == _shape(K) == _shape(V) == _shape(O)):
-        _fail(fam, "Q, K, V, Output must share a [batch, seq, heads, dim] shape")
+    kshp = _shape(K)
+    if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
+        _fail(fam, "Q, Output must be [batch, seq, heads, dim] and K, V [batch, seq, kv_heads, dim]")
+    if (kshp[0], kshp[1], kshp[3]) != (shp[0], shp[1], shp[3]) or shp[2] % kshp[2]:
+        _fail(fam, f"K/V {kshp} do not group Q {shp} (query heads a multiple of K/V heads)")
     # tiles the two gemms multiply: the fp32 program copies Q, K, V and P to fp16 tiles first
     tile_dts = {_buf(qk[0].args[0]).dtype, _buf(qk[0].args[1]).dtype, _buf(pv[0].args[0]).dtype,
                 _buf(pv[0].args[1]).dtype}
@@ -361,7 +364,8 @@ def _flashattn(pf, names) -> Plan:
         if sm_scale is None:
             _fail(fam, "could not read the softmax scale")
     return Plan(fam, pf.params, [_index(pf, O)], dict(
-        q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H, D=D,
+        q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H,
+        H_kv=kshp[2], D=D,
         causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
         operand_dtype=tile_dt if Q.dtype == "float32" else None))
 

@@ -292,6 +292,72 @@ def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
     return fa
 
 
+def flashattn_gqa(batch, heads, seq_len, dim, is_causal, groups=1, block_M=128, block_N=128,
+                  dtype="float16"):
+    """The upstream program structure of examples/flash_attention/example_gqa_fwd_bshd.py:62-178
+    (groups=1: example_mha_fwd_bshd.py): T.copy / T.gemm tiles, the causal mask written into the
+    scores with if_then_else before Q K^T accumulates onto them, softmax in the exp2 domain with
+    the scale folded in (scale * log2 e), query head by reading K/V head by // groups."""
+    scale = (1.0 / dim) ** 0.5 * 1.44269504
+    head_kv = heads // groups
+    q_shape = [batch, seq_len, heads, dim]
+    kv_shape = [batch, seq_len, head_kv, dim]
+    acc = "float"
+
+    @T.prim_func
+    def main(Q: T.Tensor(q_shape, dtype), K: T.Tensor(kv_shape, dtype),
+             V: T.Tensor(kv_shape, dtype), Output: T.Tensor(q_shape, dtype)):
+        with T.Kernel(T.ceildiv(seq_len, block_M), heads, batch, threads=128) as (bx, by, bz):
+            q_s = T.alloc_shared([block_M, dim], dtype)
+            k_s = T.alloc_shared([block_N, dim], dtype)
+            v_s = T.alloc_shared([block_N, dim], dtype)
+            o_s = T.alloc_shared([block_M, dim], dtype)
+            s = T.alloc_fragment([block_M, block_N], acc)
+            s_cast = T.alloc_fragment([block_M, block_N], dtype)
+            o = T.alloc_fragment([block_M, dim], acc)
+            m = T.alloc_fragment([block_M], acc)
+            m_prev = T.alloc_fragment([block_M], acc)
+            alpha = T.alloc_fragment([block_M], acc)
+            rsum = T.alloc_fragment([block_M], acc)
+            l = T.alloc_fragment([block_M], acc)
+            T.copy(Q[bz, bx * block_M:(bx + 1) * block_M, by, :], q_s)
+            T.fill(o, 0)
+            T.fill(l, 0)
+            T.fill(m, -T.infinity(acc))
+            n_kv = (T.min(T.ceildiv(seq_len, block_N), T.ceildiv((bx + 1) * block_M, block_N))
+                    if is_causal else T.ceildiv(seq_len, block_N))
+            for k in T.Pipelined(n_kv, num_stages=2):
+                T.copy(K[bz, k * block_N:(k + 1) * block_N, by // groups, :], k_s)
+                if is_causal:
+                    for i, j in T.Parallel(block_M, block_N):
+                        s[i, j] = T.if_then_else(bx * block_M + i >= k * block_N + j, 0,
+                                                 -T.infinity(acc))
+                else:
+                    T.clear(s)
+                T.gemm(q_s, k_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullRow)
+                T.copy(m, m_prev)
+                T.fill(m, -T.infinity(acc))
+                T.reduce_max(s, m, dim=1, clear=False)
+                for i in T.Parallel(block_M):
+                    alpha[i] = T.exp2(m_prev[i] * scale - m[i] * scale)
+                for i, j in T.Parallel(block_M, block_N):
+                    s[i, j] = T.exp2(s[i, j] * scale - m[i] * scale)
+                T.reduce_sum(s, rsum, dim=1)
+                for i in T.Parallel(block_M):
+                    l[i] = l[i] * alpha[i] + rsum[i]
+                T.copy(s, s_cast)
+                for i, j in T.Parallel(block_M, dim):
+                    o[i, j] *= alpha[i]
+                T.copy(V[bz, k * block_N:(k + 1) * block_N, by // groups, :], v_s)
+                T.gemm(s_cast, v_s, o, policy=T.GemmWarpPolicy.FullRow)
+            for i, j in T.Parallel(block_M, dim):
+                o[i, j] /= l[i]
+            T.copy(o, o_s)
+            T.copy(o_s, Output[bz, bx * block_M:(bx + 1) * block_M, by, :])
+
+    return main
+
+
 def mla_decode(batch, h_q, h_kv, max_seqlen_pad, dv, dpe, block_N, block_H, num_split,
                block_size, dtype="float16", kv_dtype=None, out_dtype=None):
     """Paged MLA decode with split-KV + LSE combine. ``kv_dtype="float8_e4m3"`` adds a trailing
