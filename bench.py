@@ -348,6 +348,40 @@ def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
     return res
 
 
+def bench_gemm_fp8(args, dev, flush, cpu):
+    """FP8 GEMM (examples/gemm_fp8/example_tilelang_gemm_fp8_2xAcc.py structure: e4m3 A [M,K],
+    B [N,K], fp32 C) at the GEMM config's 4096^3."""
+    import tilelang
+    from tilelang.testing import programs
+    M = N = K = 4096
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(M, K, generator=g).to(torch.float8_e4m3fn)
+    b = torch.randn(N, K, generator=g).to(torch.float8_e4m3fn)
+    k = tilelang.compile(programs.matmul_fp8(M, N, K, 128, 128, 64, "e4m3_float8", two_acc=True),
+                         out_idx=-1)
+    flops = 2 * M * N * K
+    ad, bd = a.to(dev), b.to(dev)
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    fns = [lambda: k(ad, bd, c)]
+    pmc_launches(args, fns, "gemm_fp8")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 10, flush)
+    res = {"workload": f"gemm_fp8_e4m3_{M}x{N}x{K}_f32out", "value": flops / (ms * 1e-3) / 1e12,
+           "unit": "TFLOP/s", "ms_per_step": ms, "dtype": "fp8-e4m3 in, fp32 accumulate",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["fp8"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": (M * K + N * K) + M * N * 4}
+    if cpu:
+        from oracle import ref
+        rows = 256
+        t = cpu_time(lambda: ref.gemm_fp8_ref(a[:rows], b), reps=1)
+        res["cpu_baseline"] = {"value": 2 * rows * N * K / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"first {rows} rows of A, oracle.ref.gemm_fp8_ref"}
+    return res
+
+
 def bench_flashattn_gqa(args, dev, flush, cpu):
     """examples/flash_attention/example_gqa_fwd_bshd.py defaults: batch 1, 64 heads, 16 groups
     (4 K/V heads), seq 8192, dim 128, fp16, non-causal; the upstream program structure."""
@@ -498,11 +532,12 @@ BENCHES = {
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
     "flashattn_gqa": bench_flashattn_gqa,
+    "gemm_fp8": bench_gemm_fp8,
     "mla": bench_mla,
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "flashattn_gqa", "mla", "kv_append"]
+         "flashattn_gqa", "gemm_fp8", "mla", "kv_append"]
 
 
 def main():

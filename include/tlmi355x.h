@@ -40,6 +40,7 @@ enum tlm_dtype {
   TLM_F32 = 2,
   TLM_F8E4M3 = 3, /* OCP e4m3fn (gfx950 native), not the FNUZ variant of gfx942 */
   TLM_I32 = 4,
+  TLM_F8E5M2 = 5, /* OCP e5m2 */
 };
 
 /* Error codes. The reference returns -1 (init), -2 (module load), 1 (launch)
@@ -100,6 +101,15 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * ppl_gemm: tlm_cast to F16, then this with out_dtype F32. */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
              int out_dtype, int trans_b, void* stream);
+
+/* FP8 GEMM: C[M,N] = A[M,K] * B^T with B [N,K] row-major (trans_b == 1; trans_b == 0 takes B
+ * [K,N] through a per-output fallback), fp32 accumulation, one rounding to out_dtype.
+ * Reference: examples/gemm_fp8/example_tilelang_gemm_fp8.py:17-37 (T.gemm transpose_B=True,
+ * fp8 C; oracle (a.half() @ b.half().T).to(fp8), :46-55) and example_tilelang_gemm_fp8_2xAcc.py
+ * (fp32 C). in_dtype: F8E4M3 | F8E5M2 (OCP); out_dtype: F32 | F16 | BF16 | in_dtype (round to
+ * nearest even without saturation, as torch's cast). */
+int tlm_gemm_fp8(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                 int in_dtype, int out_dtype, int trans_b, void* stream);
 
 /* Element-type conversion of n contiguous values, the cast of a ppl_copy between tiles of
  * different dtypes (src/target/codegen_ppl.cc:1138-1152): F32 -> F16 | BF16 rounds to nearest

@@ -47,6 +47,13 @@ def matmul_ref(a: torch.Tensor, b: torch.Tensor, out_dtype=torch.float16, trans_
     return (a.float() @ bf).to(out_dtype)
 
 
+# FP8 GEMM — examples/gemm_fp8/example_tilelang_gemm_fp8.py:46-55: ref = (a.half() @
+# b.half().T).to(fp8). fp8 products are exact in fp32, so the product is accumulated in fp32 (not
+# fp16, which the example's GPU reference rounds to before the fp8 cast) and rounded once.
+def gemm_fp8_ref(a: torch.Tensor, b_nk: torch.Tensor, out_dtype=torch.float32):
+    return (a.float() @ b_nk.float().t()).to(out_dtype)
+
+
 # ------------------------------------------------------------------------------------------------
 # RoPE — tables per tpu_demo/tpu_test_rope_bf16.py:53-74 (make_rope_cos_sin), computed in fp32;
 # rotation per rope_ref_torch (:76-92).

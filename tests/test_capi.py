@@ -25,7 +25,8 @@ def test_header_declares_entry_points():
     syms = declared_symbols()
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
-              "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex"):
+              "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex",
+              "tlm_gemm_fp8"):
         assert s in syms
 
 
@@ -75,6 +76,16 @@ def test_swiglu_rope_validation():
     assert L.tlm_rope(p, None, p, p, p, None, 0, 2, 0, 128, lib.BF16, None) == 0
     assert L.tlm_rope(p, None, p, p, p, None, 0, 2, 0, 128, lib.F32, None) == 0
     assert L.tlm_rope(p, None, p, p, p, None, 4, 2, 0, 128, lib.F8E4M3, None) == -2
+
+
+def test_gemm_fp8_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_gemm_fp8(None, p, p, 16, 16, 16, lib.F8E4M3, lib.F32, 1, None) == -1
+    assert L.tlm_gemm_fp8(p, p, p, 16, 16, 16, lib.F16, lib.F32, 1, None) == -2
+    assert L.tlm_gemm_fp8(p, p, p, 16, 16, 16, lib.F8E4M3, lib.F8E5M2, 1, None) == -2
+    assert L.tlm_gemm_fp8(p, p, p, 16, 16, 16, lib.F8E4M3, lib.F32, 2, None) == -1
+    assert L.tlm_gemm_fp8(p, p, p, 0, 16, 16, lib.F8E5M2, lib.F8E5M2, 1, None) == 0
 
 
 def test_cast_validation():

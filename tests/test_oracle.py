@@ -349,3 +349,23 @@ def test_flashattn_gqa_equals_mha_on_repeated_kv():
         assert torch.equal(got, exp)
         # and heads of one group differ from the next group's (the mapping is h // G, not h % H_kv)
         assert not torch.allclose(got[:, :, 0], got[:, :, H // Hkv])
+
+
+@pytest.mark.parametrize("dt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_gemm_fp8_ref_against_fp64_brute_force(dt):
+    """fp8 GEMM oracle: exact fp8 decode and fp32 accumulation against an fp64 triple loop of the
+    decoded values (products of fp8 values are exact; a 48-term sum stays within fp32 rounding),
+    and the fp8 output equals torch's RNE cast of that fp64 result except at rounding ties."""
+    g = torch.Generator().manual_seed(32)
+    a = (torch.randn(5, 48, generator=g) * 3).to(dt)
+    b = (torch.randn(7, 48, generator=g) * 3).to(dt)
+    got = ref.gemm_fp8_ref(a, b)
+    A, Bm = a.double().numpy(), b.double().numpy()
+    exp = np.zeros((5, 7))
+    for i in range(5):
+        for j in range(7):
+            exp[i, j] = sum(A[i, k] * Bm[j, k] for k in range(48))
+    assert np.allclose(got.double().numpy(), exp, rtol=1e-6, atol=1e-5)
+    q = ref.gemm_fp8_ref(a, b, out_dtype=dt).float().numpy()
+    e8 = torch.from_numpy(exp).float().to(dt).float().numpy()
+    assert (q == e8).mean() > 0.97

@@ -1,0 +1,381 @@
+// FP8 GEMM C = A * B^T on gfx950 MFMA: A [M, K] and B [N, K] in OCP e4m3 or e5m2, fp32
+// accumulation, C in fp32 / fp16 / bf16 / the input fp8 format.
+//
+// Reference program: examples/gemm_fp8/example_tilelang_gemm_fp8.py:17-37 (T.gemm with
+// transpose_B=True into a float fragment, copied out to an fp8 C; checked against
+// (a.half() @ b.half().T).to(fp8), :46-55) and example_tilelang_gemm_fp8_2xAcc.py:10-50 (the same
+// product kept in fp32: C is float). The two-level accumulation of the 2xAcc program is a
+// Hopper precision workaround; v_mfma_f32_32x32x64_f8f6f4 accumulates every product in fp32.
+//
+// Design: the 256x256 ping-pong of gemm_256x256 (tlm_gemm.hip) at one byte per element. A k-tile
+// is 128 k = 128 bytes per row, the same LDS tile and LDS-DMA pattern as a 64-k 16-bit tile, and
+// one v_mfma_f32_32x32x64_f8f6f4 (64 k) takes the place of four 32x32x16 16-bit MFMAs at twice
+// the FLOP rate. Operand layout of the 32x32x64 MFMA: lane l holds row (A) / column (B) l % 32;
+// lane half h = l / 32 holds k = 16 h .. 16 h + 15 and 32 + 16 h .. 32 + 16 h + 15 of the 64-k
+// step, i.e. two 16-byte chunks of the row.
+#include "tlm_common.h"
+
+namespace {
+
+constexpr int BM = 256, BN = 256, BKB = 128;  // BKB: k per tile = bytes per tile row
+constexpr int NTHREADS = 512;
+constexpr int RSRC_WORD3 = 0x00020000;
+constexpr uint32_t OOB = 0xfffffff0u;
+constexpr int ST = BM * BKB;  // bytes per stage (A or B^T)
+constexpr int NST_A = 2, NST_B = 3;
+constexpr int SMEM = (NST_A + NST_B) * ST;  // 160 KB
+
+// FMT: 0 = e4m3, 1 = e5m2 (the cbsz / blgp format codes of the f8f6f4 MFMA)
+template <int FMT>
+TLM_DEV f32x16 mma8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FMT, FMT, 0, 0, 0, 0);
+}
+
+TLM_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+TLM_DEV u32x4 lds_b128(const void* p) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+template <int N>
+TLM_DEV void lgkm_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  __builtin_amdgcn_s_waitcnt(0xc07f | (N << 8));
+}
+TLM_DEV void order_after(u32x4& a) { asm volatile("" : "+v"(a)); }
+TLM_DEV void barrier_lds() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+TLM_DEV void wait_dma() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0x3f70);
+  __builtin_amdgcn_sched_barrier(0);
+}
+TLM_DEV i32x8 cat8(u32x4 lo, u32x4 hi) {
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+               (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// [rows][128 k] tiles, 16-byte chunk c of row r at c ^ ((r >> 1) & 7): a 16-lane ds_read_b128
+// phase covers 16 rows of one chunk column (conflict free), each LDS-DMA instruction 1 KB.
+TLM_DEV int swz_rows(int r) { return (r >> 1) & 7; }
+
+TLM_DEV void tile_of(int wg, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int lin = wg;
+  if (total % 8 == 0) lin = (wg % 8) * (total / 8) + wg / 8;
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = lin / per_group;
+  const int first_m = g * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int r = lin % per_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
+template <int OUT>
+TLM_DEV void store_out(void* C, int64_t idx, float v) {
+  if constexpr (OUT == TLM_F32) {
+    ((float*)C)[idx] = v;
+  } else if constexpr (OUT == TLM_BF16) {
+    ((uint16_t*)C)[idx] = (uint16_t)f32_to_bf16_bits(v);
+  } else if constexpr (OUT == TLM_F16) {
+    ((uint16_t*)C)[idx] = (uint16_t)f32_to_f16_bits(v);
+  } else if constexpr (OUT == TLM_F8E4M3) {  // round to nearest even, no saturation (torch's cast)
+    ((uint8_t*)C)[idx] = (uint8_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.f, 0, false);
+  } else {
+    ((uint8_t*)C)[idx] = (uint8_t)__builtin_amdgcn_cvt_pk_bf8_f32(v, 0.f, 0, false);
+  }
+}
+
+template <int FMT, int OUT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __restrict__ A,
+                                                            const uint8_t* __restrict__ B,
+                                                            void* __restrict__ C, int M, int N,
+                                                            int K) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2;  // 128-row half
+  const int wn = wave & 3;   // 64-column quarter
+  int tm, tn;
+  tile_of(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = (K + BKB - 1) / BKB;
+
+  struct Dma {
+    const uint8_t* base[2];
+    uint8_t* st[2];
+  };
+  auto sa_of = [&](int kt) { return smem + (kt % NST_A) * ST; };
+  auto sb_of = [&](int kt) { return smem + NST_A * ST + (kt % NST_B) * ST; };
+  auto dma_setup = [&](int kt) {
+    const int k0 = kt * BKB;
+    return Dma{{A + ((int64_t)m0 * K + k0), B + ((int64_t)n0 * K + k0)},
+               {sa_of(kt), sb_of(kt)}};
+  };
+  // instruction d (0..3 A, 4..7 B): 8 rows of 128 bytes; chunks beyond K or rows beyond M / N
+  // read zeros through the out-of-range offset
+  auto dma = [&](const Dma& dd, int d, int kmax) {
+    const int ins = wave * 4 + (d & 3);
+    const int r = 8 * ins + (lane >> 3);
+    const int c = (lane & 7) ^ swz_rows(r);
+    const bool ok = (d < 4 ? m0 + r < M : n0 + r < N) && 16 * c < kmax;
+    const uint32_t off = (uint32_t)(r * K + 16 * c);
+    uint8_t* dst = dd.st[d >> 2] + ins * 1024;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)dd.base[d >> 2], (short)0, 0x7ffffff0, RSRC_WORD3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
+                                             ok ? off : OOB, 0, 0, 0);
+  };
+  auto issue = [&](int kt) {
+    const Dma dd = dma_setup(kt);
+    const int kmax = min(BKB, K - kt * BKB);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) dma(dd, d, kmax);
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int hf = lane >> 5;
+  const int sw = (lane >> 1) & 7;
+  const int a_row = (wm * 128 + (lane & 31)) * BKB;
+  const int b_row = (wn * 64 + (lane & 31)) * BKB;
+
+  // Ping-pong of the two waves on each SIMD (groups of 4), as in gemm_256x256: one reads the
+  // next k-tile's A operands (both 64-k steps) and its first B operands while the other issues
+  // MFMAs; every phase ends with a workgroup barrier.
+  const int grp = wave >> 2;
+  u32x4 aop[2][4][2];  // [k-step][mi][chunk]
+  u32x4 bop[2][2][2];  // [buffer][ni][chunk]
+  auto chunk = [&](int ks, int p) { return 16 * ((4 * ks + 2 * p + hf) ^ sw); };
+  auto readb = [&](int kt, int ks, u32x4 (&o)[2][2]) {
+    const uint8_t* sb = sb_of(kt);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) o[ni][p] = lds_b128(sb + b_row + ni * 32 * BKB + chunk(ks, p));
+  };
+  auto dma_quad = [&](const Dma& dd, int dma_kt, int ks) {
+    if (dma_kt >= 0) {
+      const int kmax = min(BKB, K - dma_kt * BKB);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) dma(dd, 4 * ks + d, kmax);
+    }
+  };
+  auto load_phase = [&](int kt, int dma_kt) {
+    const uint8_t* sa = sa_of(kt);
+    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          aop[ks][mi][p] = lds_b128(sa + a_row + mi * 32 * BKB + chunk(ks, p));
+      dma_quad(dd, dma_kt, ks);
+    }
+    readb(kt, 0, bop[0]);
+    lgkm_wait<0>();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) order_after(aop[ks][mi][p]);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) order_after(bop[0][ni][p]);
+  };
+  auto compute_phase = [&](int kt, int dma_kt) {
+    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks == 0) {
+        readb(kt, 1, bop[1]);
+        lgkm_wait<4>();  // B of k-step 0 landed; k-step 1's 4 reads stay in flight
+      } else {
+        lgkm_wait<0>();
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) order_after(bop[ks][ni][p]);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = mma8<FMT>(cat8(aop[ks][mi][0], aop[ks][mi][1]),
+                                  cat8(bop[ks][ni][0], bop[ks][ni][1]), acc[mi][ni]);
+        if (mi == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          dma_quad(dd, dma_kt, ks);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+  issue(0);
+  wait_dma();
+  barrier_lds();
+  if (grp == 0) {
+    for (int kt = 0; kt < KT; ++kt) {
+      load_phase(kt, kt + 1 < KT ? kt + 1 : -1);
+      barrier_lds();
+      compute_phase(kt, -1);
+      wait_dma();
+      barrier_lds();
+    }
+    barrier_lds();
+  } else {
+    if (1 < KT) issue(1);
+    barrier_lds();
+    for (int kt = 0; kt < KT; ++kt) {
+      load_phase(kt, -1);
+      wait_dma();
+      barrier_lds();
+      compute_phase(kt, kt + 2 < KT ? kt + 2 : -1);
+      barrier_lds();
+    }
+  }
+
+  // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8 (i / 4) + 4 (lane / 32)
+  // + i % 4
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = m0 + wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mi][ni][i]);
+      }
+    }
+}
+
+// fp8 byte -> float, exact (e4m3: bias 7, no infinities, 0x7f / 0xff NaN; e5m2: IEEE-like)
+template <int FMT>
+TLM_DEV float f8_to_f32(uint8_t b) {
+  const uint32_t s = (b & 0x80u) << 24;
+  if constexpr (FMT == 0) {
+    const uint32_t e = (b >> 3) & 15, m = b & 7;
+    if (e == 15 && m == 7) return __uint_as_float(0x7fc00000u | s);
+    if (e == 0) return __uint_as_float(s) + (s ? -1.f : 1.f) * (float)m * 0x1p-9f;
+    return __uint_as_float(s | ((e + 120) << 23) | (m << 20));
+  } else {
+    const uint32_t e = (b >> 2) & 31, m = b & 3;
+    if (e == 31) return __uint_as_float(s | 0x7f800000u | (m ? 0x400000u : 0u));
+    if (e == 0) return __uint_as_float(s) + (s ? -1.f : 1.f) * (float)m * 0x1p-16f;
+    return __uint_as_float(s | ((e + 112) << 23) | (m << 21));
+  }
+}
+
+// Any shape and either B layout: one thread per output, fp32 accumulation in k order.
+template <int FMT, bool TRANS_B, int OUT>
+__global__ __launch_bounds__(256) void gemm8_generic(const uint8_t* __restrict__ A,
+                                                     const uint8_t* __restrict__ B,
+                                                     void* __restrict__ C, int M, int N, int K) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx % N);
+  float s = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float a = f8_to_f32<FMT>(A[(int64_t)m * K + k]);
+    const float b = f8_to_f32<FMT>(TRANS_B ? B[(int64_t)n * K + k] : B[(int64_t)k * N + n]);
+    s = fmaf(a, b, s);
+  }
+  store_out<OUT>(C, idx, s);
+}
+
+template <int FMT, int OUT>
+int launch(const void* A, const void* B, void* C, int M, int N, int K, bool trans_b,
+           hipStream_t s) {
+  // 32-bit LDS-DMA offsets within a 256-row panel: K < 2^24
+  const bool tiled = trans_b && M > 16 && K % 16 == 0 && K < (1 << 24) && tlm_aligned(A, 16) &&
+                     tlm_aligned(B, 16);
+  if (tiled) {
+    const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    gemm8_256x256<FMT, OUT><<<(unsigned)tiles, NTHREADS, 0, s>>>(
+        (const uint8_t*)A, (const uint8_t*)B, C, M, N, K);
+  } else {
+    const int64_t n = (int64_t)M * N;
+    if (trans_b)
+      gemm8_generic<FMT, true, OUT><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+          (const uint8_t*)A, (const uint8_t*)B, C, M, N, K);
+    else
+      gemm8_generic<FMT, false, OUT><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+          (const uint8_t*)A, (const uint8_t*)B, C, M, N, K);
+  }
+  TLM_LAUNCH_CHECK("tlm_gemm_fp8");
+  return TLM_OK;
+}
+
+template <int FMT>
+int by_out(const void* A, const void* B, void* C, int M, int N, int K, bool tb, int out,
+           hipStream_t s) {
+  switch (out) {
+    case TLM_F32: return launch<FMT, TLM_F32>(A, B, C, M, N, K, tb, s);
+    case TLM_F16: return launch<FMT, TLM_F16>(A, B, C, M, N, K, tb, s);
+    case TLM_BF16: return launch<FMT, TLM_BF16>(A, B, C, M, N, K, tb, s);
+    case TLM_F8E4M3: return launch<FMT, TLM_F8E4M3>(A, B, C, M, N, K, tb, s);
+    default: return launch<FMT, TLM_F8E5M2>(A, B, C, M, N, K, tb, s);
+  }
+}
+
+}  // namespace
+
+extern "C" int tlm_gemm_fp8(const void* A, const void* B, void* C, int64_t M, int64_t N,
+                            int64_t K, int in_dtype, int out_dtype, int trans_b, void* stream) {
+  if (!A || !B || !C) {
+    tlm_set_error("tlm_gemm_fp8: null pointer argument");
+    return TLM_EINVAL;
+  }
+  if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX ||
+      M * N > ((int64_t)1 << 40) || (M > 0 && K > 0 && (M - 1) * K + K > INT32_MAX) ||
+      (N > 0 && K > 0 && (N - 1) * K + K > INT32_MAX)) {
+    tlm_set_error("tlm_gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                  (long long)K);
+    return TLM_EINVAL;
+  }
+  if (trans_b != 0 && trans_b != 1) {
+    tlm_set_error("tlm_gemm_fp8: trans_b must be 0 or 1");
+    return TLM_EINVAL;
+  }
+  if (in_dtype != TLM_F8E4M3 && in_dtype != TLM_F8E5M2) {
+    tlm_set_error("tlm_gemm_fp8: in_dtype %d unsupported (F8E4M3 or F8E5M2)", in_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  if (out_dtype != TLM_F32 && out_dtype != TLM_F16 && out_dtype != TLM_BF16 &&
+      out_dtype != in_dtype) {
+    tlm_set_error("tlm_gemm_fp8: out_dtype %d unsupported (F32, F16, BF16 or the input format)",
+                  out_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  const int osz =
+      out_dtype == TLM_F32 ? 4 : (out_dtype == TLM_F16 || out_dtype == TLM_BF16) ? 2 : 1;
+  if (!tlm_aligned(C, osz)) {
+    tlm_set_error("tlm_gemm_fp8: misaligned C");
+    return TLM_EINVAL;
+  }
+  if (M == 0 || N == 0) return TLM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  return in_dtype == TLM_F8E4M3 ? by_out<0>(A, B, C, m, n, k, trans_b != 0, out_dtype, s)
+                                : by_out<1>(A, B, C, m, n, k, trans_b != 0, out_dtype, s);
+}

@@ -14,7 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _DEFAULT = os.path.normpath(os.path.join(_HERE, "..", "..", "..", "lib", "libtlmi355x.so"))
 
 # enum tlm_dtype
-F16, BF16, F32, F8E4M3, I32 = 0, 1, 2, 3, 4
+F16, BF16, F32, F8E4M3, I32, F8E5M2 = 0, 1, 2, 3, 4, 5
 
 _lock = threading.Lock()
 _lib = None
@@ -32,6 +32,7 @@ _SIGNATURES = {
     "tlm_swiglu": ([c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p], c_int),
     "tlm_rope": ([c_void_p] * 6 + [c_int64] * 4 + [c_int, c_void_p], c_int),
     "tlm_gemm": ([c_void_p] * 3 + [c_int64] * 3 + [c_int] * 3 + [c_void_p], c_int),
+    "tlm_gemm_fp8": ([c_void_p] * 3 + [c_int64] * 3 + [c_int] * 3 + [c_void_p], c_int),
     "tlm_flash_attn_fwd": ([c_void_p] * 4 + [c_int64] * 4 + [c_int, c_float, c_int, c_void_p],
                            c_int),
     "tlm_flash_attn_fwd_ex": ([c_void_p] * 4 + [c_int64] * 5 +

@@ -11,7 +11,8 @@ import torch
 from . import lib
 
 _DT = {torch.float16: lib.F16, torch.bfloat16: lib.BF16, torch.float32: lib.F32,
-       torch.float8_e4m3fn: lib.F8E4M3, torch.int32: lib.I32}
+       torch.float8_e4m3fn: lib.F8E4M3, torch.float8_e5m2: lib.F8E5M2, torch.int32: lib.I32}
+_FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
 def dtype_code(dt: torch.dtype) -> int:
@@ -143,8 +144,9 @@ def gemm(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, trans_b: bool = Fals
         raise ValueError(f"shape mismatch A{tuple(a.shape)} B{tuple(b.shape)} C{tuple(c.shape)}")
     if a.dtype != b.dtype:
         raise ValueError("A and B must share a dtype")
-    lib.call("tlm_gemm", _ptr(a), _ptr(b), _ptr(c), M, N, K, dtype_code(a.dtype),
-             dtype_code(c.dtype), 1 if trans_b else 0, _stream(dev))
+    fn = "tlm_gemm_fp8" if a.dtype in _FP8 else "tlm_gemm"
+    lib.call(fn, _ptr(a), _ptr(b), _ptr(c), M, N, K, dtype_code(a.dtype), dtype_code(c.dtype),
+             1 if trans_b else 0, _stream(dev))
     return c
 
 

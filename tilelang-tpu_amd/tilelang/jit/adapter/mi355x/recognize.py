@@ -12,7 +12,8 @@ Families and the reference programs they accept:
            optional weight parameter) and the split-K programs rmsnorm_splitk_{fp16,bf16,
            fp32}.py:9-47 (row sum accumulated over column blocks)
   gemm     tpu_demo/matmul/tpu_test_matmul_fp16.py:9-31 (+ bf16 / fp32-out variants, and
-           tpu_test_matmul_fp32.py: fp32 A/B copied to fp16 tiles before ppl_gemm)
+           tpu_test_matmul_fp32.py: fp32 A/B copied to fp16 tiles before ppl_gemm) and the
+           fp8 programs examples/gemm_fp8/example_tilelang_gemm_fp8{,_2xAcc}.py
   rope     tpu_demo/tpu_test_rope_bf16.py:5-51 (4 params; fp16 / fp32 twins and tpu_test_rope.py)
            and a fused q+k form (6 params)
   swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54 (+ tpu_test_swiglu_fp32.py)
@@ -274,7 +275,17 @@ def _gemm(pf, names) -> Plan:
         _fail(fam, "transpose_A is not supported")
     A = _source_param(pf, _buf(g[0].args[0]))
     B = _source_param(pf, _buf(g[0].args[1]))
-    C = _sink_param(pf, _buf(g[0].args[2]))
+    acc = _buf(g[0].args[2])
+    C = _sink_param(pf, acc)
+    if C is None:
+        # the accumulator folded into a second fragment by element stores before the copy-out
+        # (examples/gemm_fp8/example_tilelang_gemm_fp8_2xAcc.py:36-44)
+        for op in _ops(pf, ("store",)):
+            v = op.args[2]
+            if isinstance(v, Expr) and any(e.op == "load" and e.args[0] is acc for e in v.walk()):
+                C = _sink_param(pf, op.args[0])
+                if C is not None:
+                    break
     if A is None or B is None or C is None:
         _fail(fam, "could not trace A, B and C through the tile copies")
     M, K = _shape(A)
@@ -286,13 +297,17 @@ def _gemm(pf, names) -> Plan:
         _fail(fam, f"shapes A{_shape(A)} B{_shape(B)} C{_shape(C)} do not chain")
     # dtype of the tiles the gemm multiplies (fp32 programs copy their tiles to fp16 first)
     ta_dt, tb_dt = _buf(g[0].args[0]).dtype, _buf(g[0].args[1]).dtype
-    if ta_dt != tb_dt or ta_dt not in ("float16", "bfloat16"):
-        _fail(fam, f"matrix tiles must both be float16 or both bfloat16 (got {ta_dt}, {tb_dt})")
-    if A.dtype != B.dtype or A.dtype not in ("float16", "bfloat16", "float32"):
-        _fail(fam, "A and B must share a dtype: float16, bfloat16, or float32 cast to the tiles")
+    fp8 = ("float8_e4m3", "float8_e5m2")
+    if ta_dt != tb_dt or ta_dt not in ("float16", "bfloat16") + fp8:
+        _fail(fam, f"matrix tiles must be float16, bfloat16 or fp8 pairs (got {ta_dt}, {tb_dt})")
+    if A.dtype != B.dtype or A.dtype not in ("float16", "bfloat16", "float32") + fp8:
+        _fail(fam, "A and B must share a dtype: float16, bfloat16, fp8, or float32 cast to the "
+                   "tiles")
     if A.dtype != "float32" and A.dtype != ta_dt:
         _fail(fam, f"A is {A.dtype} but the gemm multiplies {ta_dt} tiles")
-    if C.dtype not in ("float16", "bfloat16", "float32"):
+    if A.dtype in fp8 and C.dtype not in ("float16", "bfloat16", "float32", A.dtype):
+        _fail(fam, f"fp8 GEMM output {C.dtype} (float32, float16, bfloat16 or {A.dtype})")
+    if A.dtype not in fp8 and C.dtype not in ("float16", "bfloat16", "float32"):
         _fail(fam, f"C dtype {C.dtype}")
     return Plan(fam, pf.params, [_index(pf, C)], dict(
         a=_index(pf, A), b=_index(pf, B), c=_index(pf, C), M=M, N=N, K=K, trans_b=bool(tb),

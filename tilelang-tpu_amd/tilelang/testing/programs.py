@@ -134,6 +134,45 @@ def matmul(M, N, K, block_M, block_N, block_K, dtype="float16", out_dtype="float
     return gemm
 
 
+def matmul_fp8(M, N, K, block_M=128, block_N=128, block_K=64, dtype="e4m3_float8",
+               out_dtype=None, two_acc=False):
+    """examples/gemm_fp8/example_tilelang_gemm_fp8.py:17-37 (C in the fp8 input type) and, with
+    two_acc, example_tilelang_gemm_fp8_2xAcc.py:10-50 (fp32 C; the gemm accumulates into a
+    fragment that is added into a second one every 128 / block_K k-tiles)."""
+    out_dtype = out_dtype or ("float" if two_acc else dtype)
+    update_interval = 128 // block_K if block_K < 128 else 1
+
+    @T.prim_func
+    def main(A: T.Tensor((M, K), dtype), B: T.Tensor((N, K), dtype),
+             C: T.Tensor((M, N), out_dtype)):
+        with T.Kernel(T.ceildiv(N, block_N), T.ceildiv(M, block_M), threads=128) as (bx, by):
+            A_shared = T.alloc_shared((block_M, block_K), dtype)
+            B_shared = T.alloc_shared((block_N, block_K), dtype)
+            C_local = T.alloc_fragment((block_M, block_N), "float")
+            if two_acc:
+                C_shared = T.alloc_shared((block_M, block_N), "float")
+                C_acc = T.alloc_fragment((block_M, block_N), "float")
+                T.clear(C_acc)
+            T.clear(C_local)
+            k_iters = T.ceildiv(K, block_K)
+            for k in T.Pipelined(k_iters, num_stages=3):
+                T.copy(A[by * block_M, k * block_K], A_shared)
+                T.copy(B[bx * block_N, k * block_K], B_shared)
+                T.gemm(A_shared, B_shared, C_local, transpose_B=True)
+                if two_acc:
+                    if (k + 1) % update_interval == 0:
+                        for i, j in T.Parallel(block_M, block_N):
+                            C_acc[i, j] += C_local[i, j]
+                        T.clear(C_local)
+            if two_acc:
+                T.copy(C_acc, C_shared)
+                T.copy(C_shared, C[by * block_M, bx * block_N])
+            else:
+                T.copy(C_local, C[by * block_M, bx * block_N])
+
+    return main
+
+
 def _rope_tile(x_src, cos_src, sin_src, dst, shape, dtype):
     x = T.alloc_shared(shape, dtype)
     c = T.alloc_shared(shape, dtype)
