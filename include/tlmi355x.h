@@ -41,6 +41,13 @@ enum tlm_dtype {
   TLM_F8E4M3 = 3, /* OCP e4m3fn (gfx950 native), not the FNUZ variant of gfx942 */
   TLM_I32 = 4,
   TLM_F8E5M2 = 5, /* OCP e5m2 */
+  TLM_U32 = 6,
+};
+
+/* Row reductions of tlm_row_reduce (ppl_reduce_max / ppl_reduce_sum). */
+enum tlm_reduce_op {
+  TLM_REDUCE_MAX = 0,
+  TLM_REDUCE_SUM = 1,
 };
 
 /* Error codes. The reference returns -1 (init), -2 (module load), 1 (launch)
@@ -110,6 +117,34 @@ int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_
  * nearest even without saturation, as torch's cast). */
 int tlm_gemm_fp8(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                  int in_dtype, int out_dtype, int trans_b, void* stream);
+
+/* Elementwise sigmoid y = 1 / (1 + exp(-x)) in fp32, one rounding for 16-bit y.
+ * Reference: tpu_demo/tpu_test_sigmoid_fp32.py:6-31 (T.ppl_sigmoid, fp32; customize.py:343-350),
+ * checked against torch.sigmoid (:48-60). dtype: F32 | F16 | BF16; n elements. */
+int tlm_sigmoid(const void* x, void* y, int64_t n, int dtype, void* stream);
+
+/* Row gather out[i, :] = param[index[i], :] (row_bytes bytes per row; any element type).
+ * Reference: tpu_demo/tpu_test_gather_fp32.py:8-18, T.ppl_gather (customize.py:352-356) ->
+ * tpu_gdma_h_gather_S2S (src/target/codegen_ppl.cc:1849-1877), param_h = param_rows, uint32
+ * indices. An index >= param_rows writes a zero row. */
+int tlm_gather_rows(const void* param, int64_t param_rows, int64_t row_bytes,
+                    const uint32_t* index, int64_t n_index, void* out, void* stream);
+
+/* Sort of a vector with its indices; the first k entries are the top k.
+ * Reference: tpu_demo/tpu_test_topk_fp32.py:6-18, T.ppl_topk (customize.py:358-362) ->
+ * tpu_hau_sort_natural_index(dst, dst_idx, src, length, K, descended) (codegen_ppl.cc:1878-1907),
+ * which writes `length` sorted entries. Order: by value (descending when `descending` != 0),
+ * ties by index, every NaN above +inf, -0.0 equal to +0.0 (torch.sort(stable=True)).
+ * dtype: F32 | I32 | U32; length <= 16384 (one workgroup, LDS bitonic sort). */
+int tlm_topk(const void* src, int64_t length, int64_t k, int descending, int dtype,
+             void* out_values, int32_t* out_indices, void* stream);
+
+/* Row reduction y[r] = max_c / sum_c x[r, c] (op TLM_REDUCE_MAX | TLM_REDUCE_SUM).
+ * Reference: tpu_demo/tpu_test_reduce_max.py, tpu_test_reduce_sum.py (X [M, N] -> Y [M, 1],
+ * T.ppl_reduce_max / ppl_reduce_sum, customize.py:476-573). Sum in fp32, rounded once; max
+ * propagates NaN. in_dtype, out_dtype: F32 | F16 | BF16. */
+int tlm_row_reduce(const void* x, void* y, int64_t rows, int64_t cols, int op, int in_dtype,
+                   int out_dtype, void* stream);
 
 /* Element-type conversion of n contiguous values, the cast of a ppl_copy between tiles of
  * different dtypes (src/target/codegen_ppl.cc:1138-1152): F32 -> F16 | BF16 rounds to nearest

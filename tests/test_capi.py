@@ -26,7 +26,7 @@ def test_header_declares_entry_points():
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
               "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex",
-              "tlm_gemm_fp8"):
+              "tlm_gemm_fp8", "tlm_sigmoid", "tlm_gather_rows", "tlm_topk", "tlm_row_reduce"):
         assert s in syms
 
 
@@ -86,6 +86,25 @@ def test_gemm_fp8_validation():
     assert L.tlm_gemm_fp8(p, p, p, 16, 16, 16, lib.F8E4M3, lib.F8E5M2, 1, None) == -2
     assert L.tlm_gemm_fp8(p, p, p, 16, 16, 16, lib.F8E4M3, lib.F32, 2, None) == -1
     assert L.tlm_gemm_fp8(p, p, p, 0, 16, 16, lib.F8E5M2, lib.F8E5M2, 1, None) == 0
+
+
+def test_ppl_ops_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    assert L.tlm_sigmoid(None, p, 8, lib.F32, None) == -1
+    assert L.tlm_sigmoid(p, p, 8, lib.I32, None) == -2
+    assert L.tlm_sigmoid(p, p, 0, lib.F32, None) == 0
+    assert L.tlm_gather_rows(p, 10, 256, None, 4, p, None) == -1
+    assert L.tlm_gather_rows(p, 10, 3, p, 4, p, None) == -1  # odd row bytes
+    assert L.tlm_gather_rows(p, 10, 256, p, 0, p, None) == 0
+    assert L.tlm_topk(p, 100, 101, 1, lib.F32, p, p, None) == -1  # k > length
+    assert L.tlm_topk(p, 100, 8, 1, lib.F16, p, p, None) == -2
+    assert L.tlm_topk(p, 16385, 8, 1, lib.F32, p, p, None) == -2  # one-workgroup limit
+    assert "limit" in _err()
+    assert L.tlm_topk(p, 0, 0, 1, lib.U32, p, p, None) == 0
+    assert L.tlm_row_reduce(p, p, 4, 4, 7, lib.F16, lib.F16, None) == -1  # unknown op
+    assert L.tlm_row_reduce(p, p, 4, 4, lib.REDUCE_MAX, lib.I32, lib.F16, None) == -2
+    assert L.tlm_row_reduce(p, p, 0, 4, lib.REDUCE_SUM, lib.F16, lib.F32, None) == 0
 
 
 def test_cast_validation():

@@ -83,7 +83,7 @@ def test_unsupported_program_rejected():
         with T.Kernel(1, is_cpu=True) as (bx,):
             a = T.alloc_shared((64, 64), "float32")
             T.ppl_copy(A[0, 0], a)
-            T.ppl_sigmoid(a, a)
+            T.ppl_rsqrt(a, a)  # an elementwise rsqrt alone is no kernel family
             T.ppl_copy(a, B[0, 0])
 
     with pytest.raises(UnsupportedProgram, match="no gfx950 kernel"):
@@ -125,6 +125,16 @@ def test_unsupported_variants_have_clear_errors():
                                                               dtype="float32",
                                                               gemm_dtype="float16"),
      dict(dtype="float32", D=8, operand_dtype="float16")),
+    ("tpu_test_sigmoid_fp32.py", lambda: programs.sigmoid(32, 32, 1024, 1024),
+     dict(dtype="float32", n=1024 * 1024)),
+    ("tpu_test_gather_fp32.py", lambda: programs.gather(128, 64, 8),
+     dict(rows=128, hidden=64, n=8, dtype="float32")),
+    ("tpu_test_topk_fp32.py", lambda: programs.topk(1024, 8),
+     dict(k=8, descending=True, length=1024)),
+    ("tpu_test_reduce_max.py", lambda: programs.row_reduce(64, 64, 32, 64, "max"),
+     dict(op="max", rows=64, cols=64)),
+    ("tpu_test_reduce_sum.py", lambda: programs.row_reduce(64, 64, 32, 64, "sum"),
+     dict(op="sum", in_dtype="float16")),
 ])
 def test_demo_variants_recognised(name, prog, attrs):
     """The remaining tpu_demo programs (fp32 / fp16 twins, split-K RMSNorm) map to a family."""

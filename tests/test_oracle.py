@@ -369,3 +369,54 @@ def test_gemm_fp8_ref_against_fp64_brute_force(dt):
     q = ref.gemm_fp8_ref(a, b, out_dtype=dt).float().numpy()
     e8 = torch.from_numpy(exp).float().to(dt).float().numpy()
     assert (q == e8).mean() > 0.97
+
+
+def test_sigmoid_ref_closed_form():
+    """sigmoid against the fp64 closed form 1 / (1 + e^-x), its symmetry and s(0) = 1/2."""
+    x = torch.linspace(-30, 30, 2001)
+    exp = 1.0 / (1.0 + np.exp(-x.double().numpy()))
+    assert np.allclose(ref.sigmoid_ref(x).double().numpy(), exp, rtol=1e-6, atol=1e-7)
+    assert float(ref.sigmoid_ref(torch.zeros(1))[0]) == 0.5
+    assert torch.allclose(ref.sigmoid_ref(-x), 1 - ref.sigmoid_ref(x), atol=1e-6)
+
+
+def test_gather_ref_against_loop():
+    g = torch.Generator().manual_seed(33)
+    param = torch.randn(10, 5, generator=g)
+    index = torch.tensor([[3], [0], [9], [10], [-1], [3]], dtype=torch.int32)  # 10, -1: out of range
+    got = ref.gather_ref(param, index)
+    for i, v in enumerate(index.view(-1).tolist()):
+        u = v & 0xFFFFFFFF
+        exp = param[u] if u < 10 else torch.zeros(5)
+        assert torch.equal(got[i], exp)
+
+
+@pytest.mark.parametrize("descending", [True, False])
+def test_topk_ref_against_python_sort(descending):
+    """Full stable order with ties, NaN (above every number) and -0.0 == +0.0, checked against
+    Python's sorted() with an explicit (value class, value, index) key."""
+    vals = [1.5, -0.0, float("nan"), 0.0, 2.0, 1.5, float("-inf"), float("inf"), -3.0, 0.0,
+            float("nan"), 1.5]
+    src = torch.tensor(vals, dtype=torch.float32)
+    got_v, got_i = ref.topk_ref(src, descending)
+
+    def key(i):
+        v = vals[i]
+        cls = 1 if math.isnan(v) else 0
+        val = 0.0 if math.isnan(v) else v
+        return (-cls, -val, i) if descending else (cls, val, i)
+
+    order = sorted(range(len(vals)), key=key)
+    assert got_i.tolist() == order
+    assert torch.equal(got_v.view(torch.int32), src[order].view(torch.int32))
+    u = torch.tensor([5, 0, 4294967295, 7, 5], dtype=torch.int64).to(torch.uint32)
+    uv, ui = ref.topk_ref(u, descending)
+    uorder = sorted(range(5), key=lambda i: ((-1 if descending else 1) * [5, 0, 4294967295, 7, 5][i], i))
+    assert ui.tolist() == uorder
+
+
+def test_row_reduce_ref():
+    x = torch.tensor([[1.0, -2.0, 3.5], [float("nan"), 1.0, 2.0]])
+    assert ref.row_reduce_ref(x, "max").view(-1)[0] == 3.5
+    assert torch.isnan(ref.row_reduce_ref(x, "max").view(-1)[1])
+    assert ref.row_reduce_ref(x, "sum").view(-1)[0] == 2.5

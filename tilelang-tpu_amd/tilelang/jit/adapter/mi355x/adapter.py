@@ -39,6 +39,14 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     elif f == "flashattn":
         ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"],
                            operand_dtype=odt)
+    elif f == "sigmoid":
+        ops.sigmoid(t[a["x"]], t[a["y"]])
+    elif f == "gather":
+        ops.gather_rows(t[a["param"]], t[a["index"]], t[a["out"]])
+    elif f == "topk":
+        ops.topk(t[a["src"]], a["k"], a["descending"], t[a["values"]], t[a["indices"]])
+    elif f == "row_reduce":
+        ops.row_reduce(t[a["x"]], t[a["y"]], a["op"])
     elif f == "mla":
         q = t[a["q"]]
         dev = q.device

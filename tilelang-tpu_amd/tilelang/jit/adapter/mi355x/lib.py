@@ -14,7 +14,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _DEFAULT = os.path.normpath(os.path.join(_HERE, "..", "..", "..", "lib", "libtlmi355x.so"))
 
 # enum tlm_dtype
-F16, BF16, F32, F8E4M3, I32, F8E5M2 = 0, 1, 2, 3, 4, 5
+F16, BF16, F32, F8E4M3, I32, F8E5M2, U32 = 0, 1, 2, 3, 4, 5, 6
+REDUCE_MAX, REDUCE_SUM = 0, 1
 
 _lock = threading.Lock()
 _lib = None
@@ -38,6 +39,12 @@ _SIGNATURES = {
     "tlm_flash_attn_fwd_ex": ([c_void_p] * 4 + [c_int64] * 5 +
                               [c_int, c_float, c_int, c_int, c_void_p], c_int),
     "tlm_cast": ([c_void_p, c_int, c_void_p, c_int, c_int64, c_void_p], c_int),
+    "tlm_sigmoid": ([c_void_p, c_void_p, c_int64, c_int, c_void_p], c_int),
+    "tlm_gather_rows": ([c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p],
+                        c_int),
+    "tlm_topk": ([c_void_p, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p], c_int),
+    "tlm_row_reduce": ([c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p],
+                       c_int),
     "tlm_mla_decode": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                         c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
                        [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int, c_void_p], c_int),

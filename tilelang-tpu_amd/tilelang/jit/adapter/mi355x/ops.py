@@ -11,7 +11,8 @@ import torch
 from . import lib
 
 _DT = {torch.float16: lib.F16, torch.bfloat16: lib.BF16, torch.float32: lib.F32,
-       torch.float8_e4m3fn: lib.F8E4M3, torch.float8_e5m2: lib.F8E5M2, torch.int32: lib.I32}
+       torch.float8_e4m3fn: lib.F8E4M3, torch.float8_e5m2: lib.F8E5M2, torch.int32: lib.I32,
+       torch.uint32: lib.U32}
 _FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
@@ -174,6 +175,65 @@ def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float,
              1 if causal else 0, float(sm_scale), dtype_code(q.dtype), dtype_code(o.dtype),
              _stream(dev))
     return o
+
+
+def sigmoid(x: torch.Tensor, y: torch.Tensor):
+    """y = sigmoid(x), fp32 math."""
+    dev = _dev(x, y)
+    _contig("x", x)
+    _contig("y", y)
+    if x.shape != y.shape or x.dtype != y.dtype:
+        raise ValueError("x and y must share shape and dtype")
+    lib.call("tlm_sigmoid", _ptr(x), _ptr(y), x.numel(), dtype_code(x.dtype), _stream(dev))
+    return y
+
+
+def gather_rows(param: torch.Tensor, index: torch.Tensor, out: torch.Tensor):
+    """out[i, :] = param[index[i], :] (index uint32 or int32, read as unsigned; an index past the
+    last row gives a zero row)."""
+    dev = _dev(param, index, out)
+    for n, t in (("param", param), ("index", index), ("out", out)):
+        _contig(n, t)
+    if param.dim() != 2 or out.dim() != 2 or out.shape[1] != param.shape[1]:
+        raise ValueError("param [rows, H] and out [n, H] must share H")
+    if index.dtype not in (torch.int32, torch.uint32) or index.numel() != out.shape[0]:
+        raise ValueError("index must hold one int32 / uint32 per output row")
+    if out.dtype != param.dtype:
+        raise ValueError("out must have param's dtype")
+    lib.call("tlm_gather_rows", _ptr(param), param.shape[0], param.shape[1] * param.element_size(),
+             _ptr(index), index.numel(), _ptr(out), _stream(dev))
+    return out
+
+
+def topk(src: torch.Tensor, k: int, descending: bool, values: torch.Tensor,
+         indices: torch.Tensor):
+    """Sort src (1-D) with its indices into values / indices; the first k are the top k."""
+    dev = _dev(src, values, indices)
+    for n, t in (("src", src), ("values", values), ("indices", indices)):
+        _contig(n, t)
+    L = src.numel()
+    if values.numel() != L or indices.numel() != L or values.dtype != src.dtype:
+        raise ValueError("values and indices must have src's length (and values its dtype)")
+    if indices.dtype != torch.int32:
+        raise ValueError("indices must be int32")
+    lib.call("tlm_topk", _ptr(src), L, int(k), 1 if descending else 0, dtype_code(src.dtype),
+             _ptr(values), _ptr(indices), _stream(dev))
+    return values, indices
+
+
+def row_reduce(x: torch.Tensor, y: torch.Tensor, op: str):
+    """y[r] = max / sum over the last dim of x (op "max" or "sum")."""
+    dev = _dev(x, y)
+    _contig("x", x)
+    _contig("y", y)
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if y.numel() != rows:
+        raise ValueError(f"y must hold one value per row ({rows})")
+    code = {"max": lib.REDUCE_MAX, "sum": lib.REDUCE_SUM}[op]
+    lib.call("tlm_row_reduce", _ptr(x), _ptr(y), rows, cols, code, dtype_code(x.dtype),
+             dtype_code(y.dtype), _stream(dev))
+    return y
 
 
 def mla_workspace_bytes(B, Hq, dv, num_split) -> int:

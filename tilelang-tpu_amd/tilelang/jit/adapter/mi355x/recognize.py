@@ -20,6 +20,10 @@ Families and the reference programs they accept:
   flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, and fp32 with fp16
            matrix tiles) and the upstream examples/flash_attention/example_mha_fwd_bshd.py:30-151
            structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178)
+  sigmoid  tpu_demo/tpu_test_sigmoid_fp32.py:6-31 (ppl_sigmoid)
+  gather   tpu_demo/tpu_test_gather_fp32.py:8-18 (ppl_gather)
+  topk     tpu_demo/tpu_test_topk_fp32.py:6-18 (ppl_topk)
+  row_reduce tpu_demo/tpu_test_reduce_max.py, tpu_test_reduce_sum.py
   mla      examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split and no-split forms),
            with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV
 """
@@ -489,6 +493,79 @@ def _mla(pf, names) -> Plan:
         q_dtype=Q.dtype, kv_dtype=KV.dtype, o_dtype=O.dtype))
 
 
+def _sigmoid(pf, names) -> Plan:
+    fam = "sigmoid"
+    op = next(_ops(pf, ("ppl_sigmoid",)))
+    x = _source_param(pf, _buf(op.args[1]))
+    y = _sink_param(pf, _buf(op.args[0]))
+    if x is None or y is None or _shape(x) != _shape(y):
+        _fail(fam, "expected one input and one output of the same shape")
+    if x.dtype != y.dtype or x.dtype not in ("float32", "float16", "bfloat16"):
+        _fail(fam, f"dtypes {x.dtype} -> {y.dtype} (float32, float16 or bfloat16, matching)")
+    return Plan(fam, pf.params, [_index(pf, y)], dict(
+        x=_index(pf, x), y=_index(pf, y), n=math.prod(_shape(x)), dtype=x.dtype))
+
+
+def _gather(pf, names) -> Plan:
+    fam = "gather"
+    op = next(_ops(pf, ("ppl_gather",)))
+    out, param, index = (_buf(a) for a in op.args[:3])
+    if None in (out, param, index) or any(b.scope != "global" for b in (out, param, index)):
+        _fail(fam, "expected ppl_gather on global Output, Param and Index tensors")
+    param_h = int(_const(op.args[3]))
+    ps, os_, is_ = _shape(param), _shape(out), _shape(index)
+    if len(ps) != 2 or len(os_) != 2 or os_[1] != ps[1] or math.prod(is_) != os_[0]:
+        _fail(fam, f"shapes Param{ps} Index{is_} Output{os_} do not match a row gather")
+    if param_h != ps[0]:
+        _fail(fam, f"param_h {param_h} is not Param's row count {ps[0]}")
+    if index.dtype not in ("uint32", "int32") or out.dtype != param.dtype:
+        _fail(fam, "Index must be uint32 / int32 and Output share Param's dtype")
+    return Plan(fam, pf.params, [_index(pf, out)], dict(
+        param=_index(pf, param), index=_index(pf, index), out=_index(pf, out), rows=ps[0],
+        hidden=ps[1], n=os_[0], dtype=param.dtype))
+
+
+def _topk(pf, names) -> Plan:
+    fam = "topk"
+    op = next(_ops(pf, ("ppl_topk",)))
+    vals, idx, src = (_buf(a) for a in op.args[:3])
+    k, desc, length = (int(_const(a)) for a in op.args[3:6])
+    if None in (vals, idx, src):
+        _fail(fam, "expected ppl_topk on global tensors")
+    if math.prod(_shape(src)) != length or math.prod(_shape(vals)) != length or \
+            math.prod(_shape(idx)) != length:
+        _fail(fam, f"length {length} does not match the tensors")
+    if src.dtype not in ("float32", "int32", "uint32") or vals.dtype != src.dtype or \
+            idx.dtype != "int32":
+        _fail(fam, "src / values float32, int32 or uint32 and indices int32")
+    if not 0 <= k <= length:
+        _fail(fam, f"K = {k} outside [0, {length}]")
+    return Plan(fam, pf.params, [_index(pf, vals), _index(pf, idx)], dict(
+        src=_index(pf, src), values=_index(pf, vals), indices=_index(pf, idx), k=k,
+        descending=bool(desc), length=length, dtype=src.dtype))
+
+
+def _row_reduce(pf, names) -> Plan:
+    fam = "row_reduce"
+    reds = list(_ops(pf, ("ppl_reduce_max", "ppl_reduce_sum", "reduce_max", "reduce_sum")))
+    if len(reds) != 1 or reds[0].kwargs.get("dim", 1) not in (1, -1):
+        _fail(fam, "expected one row reduction over the last dim")
+    op = reds[0]
+    x = _source_param(pf, _buf(op.args[0]))
+    y = _sink_param(pf, _buf(op.args[1]))
+    if x is None or y is None:
+        _fail(fam, "could not trace X and Y through the tile copies")
+    xs, ys = _shape(x), _shape(y)
+    if math.prod(ys) != math.prod(xs[:-1]):
+        _fail(fam, f"Y{ys} does not hold one value per row of X{xs}")
+    if x.dtype not in ("float32", "float16", "bfloat16") or \
+            y.dtype not in ("float32", "float16", "bfloat16"):
+        _fail(fam, f"dtypes {x.dtype} -> {y.dtype}")
+    return Plan(fam, pf.params, [_index(pf, y)], dict(
+        x=_index(pf, x), y=_index(pf, y), op="max" if "max" in op.name else "sum",
+        rows=math.prod(xs[:-1]), cols=xs[-1], in_dtype=x.dtype, out_dtype=y.dtype))
+
+
 def recognize(pf) -> Plan:
     """Return the :class:`Plan` for ``pf`` or raise :class:`UnsupportedProgram`."""
     names = set(_op_names(pf))
@@ -507,10 +584,21 @@ def recognize(pf) -> Plan:
             return _rmsnorm(pf, names)
         if {"ppl_exp", "ppl_div"} <= names:
             return _swiglu(pf, names)
+        if "ppl_sigmoid" in names:
+            return _sigmoid(pf, names)
+        if "ppl_gather" in names:
+            return _gather(pf, names)
+        if "ppl_topk" in names:
+            return _topk(pf, names)
+        if n_gemm == 0 and len(names & {"ppl_reduce_max", "ppl_reduce_sum", "reduce_max",
+                                        "reduce_sum"}) == 1 and \
+                not names & {"ppl_exp", "ppl_rsqrt", "ppl_div", "ppl_mul"}:
+            return _row_reduce(pf, names)
     except UnsupportedProgram:
         raise
     except (TypeError, ValueError, IndexError) as e:  # malformed trace
         raise UnsupportedProgram(f"{pf.name}: could not analyse program: {e}") from e
     raise UnsupportedProgram(
         f"{pf.name}: no gfx950 kernel matches this program (ops: {sorted(names)}). Supported "
-        f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla")
+        f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla, sigmoid, gather, topk, "
+        f"row_reduce")

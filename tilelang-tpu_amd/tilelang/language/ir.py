@@ -48,6 +48,7 @@ _DTYPE_ALIASES = {
     "int64": "int64",
     "int8": "int8",
     "uint8": "uint8",
+    "uint32": "uint32",
     "bool": "bool",
     "float8_e4m3": "float8_e4m3",
     "float8_e4m3fn": "float8_e4m3",

@@ -173,6 +173,72 @@ def matmul_fp8(M, N, K, block_M=128, block_N=128, block_K=64, dtype="e4m3_float8
     return main
 
 
+def sigmoid(Block_w, Block_c, C, W, dtype="float32"):
+    """tpu_demo/tpu_test_sigmoid_fp32.py:6-31."""
+    shape = (C, W)
+
+    @T.prim_func
+    def main(G_in: T.Tensor(shape, dtype), G_out: T.Tensor(shape, dtype)):
+        with T.Kernel(T.ceildiv(C, Block_c), T.ceildiv(W, Block_w), is_cpu=True) as (bx, by):
+            tile = (Block_c, Block_w)
+            x = T.alloc_shared(tile, dtype)
+            out = T.alloc_shared(tile, dtype)
+            work0 = T.alloc_shared(tile, dtype)
+            work1 = T.alloc_shared(tile, dtype)
+            coeff = T.alloc_shared([64, 32], dtype)
+            table = T.alloc_shared([64, 192], dtype)
+            T.ppl_copy(G_in[bx * Block_c, by * Block_w], x)
+            T.ppl_sigmoid(out, x, work0, work1, coeff, table)
+            T.ppl_copy(out, G_out[bx * Block_c, by * Block_w])
+
+    return main
+
+
+def gather(num_rows, hidden_size, num_indices, dtype="float32"):
+    """tpu_demo/tpu_test_gather_fp32.py:8-18."""
+
+    @T.prim_func
+    def main(Param: T.Tensor((num_rows, hidden_size), dtype),
+             Index: T.Tensor((num_indices, 1), "uint32"),
+             Output: T.Tensor((num_indices, hidden_size), dtype)):
+        with T.Kernel(1, 1, is_cpu=True) as (bx, by):
+            T.ppl_gather(Output, Param, Index, num_rows)
+
+    return main
+
+
+def topk(length, K, descended=True, dtype="float32"):
+    """tpu_demo/tpu_test_topk_fp32.py:6-18."""
+
+    @T.prim_func
+    def main(Input: T.Tensor((length,), dtype), Output: T.Tensor((length,), dtype),
+             Indices: T.Tensor((length,), "int32")):
+        with T.Kernel(1, 1, is_cpu=True) as (bx, by):
+            T.ppl_topk(Output, Indices, Input, K, 1 if descended else 0, length)
+
+    return main
+
+
+def row_reduce(M, N, block_M, block_N, op="max", dtype="float16", accum_dtype="float16"):
+    """tpu_demo/tpu_test_reduce_max.py and tpu_test_reduce_sum.py."""
+
+    @T.prim_func
+    def main(X: T.Tensor((M, N), dtype), Y: T.Tensor((M, 1), accum_dtype)):
+        with T.Kernel(1, T.ceildiv(M, block_M), is_cpu=True) as (bx, by):
+            X_shared = T.alloc_shared((block_M, block_N), dtype)
+            Y_shared = T.alloc_shared((block_M, 1), accum_dtype)
+            if op == "sum":
+                T.ppl_fill(Y_shared, T.float32(0))
+            T.ppl_copy(X[by * block_M, 0], X_shared)
+            if op == "max":
+                T.ppl_reduce_max(X_shared, Y_shared, 1, True)
+            else:
+                T.ppl_reduce_sum(X_shared, Y_shared, 1)
+            T.ppl_copy(Y_shared, Y[by * block_M, 0])
+
+    return main
+
+
 def _rope_tile(x_src, cos_src, sin_src, dst, shape, dtype):
     x = T.alloc_shared(shape, dtype)
     c = T.alloc_shared(shape, dtype)

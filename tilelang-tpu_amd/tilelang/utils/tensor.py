@@ -28,6 +28,7 @@ _TORCH = {
     "int64": torch.int64,
     "int8": torch.int8,
     "uint8": torch.uint8,
+    "uint32": torch.uint32,
     "bool": torch.bool,
     "float8_e4m3": torch.float8_e4m3fn,
     "float8_e5m2": torch.float8_e5m2,
