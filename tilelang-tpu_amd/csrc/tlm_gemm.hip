@@ -23,6 +23,8 @@
 // Skinny kernel (M <= 16): see gemm_skinny below.
 #include "tlm_common.h"
 
+#include <type_traits>
+
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -162,9 +164,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = (K + BK - 1) / BK;
 
-  // ---- LDS-DMA fill: 8 wave-instructions of 1 KB per thread per k-tile (4 for A, 4 for B).
-  // Instruction d covers LDS slots [64 ins, 64 ins + 64) of its operand (ins = 4 wave + d % 4);
-  // lanes whose chunk lies outside A, B (rows against M / N, columns against K) read zeros.
+  // ---- LDS-DMA fill: a 32 KB stage is 32 wave-instructions of 1 KB; instruction `ins` covers
+  // LDS slots [64 ins, 64 ins + 64) of its operand. Lanes whose chunk lies outside A, B (rows
+  // against M / N, columns against K) read zeros.
   struct Dma {  // the k-tile's A and B base addresses and LDS destinations
     const uint16_t* base[2];
     uint8_t* st[2];
@@ -177,15 +179,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
                 TRANS_B ? B + ((int64_t)n0 * K + k0) : B + ((int64_t)k0 * N + n0)},
                {sa_of(kt), sb_of(kt)}};
   };
-  // kmax: number of valid k (columns for A / B^T, rows for row-major B) in this k-tile
-  auto dma = [&](const Dma& dd, int d, int kmax) {
-    const int ins = wave * 4 + (d & 3);
+  // kmax: number of valid k (columns for A / B^T, rows for row-major B) in this k-tile;
+  // op: 0 = A, 1 = B
+  auto dma = [&](const Dma& dd, auto OPc, int ins, int kmax) {
+    constexpr int op = decltype(OPc)::value;
     uint32_t off;
     bool ok;
-    if (d < 4 || TRANS_B) {  // [rows][64 k]: 8 rows of 128 bytes
+    if constexpr (op == 0 || TRANS_B) {  // [rows][64 k]: 8 rows of 128 bytes
       const int r = 8 * ins + (lane >> 3);
       const int c = (lane & 7) ^ swz_rows(r);
-      ok = (d < 4 ? m0 + r < M : n0 + r < N) && 8 * c < kmax;
+      ok = (op == 0 ? m0 + r < M : n0 + r < N) && 8 * c < kmax;
       off = (uint32_t)(r * K + 8 * c) * 2u;
     } else {  // row-major B [64 k][256 n]: 2 k-rows of 512 bytes
       const int k = 2 * ins + (lane >> 5);
@@ -193,17 +196,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
       ok = n0 + 8 * c < N && k < kmax;
       off = (uint32_t)(k * N + 8 * c) * 2u;
     }
-    uint8_t* dst = dd.st[d >> 2] + ins * 1024;
+    uint8_t* dst = dd.st[op] + ins * 1024;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)dd.base[d >> 2], (short)0, 0x7ffffff0, RSRC_WORD3);
+        (void*)dd.base[op], (short)0, 0x7ffffff0, RSRC_WORD3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
                                              ok ? off : OOB, 0, 0, 0);
   };
-  auto issue = [&](int kt) {
+  // a group's share of one operand stage: wave wl of the group issues instructions
+  // 8 wl .. 8 wl + 7
+  using OpA = std::integral_constant<int, 0>;
+  using OpB = std::integral_constant<int, 1>;
+  auto issue_op = [&](int kt, auto OPc) {
     const Dma dd = dma_setup(kt);
     const int kmax = min(BK, K - kt * BK);
 #pragma unroll
-    for (int d = 0; d < 8; ++d) dma(dd, d, kmax);
+    for (int j = 0; j < 8; ++j) dma(dd, OPc, 8 * (wave & 3) + j, kmax);
   };
 
   f32x16 acc[4][2];
@@ -227,10 +234,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   // k-tile apart: in each phase one of them issues MFMAs while the other reads the next k-tile's
   // A operands (all four k-steps) and first B operand from LDS into registers; the computing
   // wave reads B one k-step ahead. Group 0 loads k-tile kt in phase 2 kt and computes it in
-  // phase 2 kt + 1; group 1 is one phase later. Every phase ends with a workgroup barrier. Each
-  // thread's LDS-DMA of k-tile kt + 1 is issued at the start of phase 2 kt and has landed by the
-  // end of phase 2 kt + 1. A k-tile's A stage is read in phases 2 kt, 2 kt + 1 and its B stage
-  // through phase 2 kt + 2, hence 2 A stages and 3 B stages.
+  // phase 2 kt + 1; group 1 is one phase later. Every phase ends with a workgroup barrier.
+  // A k-tile's A stage is read in phases 2 kt, 2 kt + 1 and its B stage through phase 2 kt + 2,
+  // hence 2 A stages and 3 B stages. LDS-DMA is issued only in load phases, where the waves
+  // have no MFMAs to delay (issue stalls on the vector memory path, ~80 cycles per 1 KB
+  // instruction, measured ~700 cycles per phase when issued from a compute phase): group 0
+  // loads A of k-tile kt + 1 in phase 2 kt (its stage held A of kt - 1, read by phase 2 kt - 1),
+  // group 1 loads B of k-tile kt + 2 in phase 2 kt + 1 (its stage held B of kt - 1, read by
+  // phase 2 kt). A lands within two phases, B within three.
   const int grp = wave >> 2;
   u32x4 aop[BK / 16][4];  // A operands of a whole k-tile
   u32x4 bop[2][2];        // B operands of one k-step
@@ -250,17 +261,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
     }
   };
   constexpr int BREADS = TRANS_B ? 2 : 4;  // LDS instructions of readb()
-  // The CU's vector memory path takes ~1 KB per 16 cycles, so the 64 LDS-DMA instructions of a
-  // k-tile are interleaved with other work (two per k-step) instead of stalling a wave in a burst.
-  // dma_kt < 0: nothing to issue.
-  auto dma_pair = [&](const Dma& dd, int dma_kt, int ks) {
+  // The group's 8 LDS-DMA instructions of the phase go two per k-step between the operand
+  // reads instead of in one burst. dma_kt < 0: nothing to issue; op: operand of the group.
+  auto dma_pair = [&](const Dma& dd, int dma_kt, auto OPc, int ks) {
     if (dma_kt >= 0) {
       const int kmax = min(BK, K - dma_kt * BK);
-      dma(dd, 2 * ks, kmax);
-      dma(dd, 2 * ks + 1, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * ks, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * ks + 1, kmax);
     }
   };
-  auto load_phase = [&](int kt, int dma_kt) {
+  auto load_phase = [&](int kt, int dma_kt, auto OPc) {
     const uint8_t* sa = sa_of(kt);
     const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
 #pragma unroll
@@ -268,7 +278,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
         aop[ks][mi] = lds_b128(sa + a_row + mi * 32 * BK * 2 + 16 * ((2 * ks + hf) ^ sw));
-      dma_pair(dd, dma_kt, ks);
+      dma_pair(dd, dma_kt, OPc, ks);
     }
     readb(kt, 0, bop[0]);
     lgkm_wait(0);
@@ -279,8 +289,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
     order_after(bop[0][0]);
     order_after(bop[0][1]);
   };
-  auto compute_phase = [&](int kt, int dma_kt) {
-    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
+  auto compute_phase = [&](int kt) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       // B of k-step ks has landed; the reads of k-step ks + 1 stay in flight
@@ -298,34 +307,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
         for (int ni = 0; ni < 2; ++ni)
           acc[mi][ni] = MT::mma(__builtin_bit_cast(v8, aop[ks][mi]),
                                 __builtin_bit_cast(v8, bop[ks & 1][ni]), acc[mi][ni]);
-        if (mi == 1) {
-          __builtin_amdgcn_sched_barrier(0);
-          dma_pair(dd, dma_kt, ks);
-          __builtin_amdgcn_sched_barrier(0);
-        }
       }
     }
   };
-  issue(0);
+  // prologue: A of k-tile 0 (group 0), B of k-tiles 0 and 1 (group 1)
+  if (grp == 0) {
+    issue_op(0, OpA{});
+  } else {
+    issue_op(0, OpB{});
+    if (1 < KT) issue_op(1, OpB{});
+  }
   wait_dma();
   barrier_lds();
   if (grp == 0) {
     for (int kt = 0; kt < KT; ++kt) {
-      load_phase(kt, kt + 1 < KT ? kt + 1 : -1);  // phase 2 kt (+ this thread's DMA of kt + 1)
+      load_phase(kt, kt + 1 < KT ? kt + 1 : -1, OpA{});  // phase 2 kt (+ A of kt + 1)
       barrier_lds();
-      compute_phase(kt, -1);  // phase 2 kt + 1
-      wait_dma();
+      compute_phase(kt);  // phase 2 kt + 1
+      wait_dma();         // A of kt + 1 landed
       barrier_lds();
     }
     barrier_lds();  // phase 2 KT: group 1 computes the last k-tile
   } else {
-    if (1 < KT) issue(1);  // phase 0
-    barrier_lds();
+    barrier_lds();  // phase 0
     for (int kt = 0; kt < KT; ++kt) {
-      load_phase(kt, -1);  // phase 2 kt + 1
-      wait_dma();
+      const bool dma = kt + 2 < KT;
+      load_phase(kt, dma ? kt + 2 : -1, OpB{});  // phase 2 kt + 1 (+ B of kt + 2)
+      // B of kt + 1 (issued one load phase earlier, or in the prologue) has landed
+      __builtin_amdgcn_sched_barrier(0);
+      if (dma)
+        __builtin_amdgcn_s_waitcnt(0x3f78);  // vmcnt(8): this phase's 8 may stay in flight
+      else
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
       barrier_lds();
-      compute_phase(kt, kt + 2 < KT ? kt + 2 : -1);  // phase 2 kt + 2 (+ DMA of kt + 2)
+      compute_phase(kt);  // phase 2 kt + 2
       barrier_lds();
     }
   }
