@@ -12,8 +12,8 @@
 //     into unpadded, XOR-swizzled stages (2 for A, 3 for B: 160 KB); lanes whose chunk lies
 //     outside the matrix read zeros through the buffer descriptor's bounds;
 //   * the two waves on each SIMD (groups of 4) run half a k-tile apart: one reads the next
-//     k-tile's operands from LDS while the other issues MFMAs; each LDS-DMA instruction is
-//     issued between operand reads or MFMAs rather than in a burst;
+//     k-tile's operands from LDS while the other issues MFMAs; LDS-DMA is issued only by the
+//     reading group, between its operand reads (group 0 fills A stages, group 1 B stages);
 //   * the B operand (8 consecutive k of one column per lane) is read with ds_read_b64_tr_b16,
 //     which transposes 4x16 blocks of 16-bit values across each 16-lane group, so B needs no
 //     transpose in registers or in a separate pass;
