@@ -15,6 +15,8 @@
 // step, i.e. two 16-byte chunks of the row.
 #include "tlm_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int BM = 256, BN = 256, BKB = 128;  // BKB: k per tile = bytes per tile row
@@ -123,25 +125,29 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
     return Dma{{A + ((int64_t)m0 * K + k0), B + ((int64_t)n0 * K + k0)},
                {sa_of(kt), sb_of(kt)}};
   };
-  // instruction d (0..3 A, 4..7 B): 8 rows of 128 bytes; chunks beyond K or rows beyond M / N
-  // read zeros through the out-of-range offset
-  auto dma = [&](const Dma& dd, int d, int kmax) {
-    const int ins = wave * 4 + (d & 3);
+  // instruction ins (0..31) of operand op (0 = A, 1 = B): 8 rows of 128 bytes; chunks beyond K
+  // or rows beyond M / N read zeros through the out-of-range offset
+  auto dma = [&](const Dma& dd, auto OPc, int ins, int kmax) {
+    constexpr int op = decltype(OPc)::value;
     const int r = 8 * ins + (lane >> 3);
     const int c = (lane & 7) ^ swz_rows(r);
-    const bool ok = (d < 4 ? m0 + r < M : n0 + r < N) && 16 * c < kmax;
+    const bool ok = (op == 0 ? m0 + r < M : n0 + r < N) && 16 * c < kmax;
     const uint32_t off = (uint32_t)(r * K + 16 * c);
-    uint8_t* dst = dd.st[d >> 2] + ins * 1024;
+    uint8_t* dst = dd.st[op] + ins * 1024;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)dd.base[d >> 2], (short)0, 0x7ffffff0, RSRC_WORD3);
+        (void*)dd.base[op], (short)0, 0x7ffffff0, RSRC_WORD3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
                                              ok ? off : OOB, 0, 0, 0);
   };
-  auto issue = [&](int kt) {
+  // a group's share of one operand stage: wave wl of the group issues instructions
+  // 8 wl .. 8 wl + 7
+  using OpA = std::integral_constant<int, 0>;
+  using OpB = std::integral_constant<int, 1>;
+  auto issue_op = [&](int kt, auto OPc) {
     const Dma dd = dma_setup(kt);
     const int kmax = min(BKB, K - kt * BKB);
 #pragma unroll
-    for (int d = 0; d < 8; ++d) dma(dd, d, kmax);
+    for (int j = 0; j < 8; ++j) dma(dd, OPc, 8 * (wave & 3) + j, kmax);
   };
 
   f32x16 acc[4][2];
@@ -157,7 +163,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
 
   // Ping-pong of the two waves on each SIMD (groups of 4), as in gemm_256x256: one reads the
   // next k-tile's A operands (both 64-k steps) and its first B operands while the other issues
-  // MFMAs; every phase ends with a workgroup barrier.
+  // MFMAs; every phase ends with a workgroup barrier. LDS-DMA is issued only in load phases:
+  // group 0 fills A of k-tile kt + 1 in phase 2 kt (its stage held A of kt - 1, last read in
+  // phase 2 kt - 1), group 1 fills B of kt + 2 in phase 2 kt + 1 (its stage held B of kt - 1,
+  // last read in phase 2 kt), so each phase carries one 32 KB operand stage of DMA.
   const int grp = wave >> 2;
   u32x4 aop[2][4][2];  // [k-step][mi][chunk]
   u32x4 bop[2][2][2];  // [buffer][ni][chunk]
@@ -169,14 +178,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
 #pragma unroll
       for (int p = 0; p < 2; ++p) o[ni][p] = lds_b128(sb + b_row + ni * 32 * BKB + chunk(ks, p));
   };
-  auto dma_quad = [&](const Dma& dd, int dma_kt, int ks) {
+  // the wave's 8 instructions of the phase, 4 after each k-step's operand reads
+  auto dma_quad = [&](const Dma& dd, int dma_kt, auto OPc, int ks) {
     if (dma_kt >= 0) {
       const int kmax = min(BKB, K - dma_kt * BKB);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) dma(dd, 4 * ks + d, kmax);
+      for (int d = 0; d < 4; ++d) dma(dd, OPc, 8 * (wave & 3) + 4 * ks + d, kmax);
     }
   };
-  auto load_phase = [&](int kt, int dma_kt) {
+  auto load_phase = [&](int kt, int dma_kt, auto OPc) {
     const uint8_t* sa = sa_of(kt);
     const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
 #pragma unroll
@@ -186,7 +196,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
 #pragma unroll
         for (int p = 0; p < 2; ++p)
           aop[ks][mi][p] = lds_b128(sa + a_row + mi * 32 * BKB + chunk(ks, p));
-      dma_quad(dd, dma_kt, ks);
+      dma_quad(dd, dma_kt, OPc, ks);
     }
     readb(kt, 0, bop[0]);
     lgkm_wait<0>();
@@ -201,8 +211,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
 #pragma unroll
       for (int p = 0; p < 2; ++p) order_after(bop[0][ni][p]);
   };
-  auto compute_phase = [&](int kt, int dma_kt) {
-    const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
+  auto compute_phase = [&](int kt) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (ks == 0) {
@@ -221,34 +230,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
         for (int ni = 0; ni < 2; ++ni)
           acc[mi][ni] = mma8<FMT>(cat8(aop[ks][mi][0], aop[ks][mi][1]),
                                   cat8(bop[ks][ni][0], bop[ks][ni][1]), acc[mi][ni]);
-        if (mi == 1) {
-          __builtin_amdgcn_sched_barrier(0);
-          dma_quad(dd, dma_kt, ks);
-          __builtin_amdgcn_sched_barrier(0);
-        }
       }
     }
   };
-  issue(0);
+  // prologue: A of k-tile 0 (group 0), B of k-tiles 0 and 1 (group 1)
+  if (grp == 0) {
+    issue_op(0, OpA{});
+  } else {
+    issue_op(0, OpB{});
+    if (1 < KT) issue_op(1, OpB{});
+  }
   wait_dma();
   barrier_lds();
   if (grp == 0) {
     for (int kt = 0; kt < KT; ++kt) {
-      load_phase(kt, kt + 1 < KT ? kt + 1 : -1);
+      load_phase(kt, kt + 1 < KT ? kt + 1 : -1, OpA{});  // phase 2 kt (+ A of kt + 1)
       barrier_lds();
-      compute_phase(kt, -1);
-      wait_dma();
+      compute_phase(kt);  // phase 2 kt + 1
+      wait_dma();         // A of kt + 1 landed
       barrier_lds();
     }
-    barrier_lds();
+    barrier_lds();  // phase 2 KT: group 1 computes the last k-tile
   } else {
-    if (1 < KT) issue(1);
-    barrier_lds();
+    barrier_lds();  // phase 0
     for (int kt = 0; kt < KT; ++kt) {
-      load_phase(kt, -1);
-      wait_dma();
+      const bool dma = kt + 2 < KT;
+      load_phase(kt, dma ? kt + 2 : -1, OpB{});  // phase 2 kt + 1 (+ B of kt + 2)
+      // B of kt + 1 (issued one load phase earlier, or in the prologue) has landed
+      __builtin_amdgcn_sched_barrier(0);
+      if (dma)
+        __builtin_amdgcn_s_waitcnt(0x3f78);  // vmcnt(8): this phase's 8 may stay in flight
+      else
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+      __builtin_amdgcn_sched_barrier(0);
       barrier_lds();
-      compute_phase(kt, kt + 2 < KT ? kt + 2 : -1);
+      compute_phase(kt);  // phase 2 kt + 2
       barrier_lds();
     }
   }
