@@ -18,6 +18,7 @@ cpu_baseline = the oracle (restated reference torch path) on a bounded sample, t
 host's cores.
 """
 import argparse
+import itertools
 import json
 import math
 import os
@@ -417,6 +418,49 @@ def bench_flashattn_gqa(args, dev, flush, cpu):
     return res
 
 
+def bench_flashattn_varlen(args, dev, flush, cpu):
+    """examples/flash_attention/example_mha_fwd_varlen.py program structure (unpadded Q/K/V,
+    cu_seqlens, non-causal, fp16) at a prefill size: 16 sequences of U[512, 4096] tokens
+    (queries and keys of one sequence equally long), 32 heads, dim 128. Algorithmic FLOPs
+    = sum over sequences of 4 H D nq nk (the example's 2 matmuls, :372-373, per sequence)."""
+    import tilelang
+    from tilelang.testing import programs
+    B, H, D = 16, 32, 128
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 4097, (B,), generator=g).tolist()
+    cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32)
+    T = int(cu[-1])
+    q = torch.randn(T, H, D, generator=g).half()
+    kk = torch.randn(T, H, D, generator=g).half()
+    v = torch.randn(T, H, D, generator=g).half()
+    k = tilelang.compile(programs.flashattn_varlen(B, T, T, H, D), out_idx=-1)
+    flops = sum(4 * H * D * n * n for n in lens)
+    nbytes = 4 * T * H * D * 2
+    qd, kd, vd, cud = q.to(dev), kk.to(dev), v.to(dev), cu.to(dev)
+    o = torch.empty_like(qd)
+    fns = [lambda: k(qd, kd, vd, cud, cud, max(lens), o)]
+    pmc_launches(args, fns, "flashattn_varlen")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 10, flush)
+    res = {"workload": f"flashattn_varlen_fp16_b{B}h{H}d{D}_tokens{T}_full",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "dtype": "f16",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["fp16"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes, "seqlens": lens}
+    if cpu:
+        from oracle import ref
+        n0 = lens[0]
+        t = cpu_time(lambda: ref.flashattn_varlen_ref(q[:n0, :1], kk[:n0, :1], v[:n0, :1],
+                                                      cu[:2], cu[:2]), reps=1)
+        res["cpu_baseline"] = {"value": 4 * D * n0 * n0 / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"sequence 0 ({n0} tokens), head 0, "
+                                         "oracle.ref.flashattn_varlen_ref"}
+    return res
+
+
 def bench_mla(args, dev, flush, cpu):
     from tilelang.jit.adapter.mi355x import ops
     from tilelang.testing import workloads
@@ -532,12 +576,13 @@ BENCHES = {
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
     "flashattn_gqa": bench_flashattn_gqa,
+    "flashattn_varlen": bench_flashattn_varlen,
     "gemm_fp8": bench_gemm_fp8,
     "mla": bench_mla,
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "flashattn_gqa", "gemm_fp8", "mla", "kv_append"]
+         "flashattn_gqa", "flashattn_varlen", "gemm_fp8", "mla", "kv_append"]
 
 
 def main():

@@ -173,6 +173,26 @@ int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, 
                           int64_t S, int64_t H, int64_t H_kv, int64_t D, int causal,
                           float sm_scale, int in_dtype, int out_dtype, void* stream);
 
+/* Variable-length FlashAttention forward on unpadded sequences.
+ * Reference: examples/flash_attention/example_mha_fwd_varlen.py:222-358 (params Q_unpad,
+ * K_unpad, V_unpad, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, Output_unpad, :239-247).
+ *   q, o [total_q, H, D]; k, v [total_k, H_kv, D]; sequence b holds query rows
+ *   cu_seqlens_q[b] .. cu_seqlens_q[b + 1] - 1 and key rows cu_seqlens_k[b] .. [b + 1] - 1
+ *   (int32 [B + 1] device arrays, :267-276). Query i of a sequence attends to every key of its
+ *   sequence (the example's mask, :304-307); causal (extension) keeps key j <= i + nk - nq, the
+ *   bottom-right alignment of the file's construct_local_mask (:156-157). A query row with no
+ *   visible key gets zeros.
+ *   max_seqlen_q sizes the grid, as the example's T.ceildiv(max_seqlen_q, block_M) (:249):
+ *   queries at positions >= max_seqlen_q are not computed and their rows of o are left as
+ *   they were. A sequence whose rows fall outside [0, total_q) / [0, total_k) is skipped (o
+ *   untouched), so device-side offsets cannot address memory outside the tensors.
+ *   Other arguments as tlm_flash_attn_fwd_ex. */
+int tlm_flash_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int64_t B, int64_t max_seqlen_q, int64_t total_q, int64_t total_k,
+                              int64_t H, int64_t H_kv, int64_t D, int causal, float sm_scale,
+                              int in_dtype, int out_dtype, void* stream);
+
 /* MLA paged decode (one query token per sequence, one shared latent KV head).
  * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,
  * LSE combine :186-221, params :224-256), torch oracle :259-308.

@@ -159,6 +159,45 @@ def flashattn_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None,
     return out.to(Q.dtype)
 
 
+def flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal: bool = False,
+                         sm_scale: Optional[float] = None, max_seqlen_q: Optional[int] = None):
+    """Attention over unpadded sequences, examples/flash_attention/example_mha_fwd_varlen.py:
+    attention_ref (:166-219) on the padded batch is, per sequence b, fp32 attention of query rows
+    cu_q[b] .. cu_q[b + 1] over key rows cu_k[b] .. cu_k[b + 1] (padded keys masked with -inf,
+    :206-207; padded query rows zeroed, :214-218); K/V head h // (H // H_kv) as attention_ref's
+    repeat (:203-204). q [total_q, H, D], k, v [total_k, H_kv, D]; returns fp32
+    [total_q, H, D].
+    causal (not exercised by the example, whose attention_ref ignores it) keeps key j <= i +
+    nk - nq, the file's construct_local_mask with window (-1, 0) (:156-157). A query that sees no
+    key gets zeros (attention_ref's softmax gives NaN there); rows at positions >= max_seqlen_q
+    are left as NaN (the kernel does not write them)."""
+    total_q, H, D = q.shape
+    G = H // k.shape[1]
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else sm_scale
+    out = torch.full((total_q, H, D), float("nan"), dtype=torch.float32)
+    cq, ck = cu_q.tolist(), cu_k.tolist()
+    for b in range(len(cq) - 1):
+        q0, q1, k0, k1 = cq[b], cq[b + 1], ck[b], ck[b + 1]
+        nq, nk = q1 - q0, k1 - k0
+        nrow = nq if max_seqlen_q is None else min(nq, max_seqlen_q)
+        if nrow <= 0:
+            continue
+        for h in range(H):
+            qq = q[q0:q0 + nrow, h, :].float()
+            kk = k[k0:k1, h // G, :].float()
+            vv = v[k0:k1, h // G, :].float()
+            s = (qq @ kk.t()) * scale
+            if causal:
+                i = torch.arange(nrow).view(-1, 1)
+                j = torch.arange(nk).view(1, -1)
+                s = s.masked_fill(j > i + (nk - nq), float("-inf"))
+            seen = torch.isfinite(s).any(dim=1, keepdim=True)
+            p = torch.softmax(s, dim=-1).nan_to_num(0.0) if nk > 0 else s
+            o = p @ vv if nk > 0 else torch.zeros(nrow, D)
+            out[q0:q0 + nrow, h, :] = torch.where(seen, o, torch.zeros_like(o))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # MLA decode — examples/deepseek_mla/example_mla_decode_paged.py:259-308 (run_torch_mla /
 # scaled_dot_product_attention): per sequence, fp32 attention of q [h_q, d] over the sequence's

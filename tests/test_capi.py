@@ -26,7 +26,8 @@ def test_header_declares_entry_points():
     for s in ("tlm_init", "tlm_last_error", "tlm_rmsnorm", "tlm_gemm", "tlm_rope", "tlm_swiglu",
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
               "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex",
-              "tlm_gemm_fp8", "tlm_sigmoid", "tlm_gather_rows", "tlm_topk", "tlm_row_reduce"):
+              "tlm_gemm_fp8", "tlm_sigmoid", "tlm_gather_rows", "tlm_topk", "tlm_row_reduce",
+              "tlm_flash_attn_varlen_fwd"):
         assert s in syms
 
 
@@ -150,6 +151,30 @@ def test_flash_attn_validation():
     assert ex(p, p, p, p, 1, 16, 8, 3, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1  # 8 % 3
     assert ex(p, p, p, p, 1, 16, 8, 0, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1
     assert ex(p, p, p, p, 1, 0, 8, 2, 128, 0, 0.1, lib.BF16, lib.BF16, None) == 0
+    vl = L.tlm_flash_attn_varlen_fwd
+    cu = ctypes.c_void_p(0x2000)
+    # q, k, v, o, cu_q, cu_k, B, max_seqlen_q, total_q, total_k, H, H_kv, D, causal, scale, ...
+    # (only rejected or empty calls: a valid one would launch on the fake pointers)
+    assert vl(p, p, p, p, None, cu, 2, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16,
+              None) == -1
+    assert vl(p, p, p, p, ctypes.c_void_p(0x2002), cu, 2, 64, 100, 90, 8, 2, 128, 0, 0.1,
+              lib.F16, lib.F16, None) == -1  # cu_seqlens alignment
+    assert vl(p, p, p, p, cu, cu, -1, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16,
+              None) == -1
+    assert vl(p, p, p, p, cu, cu, 2, 64, 2 ** 31, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16,
+              None) == -1  # total rows beyond int32
+    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 3, 128, 0, 0.1, lib.F16, lib.F16,
+              None) == -1  # 8 % 3
+    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 100, 0, 0.1, lib.F16, lib.F16,
+              None) == -2  # D % 8
+    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F32, lib.F32,
+              None) == -2
+    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 128, 0, -1.0, lib.F16, lib.F16,
+              None) == -1
+    # nothing to do: no sequences, no queries, no rows
+    assert vl(p, p, p, p, cu, cu, 0, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
+    assert vl(p, p, p, p, cu, cu, 2, 0, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
+    assert vl(p, p, p, p, cu, cu, 2, 64, 0, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
 
 
 def test_mla_validation_and_workspace():

@@ -143,6 +143,33 @@ def test_demo_variants_recognised(name, prog, attrs):
         assert plan.attrs[k] == v, (name, k, plan.attrs[k])
 
 
+def test_varlen_flashattn_program():
+    """examples/flash_attention/example_mha_fwd_varlen.py: a scalar T.int32 parameter
+    (max_seqlen_q), int32 cu_seqlens, element-wise tile fills; only the non-causal form maps."""
+    k = tilelang.compile(programs.flashattn_varlen(2, 500, 510, 16, 32), out_idx=-1)
+    a = k.plan.attrs
+    assert k.plan.family == "flashattn" and a["varlen"] and not a["causal"]
+    assert (a["q"], a["k"], a["v"], a["cu_q"], a["cu_k"], a["max_q"], a["o"]) == (0, 1, 2, 3, 4,
+                                                                                   5, 6)
+    assert (a["B"], a["H"], a["H_kv"], a["D"]) == (2, 16, 16, 32)
+    assert math.isclose(a["sm_scale"], 1 / math.sqrt(32), rel_tol=1e-9)
+    assert k.params[5].is_scalar() and k.out_idx == [6]
+    gq = recognize(programs.flashattn_varlen(3, 700, 650, 8, 128, groups=4, dtype="bfloat16"))
+    assert (gq.attrs["H_kv"], gq.attrs["total_k"]) == (2, 650)
+    with pytest.raises(UnsupportedProgram, match="causal"):
+        recognize(programs.flashattn_varlen(2, 500, 510, 16, 32, is_causal=True))
+    # scalar arguments are Python ints; tensors are validated as before
+    q = torch.zeros(500, 16, 32).half()
+    kv = torch.zeros(510, 16, 32).half()
+    cu = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="scalar"):
+        k(q, kv, kv, cu, cu, torch.tensor(256))
+    with pytest.raises(ValueError, match="scalar"):
+        k(q, kv, kv, cu, cu, 256.0)
+    with pytest.raises(ValueError, match="Expected 7 arguments"):
+        k(q, kv, kv, cu, cu)
+
+
 def test_scalar_params_rejected():
     with pytest.raises(TypeError, match="T.Tensor"):
 

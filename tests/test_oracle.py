@@ -420,3 +420,83 @@ def test_row_reduce_ref():
     assert ref.row_reduce_ref(x, "max").view(-1)[0] == 3.5
     assert torch.isnan(ref.row_reduce_ref(x, "max").view(-1)[1])
     assert ref.row_reduce_ref(x, "sum").view(-1)[0] == 2.5
+
+
+def _varlen_case(lens_q, lens_k, H, Hkv, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    cu_q = torch.tensor([0] + list(np.cumsum(lens_q)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lens_k)), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), H, D, generator=g)
+    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g)
+    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g)
+    return q, k, v, cu_q, cu_k
+
+
+def test_flashattn_varlen_equal_lengths_is_the_dense_oracle():
+    """All sequences of one length: the unpadded layout is BSHD flattened, so the varlen oracle
+    equals flashattn_ref (itself pinned by SDPA), causal and not."""
+    B, S, H, D = 3, 17, 4, 8
+    q, k, v, cu_q, cu_k = _varlen_case([S] * B, [S] * B, H, H, D, seed=40)
+    for causal in (False, True):
+        got = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal)
+        exp = ref.flashattn_ref(q.view(B, S, H, D), k.view(B, S, H, D), v.view(B, S, H, D),
+                                causal).float()
+        torch.testing.assert_close(got.view(B, S, H, D), exp, rtol=1e-6, atol=1e-6)
+
+
+def test_flashattn_varlen_matches_padded_sdpa():
+    """The example's own construction (example_mha_fwd_varlen.py:385-426): pad each sequence to
+    the longest, mask padded keys, run attention on the padded batch, unpad. Here the padded
+    attention is torch's SDPA with a boolean key mask."""
+    lens_q, lens_k, H, Hkv, D = [5, 1, 13, 9], [7, 4, 13, 2], 4, 2, 16
+    q, k, v, cu_q, cu_k = _varlen_case(lens_q, lens_k, H, Hkv, D, seed=41)
+    got = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k)
+    Sq, Sk, B = max(lens_q), max(lens_k), len(lens_q)
+    qp = torch.zeros(B, H, Sq, D)
+    kp = torch.zeros(B, H, Sk, D)
+    vp = torch.zeros(B, H, Sk, D)
+    keep = torch.zeros(B, 1, 1, Sk, dtype=torch.bool)
+    for b in range(B):
+        qs = q[cu_q[b]:cu_q[b + 1]]
+        ks = k[cu_k[b]:cu_k[b + 1]].repeat_interleave(H // Hkv, dim=1)
+        vs = v[cu_k[b]:cu_k[b + 1]].repeat_interleave(H // Hkv, dim=1)
+        qp[b, :, :lens_q[b]] = qs.transpose(0, 1)
+        kp[b, :, :lens_k[b]] = ks.transpose(0, 1)
+        vp[b, :, :lens_k[b]] = vs.transpose(0, 1)
+        keep[b, ..., :lens_k[b]] = True
+    op = F.scaled_dot_product_attention(qp, kp, vp, attn_mask=keep)
+    for b in range(B):
+        exp = op[b, :, :lens_q[b]].transpose(0, 1)
+        torch.testing.assert_close(got[cu_q[b]:cu_q[b + 1]], exp, rtol=1e-5, atol=1e-5)
+
+
+def test_flashattn_varlen_causal_alignment_and_edges():
+    """Causal keeps key j <= i + nk - nq (bottom-right): a one-query sequence sees every key (a
+    top-left mask would let it see key 0 only) and equal lengths give SDPA's is_causal. A
+    sequence without keys gives zero rows; rows at positions >= max_seqlen_q stay unwritten."""
+    H, D = 2, 8
+    q, k, v, cu_q, cu_k = _varlen_case([1, 6, 4, 3], [9, 6, 0, 5], H, H, D, seed=42)
+    full = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal=False)
+    causal = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal=True)
+    torch.testing.assert_close(causal[0], full[0])  # nq = 1: all 9 keys visible
+    qs, ks, vs = (t.transpose(0, 1) for t in (q[1:7], k[9:15], v[9:15]))
+    exp = F.scaled_dot_product_attention(qs, ks, vs, is_causal=True).transpose(0, 1)
+    torch.testing.assert_close(causal[1:7], exp, rtol=1e-5, atol=1e-5)
+    assert torch.equal(full[7:11], torch.zeros(4, H, D))  # nk = 0
+    # nq = 3 over nk = 5: query 0 sees keys 0..2 only, query 2 all five
+    s0 = (q[11, 0] @ k[15:20, 0].t()) / math.sqrt(D)
+    p0 = torch.softmax(s0[:3], dim=0)
+    torch.testing.assert_close(causal[11, 0], p0 @ v[15:18, 0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(causal[13], full[13])
+    cut = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k, max_seqlen_q=4)
+    assert torch.isnan(cut[5:7]).all() and torch.equal(cut[1:5], full[1:5])
+
+
+def test_flashattn_varlen_gqa_equals_repeated_kv():
+    lens = [3, 8, 5]
+    q, k, v, cu_q, cu_k = _varlen_case(lens, lens, 6, 2, 8, seed=43)
+    for causal in (False, True):
+        got = ref.flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal)
+        exp = ref.flashattn_varlen_ref(q, k.repeat_interleave(3, dim=1),
+                                       v.repeat_interleave(3, dim=1), cu_q, cu_k, causal)
+        assert torch.equal(got, exp)

@@ -33,6 +33,28 @@ constexpr int FA_WAVES = 8;
 constexpr int BQ = 32 * FA_WAVES;  // queries per workgroup
 constexpr int BKV = 64;            // keys per tile
 
+// Query and key rows of batch b. Dense (cu_q == nullptr): every sequence holds s_q queries and
+// s_k keys, starting at rows b s_q and b s_k. Variable length: cu_q / cu_k are the [B + 1] prefix
+// sums of the sequence lengths (examples/flash_attention/example_mha_fwd_varlen.py:267-276),
+// s_q / s_k the row counts of Q / O and K / V; a sequence whose rows fall outside them is taken
+// as empty, so bad offsets never address memory outside the tensors.
+struct SeqMap {
+  const int* cu_q;
+  const int* cu_k;
+  int s_q, s_k;
+};
+struct SeqRange {
+  int64_t q0, k0;  // first row of the sequence's queries / keys
+  int nq, nk;      // their counts
+};
+TLM_DEV SeqRange seq_range(const SeqMap& m, int b) {
+  if (m.cu_q == nullptr) return {(int64_t)b * m.s_q, (int64_t)b * m.s_k, m.s_q, m.s_k};
+  const int q0 = m.cu_q[b], q1 = m.cu_q[b + 1], k0 = m.cu_k[b], k1 = m.cu_k[b + 1];
+  const bool ok = 0 <= q0 && q0 <= q1 && q1 <= m.s_q && 0 <= k0 && k0 <= k1 && k1 <= m.s_k;
+  if (!ok) return {0, 0, 0, 0};
+  return {q0, k0, q1 - q0, k1 - k0};
+}
+
 TLM_DEV s16x4 lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
 }
@@ -350,7 +372,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
                                                    const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ V,
                                                    void* __restrict__ O, int B, int S, int H,
-                                                   int Hkv, float sc) {
+                                                   int Hkv, float sc, SeqMap sm) {
   using MT = fa_mma<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
@@ -382,16 +404,24 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     h = bh % H;
   }
   const int q0 = qt * PP_BQ;
+  // S counts the query tiles of the grid; the sequence's own query and key counts are Sq, Sk.
+  // Causal: query i sees keys j <= i + (Sk - Sq) (bottom-right aligned; 0 offset when dense).
+  const SeqRange sr = seq_range(sm, b);
+  const int Sq = sr.nq, Sk = sr.nk, coff = Sk - Sq;
+  if (q0 >= Sq) return;  // whole workgroup, before any barrier
   const int64_t rs = (int64_t)H * PP_D;      // elements between consecutive tokens of Q, O
   const int64_t rs_kv = (int64_t)Hkv * PP_D;  // ... of K, V
-  const int64_t head = ((int64_t)b * S * H + h) * PP_D;
-  const int64_t head_kv = ((int64_t)b * S * Hkv + h / G) * PP_D;
+  const int64_t head = (sr.q0 * H + h) * PP_D;
+  const int64_t head_kv = (sr.k0 * Hkv + h / G) * PP_D;
   const uint16_t* Qb = Q + head;
 
-  const int n_all = (S + PP_KV - 1) / PP_KV;
-  const int n = CAUSAL ? min(n_all, (q0 + PP_BQ) / PP_KV) : n_all;  // key tiles of the workgroup
-  const int qb0 = q0 + 32 * blk;                                     // first query of the wave
-  const int nw = qb0 >= S ? 0 : (CAUSAL ? min(n, (qb0 + 31) / PP_KV + 1) : n);
+  const int n_all = (Sk + PP_KV - 1) / PP_KV;
+  const int kv_vis = q0 + PP_BQ + coff;  // keys visible to the workgroup's last query row, + 1
+  const int n = CAUSAL ? (kv_vis <= 0 ? 0 : min(n_all, (kv_vis + PP_KV - 1) / PP_KV))
+                       : n_all;  // key tiles of the workgroup
+  const int qb0 = q0 + 32 * blk;  // first query of the wave
+  const int w_last = qb0 + 31 + coff;  // last key visible to the wave
+  const int nw = qb0 >= Sq ? 0 : (CAUSAL ? (w_last < 0 ? 0 : min(n, w_last / PP_KV + 1)) : n);
 
   const int ql = lane & 31, g = lane >> 5;
   const int my_q = qb0 + ql;
@@ -401,7 +431,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
 #pragma unroll
   for (int ds = 0; ds < PP_D / 16; ++ds) {
     u32x4 v = {0, 0, 0, 0};
-    if (my_q < S) v = *(const u32x4*)(Qb + (int64_t)my_q * rs + 16 * ds + 8 * g);
+    if (my_q < Sq) v = *(const u32x4*)(Qb + (int64_t)my_q * rs + 16 * ds + 8 * g);
     qreg[ds] = __builtin_bit_cast(v8, v);
   }
 
@@ -419,7 +449,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   }
   uint8_t* const dlds = smem + (dma_v ? PP_VRING : 0) + wl * 4096;
   auto issue = [&](int tile, int slot) TLM_INLINE {
-    const int valid = min(PP_KV, S - PP_KV * tile);
+    const int valid = min(PP_KV, Sk - PP_KV * tile);
     const uint32_t nrec = (uint32_t)(valid - 1) * rs2 + PP_D * 2;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(dsrc + (int64_t)tile * PP_KV * rs_kv), (short)0, (int)nrec, PP_RSRC_WORD3);
@@ -526,14 +556,14 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   };
   auto y_phase = [&](int j) TLM_INLINE {
     const int k0 = PP_KV * j;
-    const bool need_mask = (CAUSAL && k0 + PP_KV - 1 > qb0) || (k0 + PP_KV > S);
+    const bool need_mask = (CAUSAL && k0 + PP_KV - 1 > qb0 + coff) || (k0 + PP_KV > Sk);
     if (need_mask) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
-          if (key >= S || (CAUSAL && key > my_q)) sacc[t][i] = -INFINITY;
+          if (key >= Sk || (CAUSAL && key > my_q + coff)) sacc[t][i] = -INFINITY;
         }
     }
     float ts = exp_tile(-m_run);
@@ -624,7 +654,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if constexpr (OUT32) {  // fp32 output (fp32 programs): 16-byte stores straight from registers
     float* Of = (float*)O + head;
-    if (my_q < S) {
+    if (my_q < Sq) {
 #pragma unroll
       for (int dt = 0; dt < PP_D / 32; ++dt)
 #pragma unroll
@@ -653,20 +683,20 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     const int idx = lane + 64 * it;
     const int r = idx / (PP_D / 8), c = (idx % (PP_D / 8)) * 8;
     const int q = qb0 + r;
-    if (q < S) *(u32x4*)(Ob + (int64_t)q * rs + c) = *(const u32x4*)(stage + r * PP_OP + c);
+    if (q < Sq) *(u32x4*)(Ob + (int64_t)q * rs + c) = *(const u32x4*)(stage + r * PP_OP + c);
   }
 }
 
 template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
-              float sc, hipStream_t st) {
+              float sc, const SeqMap& sm, hipStream_t st) {
   const int64_t nwg = (int64_t)((S + PP_BQ - 1) / PP_BQ) * B * H;
   if (nwg > INT32_MAX) {
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
   fa_fwd_pp<BF16, CAUSAL, OUT32><<<(unsigned)nwg, 512, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc);
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc, sm);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
@@ -694,15 +724,18 @@ template <bool BF16, bool CAUSAL, bool OUT32, int DC>  // DC = capacity in 8-ele
 __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict__ Q,
                                                       const uint16_t* __restrict__ K,
                                                       const uint16_t* __restrict__ V,
-                                                      void* __restrict__ O, int S, int H, int Hkv,
-                                                      int D, float sc) {
+                                                      void* __restrict__ O, int H, int Hkv,
+                                                      int D, float sc, SeqMap sm) {
   using HH = h16<BF16>;
   const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const SeqRange sr = seq_range(sm, b);
+  const int S = sr.nq, Sk = sr.nk, coff = Sk - S;  // causal: query i sees keys j <= i + coff
+  if ((int)blockIdx.x * 256 >= S) return;  // whole block
   const int q = blockIdx.x * 256 + threadIdx.x;
   const int nc = D / 8;
   const int64_t rs = (int64_t)H * D, rs_kv = (int64_t)Hkv * D;
-  const int64_t head = ((int64_t)b * S * H + h) * D;
-  const int64_t head_kv = ((int64_t)b * S * Hkv + h / (H / Hkv)) * D;
+  const int64_t head = (sr.q0 * H + h) * D;
+  const int64_t head_kv = (sr.k0 * Hkv + h / (H / Hkv)) * D;
   u32x4 qv[DC];
   float o[DC][8];
 #pragma unroll
@@ -715,7 +748,7 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
   float m = -INFINITY, l = 0.f;
   // keys of the wave: causal stops after the wave's last query (wave-uniform bound)
   const int wq_last = min(S - 1, (int)(blockIdx.x * 256 + (threadIdx.x & ~63) + 63));
-  const int kend = CAUSAL ? wq_last + 1 : S;
+  const int kend = CAUSAL ? max(0, min(Sk, wq_last + coff + 1)) : Sk;
   for (int j = 0; j < kend; ++j) {
     const uint16_t* kr = K + head_kv + (int64_t)j * rs_kv;
     float s = 0.f;
@@ -731,7 +764,7 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
       }
     }
     s *= sc;
-    if (CAUSAL && j > q) s = -INFINITY;
+    if (CAUSAL && j > q + coff) s = -INFINITY;
     const float m_new = fmaxf(m, s);
     const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
     const float p = m_new == -INFINITY ? 0.f : fast_exp2(s - m_new);
@@ -772,15 +805,15 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
 
 template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_generic(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
-                   int Hkv, int D, float sc, hipStream_t st) {
+                   int Hkv, int D, float sc, const SeqMap& sm, hipStream_t st) {
   if ((int64_t)B * H > 65535) {
     tlm_set_error("tlm_flash_attn_fwd: head dim %d needs batch * heads <= 65535", D);
     return TLM_EUNSUPPORTED;
   }
   const dim3 grid((unsigned)((S + 255) / 256), (unsigned)(B * H));
   auto go = [&](auto kern) {
-    kern<<<grid, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, S,
-                               H, Hkv, D, sc);
+    kern<<<grid, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, H,
+                               Hkv, D, sc, sm);
   };
   if (D <= 16)
     go(fa_fwd_generic<BF16, CAUSAL, OUT32, 2>);
@@ -794,17 +827,71 @@ int launch_generic(const void* q, const void* k, const void* v, void* o, int B, 
   return TLM_OK;
 }
 
+// S: queries per sequence (dense) or the longest sequence's (variable length); sm: row ranges.
 template <bool BF16, bool OUT32>
 int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
-             int D, bool causal, float sc, hipStream_t st) {
+             int D, bool causal, float sc, const SeqMap& sm, hipStream_t st) {
   if (D == 128)
-    return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, sc, st)
-                  : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, sc, st);
-  if (D == 64 && !OUT32)
+    return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, sc, sm, st)
+                  : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, sc, sm, st);
+  if (D == 64 && !OUT32 && sm.cu_q == nullptr)
     return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, Hkv, sc, st)
                   : launch<BF16, false, 64>(q, k, v, o, B, S, H, Hkv, sc, st);
-  return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, st)
-                : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, st);
+  return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st)
+                : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st);
+}
+
+// Checks shared by the dense and variable-length entry points.
+int check_common(const char* fn, const void* q, const void* k, const void* v, const void* o,
+                 int64_t H, int64_t H_kv, int64_t D, float sm_scale, int in_dtype,
+                 int out_dtype) {
+  if (!q || !k || !v || !o) {
+    tlm_set_error("%s: null pointer argument", fn);
+    return TLM_EINVAL;
+  }
+  if (H < 0 || H > 65535) {
+    tlm_set_error("%s: bad head count %lld", fn, (long long)H);
+    return TLM_EINVAL;
+  }
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) {
+    tlm_set_error("%s: %lld query heads do not split into groups of %lld K/V heads", fn,
+                  (long long)H, (long long)H_kv);
+    return TLM_EINVAL;
+  }
+  if (D <= 0 || D > 256 || D % 8 != 0) {
+    tlm_set_error("%s: head dim %lld unsupported (a multiple of 8, at most 256)", fn,
+                  (long long)D);
+    return TLM_EUNSUPPORTED;
+  }
+  if (in_dtype != TLM_BF16 && in_dtype != TLM_F16) {
+    tlm_set_error("%s: dtype %d unsupported (BF16 or F16)", fn, in_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  if (out_dtype != in_dtype && out_dtype != TLM_F32) {
+    tlm_set_error("%s: output dtype %d unsupported (the input dtype or F32)", fn, out_dtype);
+    return TLM_EUNSUPPORTED;
+  }
+  if (!(sm_scale > 0.f) || !__builtin_isfinite(sm_scale)) {
+    tlm_set_error("%s: sm_scale must be positive and finite", fn);
+    return TLM_EINVAL;
+  }
+  if (!tlm_aligned(q, 16) || !tlm_aligned(k, 16) || !tlm_aligned(v, 16) || !tlm_aligned(o, 16)) {
+    tlm_set_error("%s: tensors must be 16-byte aligned", fn);
+    return TLM_EINVAL;
+  }
+  return TLM_OK;
+}
+
+int dispatch(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
+             int D, bool causal, float sm_scale, int in_dtype, int out_dtype, const SeqMap& sm,
+             hipStream_t st) {
+  const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  const bool bf = in_dtype == TLM_BF16, f32o = out_dtype == TLM_F32;
+  if (bf)
+    return f32o ? by_shape<true, true>(q, k, v, o, B, S, H, Hkv, D, causal, sc, sm, st)
+                : by_shape<true, false>(q, k, v, o, B, S, H, Hkv, D, causal, sc, sm, st);
+  return f32o ? by_shape<false, true>(q, k, v, o, B, S, H, Hkv, D, causal, sc, sm, st)
+              : by_shape<false, false>(q, k, v, o, B, S, H, Hkv, D, causal, sc, sm, st);
 }
 
 }  // namespace
@@ -813,52 +900,43 @@ extern "C" int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v
                                      int64_t B, int64_t S, int64_t H, int64_t H_kv, int64_t D,
                                      int causal, float sm_scale, int in_dtype, int out_dtype,
                                      void* stream) {
-  if (!q || !k || !v || !o) {
-    tlm_set_error("tlm_flash_attn_fwd: null pointer argument");
-    return TLM_EINVAL;
-  }
-  if (B < 0 || S < 0 || H < 0 || B > 65535 || H > 65535 || S > (1 << 24)) {
+  const int rc = check_common("tlm_flash_attn_fwd", q, k, v, o, H, H_kv, D, sm_scale, in_dtype,
+                              out_dtype);
+  if (rc != TLM_OK) return rc;
+  if (B < 0 || S < 0 || B > 65535 || S > (1 << 24)) {
     tlm_set_error("tlm_flash_attn_fwd: bad shape");
     return TLM_EINVAL;
   }
-  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) {
-    tlm_set_error("tlm_flash_attn_fwd: %lld query heads do not split into groups of %lld K/V "
-                  "heads", (long long)H, (long long)H_kv);
-    return TLM_EINVAL;
-  }
-  if (D <= 0 || D > 256 || D % 8 != 0) {
-    tlm_set_error("tlm_flash_attn_fwd: head dim %lld unsupported (a multiple of 8, at most 256)",
-                  (long long)D);
-    return TLM_EUNSUPPORTED;
-  }
-  if (in_dtype != TLM_BF16 && in_dtype != TLM_F16) {
-    tlm_set_error("tlm_flash_attn_fwd: dtype %d unsupported (BF16 or F16)", in_dtype);
-    return TLM_EUNSUPPORTED;
-  }
-  if (out_dtype != in_dtype && out_dtype != TLM_F32) {
-    tlm_set_error("tlm_flash_attn_fwd: output dtype %d unsupported (the input dtype or F32)",
-                  out_dtype);
-    return TLM_EUNSUPPORTED;
-  }
-  if (!(sm_scale > 0.f) || !__builtin_isfinite(sm_scale)) {
-    tlm_set_error("tlm_flash_attn_fwd: sm_scale must be positive and finite");
-    return TLM_EINVAL;
-  }
-  if (!tlm_aligned(q, 16) || !tlm_aligned(k, 16) || !tlm_aligned(v, 16) || !tlm_aligned(o, 16)) {
-    tlm_set_error("tlm_flash_attn_fwd: tensors must be 16-byte aligned");
-    return TLM_EINVAL;
-  }
   if (B == 0 || S == 0 || H == 0) return TLM_OK;
-  const float sc = (float)((double)sm_scale * 1.4426950408889634);
-  hipStream_t st = (hipStream_t)stream;
-  const bool bf = in_dtype == TLM_BF16, f32o = out_dtype == TLM_F32;
-  const int b = (int)B, s = (int)S, h = (int)H, hk = (int)H_kv, d = (int)D;
-  const bool c = causal != 0;
-  if (bf)
-    return f32o ? by_shape<true, true>(q, k, v, o, b, s, h, hk, d, c, sc, st)
-                : by_shape<true, false>(q, k, v, o, b, s, h, hk, d, c, sc, st);
-  return f32o ? by_shape<false, true>(q, k, v, o, b, s, h, hk, d, c, sc, st)
-              : by_shape<false, false>(q, k, v, o, b, s, h, hk, d, c, sc, st);
+  const SeqMap sm{nullptr, nullptr, (int)S, (int)S};
+  return dispatch(q, k, v, o, (int)B, (int)S, (int)H, (int)H_kv, (int)D, causal != 0, sm_scale,
+                  in_dtype, out_dtype, sm, (hipStream_t)stream);
+}
+
+extern "C" int tlm_flash_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o,
+                                         const int32_t* cu_seqlens_q,
+                                         const int32_t* cu_seqlens_k, int64_t B,
+                                         int64_t max_seqlen_q, int64_t total_q, int64_t total_k,
+                                         int64_t H, int64_t H_kv, int64_t D, int causal,
+                                         float sm_scale, int in_dtype, int out_dtype,
+                                         void* stream) {
+  const int rc = check_common("tlm_flash_attn_varlen_fwd", q, k, v, o, H, H_kv, D, sm_scale,
+                              in_dtype, out_dtype);
+  if (rc != TLM_OK) return rc;
+  if (!cu_seqlens_q || !cu_seqlens_k || !tlm_aligned(cu_seqlens_q, 4) ||
+      !tlm_aligned(cu_seqlens_k, 4)) {
+    tlm_set_error("tlm_flash_attn_varlen_fwd: cu_seqlens must be non-null, 4-byte aligned");
+    return TLM_EINVAL;
+  }
+  if (B < 0 || B > 65535 || max_seqlen_q < 0 || max_seqlen_q > (1 << 24) || total_q < 0 ||
+      total_k < 0 || total_q > INT32_MAX || total_k > INT32_MAX) {
+    tlm_set_error("tlm_flash_attn_varlen_fwd: bad shape");
+    return TLM_EINVAL;
+  }
+  if (B == 0 || max_seqlen_q == 0 || H == 0 || total_q == 0) return TLM_OK;
+  const SeqMap sm{cu_seqlens_q, cu_seqlens_k, (int)total_q, (int)total_k};
+  return dispatch(q, k, v, o, (int)B, (int)max_seqlen_q, (int)H, (int)H_kv, (int)D, causal != 0,
+                  sm_scale, in_dtype, out_dtype, sm, (hipStream_t)stream);
 }
 
 extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,

@@ -36,6 +36,9 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
         ops.rope(t[a["q"]], t[a["cos"]], t[a["sin"]], t[a["q_out"]], k, ko)
     elif f == "gemm":
         ops.gemm(t[a["a"]], t[a["b"]], t[a["c"]], a["trans_b"], operand_dtype=odt)
+    elif f == "flashattn" and a.get("varlen"):
+        ops.flash_attn_varlen_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["cu_q"]], t[a["cu_k"]],
+                                  t[a["max_q"]], t[a["o"]], a["causal"], a["sm_scale"])
     elif f == "flashattn":
         ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"],
                            operand_dtype=odt)
@@ -80,6 +83,11 @@ class MI355XKernelAdapter(BaseKernelAdapter):
 
     def _check(self, i, t):
         p = self.params[i]
+        if p.is_scalar():  # a plain Python int, as cython_wrapper.pyx:117-122 passes it
+            if isinstance(t, bool) or not isinstance(t, int):
+                raise ValueError(f"parameter {i} is a scalar {p.dtype}: pass a Python int, got "
+                                 f"{type(t)}")
+            return
         if not isinstance(t, torch.Tensor):
             raise ValueError(f"parameter {i} must be a torch.Tensor, got {type(t)}")
         if t.dtype != p.dtype:
@@ -107,7 +115,7 @@ class MI355XKernelAdapter(BaseKernelAdapter):
             for i, t in enumerate(full):
                 if t is not None:
                     self._check(i, t)
-            ins = [t for t in full if t is not None]
+            ins = [t for t in full if isinstance(t, torch.Tensor)]
             if not torch.cuda.is_available():
                 raise RuntimeError("no HIP device visible: the mi355x target runs on gfx950 only "
                                    "and has no CPU fallback")
@@ -123,6 +131,8 @@ class MI355XKernelAdapter(BaseKernelAdapter):
                     p = self.params[i]
                     dev_t.append(torch.empty([int(s) for s in p.shape], dtype=p.dtype,
                                              device=gpu))
+                elif not isinstance(t, torch.Tensor):  # scalar argument
+                    dev_t.append(t)
                 elif t.device != gpu:
                     dev_t.append(t.to(gpu))
                 else:

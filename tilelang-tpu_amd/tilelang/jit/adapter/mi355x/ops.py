@@ -177,6 +177,38 @@ def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float,
     return o
 
 
+def flash_attn_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, o,
+                          causal: bool, sm_scale: float):
+    """Attention over unpadded sequences: q, o [total_q, H, D]; k, v [total_k, H_kv, D];
+    sequence b is rows cu_seqlens_q[b] .. cu_seqlens_q[b + 1] of q (int32 [B + 1]) and the
+    matching rows of k, v. Queries at positions >= max_seqlen_q are not computed."""
+    dev = _dev(q, k, v, o, cu_seqlens_q, cu_seqlens_k)
+    for n, t in (("Q", q), ("K", k), ("V", v), ("O", o), ("cu_seqlens_q", cu_seqlens_q),
+                 ("cu_seqlens_k", cu_seqlens_k)):
+        _contig(n, t)
+    if q.dim() != 3 or q.shape != o.shape or k.shape != v.shape or k.dim() != 3:
+        raise ValueError("Q, O must be [total_q, H, D] and K, V [total_k, H_kv, D]")
+    total_q, H, D = q.shape
+    total_k, Hkv = k.shape[0], k.shape[1]
+    if k.shape[2] != D or Hkv == 0 or H % Hkv:
+        raise ValueError(f"K/V {tuple(k.shape)} do not match Q {tuple(q.shape)} "
+                         "(same D; H a multiple of H_kv)")
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32 or \
+            cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape != cu_seqlens_k.shape or \
+            cu_seqlens_q.numel() < 1:
+        raise ValueError("cu_seqlens_q / cu_seqlens_k must be int32 [B + 1]")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("Q, K and V must share a dtype")
+    if o.dtype not in (q.dtype, torch.float32):
+        raise ValueError(f"O must be {q.dtype} or float32")
+    B = cu_seqlens_q.numel() - 1
+    lib.call("tlm_flash_attn_varlen_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o),
+             _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), B, int(max_seqlen_q), total_q, total_k, H,
+             Hkv, D, 1 if causal else 0, float(sm_scale), dtype_code(q.dtype),
+             dtype_code(o.dtype), _stream(dev))
+    return o
+
+
 def sigmoid(x: torch.Tensor, y: torch.Tensor):
     """y = sigmoid(x), fp32 math."""
     dev = _dev(x, y)

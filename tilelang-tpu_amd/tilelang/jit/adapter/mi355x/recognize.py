@@ -1,7 +1,7 @@
 """Match a traced prim_func to one of the operator families that have gfx950 kernels.
 
 The reference lowers any TIR program through its PPL code generator (src/target/codegen_ppl.cc).
-This build has hand-written kernels for six families only, so compilation is recognition: the op
+This build has hand-written kernels for a fixed set of families, so compilation is recognition: the op
 trace is fingerprinted (which tile ops occur, how data flows from parameters through tiles), the
 family's static parameters (shapes, dtypes, eps, scale, causal, page size, splits) are read out
 of the program, and anything that does not fit a family is rejected with a clear error. There is
@@ -19,7 +19,8 @@ Families and the reference programs they accept:
   swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54 (+ tpu_test_swiglu_fp32.py)
   flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, and fp32 with fp16
            matrix tiles) and the upstream examples/flash_attention/example_mha_fwd_bshd.py:30-151
-           structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178)
+           structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178), and the
+           non-causal variable-length program example_mha_fwd_varlen.py:222-358
   sigmoid  tpu_demo/tpu_test_sigmoid_fp32.py:6-31 (ppl_sigmoid)
   gather   tpu_demo/tpu_test_gather_fp32.py:8-18 (ppl_gather)
   topk     tpu_demo/tpu_test_topk_fp32.py:6-18 (ppl_topk)
@@ -84,7 +85,8 @@ def _op_names(pf):
 
 
 def _source_param(pf, buf: Buffer, depth=0) -> Optional[Buffer]:
-    """Follow tile copies backwards from ``buf`` to the global parameter it was loaded from."""
+    """Follow tile copies (or element stores ``tile[i, j] = param[...]``) backwards from ``buf``
+    to the global parameter it was loaded from."""
     if buf is None or depth > 8:
         return None
     if buf.scope == "global":
@@ -92,6 +94,11 @@ def _source_param(pf, buf: Buffer, depth=0) -> Optional[Buffer]:
     for op in _ops(pf, _COPY):
         if _buf(op.args[1]) is buf:
             src = _source_param(pf, _buf(op.args[0]), depth + 1)
+            if src is not None:
+                return src
+    for op in _ops(pf, ("store",)):
+        if op.args[0] is buf and isinstance(op.args[2], BufferAccess):
+            src = _source_param(pf, op.args[2].buffer, depth + 1)
             if src is not None:
                 return src
     return None
@@ -106,6 +113,12 @@ def _sink_param(pf, buf: Buffer, depth=0) -> Optional[Buffer]:
     for op in _ops(pf, _COPY):
         if _buf(op.args[0]) is buf:
             dst = _sink_param(pf, _buf(op.args[1]), depth + 1)
+            if dst is not None:
+                return dst
+    for op in _ops(pf, ("store",)):
+        v = op.args[2]
+        if isinstance(v, BufferAccess) and v.buffer is buf:
+            dst = _sink_param(pf, op.args[0], depth + 1)
             if dst is not None:
                 return dst
     return None
@@ -340,6 +353,8 @@ def _flashattn(pf, names) -> Plan:
         _fail(fam, "could not trace Q, K, V and Output")
     shp = _shape(Q)
     kshp = _shape(K)
+    if len(shp) == 3:
+        return _flashattn_varlen(pf, qk[0], pv[0], Q, K, V, O)
     if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
         _fail(fam, "Q, Output must be [batch, seq, heads, dim] and K, V [batch, seq, kv_heads, dim]")
     if (kshp[0], kshp[1], kshp[3]) != (shp[0], shp[1], shp[3]) or shp[2] % kshp[2]:
@@ -387,6 +402,83 @@ def _flashattn(pf, names) -> Plan:
         H_kv=kshp[2], D=D,
         causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
         operand_dtype=tile_dt if Q.dtype == "float32" else None))
+
+
+def _index_param(pf, tile: Buffer, src: Buffer) -> Optional[Buffer]:
+    """The int32 parameter read inside the row index of the element stores that fill ``tile``
+    from ``src`` (the cu_seqlens array of ``Q_unpad[q_start_idx + ..]``)."""
+    for op in _ops(pf, ("store",)):
+        v = op.args[2]
+        if op.args[0] is not tile or not isinstance(v, BufferAccess) or v.buffer is not src:
+            continue
+        for ix in v.indices:
+            if not isinstance(ix, Expr):
+                continue
+            for e in ix.walk():
+                if isinstance(e, BufferAccess) and e.buffer.scope == "global" and \
+                        e.buffer.dtype == "int32" and len(e.buffer.shape) == 1:
+                    return e.buffer
+    return None
+
+
+def _flashattn_varlen(pf, qk, pv, Q, K, V, O) -> Plan:
+    """examples/flash_attention/example_mha_fwd_varlen.py:222-358: unpadded Q/K/V/Output
+    [tokens, heads, dim], int32 cu_seqlens_q / cu_seqlens_k [B + 1], scalar max_seqlen_q."""
+    fam = "flashattn"
+    shp, kshp = _shape(Q), _shape(K)
+    if shp != _shape(O) or kshp != _shape(V) or len(kshp) != 3:
+        _fail(fam, "variable-length Q, Output must be [tokens, heads, dim] and K, V "
+                   "[tokens, kv_heads, dim]")
+    UQ, H, D = shp
+    UKV, Hkv, Dk = kshp
+    if Dk != D or Hkv == 0 or H % Hkv:
+        _fail(fam, f"K/V {kshp} do not group Q {shp} (same dim; heads a multiple of kv_heads)")
+    tile_dts = {_buf(qk.args[0]).dtype, _buf(qk.args[1]).dtype, _buf(pv.args[0]).dtype,
+                _buf(pv.args[1]).dtype}
+    if not (Q.dtype == K.dtype == V.dtype == O.dtype) or tile_dts != {Q.dtype} or \
+            Q.dtype not in ("bfloat16", "float16"):
+        _fail(fam, "variable-length attention needs bfloat16 or float16 Q, K, V, Output and "
+                   "tiles of the same dtype")
+    cu_q = _index_param(pf, _buf(qk.args[0]), Q)
+    cu_k = _index_param(pf, _buf(qk.args[1]), K)
+    if cu_q is None or cu_k is None or cu_q is cu_k or _shape(cu_q) != _shape(cu_k):
+        _fail(fam, "could not find the cu_seqlens_q / cu_seqlens_k parameters")
+    B = _shape(cu_q)[0] - 1
+    scalars = [p for p in pf.params if isinstance(p, ir.ScalarParam)]
+    grid = pf.kernels[0].extents if pf.kernels else ()
+    max_q = None
+    for p in scalars:
+        if any(isinstance(e, Expr) and p.name in e.free_vars() for e in grid):
+            max_q = p
+    if max_q is None:
+        _fail(fam, "no scalar max_seqlen_q parameter sizes the grid")
+    # The example's causal variant (:297-302) pre-fills -inf only where a query is on or below
+    # the key's diagonal AND out of range, so in-range keys above the diagonal stay visible: it is
+    # not causal attention, and no kernel here reproduces it.
+    k_vars = {v.name for op in pf.ops if op.name == "loop_begin" and op.args[0].kind ==
+              "pipelined" for v in op.args[0].vars}
+    for op in pf.ops:
+        if op.name == "branch" and isinstance(op.args[0], Expr):
+            fv = op.args[0].free_vars()
+            if any(n.startswith("bx") for n in fv) and fv & k_vars:
+                _fail(fam, "the variable-length program's causal mask compares query and key "
+                           "positions only together with the sequence bounds "
+                           "(example_mha_fwd_varlen.py:298-302); only its non-causal form maps to "
+                           "a kernel")
+    acc_s = _buf(qk.args[2])
+    sm_scale = None
+    for op in _ops(pf, ("store",)):
+        if op.args[0] is acc_s and isinstance(op.args[2], Expr) and op.args[2].has_op("exp2"):
+            cs = [c for c in op.args[2].consts() if isinstance(c, float) and c > 0]
+            if cs:
+                sm_scale = cs[0] / LOG2E_REF
+    if sm_scale is None:
+        _fail(fam, "could not read the softmax scale")
+    return Plan(fam, pf.params, [_index(pf, O)], dict(
+        q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O),
+        cu_q=_index(pf, cu_q), cu_k=_index(pf, cu_k), max_q=_index(pf, max_q), varlen=True,
+        B=B, total_q=UQ, total_k=UKV, H=H, H_kv=Hkv, D=D, causal=False, sm_scale=sm_scale,
+        dtype=Q.dtype, operand_dtype=None))
 
 
 def _page_size_from_trace(pf, bt: Buffer) -> Optional[int]:

@@ -60,8 +60,9 @@ class PrimFunc:
 def prim_func(fn=None, *, private: bool = False, check_well_formed: bool = False):
     """Trace ``fn`` into a :class:`PrimFunc`.
 
-    Parameters must be annotated ``T.Tensor(shape, dtype)``; the annotations are evaluated when
-    the function is defined (as TVMScript does), then the body runs once with symbolic buffers.
+    Parameters are annotated ``T.Tensor(shape, dtype)`` or a scalar type such as ``T.int32``;
+    the annotations are evaluated when the function is defined (as TVMScript does), then the body
+    runs once with symbolic buffers and scalars.
     """
 
     def deco(f):
@@ -69,10 +70,14 @@ def prim_func(fn=None, *, private: bool = False, check_well_formed: bool = False
         params = []
         for name, p in sig.parameters.items():
             ann = p.annotation
+            scalar_dt = getattr(ann, "_scalar_dtype", None)
+            if scalar_dt is not None:
+                params.append(ir.ScalarParam(name, scalar_dt))
+                continue
             if not isinstance(ann, TensorType):
                 raise TypeError(
                     f"prim_func {f.__name__}: parameter {name!r} must be annotated "
-                    f"T.Tensor(shape, dtype); scalar parameters are not supported on mi355x")
+                    f"T.Tensor(shape, dtype) or a scalar type such as T.int32")
             params.append(ir.Buffer(name, ann.shape, ann.dtype, "global"))
         tracer = Tracer()
         with tracer:
@@ -374,6 +379,7 @@ def _dt_ctor(dtype):
         return Const(float(value), dtype)
 
     ctor.__name__ = dtype
+    ctor._scalar_dtype = dtype  # usable as a scalar parameter annotation
     return ctor
 
 

@@ -223,6 +223,17 @@ class Var(Expr):
         return iter((self,))
 
 
+class ScalarParam(Var):
+    """Scalar prim_func parameter (``max_seqlen_q: T.int32``): a symbolic value in the traced
+    body and a Python number at call time (the reference passes such parameters as plain
+    integers, tilelang/jit/adapter/cython/cython_wrapper.pyx:117-122)."""
+
+    __slots__ = ()
+    scope = "scalar"
+    shape = ()
+    ndim = 0
+
+
 def Const(value, dtype: Optional[str] = None) -> Expr:
     return Expr("const", (value,), dtype)
 

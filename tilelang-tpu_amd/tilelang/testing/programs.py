@@ -463,6 +463,96 @@ def flashattn_gqa(batch, heads, seq_len, dim, is_causal, groups=1, block_M=128, 
     return main
 
 
+def flashattn_varlen(batch, UQ, UKV, heads, dim, is_causal=False, groups=1, block_M=64,
+                     block_N=64, dtype="float16"):
+    """The program structure of examples/flash_attention/example_mha_fwd_varlen.py:222-358:
+    unpadded Q [UQ, heads, dim], K/V [UKV, heads // groups, dim], int32 cu_seqlens of both
+    sides, the scalar max_seqlen_q sizing the grid; tiles filled element by element with zeros
+    past the sequence's end, scores pre-filled with -inf at out-of-range positions. is_causal
+    reproduces the example's causal expression (:298-302), which masks a position only when
+    it is both on or below the diagonal and out of range."""
+    scale = (1.0 / dim) ** 0.5 * 1.44269504
+    q_shape = [UQ, heads, dim]
+    kv_shape = [UKV, heads // groups, dim]
+    acc = "float"
+
+    @T.prim_func
+    def main(Q_unpad: T.Tensor(q_shape, dtype), K_unpad: T.Tensor(kv_shape, dtype),
+             V_unpad: T.Tensor(kv_shape, dtype), cu_seqlens_q: T.Tensor([batch + 1], "int32"),
+             cu_seqlens_k: T.Tensor([batch + 1], "int32"), max_seqlen_q: T.int32,
+             Output_unpad: T.Tensor(q_shape, dtype)):
+        with T.Kernel(T.ceildiv(max_seqlen_q, block_M), heads, batch, threads=32) as (bx, by, bz):
+            q_s = T.alloc_shared([block_M, dim], dtype, "shared")
+            k_s = T.alloc_shared([block_N, dim], dtype, "shared")
+            v_s = T.alloc_shared([block_N, dim], dtype, "shared")
+            o_s = T.alloc_shared([block_M, dim], dtype, "shared")
+            s = T.alloc_fragment([block_M, block_N], acc)
+            s_cast = T.alloc_fragment([block_M, block_N], dtype)
+            o = T.alloc_fragment([block_M, dim], acc)
+            m = T.alloc_fragment([block_M], acc)
+            m_prev = T.alloc_fragment([block_M], acc)
+            alpha = T.alloc_fragment([block_M], acc)
+            rsum = T.alloc_fragment([block_M], acc)
+            l = T.alloc_fragment([block_M], acc)
+            hk = by // groups
+            q_start, k_start = cu_seqlens_q[bz], cu_seqlens_k[bz]
+            q_len = cu_seqlens_q[bz + 1] - q_start
+            k_len = cu_seqlens_k[bz + 1] - k_start
+            for i, d in T.Parallel(block_M, dim):
+                if bx * block_M + i < q_len:
+                    q_s[i, d] = Q_unpad[q_start + bx * block_M + i, by, d]
+                else:
+                    q_s[i, d] = 0
+            T.fill(o, 0)
+            T.fill(l, 0)
+            T.fill(m, -T.infinity(acc))
+            for k in T.Pipelined(T.ceildiv(k_len, block_N), num_stages=0):
+                for i, d in T.Parallel(block_N, dim):
+                    if k * block_N + i < k_len:
+                        k_s[i, d] = K_unpad[k_start + k * block_N + i, hk, d]
+                    else:
+                        k_s[i, d] = 0
+                if is_causal:
+                    for i, j in T.Parallel(block_M, block_N):
+                        s[i, j] = T.if_then_else(
+                            (bx * block_M + i >= k * block_N + j) and
+                            (bx * block_M + i >= q_len or k * block_N + j >= k_len),
+                            -T.infinity(acc), 0)
+                else:
+                    for i, j in T.Parallel(block_M, block_N):
+                        s[i, j] = T.if_then_else(
+                            (bx * block_M + i >= q_len or k * block_N + j >= k_len),
+                            -T.infinity(acc), 0)
+                T.gemm(q_s, k_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullRow)
+                T.copy(m, m_prev)
+                T.fill(m, -T.infinity(acc))
+                T.reduce_max(s, m, dim=1, clear=False)
+                for i in T.Parallel(block_M):
+                    alpha[i] = T.exp2(m_prev[i] * scale - m[i] * scale)
+                for i, j in T.Parallel(block_M, block_N):
+                    s[i, j] = T.exp2(s[i, j] * scale - m[i] * scale)
+                T.reduce_sum(s, rsum, dim=1)
+                for i in T.Parallel(block_M):
+                    l[i] = l[i] * alpha[i] + rsum[i]
+                T.copy(s, s_cast)
+                for i, j in T.Parallel(block_M, dim):
+                    o[i, j] *= alpha[i]
+                for i, d in T.grid(block_N, dim):
+                    if k * block_N + i < k_len:
+                        v_s[i, d] = V_unpad[k_start + k * block_N + i, hk, d]
+                    else:
+                        v_s[i, d] = 0
+                T.gemm(s_cast, v_s, o, policy=T.GemmWarpPolicy.FullRow)
+            for i, j in T.Parallel(block_M, dim):
+                o[i, j] /= l[i]
+            T.copy(o, o_s)
+            for i, d in T.Parallel(block_M, dim):
+                if bx * block_M + i < q_len:
+                    Output_unpad[q_start + bx * block_M + i, by, d] = o_s[i, d]
+
+    return main
+
+
 def mla_decode(batch, h_q, h_kv, max_seqlen_pad, dv, dpe, block_N, block_H, num_split,
                block_size, dtype="float16", kv_dtype=None, out_dtype=None):
     """Paged MLA decode with split-KV + LSE combine. ``kv_dtype="float8_e4m3"`` adds a trailing
