@@ -153,6 +153,51 @@ def cpu_time(fn, reps=3):
     return ts[len(ts) // 2]
 
 
+def _sclk_file():
+    """The one GPU's sysfs clock file (amdgpu pp_dpm_sclk: the marked line is the SMU's running
+    average of the shader clock), or None when it is absent or there are several cards."""
+    import glob
+    files = glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")
+    return files[0] if len(files) == 1 and os.access(files[0], os.R_OK) else None
+
+
+def settled_sclk(fns, seconds=1.5):
+    """Shader clock (MHz) while the workload runs back to back for `seconds`: mean of the sysfs
+    readings of the last half (the average needs ~0.5 s to settle from idle). Measured after
+    the timed steps, so it does not touch them; None without the sysfs file."""
+    import re
+    import threading
+    path = _sclk_file()
+    if path is None or not fns:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                m = re.search(r"(\d+)\s*Mhz\s*\*", open(path).read())
+                if m:
+                    samples.append((time.perf_counter(), int(m.group(1))))
+            except OSError:
+                return
+            time.sleep(0.01)
+
+    th = threading.Thread(target=sample, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        fns[i % len(fns)]()
+        i += 1
+        if i % 32 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    late = [v for t, v in samples if t - t0 >= seconds / 2]
+    return round(sum(late) / len(late), 1) if late else None
+
+
 def roofline(bound, achieved, unit, peak, traffic=None):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -162,9 +207,13 @@ class PmcOnly(Exception):
     """Raised by a config in --pmc-launches mode once its kernel has run the requested times."""
 
 
+_LAST_FNS = []  # launch closures of the workload being measured (for the clock pass)
+
+
 def pmc_launches(args, fns, workload):
     """--pmc-launches N: N plain launches for hardware-counter collection (rocprofv3 --pmc),
     no graphs, no timing, no cache flush."""
+    _LAST_FNS[:] = fns
     if not args.pmc_launches:
         return
     torch.cuda.synchronize()
@@ -595,6 +644,8 @@ def main():
                     help="only launch the workload's kernel N times (for rocprofv3 --pmc)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--mla-splits", type=int, default=4)
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the shader-clock pass of the matrix-core workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every kernel here is a "
@@ -617,6 +668,15 @@ def main():
             tb = traffic.get(results[n].get("workload"))
             if tb is not None and results[n].get("roofline"):
                 results[n]["roofline"]["traffic"] = tb
+            rl = results[n].get("roofline") or {}
+            if rl.get("bound") == "mfma" and not args.no_clock:
+                mhz = settled_sclk(_LAST_FNS)
+                if mhz:  # the spec peak assumes 2400 MHz; the roofline above keeps the spec peak
+                    at_clk = rl["peak"] * mhz / 2400.0
+                    results[n]["sclk"] = {
+                        "mhz": mhz, "source": "pp_dpm_sclk, last 0.75 s of 1.5 s back to back",
+                        "peak_at_sclk": round(at_clk, 1),
+                        "frac_at_sclk": round(rl["achieved"] / at_clk, 4)}
             log(f"[bench] {n}: {results[n]['value']:.1f} {results[n]['unit']} "
                 f"(roofline {results[n]['roofline']['frac'] * 100:.1f}%)")
         except PmcOnly:
@@ -647,6 +707,7 @@ def main():
         "data": "synthetic (seed 0, BASELINE.json configs)",
         "config": {"workload": head.get("workload", head_name), "device": torch.cuda.get_device_name(dev)},
         "roofline": head.get("roofline"),
+        "sclk": head.get("sclk"),
         "cpu_baseline": head.get("cpu_baseline"),
         "configs": [results[n] for n in names],
         "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()},
