@@ -19,13 +19,18 @@
 
 namespace {
 
+// One workgroup handles `rows` token rows of one sequence at a time (blockIdx.y strides over the
+// sequences, so start[b] / count[b] are uniform loads): thread t owns chunk t % chunks of row
+// t / chunks, both fixed for the whole loop; rows longer than 256 chunks loop over chunks with
+// one row per workgroup. page_shift >= 0: the page size is 2^page_shift (shift and mask instead
+// of a 64-bit division).
 template <bool BF16, int VEC>
 __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_bstride, int64_t x_rstride,
     const int32_t* __restrict__ start, const int32_t* __restrict__ count,
-    const int32_t* __restrict__ block_table, int64_t max_pages, int64_t page,
-    uint8_t* __restrict__ kv, int64_t kv_stride, int64_t kv_rows, int T, int chunks, int total,
-    const float* __restrict__ scale) {
+    const int32_t* __restrict__ block_table, int64_t max_pages, int64_t page, int page_shift,
+    uint8_t* __restrict__ kv, int64_t kv_stride, int64_t kv_rows, int B, int T, int chunks,
+    int rows, const float* __restrict__ scale) {
   using H = h16<BF16>;
   const float s = *scale;
   // x / s correctly rounded without a division per element (Markstein): with y = RN(1 / s),
@@ -38,19 +43,17 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
   // the sign of -0), and NaN inputs are passed through. Other scales divide per element.
   const float y = __fdiv_rn(1.0f, s);
   const bool fast = s >= 0x1p-90f && s <= 0x1p90f;
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
-    const int c = i % chunks;
-    const int bt = i / chunks;
-    const int b = bt / T, j = bt % T;
-    if (j >= count[b]) continue;
-    const int64_t p = (int64_t)start[b] + j;
-    if (p < 0 || p >= max_pages * page) continue;  // beyond the block table
-    const int64_t row = (int64_t)block_table[b * max_pages + p / page] * page + p % page;
-    if (row < 0 || row >= kv_rows) continue;  // a corrupt table entry never writes out of the pool
+  const int r = (int)threadIdx.x / chunks;  // row of the group (0 when chunks > 256)
+  const int c0 = (int)threadIdx.x - r * chunks;
+  if (r >= rows) return;  // threads past the last whole row (no barriers in this kernel)
+  const int64_t pool_tokens = max_pages * page;
+
+  auto load = [&](int b, int j, int c, u32x4 (&w)[VEC / 8]) {
     const u32x4* src = (const u32x4*)(x + b * x_bstride + j * x_rstride + VEC * c);
-    u32x4 w[VEC / 8];
 #pragma unroll
     for (int u = 0; u < VEC / 8; ++u) w[u] = src[u];
+  };
+  auto convert = [&](const u32x4 (&w)[VEC / 8], int c, int64_t row) {
     float v[VEC];
 #pragma unroll
     for (int u = 0; u < VEC / 8; ++u)
@@ -90,6 +93,28 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     } else {
       *(u32x2*)dst = u32x2{o[0], o[1]};
     }
+  };
+
+  for (int b = blockIdx.y; b < B; b += gridDim.y) {
+    const int cnt = min(count[b], T);
+    const int64_t st = start[b];
+    for (int j = blockIdx.x * rows + r; j < cnt; j += gridDim.x * rows) {
+      // the source row exists for every j < cnt: its load goes out before the table lookup, so
+      // the two global reads overlap instead of running back to back
+      u32x4 w[VEC / 8];
+      load(b, j, c0, w);
+      const int64_t p = st + j;
+      if (p < 0 || p >= pool_tokens) continue;  // beyond the block table
+      const int64_t pg = page_shift >= 0 ? p >> page_shift : p / page;
+      const int64_t off = page_shift >= 0 ? p & (page - 1) : p % page;
+      const int64_t row = (int64_t)block_table[b * max_pages + pg] * page + off;
+      if (row < 0 || row >= kv_rows) continue;  // a corrupt table entry never writes out of the pool
+      convert(w, c0, row);
+      for (int c = c0 + 256; c < chunks; c += 256) {  // rows of more than 256 chunks
+        load(b, j, c, w);
+        convert(w, c, row);
+      }
+    }
   }
 }
 
@@ -98,11 +123,14 @@ void launch(const void* x, int64_t xb, int64_t xr, const int32_t* start, const i
             const int32_t* bt, int64_t max_pages, int64_t page, void* kv, int64_t kv_stride,
             int64_t kv_rows, int64_t B, int64_t T, int64_t D, const float* scale, hipStream_t st) {
   const int chunks = (int)(D / VEC);
-  const int total = (int)(B * T * chunks);
-  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
-  kv_append_fp8_kernel<BF16, VEC><<<grid, 256, 0, st>>>(
-      (const uint16_t*)x, xb, xr, start, count, bt, max_pages, page, (uint8_t*)kv, kv_stride,
-      kv_rows, (int)T, chunks, total, scale);
+  const int rows = chunks > 256 ? 1 : 256 / chunks;  // token rows per workgroup
+  int shift = -1;
+  if ((page & (page - 1)) == 0) shift = __builtin_ctzll((unsigned long long)page);
+  const int64_t gy = std::min<int64_t>(B, 65535);
+  const int64_t gx = std::min<int64_t>((T + rows - 1) / rows, std::max<int64_t>(1, 8192 / gy));
+  kv_append_fp8_kernel<BF16, VEC><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, st>>>(
+      (const uint16_t*)x, xb, xr, start, count, bt, max_pages, page, shift, (uint8_t*)kv,
+      kv_stride, kv_rows, (int)B, (int)T, chunks, rows, scale);
 }
 
 }  // namespace
