@@ -383,32 +383,41 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int grp = wave >> 2, wl = wave & 3;
   const int blk = grp == 0 ? 2 * wl : 7 - 2 * wl;  // waves w and w + 4 share a SIMD
 
-  // workgroup -> (batch, head, query tile). Workgroup ids go round-robin over the 8 XCDs; each
-  // XCD takes whole K/V heads: all query tiles of the G = H / Hkv query heads that read one K/V
-  // head run there together (heaviest tiles first), so their K/V tiles come from that XCD's L2.
+  // workgroup -> (batch, head, slot). Workgroup ids go round-robin over the 8 XCDs; each XCD
+  // takes whole K/V heads: all query tiles of the G = H / Hkv query heads that read one K/V head
+  // run there together, so their K/V tiles come from that XCD's L2. Causal: slot s holds query
+  // tiles nqt - 1 - s and s of one head, (nqt - s) + (s + 1) key tiles together, so every
+  // workgroup carries the same work. The dispatcher gives every CU the same number of workgroups
+  // whatever their length (measured: 16 per CU at B 8, H 32, S 4096), so workgroups of unequal
+  // work leave CUs idle; one tile per workgroup kept them busy 79% of the time.
   const int nqt = (S + PP_BQ - 1) / PP_BQ;
+  const int nslot = CAUSAL ? (nqt + 1) / 2 : nqt;
   const int G = H / Hkv;
   const int lin = blockIdx.x;
-  int b, h, qt;
+  int b, h, slot;
   if ((B * Hkv) % 8 == 0) {
     const int xcd = lin & 7, s = lin >> 3;
-    const int per = nqt * G;  // workgroups per K/V head
+    const int per = nslot * G;  // workgroups per K/V head
     const int kvh = (s / per) * 8 + xcd, rem = s % per;
-    qt = nqt - 1 - rem % nqt;
+    slot = rem % nslot;
     b = kvh / Hkv;
-    h = (kvh % Hkv) * G + rem / nqt;
+    h = (kvh % Hkv) * G + rem / nslot;
   } else {
-    const int bh = lin / nqt;
-    qt = nqt - 1 - lin % nqt;
+    const int bh = lin / nslot;
+    slot = lin % nslot;
     b = bh / H;
     h = bh % H;
   }
-  const int q0 = qt * PP_BQ;
   // S counts the query tiles of the grid; the sequence's own query and key counts are Sq, Sk.
   // Causal: query i sees keys j <= i + (Sk - Sq) (bottom-right aligned; 0 offset when dense).
   const SeqRange sr = seq_range(sm, b);
+  const int n_items = CAUSAL && 2 * slot != nqt - 1 ? 2 : 1;
+  for (int item = 0; item < n_items; ++item) {
+  const int qt = CAUSAL && item == 0 ? nqt - 1 - slot : slot;
+  [&]() TLM_INLINE {  // one query tile; a return ends the tile
+  const int q0 = qt * PP_BQ;
   const int Sq = sr.nq, Sk = sr.nk, coff = Sk - Sq;
-  if (q0 >= Sq) return;  // whole workgroup, before any barrier
+  if (q0 >= Sq) return;  // whole workgroup
   const int64_t rs = (int64_t)H * PP_D;      // elements between consecutive tokens of Q, O
   const int64_t rs_kv = (int64_t)Hkv * PP_D;  // ... of K, V
   const int64_t head = (sr.q0 * H + h) * PP_D;
@@ -685,12 +694,17 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     const int q = qb0 + r;
     if (q < Sq) *(u32x4*)(Ob + (int64_t)q * rs + c) = *(const u32x4*)(stage + r * PP_OP + c);
   }
+  }();
+  // the next tile's LDS-DMA overwrites the epilogue's staging: every wave has read its own
+  phase_barrier();
+  }
 }
 
 template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
               float sc, const SeqMap& sm, hipStream_t st) {
-  const int64_t nwg = (int64_t)((S + PP_BQ - 1) / PP_BQ) * B * H;
+  const int64_t nqt = (S + PP_BQ - 1) / PP_BQ;
+  const int64_t nwg = (CAUSAL ? (nqt + 1) / 2 : nqt) * B * H;  // causal: two tiles per workgroup
   if (nwg > INT32_MAX) {
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
