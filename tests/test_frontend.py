@@ -168,6 +168,10 @@ def test_varlen_flashattn_program():
         k(q, kv, kv, cu, cu, 256.0)
     with pytest.raises(ValueError, match="Expected 7 arguments"):
         k(q, kv, kv, cu, cu)
+    # the profiler's random supply has nothing to give a scalar (as the reference's supply)
+    from tilelang.utils.tensor import TensorSupplyType, get_tensor_supply
+    with pytest.raises(ValueError, match="must have a shape"):
+        get_tensor_supply(TensorSupplyType.Auto)(k.params[5])
 
 
 def test_scalar_params_rejected():

@@ -46,6 +46,9 @@ def get_tensor_supply(supply_type: TensorSupplyType):
     """Return ``param -> tensor`` on the current HIP device for the given supply type."""
 
     def get_tensor(param) -> torch.Tensor:
+        if param.is_scalar():  # as the reference's supply (tilelang/utils/tensor.py)
+            raise ValueError(f"TensorType must have a shape, but got {type(param)}: scalar "
+                             "parameters have no random supply; pass the inputs explicitly")
         dtype = param.dtype
         shape = [int(s) for s in param.shape]
         device = torch.device("cuda", torch.cuda.current_device())
