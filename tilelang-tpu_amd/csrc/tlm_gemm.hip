@@ -6,7 +6,7 @@
 //
 // Main kernel (any M, N; K % 8 == 0, N % 8 == 0 for row-major B):
 //   * 256x256 output tile per workgroup, BK = 64, 512 threads = 8 waves of 128x64 sub-tiles;
-//   * v_mfma_f32_32x32x16_{f16,bf16}: per wave 4x2 accumulator tiles = 128 fp32 VGPRs;
+//   * v_mfma_f32_16x16x32_{f16,bf16}: per wave 8x4 accumulator tiles = 128 fp32 VGPRs;
 //   * A tiles [256][64] and B tiles [64][256] (row-major B kept row-major; [256][64] for B^T)
 //     are filled by buffer_load ... lds (16 bytes per lane straight into LDS, no VGPR staging)
 //     into unpadded, XOR-swizzled stages (2 for A, 3 for B: 160 KB); lanes whose chunk lies
@@ -34,19 +34,19 @@ constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int NTHREADS = 512;
 
 template <bool BF16>
-struct mfma_t;
+struct mfma16_t;
 template <>
-struct mfma_t<false> {
+struct mfma16_t<false> {
   typedef f16x8 v8;
-  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 template <>
-struct mfma_t<true> {
+struct mfma16_t<true> {
   typedef bf16x8 v8;
-  static TLM_DEV f32x16 mma(v8 a, v8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 
@@ -107,6 +107,7 @@ TLM_DEV u32x2 lds_tr16(const void* p) {
 TLM_DEV void lgkm_wait(int n) {  // lgkmcnt(n); n a compile-time constant after unrolling
   switch (n) {
     case 0: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0xc17f); break;
     case 2: __builtin_amdgcn_s_waitcnt(0xc27f); break;
     case 4: __builtin_amdgcn_s_waitcnt(0xc47f); break;
     case 8: __builtin_amdgcn_s_waitcnt(0xc87f); break;
@@ -136,10 +137,11 @@ constexpr uint32_t OOB = 0xfffffff0u;   // offset past num_records: the load ret
 // reads are bank-conflict free and every LDS-DMA instruction fills 1 KB of contiguous LDS:
 //   * [rows][64 k] tiles (A, and B^T): chunk c of row r at c ^ ((r >> 1) & 7);
 //     a 16-lane ds_read_b128 phase covers rows r0..r0+15 of one chunk column;
-//   * [64 k][256 n] row-major B: chunk c of row k at c ^ (4 (k & 3)); a 32-lane
-//     ds_read_b64_tr_b16 phase covers 4 k-rows x 64 bytes.
+//   * [64 k][256 n] row-major B: chunk c of row k at c ^ (2 (k & 3) + 8 ((k >> 3) & 1)); a
+//     32-lane ds_read_b64_tr_b16 phase covers k-rows k0..k0+3 and k0+8..k0+11 of the same 32
+//     bytes of columns (two 16x16x32 operand groups): 16 distinct chunk positions.
 TLM_DEV int swz_rows(int r) { return (r >> 1) & 7; }
-TLM_DEV int swz_k(int k) { return 4 * (k & 3); }
+TLM_DEV int swz_k(int k) { return 2 * (k & 3) + 8 * ((k >> 3) & 1); }
 constexpr int ST_A = BM * BK * 2;  // bytes per stage of A
 constexpr int ST_B = BK * BN * 2;  // bytes per stage of B (either layout)
 constexpr int NST_A = 2, NST_B = 3;
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
                                                            const uint16_t* __restrict__ B,
                                                            void* __restrict__ C, int M, int N,
                                                            int K) {
-  using MT = mfma_t<BF16>;
+  using MT = mfma16_t<BF16>;
   using v8 = typename MT::v8;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
@@ -213,27 +215,34 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
     for (int j = 0; j < 8; ++j) dma(dd, OPc, 8 * (wave & 3) + j, kmax);
   };
 
-  f32x16 acc[4][2];
+  f32x4 acc[8][4];  // [16-row tile mt][16-column tile nt] of the wave's 128 x 64 sub-tile
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
 
-  // ---- per-lane operand read offsets (bytes within a stage)
-  const int hf = lane >> 5;
+  // ---- per-lane operand read offsets (bytes within a stage). v_mfma_f32_16x16x32: lane l holds
+  // row (A) / column (B) l % 16 and k = 8 (l / 16) .. + 7 of the 32-k step. The 16x16 shape
+  // keeps the same LDS traffic per FLOP as 32x32x16 and draws less power per FLOP: a pure MFMA
+  // loop on all CUs settled at 2.39 GHz against 2.22 GHz for 32x32x16 at the same efficiency
+  // per cycle.
+  const int q4 = lane >> 4;                                    // k chunk within the step
   const int sw = (lane >> 1) & 7;                              // swz_rows of this lane's rows
-  const int a_row = (wm * 128 + (lane & 31)) * (BK * 2);       // + mi * 32 rows
-  const int bt_row = (wn * 64 + (lane & 31)) * (BK * 2);       // + ni * 32 rows (B^T)
-  // row-major B through ds_read_b64_tr_b16: group h of 16 lanes, lane j in it
+  const int a_row = (wm * 128 + (lane & 15)) * (BK * 2);       // + mt * 16 rows
+  const int bt_row = (wn * 64 + (lane & 15)) * (BK * 2);       // + nt * 16 rows (B^T)
+  // row-major B through ds_read_b64_tr_b16: 16-lane group h reads k-rows 8 h + j / 4 (+ 4 for
+  // the second read, + 32 for the second k-step); lane j addresses the 8 bytes at columns
+  // 16 nt + 4 (j % 4) and receives column j of the four rows
   const int h = lane >> 4, j = lane & 15;
-  const int tr_k = 8 * (h >> 1) + (j >> 2);                    // + 16 ks, + 4 for the 2nd read
-  const int tr_c = 8 * wn + 2 * (h & 1) + ((j & 3) >> 1);      // + 4 ni
+  const int tr_k = 8 * h + (j >> 2);
+  const int tr_c = 8 * wn + ((j & 3) >> 1);                    // chunk, + 2 nt
   const int tr_off = tr_k * (BN * 2) + 8 * (j & 1);
+  const int tr_sw = swz_k(tr_k);                               // the same for every k-step
 
   // Ping-pong schedule. The two waves on a SIMD (w and w + 4, groups grp = w / 4) run half a
   // k-tile apart: in each phase one of them issues MFMAs while the other reads the next k-tile's
-  // A operands (all four k-steps) and first B operand from LDS into registers; the computing
-  // wave reads B one k-step ahead. Group 0 loads k-tile kt in phase 2 kt and computes it in
+  // A operands (both k-steps) and first B operand from LDS into registers; the computing wave
+  // reads B two operands ahead. Group 0 loads k-tile kt in phase 2 kt and computes it in
   // phase 2 kt + 1; group 1 is one phase later. Every phase ends with a workgroup barrier.
   // A k-tile's A stage is read in phases 2 kt, 2 kt + 1 and its B stage through phase 2 kt + 2,
   // hence 2 A stages and 3 B stages. LDS-DMA is issued only in load phases, where the waves
@@ -243,71 +252,70 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   // group 1 loads B of k-tile kt + 2 in phase 2 kt + 1 (its stage held B of kt - 1, read by
   // phase 2 kt). A lands within two phases, B within three.
   const int grp = wave >> 2;
-  u32x4 aop[BK / 16][4];  // A operands of a whole k-tile
-  u32x4 bop[2][2];        // B operands of one k-step
-  auto readb = [&](int kt, int ks, u32x4 (&o)[2]) {
+  u32x4 aop[BK / 32][8];  // A operands of a whole k-tile: [k-step][mt]
+  u32x4 bop0;             // first B operand of the k-tile (read in the load phase)
+  // B operand t = 4 ks + nt of k-tile kt
+  auto readb = [&](int kt, int t) {
     const uint8_t* sb = sb_of(kt);
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      if constexpr (TRANS_B) {
-        o[ni] = lds_b128(sb + bt_row + ni * 32 * BK * 2 + 16 * ((2 * ks + hf) ^ sw));
-      } else {
-        const uint8_t* q = sb + (16 * ks) * (BN * 2) + tr_off;
-        const int c = tr_c + 4 * ni;
-        const u32x2 lo = lds_tr16(q + 16 * (c ^ swz_k(j >> 2)));
-        const u32x2 hi = lds_tr16(q + 4 * (BN * 2) + 16 * (c ^ swz_k(j >> 2)));
-        o[ni] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
+    const int ks = t >> 2, nt = t & 3;
+    if constexpr (TRANS_B) {
+      return lds_b128(sb + bt_row + nt * 16 * BK * 2 + 16 * ((4 * ks + q4) ^ sw));
+    } else {
+      const uint8_t* q = sb + (32 * ks) * (BN * 2) + tr_off + 16 * ((tr_c + 2 * nt) ^ tr_sw);
+      const u32x2 lo = lds_tr16(q);
+      const u32x2 hi = lds_tr16(q + 4 * (BN * 2));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
   };
-  constexpr int BREADS = TRANS_B ? 2 : 4;  // LDS instructions of readb()
-  // The group's 8 LDS-DMA instructions of the phase go two per k-step between the operand
-  // reads instead of in one burst. dma_kt < 0: nothing to issue; op: operand of the group.
-  auto dma_pair = [&](const Dma& dd, int dma_kt, auto OPc, int ks) {
+  constexpr int BREADS = TRANS_B ? 1 : 2;  // LDS instructions of readb()
+  // The group's 8 LDS-DMA instructions of the phase go two after every four operand reads
+  // instead of in one burst. dma_kt < 0: nothing to issue; op: operand of the group.
+  auto dma_pair = [&](const Dma& dd, int dma_kt, auto OPc, int q) {
     if (dma_kt >= 0) {
       const int kmax = min(BK, K - dma_kt * BK);
-      dma(dd, OPc, 8 * (wave & 3) + 2 * ks, kmax);
-      dma(dd, OPc, 8 * (wave & 3) + 2 * ks + 1, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * q, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * q + 1, kmax);
     }
   };
   auto load_phase = [&](int kt, int dma_kt, auto OPc) {
     const uint8_t* sa = sa_of(kt);
     const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    for (int ks = 0; ks < BK / 32; ++ks)
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        aop[ks][mi] = lds_b128(sa + a_row + mi * 32 * BK * 2 + 16 * ((2 * ks + hf) ^ sw));
-      dma_pair(dd, dma_kt, OPc, ks);
-    }
-    readb(kt, 0, bop[0]);
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4) {
+          const int mt = 4 * half + m4;
+          aop[ks][mt] = lds_b128(sa + a_row + mt * 16 * BK * 2 + 16 * ((4 * ks + q4) ^ sw));
+        }
+        dma_pair(dd, dma_kt, OPc, 2 * ks + half);
+      }
+    bop0 = readb(kt, 0);
     lgkm_wait(0);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks)
+    for (int ks = 0; ks < BK / 32; ++ks)
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) order_after(aop[ks][mi]);
-    order_after(bop[0][0]);
-    order_after(bop[0][1]);
+      for (int mt = 0; mt < 8; ++mt) order_after(aop[ks][mt]);
+    order_after(bop0);
   };
   auto compute_phase = [&](int kt) {
+    constexpr int NB = 4 * (BK / 32);  // B operands per k-tile
+    u32x4 b[3];                        // ring: operand t in b[t % 3], read two ahead
+    b[0] = bop0;
+    b[1] = readb(kt, 1);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      // B of k-step ks has landed; the reads of k-step ks + 1 stay in flight
-      if (ks + 1 < BK / 16) {
-        readb(kt, ks + 1, bop[(ks + 1) & 1]);
-        lgkm_wait(BREADS);
-      } else {
-        lgkm_wait(0);
-      }
-      order_after(bop[ks & 1][0]);
-      order_after(bop[ks & 1][1]);
+    for (int t = 0; t < NB; ++t) {
+      if (t + 2 < NB) b[(t + 2) % 3] = readb(kt, t + 2);
+      // operand t has landed; the reads of t + 1 and t + 2 stay in flight
+      const int ahead = (t + 1 < NB ? 1 : 0) + (t + 2 < NB ? 1 : 0);
+      lgkm_wait(ahead * BREADS);
+      order_after(b[t % 3]);
+      const int ks = t >> 2, nt = t & 3;
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          acc[mi][ni] = MT::mma(__builtin_bit_cast(v8, aop[ks][mi]),
-                                __builtin_bit_cast(v8, bop[ks & 1][ni]), acc[mi][ni]);
-      }
+      for (int mt = 0; mt < 8; ++mt)
+        acc[mt][nt] = MT::mma(__builtin_bit_cast(v8, aop[ks][mt]),
+                              __builtin_bit_cast(v8, b[t % 3]), acc[mt][nt]);
     }
   };
   // prologue: A of k-tile 0 (group 0), B of k-tiles 0 and 1 (group 1)
@@ -346,17 +354,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
     }
   }
 
-  // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8*(i/4) + 4*(lane/32) + i%4
+  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = n0 + wn * 64 + nt * 16 + (lane & 15);
       if (col >= N) continue;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m0 + wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mi][ni][i]);
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm * 128 + mt * 16 + 4 * (lane >> 4) + i;
+        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mt][nt][i]);
       }
     }
 }
@@ -374,22 +382,6 @@ constexpr int SK_NT = 64;
 constexpr int SK_BK = 32;
 constexpr int SK_BPITCH = SK_NT + 16;  // halves per LDS row of a B block (160 bytes)
 
-template <bool BF16>
-struct mfma16_t;
-template <>
-struct mfma16_t<false> {
-  typedef f16x8 v8;
-  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct mfma16_t<true> {
-  typedef bf16x8 v8;
-  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
 
 template <bool BF16, bool TRANS_B, int OUT>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __restrict__ A,
