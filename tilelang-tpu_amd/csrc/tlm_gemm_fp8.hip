@@ -5,14 +5,13 @@
 // transpose_B=True into a float fragment, copied out to an fp8 C; checked against
 // (a.half() @ b.half().T).to(fp8), :46-55) and example_tilelang_gemm_fp8_2xAcc.py:10-50 (the same
 // product kept in fp32: C is float). The two-level accumulation of the 2xAcc program is a
-// Hopper precision workaround; v_mfma_f32_32x32x64_f8f6f4 accumulates every product in fp32.
+// Hopper precision workaround; v_mfma_f32_16x16x128_f8f6f4 accumulates every product in fp32.
 //
 // Design: the 256x256 ping-pong of gemm_256x256 (tlm_gemm.hip) at one byte per element. A k-tile
 // is 128 k = 128 bytes per row, the same LDS tile and LDS-DMA pattern as a 64-k 16-bit tile, and
-// one v_mfma_f32_32x32x64_f8f6f4 (64 k) takes the place of four 32x32x16 16-bit MFMAs at twice
-// the FLOP rate. Operand layout of the 32x32x64 MFMA: lane l holds row (A) / column (B) l % 32;
-// lane half h = l / 32 holds k = 16 h .. 16 h + 15 and 32 + 16 h .. 32 + 16 h + 15 of the 64-k
-// step, i.e. two 16-byte chunks of the row.
+// one v_mfma_f32_16x16x128_f8f6f4 covers the whole k-tile for a 16x16 output tile at twice the
+// 16-bit FLOP rate. Each lane holds 32 bytes of its row (A) / column (B) l % 16: the 16-byte
+// chunks q and q + 4 of the row, q = l / 16.
 #include "tlm_common.h"
 
 #include <type_traits>
@@ -29,8 +28,8 @@ constexpr int SMEM = (NST_A + NST_B) * ST;  // 160 KB
 
 // FMT: 0 = e4m3, 1 = e5m2 (the cbsz / blgp format codes of the f8f6f4 MFMA)
 template <int FMT>
-TLM_DEV f32x16 mma8(i32x8 a, i32x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FMT, FMT, 0, 0, 0, 0);
+TLM_DEV f32x4 mma8(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, 0, 0, 0, 0);
 }
 
 TLM_DEV uint32_t lds_addr(const void* p) {
@@ -150,87 +149,87 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
     for (int j = 0; j < 8; ++j) dma(dd, OPc, 8 * (wave & 3) + j, kmax);
   };
 
-  f32x16 acc[4][2];
+  f32x4 acc[8][4];  // [16-row tile mt][16-column tile nt] of the wave's 128 x 64 sub-tile
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
 
-  const int hf = lane >> 5;
+  // v_mfma_f32_16x16x128_f8f6f4: lane l holds row (A) / column (B) l % 16 and 32 of the 128 k;
+  // any assignment of k to lanes gives the same product when A and B use the same one. Lane
+  // group q = l / 16 takes the 16-byte chunks q and q + 4 of the 128-byte row, so a 16-lane
+  // read covers 16 rows of one chunk column (conflict free under the row swizzle). The 16x16
+  // shape draws less power per FLOP than 32x32 (a higher sustained clock).
+  const int q4 = lane >> 4;
   const int sw = (lane >> 1) & 7;
-  const int a_row = (wm * 128 + (lane & 31)) * BKB;
-  const int b_row = (wn * 64 + (lane & 31)) * BKB;
+  const int a_row = (wm * 128 + (lane & 15)) * BKB;  // + mt * 16 rows
+  const int b_row = (wn * 64 + (lane & 15)) * BKB;   // + nt * 16 rows
 
   // Ping-pong of the two waves on each SIMD (groups of 4), as in gemm_256x256: one reads the
-  // next k-tile's A operands (both 64-k steps) and its first B operands while the other issues
-  // MFMAs; every phase ends with a workgroup barrier. LDS-DMA is issued only in load phases:
-  // group 0 fills A of k-tile kt + 1 in phase 2 kt (its stage held A of kt - 1, last read in
-  // phase 2 kt - 1), group 1 fills B of kt + 2 in phase 2 kt + 1 (its stage held B of kt - 1,
-  // last read in phase 2 kt), so each phase carries one 32 KB operand stage of DMA.
+  // next k-tile's A operands and its first B operand while the other issues MFMAs; every phase
+  // ends with a workgroup barrier. LDS-DMA is issued only in load phases: group 0 fills A of
+  // k-tile kt + 1 in phase 2 kt (its stage held A of kt - 1, last read in phase 2 kt - 1),
+  // group 1 fills B of kt + 2 in phase 2 kt + 1 (its stage held B of kt - 1, last read in
+  // phase 2 kt), so each phase carries one 32 KB operand stage of DMA.
   const int grp = wave >> 2;
-  u32x4 aop[2][4][2];  // [k-step][mi][chunk]
-  u32x4 bop[2][2][2];  // [buffer][ni][chunk]
-  auto chunk = [&](int ks, int p) { return 16 * ((4 * ks + 2 * p + hf) ^ sw); };
-  auto readb = [&](int kt, int ks, u32x4 (&o)[2][2]) {
+  u32x4 aop[8][2];  // [mt][chunk] of the k-tile
+  u32x4 bop0[2];    // first B operand of the k-tile (read in the load phase)
+  auto chunk = [&](int p) { return 16 * ((4 * p + q4) ^ sw); };
+  auto readb = [&](int kt, int nt, u32x4 (&o)[2]) {
     const uint8_t* sb = sb_of(kt);
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) o[ni][p] = lds_b128(sb + b_row + ni * 32 * BKB + chunk(ks, p));
+    for (int p = 0; p < 2; ++p) o[p] = lds_b128(sb + b_row + nt * 16 * BKB + chunk(p));
   };
-  // the wave's 8 instructions of the phase, 4 after each k-step's operand reads
-  auto dma_quad = [&](const Dma& dd, int dma_kt, auto OPc, int ks) {
+  // the wave's 8 instructions of the phase, two after every four operand reads
+  auto dma_pair = [&](const Dma& dd, int dma_kt, auto OPc, int q) {
     if (dma_kt >= 0) {
       const int kmax = min(BKB, K - dma_kt * BKB);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) dma(dd, OPc, 8 * (wave & 3) + 4 * ks + d, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * q, kmax);
+      dma(dd, OPc, 8 * (wave & 3) + 2 * q + 1, kmax);
     }
   };
   auto load_phase = [&](int kt, int dma_kt, auto OPc) {
     const uint8_t* sa = sa_of(kt);
     const Dma dd = dma_setup(dma_kt < 0 ? 0 : dma_kt);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+      for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          aop[ks][mi][p] = lds_b128(sa + a_row + mi * 32 * BKB + chunk(ks, p));
-      dma_quad(dd, dma_kt, OPc, ks);
+          aop[2 * q + m2][p] = lds_b128(sa + a_row + (2 * q + m2) * 16 * BKB + chunk(p));
+      dma_pair(dd, dma_kt, OPc, q);
     }
-    readb(kt, 0, bop[0]);
+    readb(kt, 0, bop0);
     lgkm_wait<0>();
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) order_after(aop[ks][mi][p]);
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) order_after(bop[0][ni][p]);
+      for (int p = 0; p < 2; ++p) order_after(aop[mt][p]);
+    order_after(bop0[0]);
+    order_after(bop0[1]);
   };
   auto compute_phase = [&](int kt) {
+    u32x4 b[3][2];  // ring: operand nt in b[nt % 3], read two ahead
+    b[0][0] = bop0[0];
+    b[0][1] = bop0[1];
+    readb(kt, 1, b[1]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 0) {
-        readb(kt, 1, bop[1]);
-        lgkm_wait<4>();  // B of k-step 0 landed; k-step 1's 4 reads stay in flight
-      } else {
+    for (int nt = 0; nt < 4; ++nt) {
+      if (nt + 2 < 4) readb(kt, nt + 2, b[(nt + 2) % 3]);
+      // operand nt has landed; the reads of nt + 1 and nt + 2 (2 instructions each) stay in flight
+      if (nt + 2 < 4)
+        lgkm_wait<4>();
+      else if (nt + 1 < 4)
+        lgkm_wait<2>();
+      else
         lgkm_wait<0>();
-      }
+      order_after(b[nt % 3][0]);
+      order_after(b[nt % 3][1]);
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) order_after(bop[ks][ni][p]);
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          acc[mi][ni] = mma8<FMT>(cat8(aop[ks][mi][0], aop[ks][mi][1]),
-                                  cat8(bop[ks][ni][0], bop[ks][ni][1]), acc[mi][ni]);
-      }
+      for (int mt = 0; mt < 8; ++mt)
+        acc[mt][nt] = mma8<FMT>(cat8(aop[mt][0], aop[mt][1]), cat8(b[nt % 3][0], b[nt % 3][1]),
+                                acc[mt][nt]);
     }
   };
   // prologue: A of k-tile 0 (group 0), B of k-tiles 0 and 1 (group 1)
@@ -269,18 +268,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
     }
   }
 
-  // epilogue: lane holds column (lane & 31) of each 32x32 tile, rows 8 (i / 4) + 4 (lane / 32)
-  // + i % 4
+  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
+    for (int nt = 0; nt < 4; ++nt) {
+      const int col = n0 + wn * 64 + nt * 16 + (lane & 15);
       if (col >= N) continue;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m0 + wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mi][ni][i]);
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm * 128 + mt * 16 + 4 * (lane >> 4) + i;
+        if (row < M) store_out<OUT>(C, (int64_t)row * N + col, acc[mt][nt][i]);
       }
     }
 }
