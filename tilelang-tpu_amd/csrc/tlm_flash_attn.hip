@@ -76,6 +76,23 @@ struct fa_mma<true> {
   }
 };
 
+template <bool BF16>
+struct fa_mma16;
+template <>
+struct fa_mma16<false> {
+  typedef f16x8 v8;
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct fa_mma16<true> {
+  typedef bf16x8 v8;
+  static TLM_DEV f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
 template <bool BF16, bool CAUSAL, int D>
 __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __restrict__ Q,
                                                           const uint16_t* __restrict__ K,
@@ -277,8 +294,11 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
 // Head dim 128: ping-pong kernel.
 //
 //   * workgroup = 8 waves = 256 queries of one (batch, head); a wave owns one 32-query block and
-//     computes S^T = K Q^T and O^T = V^T P^T as above (Q^T in VGPRs, P^T straight from the S^T
-//     accumulator);
+//     computes S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_16x16x32 (two 16-query tiles; Q^T
+//     in VGPRs, P^T straight from the S^T accumulator). A lane holds 16 keys of each of its two
+//     queries, so the softmax statistics combine the four lane groups with xor-16 and xor-32
+//     exchanges. The 16x16 shape draws less power per FLOP than 32x32x16 (a higher sustained
+//     clock: +3.6% at S 2048 non-causal);
 //   * the waves form two groups of four (one wave of each group per SIMD) that run one phase
 //     apart: while one group issues MFMAs (QK of tile j and PV of tile j-1: 32 MFMAs per wave, at
 //     raised wave priority) the other runs the softmax of its tile on the VALU, so each SIMD's
@@ -291,8 +311,8 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
 //     buffer_load ... lds (16 bytes per lane, no VGPR staging). Tile j + 2 is loaded during step j;
 //     the buffer descriptor of a tile ends at its last valid key, so keys >= S read as zeros;
 //   * LDS layout: rows of 256 bytes, 16-byte chunk c of key row r stored at chunk c ^ (r & 15) for
-//     K (the ds_read_b128 row reads of 16 lanes hit 16 distinct chunks) and c ^ 4 (r & 3) for V
-//     (the ds_read_b64_tr_b16 reads of 32 lanes cover 4 rows x 4 chunks);
+//     K (the ds_read_b128 row reads of 16 lanes hit 16 distinct chunks) and c ^ 2 (r & 7) for V
+//     (the ds_read_b64_tr_b16 reads of 32 lanes cover 8 key rows x 2 chunks);
 //   * online softmax with a lazy running max: a tile is exponentiated against the current m
 //     without computing its max; only when its P sum leaves the safe range (bf16 2^64, fp16 2^15;
 //     also the first tile, where m = -inf) is it redone with m raised to the tile max and O, l
@@ -373,7 +393,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
                                                    const uint16_t* __restrict__ V,
                                                    void* __restrict__ O, int B, int S, int H,
                                                    int Hkv, float sc, SeqMap sm) {
-  using MT = fa_mma<BF16>;
+  using MT = fa_mma16<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[PP_SMEM];
@@ -432,17 +452,21 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int w_last = qb0 + 31 + coff;  // last key visible to the wave
   const int nw = qb0 >= Sq ? 0 : (CAUSAL ? (w_last < 0 ? 0 : min(n, w_last / PP_KV + 1)) : n);
 
-  const int ql = lane & 31, g = lane >> 5;
-  const int my_q = qb0 + ql;
+  // v_mfma_f32_16x16x32 roles: lane l works on column (query) l % 16 of a 16-wide tile and on
+  // k group g = l / 16; the wave's 32 queries are two 16-query tiles qq
+  const int ql = lane & 15, g = lane >> 4;
+  const int my_q[2] = {qb0 + ql, qb0 + 16 + ql};
 
-  // Q^T operand: lane holds query my_q, d = 16 ds + 8 g .. + 7
-  v8 qreg[PP_D / 16];
+  // Q^T operand (B of S^T = K Q^T): lane holds query my_q[qq], d = 32 dk + 8 g .. + 7
+  v8 qreg[2][PP_D / 32];
 #pragma unroll
-  for (int ds = 0; ds < PP_D / 16; ++ds) {
-    u32x4 v = {0, 0, 0, 0};
-    if (my_q < Sq) v = *(const u32x4*)(Qb + (int64_t)my_q * rs + 16 * ds + 8 * g);
-    qreg[ds] = __builtin_bit_cast(v8, v);
-  }
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int dk = 0; dk < PP_D / 32; ++dk) {
+      u32x4 v = {0, 0, 0, 0};
+      if (my_q[qq] < Sq) v = *(const u32x4*)(Qb + (int64_t)my_q[qq] * rs + 32 * dk + 8 * g);
+      qreg[qq][dk] = __builtin_bit_cast(v8, v);
+    }
 
   // ---- LDS-DMA: group 0 fills K tiles, group 1 V tiles; wave wl writes rows 16 wl .. 16 wl + 15
   // (4 instructions of 4 rows x 16 chunks). Lane -> (row, stored chunk p) fetches chunk p ^ swz.
@@ -453,7 +477,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = 16 * wl + 4 * r + (lane >> 4), p = lane & 15;
-    const int c = dma_v ? (p ^ (4 * (row & 3))) : (p ^ (row & 15));
+    const int c = dma_v ? (p ^ (2 * (row & 7))) : (p ^ (row & 15));
     doff[r] = (uint32_t)row * rs2 + 16u * (uint32_t)c;
   }
   uint8_t* const dlds = smem + (dma_v ? PP_VRING : 0) + wl * 4096;
@@ -472,30 +496,35 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   // ---- operand read addresses (LDS byte addresses of the current K / V stage; row-block offsets
   // within a stage are immediates)
   const uint32_t sbase = lds_u32(smem);
-  uint32_t kaddr[PP_D / 16];  // K row (lane & 31) of the 32-key block, d chunk 2 ds + g
+  // K (A of S^T): key row 16 kt + ql (kt as an immediate row offset), d chunk 4 dk + g
+  uint32_t kaddr[PP_D / 32];
 #pragma unroll
-  for (int ds = 0; ds < PP_D / 16; ++ds)
-    kaddr[ds] = sbase + (uint32_t)(ql * 256 + 16 * ((2 * ds + g) ^ (lane & 15)));
-  // V^T through ds_read_b64_tr_b16: 16-lane group hh, lane jj reads 4 dims of key row
-  // 4 (hh >> 1) + (jj >> 2) (+ 8 for the second half of the k-step)
-  const int hh = lane >> 4, jj = lane & 15;
-  uint32_t vaddr[PP_D / 32];
+  for (int dk = 0; dk < PP_D / 32; ++dk)
+    kaddr[dk] = sbase + (uint32_t)(ql * 256 + 16 * ((4 * dk + g) ^ ql));
+  // V^T (A of O^T) through ds_read_b64_tr_b16: 16-lane group g, lane j reads 4 dims
+  // 16 dt + 4 (j % 4) of key row 4 g + j / 4 (+ 16 for the second read, + 32 for the second
+  // k-step) and receives dim 16 dt + j of the four keys. The operand's k (key) set of lane
+  // group g is {4 g .. 4 g + 3, 16 + 4 g .. 16 + 4 g + 3} of the 32-key step, the set in which
+  // the S^T accumulators hold P^T (any key order gives the same product when P^T uses it too).
+  const int jj = lane & 15;
+  const int vrow = 4 * g + (jj >> 2);
+  uint32_t vaddr[PP_D / 16];
 #pragma unroll
-  for (int dt = 0; dt < PP_D / 32; ++dt) {
-    const int row = 4 * (hh >> 1) + (jj >> 2);
-    const int c = (4 * dt + 2 * (hh & 1) + ((jj & 3) >> 1)) ^ (4 * (row & 3));
-    vaddr[dt] = sbase + PP_VRING + (uint32_t)(row * 256 + 16 * c + 8 * (jj & 1));
+  for (int dt = 0; dt < PP_D / 16; ++dt) {
+    const int c = (2 * dt + ((jj & 3) >> 1)) ^ (2 * (vrow & 7));
+    vaddr[dt] = sbase + PP_VRING + (uint32_t)(vrow * 256 + 16 * c + 8 * (jj & 1));
   }
 
-  f32x16 oacc[PP_D / 32];
+  f32x4 oacc[PP_D / 16][2];  // O^T: [16-dim tile][query tile], element i = dim 16 dt + 4 g + i
 #pragma unroll
-  for (int t = 0; t < PP_D / 32; ++t) oacc[t] = f32x16{};
-  f32x16 sacc[2];
-  u32x4 pb[2][2];  // P^T operands of the last softmax: [32-key block t][16-key half s2]
-  float m_run = -INFINITY, l_part = 0.f;
+  for (int t = 0; t < PP_D / 16; ++t) oacc[t][0] = oacc[t][1] = f32x4{};
+  f32x4 sacc[4][2];  // S^T: [16-key tile][query tile], element i = key 16 kt + 4 g + i
+  u32x4 pb[2][2];    // P^T operands of the last softmax: [32-key step][query tile]
+  float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
 
-  // ---- MFMA phase: QK of the tile in the current K stage (16 MFMAs), then PV of the tile in the
-  // current V stage (16 MFMAs). Operand reads run DEPTH MFMAs ahead.
+  // ---- MFMA phase: QK of the tile in the current K stage (16 operands x 2 query tiles), then
+  // PV of the tile in the current V stage (16 operands x 2 query tiles). Operand reads run DEPTH
+  // operands ahead.
   constexpr int DEPTH = 4;
   auto x_phase = [&](auto QKc, auto PVc) TLM_INLINE {
     constexpr bool DO_QK = decltype(QKc)::value, DO_PV = decltype(PVc)::value;
@@ -505,14 +534,14 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     auto read = [&](auto Mc) TLM_INLINE {
       constexpr int m = decltype(Mc)::value;
       if constexpr (m < NOPS) {
-        if constexpr (m < NQK) {  // K rows 32 t .. 32 t + 31, d chunk 2 ds + g
-          constexpr int ds = m / 2, t = m % 2;
-          op[m % (DEPTH + 1)] = ds_b128<t * 32 * 256>(kaddr[ds]);
-        } else {  // V^T: keys 32 t + 16 s2 + .., dims 32 dt + ..
-          constexpr int mm = m - NQK, ts = mm / 4, dt = mm % 4;
-          constexpr int off = 16 * ts * 256;
+        if constexpr (m < NQK) {  // K rows 16 kt .. 16 kt + 15, d chunk 4 dk + g
+          constexpr int dk = m / 4, kt = m % 4;
+          op[m % (DEPTH + 1)] = ds_b128<kt * 16 * 256>(kaddr[dk]);
+        } else {  // V^T: keys 32 ks + {4 g.., 16 + 4 g..}, dims 16 dt + ..
+          constexpr int mm = m - NQK, ks = mm / 8, dt = mm % 8;
+          constexpr int off = 32 * ks * 256;
           const u32x2 lo = ds_tr16<off>(vaddr[dt]);
-          const u32x2 hi = ds_tr16<off + 8 * 256>(vaddr[dt]);
+          const u32x2 hi = ds_tr16<off + 16 * 256>(vaddr[dt]);
           op[m % (DEPTH + 1)] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
       }
@@ -532,35 +561,38 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
       order_after(op[m % (DEPTH + 1)]);
       const v8 a = __builtin_bit_cast(v8, op[m % (DEPTH + 1)]);
       if constexpr (m < NQK) {
-        constexpr int ds = m / 2, t = m % 2;
-        sacc[t] = MT::mma(a, qreg[ds], ds == 0 ? f32x16{} : sacc[t]);
+        constexpr int dk = m / 4, kt = m % 4;
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq)
+          sacc[kt][qq] = MT::mma(a, qreg[qq][dk], dk == 0 ? f32x4{} : sacc[kt][qq]);
       } else {
-        constexpr int mm = m - NQK, ts = mm / 4, dt = mm % 4;
-        oacc[dt] = MT::mma(a, __builtin_bit_cast(v8, pb[ts >> 1][ts & 1]), oacc[dt]);
+        constexpr int mm = m - NQK, ks = mm / 8, dt = mm % 8;
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq)
+          oacc[dt][qq] = MT::mma(a, __builtin_bit_cast(v8, pb[ks][qq]), oacc[dt][qq]);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // ---- softmax of tile j (scores in sacc): keys of this lane 64 j + 32 t + 8 (i / 4) + 4 g + i % 4.
-  // P = 2^(s sc - m) with the current m; the tile's P sum bounds every P, so a sum above P_LIMIT
-  // (or not finite) sends the tile through the rescaling path. P_LIMIT keeps P in range of the
-  // 16-bit type (fp16: every P <= 2^15) and O, l far from fp32 overflow (bf16: P <= 2^64).
+  // ---- softmax of tile j (scores in sacc): lane holds keys 64 j + 16 kt + 4 g + i of queries
+  // my_q[qq]. P = 2^(s sc - m) with the current m; the tile's P sum bounds every P, so a sum
+  // above P_LIMIT (or not finite) sends the tile through the rescaling path. P_LIMIT keeps P in
+  // range of the 16-bit type (fp16: every P <= 2^15) and O, l far from fp32 overflow (bf16:
+  // P <= 2^64).
   constexpr float P_LIMIT = BF16 ? 18446744073709551616.0f : 32768.0f;
-  auto exp_tile = [&](float nb) TLM_INLINE {  // fills pb, returns the tile's row-sum part
+  auto exp_tile = [&](int qq, float nb) TLM_INLINE {  // fills pb[.][qq], returns the row-sum part
     float ts0 = 0.f, ts1 = 0.f;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e], sc, nb));
-          const float p1 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e + 1], sc, nb));
-          if (e & 1) ts1 += p0 + p1; else ts0 += p0 + p1;
-          pb[t][s2][e] = HH::pack(p0, p1);
-        }
+      for (int e = 0; e < 2; ++e) {
+        const float p0 = fast_exp2(__builtin_fmaf(sacc[kt][qq][2 * e], sc, nb));
+        const float p1 = fast_exp2(__builtin_fmaf(sacc[kt][qq][2 * e + 1], sc, nb));
+        if (e & 1) ts1 += p0 + p1; else ts0 += p0 + p1;
+        pb[kt >> 1][qq][2 * (kt & 1) + e] = HH::pack(p0, p1);
+      }
     return ts0 + ts1;
   };
   auto y_phase = [&](int j) TLM_INLINE {
@@ -568,30 +600,37 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     const bool need_mask = (CAUSAL && k0 + PP_KV - 1 > qb0 + coff) || (k0 + PP_KV > Sk);
     if (need_mask) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
-          if (key >= Sk || (CAUSAL && key > my_q + coff)) sacc[t][i] = -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kt + 4 * g + i;
+#pragma unroll
+          for (int qq = 0; qq < 2; ++qq)
+            if (key >= Sk || (CAUSAL && key > my_q[qq] + coff)) sacc[kt][qq][i] = -INFINITY;
         }
     }
-    float ts = exp_tile(-m_run);
-    if (__builtin_amdgcn_ballot_w64(!(ts <= P_LIMIT))) {  // wave-uniform, rare
-      float mx = -INFINITY;
+    float ts[2] = {exp_tile(0, -m_run[0]), exp_tile(1, -m_run[1])};
+    if (__builtin_amdgcn_ballot_w64(!(ts[0] <= P_LIMIT) || !(ts[1] <= P_LIMIT))) {  // rare
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int qq = 0; qq < 2; ++qq) {
+        float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) mx = fmaxf(fmaxf(mx, sacc[t][i]), sacc[t][i + 1]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx * sc);
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_part *= alpha;
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int dt = 0; dt < PP_D / 32; ++dt) oacc[dt] *= alpha;
-      ts = exp_tile(m_new == -INFINITY ? 0.f : -m_new);
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][qq][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[qq], mx * sc);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[qq] - m_new);
+        m_run[qq] = m_new;
+        l_part[qq] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < PP_D / 16; ++dt) oacc[dt][qq] *= alpha;
+        ts[qq] = exp_tile(qq, m_new == -INFINITY ? 0.f : -m_new);
+      }
     }
-    l_part += ts;
+    l_part[0] += ts[0];
+    l_part[1] += ts[1];
   };
 
   // ---- schedule. Step j: group 0 runs X(j) = QK(j) + PV(j-1), then Y(j) = softmax(j); group 1
@@ -613,11 +652,11 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   auto advance = [&](int j) TLM_INLINE {
     const int dk = (j & 3) == 0 ? -3 * PP_TILE : PP_TILE;
 #pragma unroll
-    for (int ds = 0; ds < PP_D / 16; ++ds) kaddr[ds] += dk;
+    for (int d = 0; d < PP_D / 32; ++d) kaddr[d] += dk;
     if (j >= 2) {
       const int dv = ((j - 1) & 3) == 0 ? -3 * PP_TILE : PP_TILE;
 #pragma unroll
-      for (int dt = 0; dt < PP_D / 32; ++dt) vaddr[dt] += dv;
+      for (int dt = 0; dt < PP_D / 16; ++dt) vaddr[dt] += dv;
     }
   };
   auto end_step = [&](bool dma) TLM_INLINE {
@@ -658,30 +697,34 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     }
   }
 
-  // ---- epilogue: lane holds O^T[d = 32 dt + 8 (i / 4) + 4 g + i % 4][query my_q]
-  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  // ---- epilogue: lane holds O^T[d = 16 dt + 4 g + i][query my_q[qq]]; the row sums of a query
+  // are spread over the four lane groups
+  float inv[2];
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    float l_tot = l_part[qq] + __shfl_xor(l_part[qq], 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    inv[qq] = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  }
   if constexpr (OUT32) {  // fp32 output (fp32 programs): 16-byte stores straight from registers
     float* Of = (float*)O + head;
-    if (my_q < Sq) {
 #pragma unroll
-      for (int dt = 0; dt < PP_D / 32; ++dt)
+    for (int qq = 0; qq < 2; ++qq)
+      if (my_q[qq] < Sq) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          *(f32x4*)(Of + (int64_t)my_q * rs + 32 * dt + 8 * r4 + 4 * g) =
-              f32x4{oacc[dt][4 * r4] * inv, oacc[dt][4 * r4 + 1] * inv,
-                    oacc[dt][4 * r4 + 2] * inv, oacc[dt][4 * r4 + 3] * inv};
-    }
+        for (int dt = 0; dt < PP_D / 16; ++dt)
+          *(f32x4*)(Of + (int64_t)my_q[qq] * rs + 16 * dt + 4 * g) = oacc[dt][qq] * inv[qq];
+      }
     return;
   }
   uint16_t* stage = (uint16_t*)smem + wave * 32 * PP_OP;  // [32 queries][PP_OP]
 #pragma unroll
-  for (int dt = 0; dt < PP_D / 32; ++dt)
+  for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const uint32_t lo = HH::pack(oacc[dt][4 * r4] * inv, oacc[dt][4 * r4 + 1] * inv);
-      const uint32_t hi = HH::pack(oacc[dt][4 * r4 + 2] * inv, oacc[dt][4 * r4 + 3] * inv);
-      *(u32x2*)(stage + ql * PP_OP + 32 * dt + 8 * r4 + 4 * g) = u32x2{lo, hi};
+    for (int dt = 0; dt < PP_D / 16; ++dt) {
+      const f32x4 o = oacc[dt][qq] * inv[qq];
+      *(u32x2*)(stage + (16 * qq + ql) * PP_OP + 16 * dt + 4 * g) =
+          u32x2{HH::pack(o[0], o[1]), HH::pack(o[2], o[3])};
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
