@@ -117,7 +117,8 @@ def time_steps(fns, steps, warmup):
 def time_launches(fns, reps, flush):
     """Mean launch duration (ms): `reps` back-to-back launches replayed from a HIP graph, HIP
     events on the stream they run on, divided by reps. Inputs rotate over copies sized to defeat
-    the Infinity Cache. Also returns the median of single launches each after a cache flush."""
+    the Infinity Cache. Also returns the median of 100 single launches, each after a 512 MiB
+    cache flush."""
     g = _capture(fns, reps)
     mean = None
     if g is not None:
@@ -128,7 +129,7 @@ def time_launches(fns, reps, flush):
         en.record()
         torch.cuda.synchronize()
         mean = st.elapsed_time(en) / reps
-    n1 = min(reps, 20)
+    n1 = 100
     st = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
     en = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
     for i in range(n1):
