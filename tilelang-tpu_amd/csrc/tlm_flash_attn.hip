@@ -98,7 +98,8 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
                                                           const uint16_t* __restrict__ K,
                                                           const uint16_t* __restrict__ V,
                                                           uint16_t* __restrict__ O, int B, int S,
-                                                          int H, int Hkv, float scale_log2) {
+                                                          int H, int Hkv, float scale_log2,
+                                                          SeqMap sm) {
   using MT = fa_mma<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
@@ -123,12 +124,17 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   const int bh = lin % (B * H);
   const int b = bh / H, h = bh % H;
   const int q0 = qt * BQ;
+  // S counts the grid's query tiles; the sequence's own counts are Sq, Sk (causal: query i sees
+  // keys j <= i + Sk - Sq)
+  const SeqRange sr = seq_range(sm, b);
+  const int Sq = sr.nq, Sk = sr.nk, coff = Sk - Sq;
+  if (q0 >= Sq) return;  // whole workgroup, before any barrier
   const int64_t row_stride = (int64_t)H * D;  // elements between consecutive tokens (Q, O)
   const int64_t kv_stride = (int64_t)Hkv * D;  // K, V: Hkv heads, query head h reads h / (H/Hkv)
   const int hk = h / (H / Hkv);
-  const uint16_t* Qb = Q + ((int64_t)b * S * H + h) * D;
-  const uint16_t* Kb = K + ((int64_t)b * S * Hkv + hk) * D;
-  const uint16_t* Vb = V + ((int64_t)b * S * Hkv + hk) * D;
+  const uint16_t* Qb = Q + (sr.q0 * H + h) * D;
+  const uint16_t* Kb = K + (sr.k0 * Hkv + hk) * D;
+  const uint16_t* Vb = V + (sr.k0 * Hkv + hk) * D;
 
   const int ql = lane & 31, g = lane >> 5;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
@@ -139,13 +145,13 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     u32x4 v = {0, 0, 0, 0};
-    if (my_q < S) v = *(const u32x4*)(Qb + (int64_t)my_q * row_stride + 16 * ds + 8 * g);
+    if (my_q < Sq) v = *(const u32x4*)(Qb + (int64_t)my_q * row_stride + 16 * ds + 8 * g);
     qreg[ds] = __builtin_bit_cast(v8, v);
   }
 
-  const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
+  const int kv_end = CAUSAL ? max(0, min(Sk, q0 + BQ + coff)) : Sk;
   const int nblk = (kv_end + BKV - 1) / BKV;
-  const int wave_qmax = min(qw0 + 31, S - 1);  // < qw0 when the whole wave is past S
+  const int wave_qmax = min(qw0 + 31, Sq - 1);  // < qw0 when the whole wave is past Sq
 
   u32x4 rk[LD_ITERS], rv[LD_ITERS];
   auto load_tile = [&](int j) {
@@ -154,7 +160,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
       const int idx = tid + p * 64 * FA_WAVES;
       const int r = idx / CH, c = (idx % CH) * 8;
       const int key = j * BKV + r;
-      if (key < S) {
+      if (key < Sk) {
         rk[p] = *(const u32x4*)(Kb + (int64_t)key * kv_stride + c);
         rv[p] = *(const u32x4*)(Vb + (int64_t)key * kv_stride + c);
       } else {
@@ -192,7 +198,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
     const bool has_next = j + 1 < nblk;
     if (has_next) load_tile(j + 1);
     const int k0 = j * BKV;
-    const bool active = (qw0 < S) && (!CAUSAL || k0 <= wave_qmax);
+    const bool active = (qw0 < Sq) && (!CAUSAL || k0 <= wave_qmax + coff);
     if (active) {
       const uint16_t* kt = sK + cur * BKV * KP;
       const uint16_t* vt = sV + cur * BKV * VP;
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
         }
       }
       // scale, mask, row max (keys of this lane: 32t + 8(i/4) + 4g + i%4)
-      const bool need_mask = (CAUSAL && k0 + BKV - 1 > qw0) || (k0 + BKV > S);
+      const bool need_mask = (CAUSAL && k0 + BKV - 1 > qw0 + coff) || (k0 + BKV > Sk);
       float mloc = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -217,7 +223,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
           float x = sacc[t][i] * scale_log2;
           if (need_mask) {
             const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
-            if (key >= S || (CAUSAL && key > my_q)) x = -INFINITY;
+            if (key >= Sk || (CAUSAL && key > my_q + coff)) x = -INFINITY;
           }
           sacc[t][i] = x;
           mloc = fmaxf(mloc, x);
@@ -280,13 +286,13 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  uint16_t* Ob = O + ((int64_t)b * S * H + h) * D;
+  uint16_t* Ob = O + (sr.q0 * H + h) * D;
 #pragma unroll
   for (int it = 0; it < 32 * CH / 64; ++it) {
     const int idx = lane + 64 * it;
     const int r = idx / CH, c = (idx % CH) * 8;
     const int q = qw0 + r;
-    if (q < S) *(u32x4*)(Ob + (int64_t)q * row_stride + c) = *(const u32x4*)(stage + r * OP + c);
+    if (q < Sq) *(u32x4*)(Ob + (int64_t)q * row_stride + c) = *(const u32x4*)(stage + r * OP + c);
   }
 }
 
@@ -760,14 +766,15 @@ int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S
 
 template <bool BF16, bool CAUSAL, int D>
 int launch(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
-           float sc, hipStream_t st) {
+           float sc, const SeqMap& sm, hipStream_t st) {
   const int64_t nwg = (int64_t)((S + BQ - 1) / BQ) * B * H;
   if (nwg > INT32_MAX) {
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
   fa_fwd<BF16, CAUSAL, D><<<(unsigned)nwg, 64 * FA_WAVES, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, Hkv, sc);
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, B, S, H, Hkv, sc,
+      sm);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
@@ -891,9 +898,9 @@ int by_shape(const void* q, const void* k, const void* v, void* o, int B, int S,
   if (D == 128)
     return causal ? launch_pp<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, sc, sm, st)
                   : launch_pp<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, sc, sm, st);
-  if (D == 64 && !OUT32 && sm.cu_q == nullptr)
-    return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, Hkv, sc, st)
-                  : launch<BF16, false, 64>(q, k, v, o, B, S, H, Hkv, sc, st);
+  if (D == 64 && !OUT32)
+    return causal ? launch<BF16, true, 64>(q, k, v, o, B, S, H, Hkv, sc, sm, st)
+                  : launch<BF16, false, 64>(q, k, v, o, B, S, H, Hkv, sc, sm, st);
   return causal ? launch_generic<BF16, true, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st)
                 : launch_generic<BF16, false, OUT32>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st);
 }
