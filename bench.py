@@ -511,6 +511,43 @@ def bench_flashattn_varlen(args, dev, flush, cpu):
     return res
 
 
+def bench_flashattn_bhsd(args, dev, flush, cpu):
+    """examples/flash_attention/example_mha_fwd_bhsd.py program structure (head-major Q, K, V,
+    seq_q != seq_kv, non-causal, fp16) at a chunked-prefill size: 1024 new queries over 8192
+    keys, batch 4, 32 heads, dim 128. Algorithmic FLOPs = 4 B H S_q S_kv D (two matmuls)."""
+    import tilelang
+    from tilelang.testing import programs
+    B, H, Sq, Sk, D = 4, 32, 1024, 8192, 128
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, Sq, D, generator=g).half()
+    kk = torch.randn(B, H, Sk, D, generator=g).half()
+    v = torch.randn(B, H, Sk, D, generator=g).half()
+    k = tilelang.compile(programs.flashattn_bhsd(B, H, Sq, Sk, D, False), out_idx=[3])
+    flops = 4 * B * H * Sq * Sk * D
+    nbytes = (2 * B * H * Sq * D + 2 * B * H * Sk * D) * 2
+    qd, kd, vd = q.to(dev), kk.to(dev), v.to(dev)
+    o = torch.empty_like(qd)
+    fns = [lambda: k(qd, kd, vd, o)]
+    pmc_launches(args, fns, "flashattn_bhsd")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 10, flush)
+    res = {"workload": f"flashattn_bhsd_fp16_b{B}h{H}sq{Sq}skv{Sk}d{D}_full",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "dtype": "f16",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["fp16"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
+    if cpu:
+        from oracle import ref
+        t = cpu_time(lambda: ref.flashattn_bhsd_ref(q[:1, :1], kk[:1, :1], v[:1, :1], False),
+                     reps=1)
+        res["cpu_baseline"] = {"value": flops / (B * H) / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "batch 0, head 0, oracle.ref.flashattn_bhsd_ref"}
+    return res
+
+
 def bench_mla(args, dev, flush, cpu):
     from tilelang.jit.adapter.mi355x import ops
     from tilelang.testing import workloads
@@ -627,12 +664,13 @@ BENCHES = {
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
     "flashattn_gqa": bench_flashattn_gqa,
     "flashattn_varlen": bench_flashattn_varlen,
+    "flashattn_bhsd": bench_flashattn_bhsd,
     "gemm_fp8": bench_gemm_fp8,
     "mla": bench_mla,
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "flashattn_gqa", "flashattn_varlen", "gemm_fp8", "mla", "kv_append"]
+         "flashattn_gqa", "flashattn_varlen", "flashattn_bhsd", "gemm_fp8", "mla", "kv_append"]
 
 
 def main():

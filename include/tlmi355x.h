@@ -193,6 +193,18 @@ int tlm_flash_attn_varlen_fwd(const void* q, const void* k, const void* v, void*
                               int64_t H, int64_t H_kv, int64_t D, int causal, float sm_scale,
                               int in_dtype, int out_dtype, void* stream);
 
+/* FlashAttention forward on head-major tensors.
+ * Reference: examples/flash_attention/example_mha_fwd_bhsd.py:30-158 (main(Q, K, V, Output),
+ * :115-119; q_shape [batch, heads, seq_q, dim], kv_shape [batch, heads, seq_kv, dim], :32-33).
+ *   q, o [B, H, S_q, D]; k, v [B, H_kv, S_kv, D], H % H_kv == 0 (query head h reads K/V head
+ *   h / (H / H_kv)). S_q and S_kv may differ. Causal keeps key j <= i + S_kv - S_q for query i,
+ *   the example's mask q_idx = bx * block_M + i + past_len, past_len = seq_kv - seq_q (:50-55);
+ *   a query row with no visible key gets zeros. Other arguments as tlm_flash_attn_fwd_ex. */
+int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void* v, void* o, int64_t B,
+                            int64_t H, int64_t H_kv, int64_t S_q, int64_t S_kv, int64_t D,
+                            int causal, float sm_scale, int in_dtype, int out_dtype,
+                            void* stream);
+
 /* MLA paged decode (one query token per sequence, one shared latent KV head).
  * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,
  * LSE combine :186-221, params :224-256), torch oracle :259-308.

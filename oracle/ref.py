@@ -198,6 +198,34 @@ def flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal: bool = False,
     return out
 
 
+def flashattn_bhsd_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None):
+    """Head-major attention, examples/flash_attention/example_mha_fwd_bhsd.py ref_program
+    (:175-188): fp32 scores Q K^T / sqrt(dim) per (batch, head), softmax over keys, times V.
+    Q [B, H, S_q, D]; K, V [B, H_kv, S_kv, D] (query head h reads K/V head h // (H // H_kv)).
+    causal keeps key j <= i + S_kv - S_q, the kernel's mask (q_idx = bx * block_M + i + past_len,
+    :50-55); ref_program's torch.tril(ones(seq_q, seq_kv)) is the same set when S_q == S_kv, the
+    only case in which the example's loop bound agrees with its mask. A query that sees no key
+    gets zeros. Returns fp32 [B, H, S_q, D]."""
+    B, H, Sq, D = Q.shape
+    Sk = K.shape[2]
+    G = H // K.shape[1]
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else sm_scale
+    out = torch.zeros(B, H, Sq, D, dtype=torch.float32)
+    if Sk == 0:
+        return out
+    keep = None
+    if causal:
+        keep = torch.arange(Sk).view(1, -1) <= torch.arange(Sq).view(-1, 1) + (Sk - Sq)
+    for b in range(B):
+        for h in range(H):
+            s = (Q[b, h].float() @ K[b, h // G].float().t()) * scale
+            if keep is not None:
+                s = s.masked_fill(~keep, float("-inf"))
+            p = torch.softmax(s, dim=-1).nan_to_num(0.0)  # rows without a key: all -inf -> 0
+            out[b, h] = p @ V[b, h // G].float()
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # MLA decode — examples/deepseek_mla/example_mla_decode_paged.py:259-308 (run_torch_mla /
 # scaled_dot_product_attention): per sequence, fp32 attention of q [h_q, d] over the sequence's

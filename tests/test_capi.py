@@ -27,7 +27,7 @@ def test_header_declares_entry_points():
               "tlm_flash_attn_fwd", "tlm_mla_decode", "tlm_mla_workspace_bytes",
               "tlm_paged_gather", "tlm_kv_append_fp8", "tlm_cast", "tlm_flash_attn_fwd_ex",
               "tlm_gemm_fp8", "tlm_sigmoid", "tlm_gather_rows", "tlm_topk", "tlm_row_reduce",
-              "tlm_flash_attn_varlen_fwd"):
+              "tlm_flash_attn_varlen_fwd", "tlm_flash_attn_bhsd_fwd"):
         assert s in syms
 
 
@@ -175,6 +175,17 @@ def test_flash_attn_validation():
     assert vl(p, p, p, p, cu, cu, 0, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
     assert vl(p, p, p, p, cu, cu, 2, 0, 100, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
     assert vl(p, p, p, p, cu, cu, 2, 64, 0, 90, 8, 2, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
+    bh = L.tlm_flash_attn_bhsd_fwd
+    # q, k, v, o, B, H, H_kv, S_q, S_kv, D, causal, scale, in, out, stream (rejected or empty only)
+    assert bh(None, p, p, p, 1, 8, 2, 64, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == -1
+    assert bh(p, p, p, p, 1, 8, 3, 64, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == -1  # 8 % 3
+    assert bh(p, p, p, p, 1, 8, 2, -1, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == -1
+    assert bh(p, p, p, p, 1, 8, 2, 64, 2 ** 25, 128, 0, 0.1, lib.F16, lib.F16, None) == -1
+    assert bh(p, p, p, p, 1, 8, 2, 64, 80, 260, 0, 0.1, lib.F16, lib.F16, None) == -2
+    assert bh(p, p, p, p, 1, 8, 2, 64, 80, 128, 0, 0.1, lib.F16, lib.BF16, None) == -2
+    assert bh(p, p, p, p, 1, 8, 2, 64, 80, 128, 1, 0.0, lib.F16, lib.F16, None) == -1
+    assert bh(p, p, p, p, 0, 8, 2, 64, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
+    assert bh(p, p, p, p, 1, 8, 2, 0, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
 
 
 def test_mla_validation_and_workspace():

@@ -143,6 +143,26 @@ def test_demo_variants_recognised(name, prog, attrs):
         assert plan.attrs[k] == v, (name, k, plan.attrs[k])
 
 
+def test_bhsd_flashattn_program():
+    """examples/flash_attention/example_mha_fwd_bhsd.py: head-major tensors, @T.macro helpers with
+    T.SharedBuffer / T.FragmentBuffer annotations, seq_q != seq_kv; causal only at equal
+    lengths (the example's mask and loop bound disagree otherwise)."""
+    k = tilelang.compile(programs.flashattn_bhsd(1, 1, 256, 256, 64, False), out_idx=[3])
+    a = k.plan.attrs
+    assert k.plan.family == "flashattn" and a["layout"] == "bhsd" and not a["causal"]
+    assert (a["B"], a["H"], a["H_kv"], a["S"], a["S_kv"], a["D"]) == (1, 1, 1, 256, 256, 64)
+    assert math.isclose(a["sm_scale"], 1 / math.sqrt(64), rel_tol=1e-9)
+    p = recognize(programs.flashattn_bhsd(2, 8, 300, 1000, 128, False, dtype="bfloat16"))
+    assert (p.attrs["S"], p.attrs["S_kv"], p.attrs["H"], p.attrs["dtype"]) == (300, 1000, 8,
+                                                                               "bfloat16")
+    c = recognize(programs.flashattn_bhsd(2, 4, 512, 512, 128, True))
+    assert c.attrs["causal"] and c.attrs["layout"] == "bhsd"
+    with pytest.raises(UnsupportedProgram, match="seq_q"):
+        recognize(programs.flashattn_bhsd(1, 4, 128, 512, 64, True))
+    # sequence-major programs keep their layout
+    assert "layout" not in recognize(programs.flashattn_gqa(1, 4, 256, 64, False)).attrs
+
+
 def test_varlen_flashattn_program():
     """examples/flash_attention/example_mha_fwd_varlen.py: a scalar T.int32 parameter
     (max_seqlen_q), int32 cu_seqlens, element-wise tile fills; only the non-causal form maps."""

@@ -29,6 +29,7 @@ REPEAT = 4
     ("flashattn_full", lambda: programs.flashattn(1, 4, 700, 128, False), -1),
     ("flashattn_gqa_causal", lambda: programs.flashattn_gqa(1, 8, 1024, 128, True, 4), [3]),
     ("flashattn_d64", lambda: programs.flashattn(1, 2, 600, 64, True), -1),
+    ("flashattn_bhsd", lambda: programs.flashattn_bhsd(2, 4, 700, 900, 128, False), [3]),
     ("rmsnorm_splitk", lambda: programs.rms_norm_splitk(512, 512, 32, 32), -1),
     ("rope", lambda: programs.rope(64, 16, 256, 128), -1),
     ("swiglu", lambda: programs.swi_glu(32, 32, 256, 1024), -1),

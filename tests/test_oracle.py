@@ -500,3 +500,39 @@ def test_flashattn_varlen_gqa_equals_repeated_kv():
         exp = ref.flashattn_varlen_ref(q, k.repeat_interleave(3, dim=1),
                                        v.repeat_interleave(3, dim=1), cu_q, cu_k, causal)
         assert torch.equal(got, exp)
+
+
+def test_flashattn_bhsd_matches_sdpa_and_the_other_layouts():
+    """Head-major oracle: equal lengths give SDPA (its is_causal is the top-left tril, equal to
+    the bottom-right mask at S_q == S_kv) and the BSHD oracle on transposed tensors; unequal
+    lengths give the variable-length oracle with one sequence per batch (its bottom-right causal
+    mask and zero rows are pinned above); grouped K/V heads equal repeated ones."""
+    g = torch.Generator().manual_seed(44)
+    B, H, S, D = 2, 3, 9, 8
+    q, k, v = (torch.randn(B, H, S, D, generator=g) for _ in range(3))
+    for causal in (False, True):
+        got = ref.flashattn_bhsd_ref(q, k, v, causal)
+        exp = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        torch.testing.assert_close(got, exp, rtol=1e-5, atol=1e-5)
+        bshd = ref.flashattn_ref(*(t.transpose(1, 2) for t in (q, k, v)), causal)
+        torch.testing.assert_close(got, bshd.transpose(1, 2), rtol=1e-6, atol=1e-6)
+    Hkv = 1
+    for Sq, Sk in ((5, 12), (12, 5), (7, 0)):
+        q = torch.randn(B, H, Sq, D, generator=g)
+        k, v = (torch.randn(B, Hkv, Sk, D, generator=g) for _ in range(2))
+        cu_q = torch.arange(B + 1, dtype=torch.int32) * Sq
+        cu_k = torch.arange(B + 1, dtype=torch.int32) * Sk
+        for causal in (False, True):
+            got = ref.flashattn_bhsd_ref(q, k, v, causal)
+            exp = ref.flashattn_varlen_ref(q.permute(0, 2, 1, 3).reshape(B * Sq, H, D),
+                                           k.permute(0, 2, 1, 3).reshape(B * Sk, Hkv, D),
+                                           v.permute(0, 2, 1, 3).reshape(B * Sk, Hkv, D),
+                                           cu_q, cu_k, causal)
+            torch.testing.assert_close(got, exp.view(B, Sq, H, D).permute(0, 2, 1, 3),
+                                       rtol=1e-6, atol=1e-6)
+            rep = ref.flashattn_bhsd_ref(q, k.repeat_interleave(H, 1), v.repeat_interleave(H, 1),
+                                         causal)
+            assert torch.equal(got, rep)
+    # S_q > S_kv causal: the first S_q - S_kv queries see no key and get zeros
+    got = ref.flashattn_bhsd_ref(*(torch.randn(1, 1, s, 4, generator=g) for s in (6, 2, 2)), True)
+    assert torch.equal(got[0, 0, :4], torch.zeros(4, 4)) and got[0, 0, 4:].abs().sum() > 0

@@ -38,10 +38,15 @@ constexpr int BKV = 64;            // keys per tile
 // sums of the sequence lengths (examples/flash_attention/example_mha_fwd_varlen.py:267-276),
 // s_q / s_k the row counts of Q / O and K / V; a sequence whose rows fall outside them is taken
 // as empty, so bad offsets never address memory outside the tensors.
+// Element strides: tq / tk between consecutive tokens of Q, O / K, V, hq / hk between heads.
+// Sequence-major [B, S, H, D] (and the unpadded [T, H, D]): tq = H D, hq = D. Head-major
+// [B, H, S, D] (examples/flash_attention/example_mha_fwd_bhsd.py:32-33): tq = D, hq = S_q D.
+// Either way batch b's rows start at element (first row) H D.
 struct SeqMap {
   const int* cu_q;
   const int* cu_k;
   int s_q, s_k;
+  int64_t tq, tk, hq, hk;
 };
 struct SeqRange {
   int64_t q0, k0;  // first row of the sequence's queries / keys
@@ -129,12 +134,13 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   const SeqRange sr = seq_range(sm, b);
   const int Sq = sr.nq, Sk = sr.nk, coff = Sk - Sq;
   if (q0 >= Sq) return;  // whole workgroup, before any barrier
-  const int64_t row_stride = (int64_t)H * D;  // elements between consecutive tokens (Q, O)
-  const int64_t kv_stride = (int64_t)Hkv * D;  // K, V: Hkv heads, query head h reads h / (H/Hkv)
+  const int64_t row_stride = sm.tq;  // elements between consecutive tokens (Q, O)
+  const int64_t kv_stride = sm.tk;   // K, V: Hkv heads, query head h reads h / (H/Hkv)
   const int hk = h / (H / Hkv);
-  const uint16_t* Qb = Q + (sr.q0 * H + h) * D;
-  const uint16_t* Kb = K + (sr.k0 * Hkv + hk) * D;
-  const uint16_t* Vb = V + (sr.k0 * Hkv + hk) * D;
+  const int64_t head = sr.q0 * H * D + h * sm.hq;
+  const uint16_t* Qb = Q + head;
+  const uint16_t* Kb = K + sr.k0 * Hkv * D + hk * sm.hk;
+  const uint16_t* Vb = V + sr.k0 * Hkv * D + hk * sm.hk;
 
   const int ql = lane & 31, g = lane >> 5;
   const int qw0 = q0 + 32 * wave;  // first query of this wave
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  uint16_t* Ob = O + (sr.q0 * H + h) * D;
+  uint16_t* Ob = O + head;
 #pragma unroll
   for (int it = 0; it < 32 * CH / 64; ++it) {
     const int idx = lane + 64 * it;
@@ -444,10 +450,10 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int q0 = qt * PP_BQ;
   const int Sq = sr.nq, Sk = sr.nk, coff = Sk - Sq;
   if (q0 >= Sq) return;  // whole workgroup
-  const int64_t rs = (int64_t)H * PP_D;      // elements between consecutive tokens of Q, O
-  const int64_t rs_kv = (int64_t)Hkv * PP_D;  // ... of K, V
-  const int64_t head = (sr.q0 * H + h) * PP_D;
-  const int64_t head_kv = (sr.k0 * Hkv + h / G) * PP_D;
+  const int64_t rs = sm.tq;     // elements between consecutive tokens of Q, O
+  const int64_t rs_kv = sm.tk;  // ... of K, V
+  const int64_t head = sr.q0 * H * PP_D + h * sm.hq;
+  const int64_t head_kv = sr.k0 * Hkv * PP_D + (h / G) * sm.hk;
   const uint16_t* Qb = Q + head;
 
   const int n_all = (Sk + PP_KV - 1) / PP_KV;
@@ -797,9 +803,9 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
   if ((int)blockIdx.x * 256 >= S) return;  // whole block
   const int q = blockIdx.x * 256 + threadIdx.x;
   const int nc = D / 8;
-  const int64_t rs = (int64_t)H * D, rs_kv = (int64_t)Hkv * D;
-  const int64_t head = (sr.q0 * H + h) * D;
-  const int64_t head_kv = (sr.k0 * Hkv + h / (H / Hkv)) * D;
+  const int64_t rs = sm.tq, rs_kv = sm.tk;
+  const int64_t head = sr.q0 * H * D + h * sm.hq;
+  const int64_t head_kv = sr.k0 * Hkv * D + (h / (H / Hkv)) * sm.hk;
   u32x4 qv[DC];
   float o[DC][8];
 #pragma unroll
@@ -972,7 +978,7 @@ extern "C" int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v
     return TLM_EINVAL;
   }
   if (B == 0 || S == 0 || H == 0) return TLM_OK;
-  const SeqMap sm{nullptr, nullptr, (int)S, (int)S};
+  const SeqMap sm{nullptr, nullptr, (int)S, (int)S, H * D, H_kv * D, D, D};
   return dispatch(q, k, v, o, (int)B, (int)S, (int)H, (int)H_kv, (int)D, causal != 0, sm_scale,
                   in_dtype, out_dtype, sm, (hipStream_t)stream);
 }
@@ -998,8 +1004,26 @@ extern "C" int tlm_flash_attn_varlen_fwd(const void* q, const void* k, const voi
     return TLM_EINVAL;
   }
   if (B == 0 || max_seqlen_q == 0 || H == 0 || total_q == 0) return TLM_OK;
-  const SeqMap sm{cu_seqlens_q, cu_seqlens_k, (int)total_q, (int)total_k};
+  const SeqMap sm{cu_seqlens_q, cu_seqlens_k, (int)total_q, (int)total_k, H * D, H_kv * D, D, D};
   return dispatch(q, k, v, o, (int)B, (int)max_seqlen_q, (int)H, (int)H_kv, (int)D, causal != 0,
+                  sm_scale, in_dtype, out_dtype, sm, (hipStream_t)stream);
+}
+
+extern "C" int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void* v, void* o,
+                                       int64_t B, int64_t H, int64_t H_kv, int64_t S_q,
+                                       int64_t S_kv, int64_t D, int causal, float sm_scale,
+                                       int in_dtype, int out_dtype, void* stream) {
+  const int rc = check_common("tlm_flash_attn_bhsd_fwd", q, k, v, o, H, H_kv, D, sm_scale,
+                              in_dtype, out_dtype);
+  if (rc != TLM_OK) return rc;
+  if (B < 0 || S_q < 0 || S_kv < 0 || B > 65535 || S_q > (1 << 24) || S_kv > (1 << 24)) {
+    tlm_set_error("tlm_flash_attn_bhsd_fwd: bad shape");
+    return TLM_EINVAL;
+  }
+  if (B == 0 || S_q == 0 || H == 0) return TLM_OK;
+  // query i sees keys j <= i + S_kv - S_q when causal (bottom-right diagonal); no keys: zero rows
+  const SeqMap sm{nullptr, nullptr, (int)S_q, (int)S_kv, D, D, S_q * D, S_kv * D};
+  return dispatch(q, k, v, o, (int)B, (int)S_q, (int)H, (int)H_kv, (int)D, causal != 0,
                   sm_scale, in_dtype, out_dtype, sm, (hipStream_t)stream);
 }
 

@@ -39,6 +39,9 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     elif f == "flashattn" and a.get("varlen"):
         ops.flash_attn_varlen_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["cu_q"]], t[a["cu_k"]],
                                   t[a["max_q"]], t[a["o"]], a["causal"], a["sm_scale"])
+    elif f == "flashattn" and a.get("layout") == "bhsd":
+        ops.flash_attn_bhsd_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"],
+                                a["sm_scale"])
     elif f == "flashattn":
         ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"],
                            operand_dtype=odt)

@@ -177,6 +177,29 @@ def flash_attn_fwd(q, k, v, o, causal: bool, sm_scale: float,
     return o
 
 
+def flash_attn_bhsd_fwd(q, k, v, o, causal: bool, sm_scale: float):
+    """BHSD attention forward: q, o [B, H, S_q, D]; k, v [B, H_kv, S_kv, D] with H % H_kv == 0.
+    S_q and S_kv may differ; causal keeps key j <= i + S_kv - S_q for query i."""
+    dev = _dev(q, k, v, o)
+    for n, t in (("Q", q), ("K", k), ("V", v), ("O", o)):
+        _contig(n, t)
+    if q.dim() != 4 or q.shape != o.shape or k.shape != v.shape or k.dim() != 4:
+        raise ValueError("Q, O must be [B, H, S_q, D] and K, V [B, H_kv, S_kv, D]")
+    B, H, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    if (k.shape[0], k.shape[3]) != (B, D) or Hkv == 0 or H % Hkv:
+        raise ValueError(f"K/V {tuple(k.shape)} do not match Q {tuple(q.shape)} "
+                         "(same B, D; H a multiple of H_kv)")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("Q, K and V must share a dtype")
+    if o.dtype not in (q.dtype, torch.float32):
+        raise ValueError(f"O must be {q.dtype} or float32")
+    lib.call("tlm_flash_attn_bhsd_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(o), B, H, Hkv, Sq, Sk, D,
+             1 if causal else 0, float(sm_scale), dtype_code(q.dtype), dtype_code(o.dtype),
+             _stream(dev))
+    return o
+
+
 def flash_attn_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, o,
                           causal: bool, sm_scale: float):
     """Attention over unpadded sequences: q, o [total_q, H, D]; k, v [total_k, H_kv, D];

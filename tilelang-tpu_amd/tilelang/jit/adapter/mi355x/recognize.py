@@ -355,10 +355,19 @@ def _flashattn(pf, names) -> Plan:
     kshp = _shape(K)
     if len(shp) == 3:
         return _flashattn_varlen(pf, qk[0], pv[0], Q, K, V, O)
-    if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
-        _fail(fam, "Q, Output must be [batch, seq, heads, dim] and K, V [batch, seq, kv_heads, dim]")
-    if (kshp[0], kshp[1], kshp[3]) != (shp[0], shp[1], shp[3]) or shp[2] % kshp[2]:
-        _fail(fam, f"K/V {kshp} do not group Q {shp} (query heads a multiple of K/V heads)")
+    bhsd = _seq_dim(pf, Q) == 2
+    if bhsd:
+        if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
+            _fail(fam, "Q, Output must be [batch, heads, seq_q, dim] and K, V "
+                       "[batch, kv_heads, seq_kv, dim]")
+        if (kshp[0], kshp[3]) != (shp[0], shp[3]) or shp[1] % kshp[1]:
+            _fail(fam, f"K/V {kshp} do not group Q {shp} (query heads a multiple of K/V heads)")
+    else:
+        if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
+            _fail(fam, "Q, Output must be [batch, seq, heads, dim] and K, V "
+                       "[batch, seq, kv_heads, dim]")
+        if (kshp[0], kshp[1], kshp[3]) != (shp[0], shp[1], shp[3]) or shp[2] % kshp[2]:
+            _fail(fam, f"K/V {kshp} do not group Q {shp} (query heads a multiple of K/V heads)")
     # tiles the two gemms multiply: the fp32 program copies Q, K, V and P to fp16 tiles first
     tile_dts = {_buf(qk[0].args[0]).dtype, _buf(qk[0].args[1]).dtype, _buf(pv[0].args[0]).dtype,
                 _buf(pv[0].args[1]).dtype}
@@ -369,7 +378,9 @@ def _flashattn(pf, names) -> Plan:
         _fail(fam, "Q, K, V and Output must share a dtype")
     if Q.dtype not in (tile_dt, "float32"):
         _fail(fam, f"parameters are {Q.dtype} but the gemms multiply {tile_dt} tiles")
-    B, S, H, D = shp
+    if bhsd and Q.dtype == "float32":
+        _fail(fam, "head-major programs take bfloat16 or float16 parameters")
+    B, S, H, D = (shp[0], shp[2], shp[1], shp[3]) if bhsd else shp
     # causal: the KV loop is truncated at the diagonal (T.min(...) in the extent), or scores
     # are masked by comparing query and key positions.
     causal = any(isinstance(e, Expr) and e.has_op("min") for e in _pipelined_extents(pf))
@@ -397,11 +408,35 @@ def _flashattn(pf, names) -> Plan:
                     sm_scale = cs[0] / LOG2E_REF
         if sm_scale is None:
             _fail(fam, "could not read the softmax scale")
+    if bhsd:
+        # example_mha_fwd_bhsd.py:50-55 masks with q_idx = bx * block_M + i + seq_kv - seq_q
+        # while its loop bound (:139-141) stops at key (bx + 1) * block_M and its reference
+        # (:183) uses the top-left torch.tril: the three agree only when seq_q == seq_kv.
+        if causal and S != kshp[2]:
+            _fail(fam, f"causal with seq_q {S} != seq_kv {kshp[2]}: the example's mask, loop "
+                       "bound and reference disagree there")
+        return Plan(fam, pf.params, [_index(pf, O)], dict(
+            q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S,
+            S_kv=kshp[2], H=H, H_kv=kshp[1], D=D, causal=causal, sm_scale=sm_scale,
+            dtype=Q.dtype, operand_dtype=None, layout="bhsd"))
     return Plan(fam, pf.params, [_index(pf, O)], dict(
         q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H,
         H_kv=kshp[2], D=D,
         causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
         operand_dtype=tile_dt if Q.dtype == "float32" else None))
+
+
+def _seq_dim(pf, Q: Buffer) -> Optional[int]:
+    """The dimension of ``Q`` that a tile copy slices by query block (``Q[bz, bx * block_M:..,
+    by, :]`` in sequence-major programs, ``Q[bz, by, bx * block_M:.., :]`` in head-major ones)."""
+    for op in _ops(pf, _COPY):
+        src = op.args[0]
+        if isinstance(src, BufferAccess) and src.buffer is Q:
+            dims = [d for d, ix in enumerate(src.indices[:-1])
+                    if isinstance(ix, slice) and ix.start is not None]
+            if len(dims) == 1:
+                return dims[0]
+    return None
 
 
 def _index_param(pf, tile: Buffer, src: Buffer) -> Optional[Buffer]:

@@ -30,6 +30,10 @@ def Tensor(shape, dtype="float32", *args, **kwargs) -> TensorType:
 
 Buffer_ = Tensor
 Buffer = Tensor  # noqa: F811  (T.Buffer is an alias of T.Tensor in annotations)
+# macro argument annotations (tile buffers passed to a @T.macro); inlining ignores them
+SharedBuffer = Tensor
+FragmentBuffer = Tensor
+LocalBuffer = Tensor
 
 
 class PrimFunc:

@@ -463,6 +463,97 @@ def flashattn_gqa(batch, heads, seq_len, dim, is_causal, groups=1, block_M=128, 
     return main
 
 
+def flashattn_bhsd(batch, heads, seq_q, seq_kv, dim, is_causal, block_M=128, block_N=128,
+                   dtype="float16"):
+    """The program structure of examples/flash_attention/example_mha_fwd_bhsd.py:30-158:
+    head-major Q, Output [batch, heads, seq_q, dim] and K, V [batch, heads, seq_kv, dim]; the
+    score, softmax, rescale and P V steps written as @T.macro helpers with tile-buffer
+    annotations; the causal mask offset by past_len = seq_kv - seq_q."""
+    scale = (1.0 / dim) ** 0.5 * 1.44269504
+    q_shape = [batch, heads, seq_q, dim]
+    kv_shape = [batch, heads, seq_kv, dim]
+    acc = "float"
+
+    @T.macro
+    def scores(K: T.Tensor(kv_shape, dtype), q_s: T.SharedBuffer([block_M, dim], dtype),
+               k_s: T.SharedBuffer([block_N, dim], dtype),
+               s: T.FragmentBuffer([block_M, block_N], acc), k: T.int32, bx: T.int32,
+               by: T.int32, bz: T.int32):
+        past_len = seq_kv - seq_q
+        T.copy(K[bz, by, k * block_N:(k + 1) * block_N, :], k_s)
+        if is_causal:
+            for i, j in T.Parallel(block_M, block_N):
+                s[i, j] = T.if_then_else(bx * block_M + i + past_len >= k * block_N + j, 0,
+                                         -T.infinity(acc))
+        else:
+            T.clear(s)
+        T.gemm(q_s, k_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullRow)
+
+    @T.macro
+    def online_softmax(s: T.FragmentBuffer([block_M, block_N], acc),
+                       s_cast: T.FragmentBuffer([block_M, block_N], dtype),
+                       m: T.FragmentBuffer([block_M], acc), m_prev: T.FragmentBuffer([block_M], acc),
+                       alpha: T.FragmentBuffer([block_M], acc),
+                       rsum: T.FragmentBuffer([block_M], acc), l: T.FragmentBuffer([block_M], acc)):
+        T.copy(m, m_prev)
+        T.fill(m, -T.infinity(acc))
+        T.reduce_max(s, m, dim=1, clear=False)
+        for i in T.Parallel(block_M):
+            alpha[i] = T.exp2(m_prev[i] * scale - m[i] * scale)
+        for i, j in T.Parallel(block_M, block_N):
+            s[i, j] = T.exp2(s[i, j] * scale - m[i] * scale)
+        T.reduce_sum(s, rsum, dim=1)
+        for i in T.Parallel(block_M):
+            l[i] = l[i] * alpha[i] + rsum[i]
+        T.copy(s, s_cast)
+
+    @T.macro
+    def rescale(o: T.FragmentBuffer([block_M, dim], acc), alpha: T.FragmentBuffer([block_M], acc)):
+        for i, j in T.Parallel(block_M, dim):
+            o[i, j] *= alpha[i]
+
+    @T.macro
+    def pv(V: T.Tensor(kv_shape, dtype), v_s: T.SharedBuffer([block_N, dim], dtype),
+           s_cast: T.FragmentBuffer([block_M, block_N], dtype),
+           o: T.FragmentBuffer([block_M, dim], acc), k: T.int32, by: T.int32, bz: T.int32):
+        T.copy(V[bz, by, k * block_N:(k + 1) * block_N, :], v_s)
+        T.gemm(s_cast, v_s, o, policy=T.GemmWarpPolicy.FullRow)
+
+    @T.prim_func
+    def main(Q: T.Tensor(q_shape, dtype), K: T.Tensor(kv_shape, dtype),
+             V: T.Tensor(kv_shape, dtype), Output: T.Tensor(q_shape, dtype)):
+        with T.Kernel(T.ceildiv(seq_q, block_M), heads, batch, threads=128) as (bx, by, bz):
+            q_s = T.alloc_shared([block_M, dim], dtype)
+            k_s = T.alloc_shared([block_N, dim], dtype)
+            v_s = T.alloc_shared([block_N, dim], dtype)
+            o_s = T.alloc_shared([block_M, dim], dtype)
+            s = T.alloc_fragment([block_M, block_N], acc)
+            s_cast = T.alloc_fragment([block_M, block_N], dtype)
+            o = T.alloc_fragment([block_M, dim], acc)
+            m = T.alloc_fragment([block_M], acc)
+            m_prev = T.alloc_fragment([block_M], acc)
+            alpha = T.alloc_fragment([block_M], acc)
+            rsum = T.alloc_fragment([block_M], acc)
+            l = T.alloc_fragment([block_M], acc)
+            T.copy(Q[bz, by, bx * block_M:(bx + 1) * block_M, :], q_s)
+            T.fill(o, 0)
+            T.fill(l, 0)
+            T.fill(m, -T.infinity(acc))
+            n_kv = (T.min(T.ceildiv(seq_kv, block_N), T.ceildiv((bx + 1) * block_M, block_N))
+                    if is_causal else T.ceildiv(seq_kv, block_N))
+            for k in T.Pipelined(n_kv, num_stages=2):
+                scores(K, q_s, k_s, s, k, bx, by, bz)
+                online_softmax(s, s_cast, m, m_prev, alpha, rsum, l)
+                rescale(o, alpha)
+                pv(V, v_s, s_cast, o, k, by, bz)
+            for i, j in T.Parallel(block_M, dim):
+                o[i, j] /= l[i]
+            T.copy(o, o_s)
+            T.copy(o_s, Output[bz, by, bx * block_M:(bx + 1) * block_M, :])
+
+    return main
+
+
 def flashattn_varlen(batch, UQ, UKV, heads, dim, is_causal=False, groups=1, block_M=64,
                      block_N=64, dtype="float16"):
     """The program structure of examples/flash_attention/example_mha_fwd_varlen.py:222-358:
