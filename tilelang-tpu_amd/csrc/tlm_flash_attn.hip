@@ -16,7 +16,8 @@
 //     lane-local. V^T comes from the row-major V tile in LDS through ds_read_b64_tr_b16;
 //   * Q stays in VGPRs for the whole loop (B operand of S^T); K and V tiles of 64 keys are
 //     double-buffered in LDS, the next tile's global loads in flight during the current MFMAs;
-//   * softmax runs in the exp2 domain with sm_scale*log2(e) folded into one multiply;
+//   * softmax runs in the exp2 domain with sm_scale*log2(e) folded into one multiply (causal) or
+//     into the exponent's fma with a lazy running max (non-causal, described at the softmax);
 //   * causal: a wave skips key tiles above its diagonal, masks only the tile it crosses, and
 //     workgroups are issued heaviest query tile first.
 #include "tlm_common.h"
@@ -219,45 +220,105 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
           sacc[t] = MT::mma(a, qreg[ds], sacc[t]);
         }
       }
-      // scale, mask, row max (keys of this lane: 32t + 8(i/4) + 4g + i%4)
-      const bool need_mask = (CAUSAL && k0 + BKV - 1 > qw0 + coff) || (k0 + BKV > Sk);
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = sacc[t][i] * scale_log2;
-          if (need_mask) {
-            const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
-            if (key >= Sk || (CAUSAL && key > my_q + coff)) x = -INFINITY;
-          }
-          sacc[t][i] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float psum = 0.f;
       v8 pb[2][2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          u32x4 pk;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p0 = fast_exp2(sacc[t][8 * s2 + 2 * e] - m_use);
-            const float p1 = fast_exp2(sacc[t][8 * s2 + 2 * e + 1] - m_use);
-            psum += p0 + p1;
-            pk[e] = HH::pack(p0, p1);
-          }
-          pb[t][s2] = __builtin_bit_cast(v8, pk);
+      if constexpr (!CAUSAL) {
+        // mask (keys of this lane: 32t + 8(i/4) + 4g + i%4), then P = 2^(s sc - m) against the
+        // running m without the tile's max (a lazy max): only when the lane's P sum of the tile
+        // leaves P_LIMIT (or is not finite: the first tile, where m = -inf) is the tile redone
+        // with m raised to its max and O, l rescaled. The common factor cancels in O / l, so the
+        // result is the same softmax at about 3.5 VALU operations per score instead of 6.5 (no
+        // separate scale, max or per-tile O rescale). P_LIMIT keeps every P in range of the 16-bit
+        // type (fp16: P <= 2^15; bf16: 2^64) and O, l far from fp32 overflow. Non-causal only
+        // (+11% at B 8, H 32, S 4096, fp16): the causal kernel measured 5% slower with it, both
+        // at 143 VGPRs (one workgroup per CU) and forced to 128 (two), so it keeps the per-tile
+        // max below.
+        constexpr float P_LIMIT = BF16 ? 18446744073709551616.0f : 32768.0f;
+        const bool need_mask = (CAUSAL && k0 + BKV - 1 > qw0 + coff) || (k0 + BKV > Sk);
+        if (need_mask) {
+  #pragma unroll
+          for (int t = 0; t < 2; ++t)
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
+              if (key >= Sk || (CAUSAL && key > my_q + coff)) sacc[t][i] = -INFINITY;
+            }
         }
-      l_part = l_part * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        auto exp_tile = [&](float nb) __attribute__((always_inline)) {  // fills pb, returns the lane's P sum
+          float s0 = 0.f, s1 = 0.f;
+  #pragma unroll
+          for (int t = 0; t < 2; ++t)
+  #pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+              u32x4 pk;
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float p0 = fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e], scale_log2, nb));
+                const float p1 =
+                    fast_exp2(__builtin_fmaf(sacc[t][8 * s2 + 2 * e + 1], scale_log2, nb));
+                if (e & 1) s1 += p0 + p1; else s0 += p0 + p1;
+                pk[e] = HH::pack(p0, p1);
+              }
+              pb[t][s2] = __builtin_bit_cast(v8, pk);
+            }
+          return s0 + s1;
+        };
+        float psum = exp_tile(-m_run);
+        if (__builtin_amdgcn_ballot_w64(!(psum <= P_LIMIT))) {  // rare: raise m to the tile max
+          float mx = -INFINITY;
+  #pragma unroll
+          for (int t = 0; t < 2; ++t)
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the query's other 32 keys
+          const float m_new = fmaxf(m_run, mx * scale_log2);
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+          m_run = m_new;
+          l_part *= alpha;
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+          psum = exp_tile(m_new == -INFINITY ? 0.f : -m_new);
+        }
+        l_part += psum;
+      } else {
+        // scale, mask, row max (keys of this lane: 32t + 8(i/4) + 4g + i%4)
+        const bool need_mask = (CAUSAL && k0 + BKV - 1 > qw0 + coff) || (k0 + BKV > Sk);
+        float mloc = -INFINITY;
+  #pragma unroll
+        for (int t = 0; t < 2; ++t)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            float x = sacc[t][i] * scale_log2;
+            if (need_mask) {
+              const int key = k0 + 32 * t + 8 * (i >> 2) + 4 * g + (i & 3);
+              if (key >= Sk || (CAUSAL && key > my_q + coff)) x = -INFINITY;
+            }
+            sacc[t][i] = x;
+            mloc = fmaxf(mloc, x);
+          }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        m_run = m_new;
+        float psum = 0.f;
+  #pragma unroll
+        for (int t = 0; t < 2; ++t)
+  #pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            u32x4 pk;
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float p0 = fast_exp2(sacc[t][8 * s2 + 2 * e] - m_use);
+              const float p1 = fast_exp2(sacc[t][8 * s2 + 2 * e + 1] - m_use);
+              psum += p0 + p1;
+              pk[e] = HH::pack(p0, p1);
+            }
+            pb[t][s2] = __builtin_bit_cast(v8, pk);
+          }
+        l_part = l_part * alpha + psum;
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      }
       // O^T += V^T P^T
 #pragma unroll
       for (int t = 0; t < 2; ++t)
