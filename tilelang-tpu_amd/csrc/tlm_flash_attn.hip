@@ -682,8 +682,13 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
             if (key >= Sk || (CAUSAL && key > my_q[qq] + coff)) sacc[kt][qq][i] = -INFINITY;
         }
     }
-    float ts[2] = {exp_tile(0, -m_run[0]), exp_tile(1, -m_run[1])};
-    if (__builtin_amdgcn_ballot_w64(!(ts[0] <= P_LIMIT) || !(ts[1] <= P_LIMIT))) {  // rare
+    // the first tile (m = -inf) always needs its max: skip the exponentials it would redo
+    float ts[2] = {0.f, 0.f};
+    if (j > 0) {
+      ts[0] = exp_tile(0, -m_run[0]);
+      ts[1] = exp_tile(1, -m_run[1]);
+    }
+    if (j == 0 || __builtin_amdgcn_ballot_w64(!(ts[0] <= P_LIMIT) || !(ts[1] <= P_LIMIT))) {
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
         float mx = -INFINITY;
