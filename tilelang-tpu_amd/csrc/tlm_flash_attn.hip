@@ -262,8 +262,9 @@ __global__ __launch_bounds__(64 * FA_WAVES, 1) void fa_fwd(const uint16_t* __res
             }
           return s0 + s1;
         };
-        float psum = exp_tile(-m_run);
-        if (__builtin_amdgcn_ballot_w64(!(psum <= P_LIMIT))) {  // rare: raise m to the tile max
+        // the first tile (m = -inf) always needs its max: skip the exponentials it would redo
+        float psum = j > 0 ? exp_tile(-m_run) : 0.f;
+        if (j == 0 || __builtin_amdgcn_ballot_w64(!(psum <= P_LIMIT))) {  // rare: raise m
           float mx = -INFINITY;
   #pragma unroll
           for (int t = 0; t < 2; ++t)
