@@ -11,11 +11,19 @@ over enough input copies (> 512 MiB in total) that no step reads another step's 
 The timed steps are replayed from one HIP graph (captured from torch's current stream, which
 is the stream every kernel is launched on), between device synchronisations, and timed with HIP
 events on that stream. Before the timed replay the graph is replayed untimed for >= 50 ms: the
-clocks dip at the start of a burst of matrix work and need ~20 ms to reach their sustained level. roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch
-duration, the mean taken over a graph of back-to-back launches (rotating input copies); each
-record also carries the median of single launches that each follow a 512 MiB cache flush.
+clocks dip at the start of a burst of matrix work and need ~20 ms to reach their sustained
+level. roofline.achieved = algorithmic bytes (or FLOPs) per launch / mean launch duration, the
+mean taken over a graph of back-to-back launches (rotating input copies); each record also
+carries the median of single launches that each follow a 512 MiB cache flush.
 cpu_baseline = the oracle (restated reference torch path) on a bounded sample, timed on this
 host's cores.
+
+Each timed replay is bracketed by two launches of a marker kernel (a one-element int16
+bitwise_not, outside the HIP-event window), so that a rocprofv3 kernel trace of this script can
+pick out exactly the timed dispatches: `python bench.py --summarize-trace <kernel_trace.csv>`
+prints, per kernel, the statistics of all dispatches and of the dispatches inside each marked
+window (window 1: the timed steps; window 2: the back-to-back launch graph behind
+roofline.achieved).
 """
 import argparse
 import itertools
@@ -32,6 +40,9 @@ sys.path.insert(0, ROOT)
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# e4m3 MACs executed per algorithmic MAC in the FP8 MLA decode: Q^T as two terms (576 of the
+# 1088 MACs per token and head), P^T as one (the other 512)
+MLA_EXEC_FACTOR = (2 * 576 + 512) / (576 + 512)
 MFMA_PEAK = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0}  # dense TFLOP/s (AMD spec)
 FLUSH_BYTES = 512 << 20
 CACHE_EVICT_BYTES = 512 << 20
@@ -49,6 +60,28 @@ def log(msg):
 
 def _copies_for(nbytes):
     return max(1, math.ceil(CACHE_EVICT_BYTES / max(nbytes, 1)))
+
+
+_MARKER = []  # one-element int16 tensor; its bitwise_not kernel brackets the timed replays
+MARKER_KERNEL = "bitwise_not"
+
+
+def _mark():
+    if _MARKER:
+        _MARKER[0].bitwise_not_()
+
+
+def _timed_replay(g):
+    """One replay of g timed with HIP events on the current stream, between two marker
+    launches (outside the event window); returns the elapsed ms."""
+    _mark()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    g.replay()
+    en.record()
+    _mark()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en)
 
 
 def _capture(fns, n):
@@ -98,12 +131,7 @@ def time_steps(fns, steps, warmup):
     g = _capture(fns, steps)
     if g is not None:
         _settle(g)
-        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        st.record()
-        g.replay()
-        en.record()
-        torch.cuda.synchronize()
-        return st.elapsed_time(en) / steps, "hip-graph"
+        return _timed_replay(g) / steps, "hip-graph"
     torch.cuda.synchronize()
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     st.record()
@@ -123,12 +151,7 @@ def time_launches(fns, reps, flush):
     mean = None
     if g is not None:
         _settle(g)
-        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        st.record()
-        g.replay()
-        en.record()
-        torch.cuda.synchronize()
-        mean = st.elapsed_time(en) / reps
+        mean = _timed_replay(g) / reps
     n1 = 100
     st = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
     en = [torch.cuda.Event(enable_timing=True) for _ in range(n1)]
@@ -340,9 +363,11 @@ def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float1
     k = tilelang.compile(programs.matmul(M, N, K, 128, 128, 64, dn, "float16"), out_idx=-1)
     flops = 2 * M * N * K
     nbytes = 2 * (M * K + K * N + M * N)
-    a, b = w.tensors["a"].to(dev), w.tensors["b"].to(dev)
-    c = torch.empty(M, N, dtype=torch.float16, device=dev)
-    fns = [lambda: k(a, b, c)]
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        sets.append((w.tensors["a"].to(dev), w.tensors["b"].to(dev),
+                     torch.empty(M, N, dtype=torch.float16, device=dev)))
+    fns = [lambda s=s: k(*s) for s in sets]
     pmc_launches(args, fns, "gemm")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 50, flush)
@@ -411,9 +436,10 @@ def bench_gemm_fp8(args, dev, flush, cpu):
     k = tilelang.compile(programs.matmul_fp8(M, N, K, 128, 128, 64, "e4m3_float8", two_acc=True),
                          out_idx=-1)
     flops = 2 * M * N * K
-    ad, bd = a.to(dev), b.to(dev)
-    c = torch.empty(M, N, dtype=torch.float32, device=dev)
-    fns = [lambda: k(ad, bd, c)]
+    nbytes = (M * K + N * K) + M * N * 4
+    sets = [(a.to(dev), b.to(dev), torch.empty(M, N, dtype=torch.float32, device=dev))
+            for _ in range(_copies_for(nbytes))]
+    fns = [lambda s=s: k(*s) for s in sets]
     pmc_launches(args, fns, "gemm_fp8")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 10, flush)
@@ -422,7 +448,7 @@ def bench_gemm_fp8(args, dev, flush, cpu):
            "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
                                 MFMA_PEAK["fp8"]),
            "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
-           "algorithmic_flops": flops, "algorithmic_bytes": (M * K + N * K) + M * N * 4}
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes}
     if cpu:
         from oracle import ref
         rows = 256
@@ -446,9 +472,9 @@ def bench_flashattn_gqa(args, dev, flush, cpu):
     k = tilelang.compile(programs.flashattn_gqa(B, H, S, D, False, G), out_idx=[3])
     flops = 4 * B * H * S * S * D
     nbytes = (2 * B * S * H * D + 2 * B * S * (H // G) * D) * 2
-    qd, kd, vd = q.to(dev), kk.to(dev), v.to(dev)
-    o = torch.empty_like(qd)
-    fns = [lambda: k(qd, kd, vd, o)]
+    sets = [(q.to(dev), kk.to(dev), v.to(dev), torch.empty(q.shape, dtype=q.dtype, device=dev))
+            for _ in range(_copies_for(nbytes))]
+    fns = [lambda s=s: k(*s) for s in sets]
     pmc_launches(args, fns, "flashattn_gqa")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 10, flush)
@@ -559,30 +585,39 @@ def bench_mla(args, dev, flush, cpu):
         w.tensors["block_table"].numel() * 4 + B * 4
     flops = sum_l * Hq * (dv + dpe + dv) * 2
     num_split = args.mla_splits
-    t = {n: x.to(dev) for n, x in w.tensors.items()}
-    out = torch.empty(B, Hq, dv, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(ops.mla_workspace_bytes(B, Hq, dv, num_split), dtype=torch.uint8,
                      device=dev)
-    q, kv = t["q"], t["kv"]
+    # input copies (the whole KV pool, Q, table, lengths, scale) so that no launch reads the
+    # previous launch's KV from the Infinity Cache; the workspace is shared (scratch written and
+    # read within one call, as in a decode loop)
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        t = {n: x.to(dev) for n, x in w.tensors.items()}
+        t["out"] = torch.empty(B, Hq, dv, dtype=torch.bfloat16, device=dev)
+        sets.append(t)
 
-    def run():
+    def run(t):
+        q, kv = t["q"], t["kv"]
         ops.mla_decode(q[..., :dv], q[..., dv:], kv[:, :dv], kv[:, dv:], t["block_table"],
-                       t["seqlens"], out, ws, a["page"], num_split, a["sm_scale"], t["kv_scale"])
+                       t["seqlens"], t["out"], ws, a["page"], num_split, a["sm_scale"],
+                       t["kv_scale"])
 
-    pmc_launches(args, [run], "mla")
-    ms, how = time_steps([run], args.steps, args.warmup)
-    mean_ms, med_ms = time_launches([run], 100, flush)
-    # 128 heads share each KV row: ~480 flop per KV byte, above the bf16 ridge, so the decode is
-    # bound by the matrix cores. Each algorithmic MAC runs as two e4m3 MACs (Q and P are split
-    # into hi + lo terms), so algorithmic flops over the bf16-equivalent peak equal executed fp8
-    # flops over the fp8 peak. Durations are whole tlm_mla_decode calls (prep + decode + combine).
-    res = {"workload": "mla_decode_fp8_b64_h128_d576", "value": flops / (ms * 1e-3) / 1e12,
-           "unit": "TFLOP/s", "ms_per_step": ms, "dtype": "fp8e4m3 (kv, q and p as two e4m3 terms)",
-           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
-                                MFMA_PEAK["bf16"]),
-           "executed_fp8_tflops": 2 * flops / (mean_ms * 1e-3) / 1e12,
-           "hbm_gbs": nbytes / (mean_ms * 1e-3) / 1e9,
-           "hbm_frac": nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    fns = [lambda t=t: run(t) for t in sets]
+    pmc_launches(args, fns, "mla")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 100, flush)
+    # BASELINE.md bounds this config by HBM (576 B per cached token, Q, O, table, lengths), so
+    # roofline.frac is against 8 TB/s. The matrix-core rate is reported beside it: algorithmic
+    # flops over the bf16-equivalent peak, and the executed e4m3 flops (Q^T runs as two e4m3
+    # terms, P^T as one) over the fp8 peak. Durations are whole tlm_mla_decode calls (prep +
+    # decode + combine).
+    res = {"workload": "mla_decode_fp8_b64_h128_d576", "value": nbytes / (ms * 1e-3) / 1e9,
+           "unit": "GB/s", "ms_per_step": ms,
+           "dtype": "fp8e4m3 (kv; q as two e4m3 terms, p as one)",
+           "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+           "tflops": flops / (mean_ms * 1e-3) / 1e12,
+           "mfma_frac_bf16_equivalent": flops / (mean_ms * 1e-3) / 1e12 / MFMA_PEAK["bf16"],
+           "executed_fp8_tflops": MLA_EXEC_FACTOR * flops / (mean_ms * 1e-3) / 1e12,
            "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
            "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "sum_seqlens": sum_l,
            "num_split": num_split}
@@ -594,8 +629,9 @@ def bench_mla(args, dev, flush, cpu):
             w.tensors["kv"][:, dv:], w.tensors["block_table"], w.tensors["seqlens"][:nb],
             a["page"], a["sm_scale"], float(w.tensors["kv_scale"])), reps=1)
         sl = int(w.tensors["seqlens"][:nb].sum())
-        res["cpu_baseline"] = {"value": sl * Hq * (dv + dpe + dv) * 2 / t0 / 1e12,
-                               "unit": "TFLOP/s",
+        sb = sl * (dv + dpe) + nb * Hq * (dv + dpe) * 2 + nb * Hq * dv * 2 + \
+            w.tensors["block_table"][:nb].numel() * 4 + nb * 4
+        res["cpu_baseline"] = {"value": sb / t0 / 1e9, "unit": "GB/s",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"first {nb} of {B} sequences ({sl} tokens), "
                                          f"oracle.ref.mla_decode_ref"}
@@ -629,9 +665,12 @@ def bench_kv_append(args, dev, flush, cpu):
     count = torch.full((B,), T, dtype=torch.int32)
     scale = torch.tensor([float(x.float().abs().max()) / 448.0], dtype=torch.float32)
     nbytes = B * T * D * (2 + 1) + B * pages * 4 + 2 * B * 4
-    xs, bts, sts, cns, scs = (t.to(dev) for t in (x, bt, start, count, scale))
-    kv = torch.zeros(B * pages * page, D, dtype=torch.float8_e4m3fn, device=dev)
-    fns = [lambda: ops.kv_append_fp8(xs, sts, cns, bts, kv, page, scs)]
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        xs, bts, sts, cns, scs = (t.to(dev) for t in (x, bt, start, count, scale))
+        kv = torch.zeros(B * pages * page, D, dtype=torch.float8_e4m3fn, device=dev)
+        sets.append((xs, sts, cns, bts, kv, page, scs))
+    fns = [lambda s=s: ops.kv_append_fp8(*s) for s in sets]
     pmc_launches(args, fns, "kv_append")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 200, flush)
@@ -651,6 +690,52 @@ def bench_kv_append(args, dev, flush, cpu):
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"first {nb} of {B} sequences, oracle.ref.kv_append_fp8_ref"}
     return res
+
+
+def summarize_trace(path):
+    """Markdown summary of a rocprofv3 kernel trace (run_kernel_trace.csv) of this script: per
+    kernel, all dispatches and the dispatches inside each marker-bracketed timed window (two
+    windows per workload, in run order: the timed steps, then the back-to-back launch graph)."""
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    windows, cur, inside = [], [], False
+    for st, en, name in rows:
+        if MARKER_KERNEL in name:
+            if inside:
+                windows.append(cur)
+                cur = []
+            inside = not inside
+        elif inside:
+            cur.append((name, en - st, st, en))
+
+    def short(name):
+        n = name.split("(")[0] if not name.startswith("void (") else name
+        return n[:110]
+
+    def table(disp, title):
+        by = {}
+        for name, d, *_ in disp:
+            by.setdefault(name, []).append(d)
+        out = [f"**{title}**", "", "| Kernel | Calls | Avg ns | Median ns | Min ns | Max ns |",
+               "|---|---|---|---|---|---|"]
+        for name, ds in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+            ds = sorted(ds)
+            out.append(f"| `{short(name)}` | {len(ds)} | {sum(ds) / len(ds):.0f} | "
+                       f"{ds[len(ds) // 2]} | {ds[0]} | {ds[-1]} |")
+        return out
+
+    lines = table([(n, e - s_) for s_, e, n in rows if MARKER_KERNEL not in n],
+                  f"All dispatches ({path.split('/')[-1]})")
+    for i, w in enumerate(windows):
+        span = (w[-1][3] - w[0][2]) if w else 0
+        kind = "timed steps" if i % 2 == 0 else "back-to-back launch graph (roofline.achieved)"
+        lines += [""] + table(w, f"Window {i + 1}: {kind}, first start to last end "
+                                 f"{span / 1e3:.1f} us")
+    return "\n".join(lines)
 
 
 BENCHES = {
@@ -685,7 +770,13 @@ def main():
     ap.add_argument("--mla-splits", type=int, default=4)
     ap.add_argument("--no-clock", action="store_true",
                     help="skip the shader-clock pass of the matrix-core workloads")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="print a markdown summary of a rocprofv3 kernel trace of this script "
+                         "(all dispatches and the marker-bracketed timed windows), then exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every kernel here is a "
                                    "single-GPU kernel); run with --gpus 1"}))
@@ -697,6 +788,7 @@ def main():
     torch.cuda.set_device(dev)
     torch.set_num_threads(os.cpu_count() or 1)
     flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+    _MARKER[:] = [torch.zeros(1, dtype=torch.int16, device=dev)]
     names = ORDER if args.workload == "all" else [args.workload]
     traffic = load_traffic()
     results = {}

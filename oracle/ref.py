@@ -159,6 +159,29 @@ def flashattn_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None,
     return out.to(Q.dtype)
 
 
+def flashattn_rows_ref(Q, K, V, causal: bool, rows, sm_scale: Optional[float] = None):
+    """flashattn_ref restricted to the query positions ``rows`` (every batch and head): the same
+    fp32 softmax(Q K^T * scale) V of tpu_test_flashattn_bf16.py:171-182 with the causal tril
+    mask, computed per batch for all heads at once. Returns fp32 [B, len(rows), H, D]."""
+    B, S, H, D = Q.shape
+    G = H // K.shape[2]
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else sm_scale
+    rows = torch.as_tensor(rows, dtype=torch.long)
+    out = torch.empty(B, len(rows), H, D, dtype=torch.float32)
+    keep = None
+    if causal:
+        keep = torch.arange(S)[None, :] <= rows[:, None]  # [R, S]
+    for b in range(B):
+        q = Q[b, rows].float().permute(1, 0, 2)  # [H, R, D]
+        k = K[b].float().repeat_interleave(G, dim=1).permute(1, 2, 0)  # [H, D, S]
+        v = V[b].float().repeat_interleave(G, dim=1).permute(1, 0, 2)  # [H, S, D]
+        s = torch.bmm(q, k.contiguous()) * scale
+        if keep is not None:
+            s = s.masked_fill(~keep[None], float("-inf"))
+        out[b] = torch.bmm(torch.softmax(s, dim=-1), v.contiguous()).permute(1, 0, 2)
+    return out
+
+
 def flashattn_varlen_ref(q, k, v, cu_q, cu_k, causal: bool = False,
                          sm_scale: Optional[float] = None, max_seqlen_q: Optional[int] = None):
     """Attention over unpadded sequences, examples/flash_attention/example_mha_fwd_varlen.py:

@@ -248,3 +248,79 @@ def test_argument_validation_before_device():
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="no CPU fallback"):
             k(a, a)
+
+
+def _gemm_with_epilogue(M=64, N=64, K=64, blk=32, kind="scale"):
+    """ppl GEMM programs whose result is not A @ B: a scaled accumulator, a bias tile added
+    before the copy-out, a bias parameter loaded into the accumulator, an unused extra tensor,
+    or an accumulator filled with 1."""
+    @T.prim_func
+    def main(A: T.Tensor((M, K), "float16"), B: T.Tensor((K, N), "float16"),
+             Bias: T.Tensor((M, N), "float32"), C: T.Tensor((M, N), "float16")):
+        with T.Kernel(T.ceildiv(N, blk), T.ceildiv(M, blk), is_cpu=True) as (bx, by):
+            a_s = T.alloc_shared((blk, blk), "float16")
+            b_s = T.alloc_shared((blk, blk), "float16")
+            acc = T.alloc_shared((blk, blk), "float32")
+            bias = T.alloc_shared((blk, blk), "float32")
+            c_s = T.alloc_shared((blk, blk), "float16")
+            if kind == "bias_init":
+                T.ppl_copy(Bias[by * blk, bx * blk], acc)
+            else:
+                T.ppl_fill(acc, T.float32(1.0 if kind == "fill_one" else 0.0))
+            for k in T.Pipelined(T.ceildiv(K, blk), num_stages=2):
+                T.ppl_copy(A[by * blk, k * blk], a_s)
+                T.ppl_copy(B[k * blk, bx * blk], b_s)
+                T.ppl_gemm(a_s, b_s, acc)
+            if kind == "scale":
+                T.ppl_mul_C(acc, acc, T.float32(2.0))
+            if kind == "bias_add":
+                T.ppl_copy(Bias[by * blk, bx * blk], bias)
+                T.ppl_add(acc, acc, bias)
+            T.ppl_copy(acc, c_s)
+            T.ppl_copy(c_s, C[by * blk, bx * blk])
+
+    return main
+
+
+@pytest.mark.parametrize("kind", ["scale", "bias_add", "bias_init", "unused", "fill_one"])
+def test_gemm_with_epilogue_or_extra_tensor_is_rejected(kind):
+    with pytest.raises(UnsupportedProgram):
+        recognize(_gemm_with_epilogue(kind=kind))
+
+
+def test_gemm_element_epilogue_is_rejected_but_2xacc_fold_is_not():
+    """The fp8 2xAcc fold (acc2[i, j] += acc[i, j]) is the only element store a GEMM may have;
+    a scaling store in the same place is rejected."""
+    assert recognize(programs.matmul_fp8(256, 256, 256, two_acc=True)).family == "gemm"
+
+    @T.prim_func
+    def main(A: T.Tensor((64, 64), "float16"), B: T.Tensor((64, 64), "float16"),
+             C: T.Tensor((64, 64), "float32")):
+        with T.Kernel(2, 2, threads=128) as (bx, by):
+            a_s = T.alloc_shared((32, 64), "float16")
+            b_s = T.alloc_shared((64, 32), "float16")
+            acc = T.alloc_fragment((32, 32), "float")
+            T.clear(acc)
+            T.copy(A[by * 32, 0], a_s)
+            T.copy(B[0, bx * 32], b_s)
+            T.gemm(a_s, b_s, acc)
+            for i, j in T.Parallel(32, 32):
+                acc[i, j] = acc[i, j] * 0.5
+            T.copy(acc, C[by * 32, bx * 32])
+
+    with pytest.raises(UnsupportedProgram):
+        recognize(main)
+
+
+def test_flashattn_with_extra_parameter_is_rejected():
+    """A tensor parameter that the matched attention pattern never touches is an error (the
+    kernel would silently leave it unwritten or ignore it)."""
+    import copy
+    from tilelang.language import ir
+    base = programs.flashattn(1, 2, 256, 128, False)
+    assert recognize(base).family == "flashattn"
+    extra = copy.copy(base)
+    extra.params = list(base.params[:3]) + [ir.Buffer("Extra", (1, 256, 2, 128), "bfloat16",
+                                                      "global")] + list(base.params[3:])
+    with pytest.raises(UnsupportedProgram, match="Extra"):
+        recognize(extra)

@@ -536,3 +536,21 @@ def test_flashattn_bhsd_matches_sdpa_and_the_other_layouts():
     # S_q > S_kv causal: the first S_q - S_kv queries see no key and get zeros
     got = ref.flashattn_bhsd_ref(*(torch.randn(1, 1, s, 4, generator=g) for s in (6, 2, 2)), True)
     assert torch.equal(got[0, 0, :4], torch.zeros(4, 4)) and got[0, 0, 4:].abs().sum() > 0
+
+
+def test_flashattn_rows_ref_equals_full_oracle_rows():
+    """The row-subset oracle is the full oracle's rows (causal and not, grouped K/V heads)."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 96, 4, 32, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, 96, 2, 32, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 96, 2, 32, generator=g).to(torch.bfloat16)
+    rows = [0, 1, 17, 50, 95]
+    for causal in (True, False):
+        full = ref.flashattn_ref(q, k, v, causal).float()
+        sub = ref.flashattn_rows_ref(q, k, v, causal, rows)
+        assert torch.allclose(sub.to(torch.bfloat16).float(), full[:, rows], atol=1e-2,
+                              rtol=1e-2)
+        # first causal query sees only key 0: its output is V[0] of its K/V head
+        if causal:
+            assert torch.allclose(sub[:, 0], v[:, 0].float().repeat_interleave(2, dim=1),
+                                  atol=1e-6)

@@ -6,20 +6,27 @@
 // finally O / l. Causal keeps key j <= query i (element mask of ref_program :171-182 and of the
 // upstream example_mha_fwd_bshd.py:50-53).
 //
-// Layout of the work on gfx950:
-//   * workgroup = 8 waves = 256 queries of one (batch, head); wave w owns 32 queries;
-//   * scores are computed transposed, S^T = K * Q^T, with v_mfma_f32_32x32x16: the accumulator
-//     layout then gives every lane ONE query (lane % 32) and 16 keys, so the row max / row sum of
-//     the online softmax are lane-local plus one xor-32 shuffle;
-//   * the output is accumulated transposed too, O^T = V^T * P^T: P^T is the S^T accumulator
-//     itself (rounded to bf16/fp16 in registers, no LDS round trip) and alpha rescales stay
-//     lane-local. V^T comes from the row-major V tile in LDS through ds_read_b64_tr_b16;
-//   * Q stays in VGPRs for the whole loop (B operand of S^T); K and V tiles of 64 keys are
-//     double-buffered in LDS, the next tile's global loads in flight during the current MFMAs;
-//   * softmax runs in the exp2 domain with sm_scale*log2(e) folded into one multiply (causal) or
-//     into the exponent's fma with a lazy running max (non-causal, described at the softmax);
-//   * causal: a wave skips key tiles above its diagonal, masks only the tile it crosses, and
-//     workgroups are issued heaviest query tile first.
+// Kernels:
+//   * fa_fwd_pp (head dim 128, the config kernel): workgroup = 8 waves = 256 queries of one
+//     (batch, head); wave w owns a 32-query block and computes S^T = K Q^T and O^T = V^T P^T on
+//     v_mfma_f32_16x16x32 as two 16-query tiles (each lane holds 16 keys of each of its two
+//     queries; the softmax statistics combine the four lane groups with xor-16 / xor-32
+//     exchanges). P^T goes from the S^T accumulator to the PV B operand in registers; V^T comes
+//     from the row-major V tile through ds_read_b64_tr_b16; Q stays in VGPRs. K and V tiles of 64
+//     keys stream through 4-stage LDS rings fed by buffer_load ... lds (the tile two steps ahead
+//     is loaded during the current step; descriptor bounds zero the keys past the sequence).
+//     Waves w and w + 4 share a SIMD and run one phase apart (ping-pong): while one issues its
+//     QK + PV MFMAs the other runs its softmax on the VALU. Softmax with a lazy running max: a
+//     tile is exponentiated against the current maximum and only redone (maximum raised, O and l
+//     rescaled) when its P sum leaves the 16-bit P range. Causal workgroups take two query tiles
+//     of one head (nqt - 1 - s and s), so every workgroup does the same number of key tiles;
+//     workgroup ids are regrouped so all query tiles of a (batch, head) run on one XCD.
+//   * fa_fwd (head dim 64): 8 waves x 32 queries on v_mfma_f32_32x32x16 (S^T = K Q^T, one query
+//     and 16 keys per lane), K/V tiles double-buffered in padded LDS with register staging; the
+//     non-causal form uses the same lazy-max softmax, the causal form a per-tile maximum.
+//   * fa_fwd_generic (other head dims up to 256, fp32 output at D = 64): one query per lane, q
+//     and O in VGPRs, per-key online softmax, P rounded to the input type.
+// Softmax runs in the exp2 domain with sm_scale * log2(e) folded into one fma.
 #include "tlm_common.h"
 
 #include <type_traits>

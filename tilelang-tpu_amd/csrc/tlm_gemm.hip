@@ -495,7 +495,10 @@ int launch(const void* A, const void* B, void* C, int M, int N, int K, hipStream
   if (vec && M <= 16) {
     gemm_skinny<BF16, TRANS_B, OUT><<<(unsigned)((N + SK_NT - 1) / SK_NT), 64 * SK_WAVES, 0, s>>>(
         (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
-  } else if (vec) {
+  } else if (vec && (int64_t)BM * K * 2 < 0x7ffffff0 &&
+             (TRANS_B ? (int64_t)BN * K * 2 : (int64_t)BK * N * 2) < 0x7ffffff0) {
+    // the LDS-DMA offsets of a 256-row panel (or a 64-row k-tile of row-major B) are 32-bit
+    // byte offsets below the descriptor's num_records; larger shapes take gemm_generic
     const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     gemm_256x256<BF16, TRANS_B, OUT><<<(unsigned)tiles, NTHREADS, 0, s>>>(
         (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);

@@ -320,8 +320,9 @@ __global__ __launch_bounds__(256) void gemm8_generic(const uint8_t* __restrict__
 template <int FMT, int OUT>
 int launch(const void* A, const void* B, void* C, int M, int N, int K, bool trans_b,
            hipStream_t s) {
-  // 32-bit LDS-DMA offsets within a 256-row panel: K < 2^24
-  const bool tiled = trans_b && M > 16 && K % 16 == 0 && K < (1 << 24) && tlm_aligned(A, 16) &&
+  // 32-bit LDS-DMA byte offsets r * K + 16 c within a 256-row panel stay below the
+  // descriptor's num_records (2^31 - 16): K < 2^23
+  const bool tiled = trans_b && M > 16 && K % 16 == 0 && K < (1 << 23) && tlm_aligned(A, 16) &&
                      tlm_aligned(B, 16);
   if (tiled) {
     const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);

@@ -335,6 +335,8 @@ int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, cons
 
 // FP8 path on the fp8 matrix cores (tlm_mla_fp8.hip); TLM_EUNSUPPORTED for shapes it does not take
 size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split);
+bool tlm_mla_fp8_applies(int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                         int64_t kv_stride, int64_t kpe_stride);
 int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
                        const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
                        int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
@@ -342,77 +344,99 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
                        int num_split, float score_scale, const float* kv_scale, bool q_bf16,
                        bool o_bf16, void* stream);
 
-extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
-  if (B <= 0 || Hq <= 0 || dv <= 0 || num_split <= 0) return 0;
-  // split path: partial outputs fp32 + log2-sum-exp fp32, one slot per (sequence, split, head);
-  // the fp8 path needs its own layout: the larger of the two serves both
-  const size_t split = (size_t)B * num_split * Hq * (dv + 1) * sizeof(float);
-  return std::max(split, tlm_mla_fp8_workspace_bytes(B, Hq, num_split));
+// Workspace bytes of the two paths: the fp8 matrix-core path (fp8 KV, page a multiple of 64, Hq
+// a multiple of 64; its own layout) and the split path (fp32 partial outputs + log2-sum-exp,
+// one slot per (sequence, split, head)).
+static size_t mla_split_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
+  return (size_t)B * num_split * Hq * (dv + 1) * sizeof(float);
 }
 
-extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
-                              int64_t q_pe_stride, const void* kv, const void* k_pe,
-                              int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
-                              const int32_t* block_table, const int32_t* seqlens, void* o,
-                              void* ws, size_t ws_bytes,
-                              int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
-                              int64_t max_pages, int num_split, float sm_scale,
-                              const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
-                              void* stream) {
+extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
+  if (B <= 0 || Hq <= 0 || dv <= 0 || num_split <= 0) return 0;
+  // the larger of the two layouts serves both paths
+  return std::max(mla_split_workspace_bytes(B, Hq, dv, num_split),
+                  tlm_mla_fp8_workspace_bytes(B, Hq, num_split));
+}
+
+// Argument checks shared by tlm_mla_decode and tlm_mla_decode_noalloc (no HIP call).
+static int mla_validate(const char* fn, const void* q, const void* q_pe, int64_t q_stride,
+                        int64_t q_pe_stride, const void* kv, const void* k_pe, int64_t kv_stride,
+                        int64_t kpe_stride, int64_t kv_rows, const int32_t* block_table,
+                        const int32_t* seqlens, void* o, int64_t B, int64_t Hq, int64_t dv,
+                        int64_t dpe, int64_t page, int64_t max_pages, int num_split,
+                        int q_dtype, int kv_dtype, int o_dtype) {
   if (!q || !q_pe || !kv || !k_pe || !block_table || !seqlens || !o) {
-    tlm_set_error("tlm_mla_decode: null pointer argument");
+    tlm_set_error("%s: null pointer argument", fn);
     return TLM_EINVAL;
   }
   if (B < 0 || B > (1 << 20) || Hq <= 0 || page <= 0 || max_pages <= 0 || num_split <= 0 ||
       num_split > 64 || page > (1 << 20) || max_pages > (1 << 20)) {
-    tlm_set_error("tlm_mla_decode: bad sizes B=%lld Hq=%lld page=%lld max_pages=%lld splits=%d",
+    tlm_set_error("%s: bad sizes B=%lld Hq=%lld page=%lld max_pages=%lld splits=%d", fn,
                   (long long)B, (long long)Hq, (long long)page, (long long)max_pages, num_split);
     return TLM_EINVAL;
   }
   if (max_pages * page > INT32_MAX) {
-    tlm_set_error("tlm_mla_decode: max_pages * page exceeds the int32 token range");
+    tlm_set_error("%s: max_pages * page exceeds the int32 token range", fn);
     return TLM_EINVAL;
   }
   if (dv != MLA_DV || dpe != MLA_DPE || Hq % MLA_HEADS != 0 || Hq > 4096) {
-    tlm_set_error("tlm_mla_decode: kernels exist for dv=512, dpe=64, Hq a multiple of 64 "
-                  "(got dv=%lld dpe=%lld Hq=%lld)", (long long)dv, (long long)dpe, (long long)Hq);
+    tlm_set_error("%s: kernels exist for dv=512, dpe=64, Hq a multiple of 64 "
+                  "(got dv=%lld dpe=%lld Hq=%lld)", fn, (long long)dv, (long long)dpe,
+                  (long long)Hq);
     return TLM_EUNSUPPORTED;
   }
   if (q_stride < dv || q_pe_stride < dpe || kv_stride < dv || kpe_stride < dpe || kv_rows < 0) {
-    tlm_set_error("tlm_mla_decode: row strides smaller than the row widths");
+    tlm_set_error("%s: row strides smaller than the row widths", fn);
     return TLM_EINVAL;
-  }
-  if (ws_bytes < tlm_mla_workspace_bytes(B, Hq, dv, num_split) || (B > 0 && !ws)) {
-    tlm_set_error("tlm_mla_decode: workspace of %zu bytes is smaller than the %zu required",
-                  ws_bytes, tlm_mla_workspace_bytes(B, Hq, dv, num_split));
-    return TLM_EWORKSPACE;
   }
   if ((q_dtype != TLM_BF16 && q_dtype != TLM_F16) || (o_dtype != TLM_BF16 && o_dtype != TLM_F16) ||
       (kv_dtype != TLM_F8E4M3 && kv_dtype != q_dtype)) {
-    tlm_set_error("tlm_mla_decode: dtype combination q=%d kv=%d o=%d unsupported (kv must be "
-                  "fp8 e4m3 or Q's dtype)", q_dtype, kv_dtype, o_dtype);
+    tlm_set_error("%s: dtype combination q=%d kv=%d o=%d unsupported (kv must be "
+                  "fp8 e4m3 or Q's dtype)", fn, q_dtype, kv_dtype, o_dtype);
     return TLM_EUNSUPPORTED;
   }
   const int64_t kv_elt = kv_dtype == TLM_F8E4M3 ? 1 : 2;
   // every 16-byte chunk of Q and KV rows must be aligned
   if (!tlm_aligned(q, 16) || !tlm_aligned(q_pe, 16) || !tlm_aligned(kv, 16) ||
       !tlm_aligned(k_pe, 16) || q_stride % 8 || q_pe_stride % 8 || (kv_stride * kv_elt) % 16 ||
-      (kpe_stride * kv_elt) % 16 || !tlm_aligned(o, 8) || !tlm_aligned(ws, 16)) {
-    tlm_set_error("tlm_mla_decode: Q/KV rows must start on 16-byte boundaries");
+      (kpe_stride * kv_elt) % 16 || !tlm_aligned(o, 8)) {
+    tlm_set_error("%s: Q/KV rows must start on 16-byte boundaries", fn);
     return TLM_EUNSUPPORTED;
   }
-  if (B == 0) return TLM_OK;
-  if (kv_rows < 1) {
-    tlm_set_error("tlm_mla_decode: empty KV pool");
+  if (B > 0 && kv_rows < 1) {
+    tlm_set_error("%s: empty KV pool", fn);
     return TLM_EINVAL;
   }
+  return TLM_OK;
+}
+
+// The decode proper on validated arguments. ws_bytes is checked against the need of the path
+// taken (ws is 16-byte aligned).
+static int mla_run(const char* fn, const void* q, const void* q_pe, int64_t q_stride,
+                   int64_t q_pe_stride, const void* kv, const void* k_pe, int64_t kv_stride,
+                   int64_t kpe_stride, int64_t kv_rows, const int32_t* block_table,
+                   const int32_t* seqlens, void* o, void* ws, size_t ws_bytes, int64_t B,
+                   int64_t Hq, int64_t dv, int64_t page, int64_t max_pages, int num_split,
+                   float sm_scale, const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
+                   void* stream) {
+  if (B == 0) return TLM_OK;
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
   if (kv_dtype == TLM_F8E4M3) {
-    const int rc = tlm_mla_fp8_launch(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
-                                      kpe_stride, kv_rows, block_table, seqlens, o, ws, B, Hq,
-                                      page, max_pages, num_split, sc, kv_scale,
-                                      q_dtype == TLM_BF16, o_dtype == TLM_BF16, stream);
-    if (rc != TLM_EUNSUPPORTED) return rc;
+    const size_t need = tlm_mla_fp8_workspace_bytes(B, Hq, num_split);
+    if (need > 0 && need <= ws_bytes) {
+      const int rc = tlm_mla_fp8_launch(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                        kpe_stride, kv_rows, block_table, seqlens, o, ws, B, Hq,
+                                        page, max_pages, num_split, sc, kv_scale,
+                                        q_dtype == TLM_BF16, o_dtype == TLM_BF16, stream);
+      if (rc != TLM_EUNSUPPORTED) return rc;
+    }
+  }
+  if (ws_bytes < mla_split_workspace_bytes(B, Hq, dv, num_split)) {
+    tlm_set_error("%s: %zu bytes of workspace, %zu required", fn, ws_bytes,
+                  std::max(mla_split_workspace_bytes(B, Hq, dv, num_split),
+                           kv_dtype == TLM_F8E4M3 ? tlm_mla_fp8_workspace_bytes(B, Hq, num_split)
+                                                  : (size_t)0));
+    return TLM_EWORKSPACE;
   }
   hipStream_t st = (hipStream_t)stream;
   float* ws_o = (float*)ws;
@@ -444,6 +468,34 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
                                                      kv_scale, kv_dtype == TLM_F8E4M3);
   TLM_LAUNCH_CHECK("tlm_mla_decode (combine)");
   return TLM_OK;
+}
+
+extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
+                              int64_t q_pe_stride, const void* kv, const void* k_pe,
+                              int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                              const int32_t* block_table, const int32_t* seqlens, void* o,
+                              void* ws, size_t ws_bytes,
+                              int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
+                              int64_t max_pages, int num_split, float sm_scale,
+                              const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
+                              void* stream) {
+  const char* fn = "tlm_mla_decode";
+  int rc = mla_validate(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride,
+                        kv_rows, block_table, seqlens, o, B, Hq, dv, dpe, page, max_pages,
+                        num_split, q_dtype, kv_dtype, o_dtype);
+  if (rc) return rc;
+  if (ws_bytes < tlm_mla_workspace_bytes(B, Hq, dv, num_split) || (B > 0 && !ws)) {
+    tlm_set_error("tlm_mla_decode: workspace of %zu bytes is smaller than the %zu required",
+                  ws_bytes, tlm_mla_workspace_bytes(B, Hq, dv, num_split));
+    return TLM_EWORKSPACE;
+  }
+  if (!tlm_aligned(ws, 16)) {
+    tlm_set_error("tlm_mla_decode: workspace must be 16-byte aligned");
+    return TLM_EUNSUPPORTED;
+  }
+  return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
+                 block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, page, max_pages, num_split,
+                 sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype, stream);
 }
 
 extern "C" int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, int64_t kv_rows,

@@ -13,21 +13,24 @@
 //   * work partition: the sequences' 64-token tiles are concatenated and cut into G equal ranges,
 //     so every CU gets the same number of tiles whatever the length mix. A range holds pieces of
 //     one or more sequences: a sequence entirely inside one range is written to the output
-//     directly; the pieces of a longer one go to fp32 partial slots (one for the range's first
-//     piece, one for its last) merged by the combine kernel;
+//     directly; the pieces of a longer one go to partial slots (bf16 O, fp32 lse; one for the
+//     range's first piece, one for its last) merged by the combine kernel;
 //   * workgroup = 64 heads x one range = 2 wave pairs x 32 heads. The two waves of a pair split a
 //     64-token tile by tokens for S^T = K Q^T (one 32-token block each, all 576 dims) and by V
-//     dims for O^T = V^T P^T (256 dims each, all 64 tokens), exchanging block maxima and the bf16
+//     dims for O^T = V^T P^T (256 dims each, all 64 tokens), exchanging block maxima and the e4m3
 //     P^T block through LDS: no work is duplicated and each wave holds only 128 O accumulators;
 //   * Q^T stays in VGPRs for the whole piece, split per head into two e4m3 terms
 //     q / s = hi + lo (s a power of two putting max|q| at <= 448), which keeps bf16-level accuracy
 //     while S^T runs on v_mfma_f32_32x32x64_f8f6f4 straight from the fp8 cache bytes (2 MFMAs per
 //     64 dims: the cost of one bf16 MFMA and no K conversion);
-//   * O^T on v_mfma_f32_32x32x16_bf16: V^T comes from the row-major fp8 tile through
-//     ds_read_b64_tr_b8 (8 tokens of one dim per lane), widened exactly to bf16; P^T is the S^T
-//     accumulator itself: K rows are fed to the MFMA in the order tau (bits 2 and 3 of the row
-//     index swapped) so accumulator element i of lane l is token 16(i/8) + 8(l/32) + i%8, the
-//     B-operand layout of the PV MFMA;
+//   * O^T = V^T P^T on the MX-scaled fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): V^T comes
+//     straight from the row-major fp8 tile through ds_read_b64_tr_b8 (8 tokens of one dim per
+//     lane); P^T is rounded once to e4m3 on a power-of-two scale per (head, 32-token block),
+//     passed to the MFMA as its E8M0 block scale (one e4m3 term: relative RMS error ~1.3% of the
+//     output against the exact softmax, against ~0.2% for two terms at one more MFMA per dim
+//     block). K rows are fed to the S^T MFMA in the order tau (bits 2 and 3 of the row index
+//     swapped) so S^T accumulator element i of lane l is token 16(i/8) + 8(l/32) + i%8, the
+//     order of the P^T blocks exchanged through LDS;
 //   * softmax without accumulator rescaling: a segment fixes its reference max m from its first
 //     tile and accumulates 2^(x - m); only when a tile's max exceeds m by more than 64 (log2
 //     units) does the segment end (its normalised partial is merged into a scratch slot) and a new
@@ -63,8 +66,14 @@ constexpr int F8_LOADS = 9;                          // LDS-DMA loads per thread
 constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
-constexpr int F8_WAVE_F4 = 8 * 4 * 64;               // float4 per wave in a partial slot
+constexpr int F8_WAVE_F4 = 8 * 4 * 64;               // 4-element groups per wave in a partial slot
 constexpr int F8_QREG = 4;                           // Q k-steps held in VGPRs; the rest in LDS
+#ifndef F8_DMA_STEPS
+#define F8_DMA_STEPS 3
+#endif
+// The refill of the ring (F8_LOADS LDS-DMA instructions per thread) is spread over the first
+// F8_DMA_STEPS k-steps of the S^T MFMAs, so the tile two ahead is requested early in the step.
+constexpr int F8_DMA_PER_STEP = (F8_LOADS + F8_DMA_STEPS - 1) / F8_DMA_STEPS;
 
 // swizzled 16-byte chunk index of latent row r / rope row r
 TLM_DEV int swz_lat(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
@@ -173,6 +182,12 @@ TLM_DEV bf16x8 fp8x8_to_bf16(i32x2 v) {
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// four bf16 (two dwords) -> four floats (exact)
+TLM_DEV f32x4 bf16x4_to_f32(u32x2 w) {
+  return f32x4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+               __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u)};
+}
+
 // four floats -> four e4m3 bytes (round to nearest even)
 TLM_DEV int pack_fp8x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
@@ -192,7 +207,7 @@ struct F8Args {
   uint8_t* qsplit;  // [B * Hq][2][576] e4m3 hi and lo terms of q / 2^qexp (written by prep)
   int32_t* qexp;    // [B * Hq] power-of-two exponent of each head's Q scale
   float* part_lse;
-  float* part_o;
+  u32x2* part_o;  // bf16 partial outputs, four per element
   uint16_t* out;
   int B, Hq, page, max_pages, G;
   int lmax;           // seqlens are clamped to [0, lmax = max_pages * page]
@@ -323,9 +338,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[F8_NSTAGE * F8_STAGE];
   __shared__ float xmax[2][2][32];  // [pair][token block][head]: block maxima
   __shared__ float xsum[2][2][32];  // [pair][token block][head]: block sums of P
-  // P^T blocks as e4m3 hi / lo terms: [pair][token block][hi, lo][head][32 tokens], and the
-  // E8M0 scale of each (block, head)
-  __shared__ __attribute__((aligned(16))) uint8_t xq[2][2][2][32][32];
+  // P^T blocks as e4m3: [pair][token block][head][32 tokens], and the E8M0 scale of each
+  // (block, head)
+  __shared__ __attribute__((aligned(16))) uint8_t xq[2][2][32][32];
   __shared__ int xsc[2][2][32];
   // Q^T k-steps F8_QREG..8 of each pair: [pair][(k - F8_QREG) * 2 + hi/lo][lane]
   __shared__ __attribute__((aligned(16))) i32x8 qt[2][(9 - F8_QREG) * 2][64];
@@ -471,8 +486,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     return false;
   };
   // S^T = K Q^T of tile x for this wave's 32 tokens (rows past the sequence read as zeros and
-  // are masked later), one LDS-DMA instruction of the refill per k-step (REFILL) and the work
-  // hook(k) after the k-step k MFMAs. No branches inside: the k-steps form one block.
+  // are masked later), the LDS-DMA instructions of the refill in the first k-steps (REFILL) and
+  // the work hook(k) after the k-step k MFMAs. No branches inside: the k-steps form one block.
   auto qk_body = [&](int64_t x, f32x16& so, const Dma& dma, auto REFILLc, auto&& hook) {
     constexpr bool REFILL = decltype(REFILLc)::value;
     const uint8_t* st = ring + (int)((x - t_lo) % F8_NSTAGE) * F8_STAGE;
@@ -503,7 +518,11 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         order_after(qop[k % 3][1]);
       }
       if (k + 2 < 9) kread(k + 2);
-      if constexpr (REFILL) issue_dma(dma, k);
+      if constexpr (REFILL) {
+#pragma unroll
+        for (int j = 0; j < F8_DMA_PER_STEP; ++j)
+          if (k * F8_DMA_PER_STEP + j < F8_LOADS) issue_dma(dma, k * F8_DMA_PER_STEP + j);
+      }
       so = mfma_fp8(kop[k % 3], k < F8_QREG ? qhi[k] : qop[k % 3][0], so);
       so = mfma_fp8(kop[k % 3], k < F8_QREG ? qlo[k] : qop[k % 3][1], so);
       hook(k);
@@ -551,24 +570,26 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         w_seg *= e_seg / tot;
       }
       const int64_t scr_slot = (int64_t)g * F8_SLOTS + 2;
-      const f32x4* scr =
-          (const f32x4*)a.part_o + ((scr_slot * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
-      // value of output float4 (dt, q4) of this wave
+      const u32x2* scr = a.part_o + ((scr_slot * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
+      // value of output group (dt, q4) of this wave (four consecutive dims)
       auto val = [&](int dt, int q4, auto merge) {
         f32x4 v = {oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
                    oacc[dt][4 * q4 + 3]};
         v *= w_seg;
-        if constexpr (decltype(merge)::value) v += scr[(dt * 4 + q4) * 64] * w_old;
+        if constexpr (decltype(merge)::value) v += bf16x4_to_f32(scr[(dt * 4 + q4) * 64]) * w_old;
         return v;
       };
       auto store = [&](auto merge) {
         if (cut || !complete) {
           const int64_t sb = (int64_t)g * F8_SLOTS + (cut ? 2 : slot);
-          f32x4* dst = (f32x4*)a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
+          u32x2* dst = a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) dst[(dt * 4 + q4) * 64] = val(dt, q4, merge);
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const f32x4 v = val(dt, q4, merge);
+              dst[(dt * 4 + q4) * 64] = u32x2{h16<true>::pack(v[0], v[1]), h16<true>::pack(v[2], v[3])};
+            }
             sched_fence();
           }
           if (dh == 0 && hf == 0) a.part_lse[sb * a.Hq + head] = lse_out;
@@ -610,13 +631,13 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
       const bool nxt = t + 1 < p_hi;
       // softmax of tile t, in pieces placed after the k-steps of the next tile's S^T:
       //   0: block max -> LDS; 2: barrier; 3: tile max, segment check, block scale; 3..6: P^T
-      //   as two e4m3 terms, 4 elements per step; 6: P^T blocks -> LDS; 7: block sums and
-      //   scales -> LDS, barrier; 8: row sums, B operands
+      //   in e4m3, 4 elements per step; 6: P^T blocks -> LDS; 7: block sums and scales -> LDS,
+      //   barrier; 8: row sums, B operand
       float mb = -INFINITY, ps = 0.f, sh = 0.f, m_old = 0.f, tsum = 0.f;
       int es = 0;
       bool cut = false;  // a new segment starts at this tile (flushed before its O^T update)
-      int phi4[4], plo4[4];
-      i32x8 pbh, pbl;
+      int phi4[4];
+      i32x8 pbh;
       int psc = 0;
       auto hook = [&](int k) {
         if (k == 0) {
@@ -644,9 +665,11 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
           m_old = mref;
           mref = (first || cut) ? mt : mref;
           first = false;
-          // P^T of this wave's block as two e4m3 terms on a per-head power-of-two scale 2^es
-          // (es = exponent of the block's largest P minus 8, so scaled values are below 256),
-          // folded into the exp2 argument
+          // P^T of this wave's block in e4m3 on a per-head power-of-two scale 2^es (es =
+          // exponent of the block's largest P minus 8, so scaled values are below 256), folded
+          // into the exp2 argument. The row sums add the rounded P, so the weights applied to V
+          // sum to one (a one-token sequence returns its V row exactly) and the largest P of a
+          // segment, 2^0, is exact
           int e2 = 0;
           (void)frexpf(__builtin_amdgcn_exp2f(mb - mref), &e2);
           es = mb == -INFINITY ? 0 : max(-127, min(127, e2 - 8));
@@ -656,24 +679,18 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
           const int q4 = k - 3;
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            y[e] = __builtin_amdgcn_exp2f(fmaf(s[4 * q4 + e], ch, sh));
-            ps += y[e];
-          }
+          for (int e = 0; e < 4; ++e) y[e] = __builtin_amdgcn_exp2f(fmaf(s[4 * q4 + e], ch, sh));
           phi4[q4] = pack_fp8x4(y[0], y[1], y[2], y[3]);
           typedef float f2 __attribute__((ext_vector_type(2)));
           const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], false);
           const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], true);
-          plo4[q4] = pack_fp8x4(y[0] - r01[0], y[1] - r01[1], y[2] - r23[0], y[3] - r23[1]);
+          ps += (r01[0] + r01[1]) + (r23[0] + r23[1]);
         }
         if (k == 6) {
           // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
-          uint8_t* rh = &xq[pr][dh][0][hh][8 * hf];
-          uint8_t* rl = &xq[pr][dh][1][hh][8 * hf];
+          uint8_t* rh = &xq[pr][dh][hh][8 * hf];
           lds_write_b64(rh, u32x2{(uint32_t)phi4[0], (uint32_t)phi4[1]});
           lds_write_b64(rh + 16, u32x2{(uint32_t)phi4[2], (uint32_t)phi4[3]});
-          lds_write_b64(rl, u32x2{(uint32_t)plo4[0], (uint32_t)plo4[1]});
-          lds_write_b64(rl + 16, u32x2{(uint32_t)plo4[2], (uint32_t)plo4[3]});
         }
         if (k == 7) {
           ps = xhalf_sum(ldexpf(ps, es));
@@ -685,8 +702,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
           tsum = dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
           // B operand: lane (head hh, half hf) holds tokens 16 hf + 0..15 of both blocks; its
           // scale is that of block hf
-          pbh = lds_2xb128(&xq[pr][0][0][hh][16 * hf], &xq[pr][1][0][hh][16 * hf]);
-          pbl = lds_2xb128(&xq[pr][0][1][hh][16 * hf], &xq[pr][1][1][hh][16 * hf]);
+          pbh = lds_2xb128(&xq[pr][0][hh][16 * hf], &xq[pr][1][hh][16 * hf]);
           psc = xsc[pr][hf][hh];
         }
       };
@@ -706,7 +722,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         lsum = 0.f;
       }
       lsum += tsum;
-      // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks x hi/lo
+      // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks
       auto vread = [&](int dt) {
         i32x2 r[4];
 #pragma unroll
@@ -717,7 +733,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
       i32x8 vop[2][2];
       vop[0][0] = vread(0);
       vop[0][1] = vread(1);
-      lds_wait(pbh, pbl);
+      lds_wait(pbh);
 #pragma unroll
       for (int g2 = 0; g2 < 4; ++g2) {
         lds_wait(vop[g2 & 1][0], vop[g2 & 1][1]);
@@ -729,7 +745,6 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         for (int u = 0; u < 2; ++u) {
           const int dt = 2 * g2 + u;
           oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbh, oacc[dt], psc);
-          oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbl, oacc[dt], psc);
         }
         sched_fence();
       }
@@ -782,10 +797,9 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
     if (start(g) == start(g + 1)) continue;
     const int64_t sb = slot_of(g);
     const float w = __builtin_amdgcn_exp2f(a.part_lse[sb * a.Hq + head] - lse);
-    const f32x4* src =
-        (const f32x4*)a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
+    const u32x2* src = a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) acc[q4] += src[q4 * 64] * w;
+    for (int q4 = 0; q4 < 4; ++q4) acc[q4] += bf16x4_to_f32(src[q4 * 64]) * w;
   }
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
@@ -805,12 +819,21 @@ int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
 
 }  // namespace
 
-// Workspace of the fp8 path: tile prefix, then lse and O partial slots (three 64-head x 512 slots
-// per range and head group).
+// Workspace of the fp8 path: tile prefix, Q terms, then lse (fp32) and O (bf16) partial slots
+// (three 64-head x 512 slots per range and head group).
 size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split) {
   if (Hq % F8_HEADS) return 0;
   const size_t G = (size_t)f8_ranges(B, Hq, num_split);
-  return f8_cu_bytes(B) + f8_q_bytes(B, Hq) + G * F8_SLOTS * (size_t)Hq * (F8_DV + 1) * sizeof(float);
+  return f8_cu_bytes(B) + f8_q_bytes(B, Hq) +
+         G * F8_SLOTS * (size_t)Hq * (F8_DV * sizeof(uint16_t) + sizeof(float));
+}
+
+// Whether the fp8 matrix-core path takes this shape (fp8 KV is checked by the caller).
+bool tlm_mla_fp8_applies(int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                         int64_t kv_stride, int64_t kpe_stride) {
+  const int64_t tiles_per_seq = (max_pages * page + F8_TILE - 1) / F8_TILE;
+  return Hq % F8_HEADS == 0 && page % F8_TILE == 0 && kv_stride <= (1 << 24) &&
+         kpe_stride <= (1 << 24) && B * tiles_per_seq <= INT32_MAX;
 }
 
 // Returns TLM_EUNSUPPORTED (launching nothing) when the shape is outside this kernel's domain.
@@ -820,9 +843,7 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
                        void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
                        int num_split, float score_scale, const float* kv_scale, bool q_bf16,
                        bool o_bf16, void* stream) {
-  const int64_t tiles_per_seq = (max_pages * page + F8_TILE - 1) / F8_TILE;
-  if (Hq % F8_HEADS != 0 || page % F8_TILE != 0 || kv_stride > (1 << 24) ||
-      kpe_stride > (1 << 24) || B * tiles_per_seq > INT32_MAX)
+  if (!tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride))
     return TLM_EUNSUPPORTED;
   F8Args a;
   a.q = (const uint16_t*)q;
@@ -841,7 +862,7 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.qsplit = (uint8_t*)ws + f8_cu_bytes(B);
   a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
   a.part_lse = (float*)((char*)ws + f8_cu_bytes(B) + f8_q_bytes(B, Hq));
-  a.part_o = a.part_lse + G * F8_SLOTS * Hq;
+  a.part_o = (u32x2*)(a.part_lse + G * F8_SLOTS * Hq);
   a.out = (uint16_t*)o;
   a.B = (int)B;
   a.Hq = (int)Hq;

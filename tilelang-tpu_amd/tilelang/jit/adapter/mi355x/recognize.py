@@ -160,6 +160,61 @@ def _fail(family, msg):
     raise UnsupportedProgram(f"{family}: {msg}")
 
 
+# Tile ops each family's kernel implements. A program that issues any other op (an epilogue, a
+# bias add, a scale) computes something the kernel does not, and is rejected.
+_FILL_OPS = ("ppl_fill", "fill")
+_ALLOWED_OPS = {
+    "rmsnorm": _COPY + _FILL_OPS + ("ppl_reduce_sum", "ppl_mul", "ppl_add", "ppl_add_C",
+                                    "ppl_mul_C", "ppl_rsqrt"),
+    "gemm": _COPY + _FILL_OPS + _GEMM + ("store",),
+    "rope": _COPY + ("ppl_mul", "ppl_mul_C", "ppl_rope_add"),
+    "swiglu": _COPY + _FILL_OPS + ("ppl_exp", "ppl_mul_C", "ppl_add", "ppl_div", "ppl_mul"),
+    "flashattn": _COPY + _FILL_OPS + _GEMM + ("store", "ppl_add", "ppl_sub", "ppl_mul",
+                                              "ppl_div", "ppl_exp", "ppl_mul_C", "ppl_reduce_max",
+                                              "ppl_reduce_sum", "reduce_max", "reduce_sum"),
+    "mla": _COPY + _FILL_OPS + _GEMM + ("store", "reduce_max", "reduce_sum"),
+    "sigmoid": _COPY + ("ppl_sigmoid",),
+    "gather": ("ppl_gather",),
+    "topk": ("ppl_topk",),
+    "row_reduce": _COPY + _FILL_OPS + ("ppl_reduce_max", "ppl_reduce_sum", "reduce_max",
+                                       "reduce_sum"),
+}
+
+
+def _audit(pf, plan: "Plan", used: Optional[List] = None) -> "Plan":
+    """Reject a matched program that issues an op outside its family's kernel or has a
+    parameter the kernel never reads or writes. ``used`` lists the parameters the matched
+    pattern consumed (default: every integer-valued attr that indexes ``pf.params``)."""
+    fam = plan.family
+    extra = sorted({op.name for op in _ops(pf)} - set(_ALLOWED_OPS[fam]))
+    if extra:
+        _fail(fam, f"op(s) {extra} are not part of the {fam} kernel (an epilogue or extra "
+                   f"elementwise step would be dropped), so the program is not compiled")
+    if used is None:
+        idx = {plan.attrs[k] for k in _PARAM_ATTRS[fam] if plan.attrs.get(k) is not None}
+        used = [pf.params[i] for i in sorted(idx)]
+    unused = [getattr(p, "name", repr(p)) for p in pf.params if all(p is not u for u in used)]
+    if unused:
+        _fail(fam, f"parameter(s) {unused} are not read or written by the {fam} kernel")
+    return plan
+
+
+# plan attrs that hold parameter indices, per family
+_PARAM_ATTRS = {
+    "rmsnorm": ("x", "w", "y"),
+    "gemm": ("a", "b", "c"),
+    "rope": ("q", "k", "cos", "sin", "q_out", "k_out"),
+    "swiglu": ("gate", "up", "out"),
+    "flashattn": ("q", "k", "v", "o", "cu_q", "cu_k", "max_q"),
+    "mla": ("q", "q_pe", "kv", "k_pe", "block_table", "seqlens", "o", "glse", "o_partial",
+            "kv_scale"),
+    "sigmoid": ("x", "y"),
+    "gather": ("param", "index", "out"),
+    "topk": ("src", "values", "indices"),
+    "row_reduce": ("x", "y"),
+}
+
+
 # ------------------------------------------------------------------------------------------------
 # families
 
@@ -326,6 +381,23 @@ def _gemm(pf, names) -> Plan:
         _fail(fam, f"fp8 GEMM output {C.dtype} (float32, float16, bfloat16 or {A.dtype})")
     if A.dtype not in fp8 and C.dtype not in ("float16", "bfloat16", "float32"):
         _fail(fam, f"C dtype {C.dtype}")
+    # the accumulator starts at zero (ppl_gemm accumulates into C) and the only element stores
+    # allowed are the 2xAcc fold acc2[i, j] = acc2[i, j] + acc[i, j] of two local fragments
+    for op in _ops(pf, _FILL_OPS):
+        if _const(op.args[1]) != 0.0:
+            _fail(fam, f"{op.name} of {_buf(op.args[0])!r} with {op.args[1]!r}: the kernel's "
+                       "accumulators start at zero")
+    for op in _ops(pf, ("store",)):
+        v = op.args[2]
+        nodes = list(v.walk()) if isinstance(v, Expr) else [v]
+        loads = [e for e in nodes if isinstance(e, Expr) and e.op == "load"]
+        other = [e for e in nodes if not (isinstance(e, Expr) and e.op in ("load", "add"))
+                 and not isinstance(e, (BufferAccess, ir.Var))]
+        if op.args[0].scope == "global" or other or len(loads) != 2 or \
+                any(e.args[0].scope == "global" for e in loads) or \
+                all(e.args[0] is not op.args[0] for e in loads):
+            _fail(fam, f"element store into {op.args[0]!r} is not the accumulator fold "
+                       "acc2[i, j] += acc[i, j]; epilogues are not part of the gemm kernel")
     return Plan(fam, pf.params, [_index(pf, C)], dict(
         a=_index(pf, A), b=_index(pf, B), c=_index(pf, C), M=M, N=N, K=K, trans_b=bool(tb),
         in_dtype=A.dtype, out_dtype=C.dtype,
@@ -700,27 +772,27 @@ def recognize(pf) -> Plan:
     n_gemm = sum(1 for op in _ops(pf, _GEMM))
     try:
         if ints and n_gemm >= 3:
-            return _mla(pf, names)
+            return _audit(pf, _mla(pf, names))
         if n_gemm == 2 and names & {"ppl_reduce_max", "reduce_max"}:
-            return _flashattn(pf, names)
+            return _audit(pf, _flashattn(pf, names))
         if n_gemm == 1 and not names & {"ppl_exp", "ppl_reduce_max", "reduce_max"}:
-            return _gemm(pf, names)
+            return _audit(pf, _gemm(pf, names))
         if "ppl_rope_add" in names:
-            return _rope(pf, names)
+            return _audit(pf, _rope(pf, names))
         if {"ppl_reduce_sum", "ppl_rsqrt"} <= names:
-            return _rmsnorm(pf, names)
+            return _audit(pf, _rmsnorm(pf, names))
         if {"ppl_exp", "ppl_div"} <= names:
-            return _swiglu(pf, names)
+            return _audit(pf, _swiglu(pf, names))
         if "ppl_sigmoid" in names:
-            return _sigmoid(pf, names)
+            return _audit(pf, _sigmoid(pf, names))
         if "ppl_gather" in names:
-            return _gather(pf, names)
+            return _audit(pf, _gather(pf, names))
         if "ppl_topk" in names:
-            return _topk(pf, names)
+            return _audit(pf, _topk(pf, names))
         if n_gemm == 0 and len(names & {"ppl_reduce_max", "ppl_reduce_sum", "reduce_max",
                                         "reduce_sum"}) == 1 and \
                 not names & {"ppl_exp", "ppl_rsqrt", "ppl_div", "ppl_mul"}:
-            return _row_reduce(pf, names)
+            return _audit(pf, _row_reduce(pf, names))
     except UnsupportedProgram:
         raise
     except (TypeError, ValueError, IndexError) as e:  # malformed trace
