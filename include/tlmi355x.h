@@ -13,7 +13,8 @@
  *
  * Conventions (all entry points):
  *  - every pointer is a DEVICE pointer owned by the caller (torch allocates); the
- *    library allocates nothing on the hot path (MLA takes its workspace from the caller);
+ *    library allocates nothing on the hot path (MLA takes its workspace from the caller, or
+ *    uses the library-owned scratch array of tlm_mla_decode_noalloc);
  *  - tensors are dense, row-major (C-contiguous) unless a stride argument says otherwise;
  *  - return 0 on success or a negative TLM_E* code; the message is available from
  *    tlm_last_error() (thread-local). Nothing aborts or prints;
@@ -239,6 +240,30 @@ int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_
 
 /* Workspace bytes that tlm_mla_decode needs for (B, Hq, dv, num_split). */
 size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split);
+
+/* Bytes of the library-owned scratch of tlm_mla_decode_noalloc (per GPU). */
+#define TLM_MLA_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* tlm_mla_decode without a caller workspace and without any allocation: the kernels' scratch
+ * (tile prefix, Q terms, partial outputs and log-sum-exps) lives in a library-owned device array
+ * of TLM_MLA_SCRATCH_BYTES, one per GPU, held from the library's first use on that GPU until the
+ * process ends. No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, validation and results as tlm_mla_decode (ws / ws_bytes dropped). Returns
+ * TLM_EWORKSPACE, before any HIP call, when the path taken needs more scratch than
+ * TLM_MLA_SCRATCH_BYTES (the FP8 config B 64, Hq 128 with num_split <= 5 fits). Every call on a
+ * GPU shares that GPU's array and nothing in it has to start zeroed; calls that overlap in time on
+ * one GPU (several streams or host threads) race on it and must be serialised by the caller. */
+int tlm_mla_decode_noalloc(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                           const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                           int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
+                           void* o, int64_t B, int64_t Hq, int64_t dv, int64_t dpe, int64_t page,
+                           int64_t max_pages, int num_split, float sm_scale,
+                           const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
+                           void* stream);
+
+/* TLM_MLA_SCRATCH_BYTES, for bindings that cannot read the macro. */
+size_t tlm_mla_scratch_bytes(void);
 
 /* Integer-path check: out[i, :] = kv_bytes[row(i), :] for every token i of every sequence,
  * rows resolved through the block table exactly as tlm_mla_decode does; tokens of sequence b

@@ -22,6 +22,8 @@ int tlm_hip_fail(hipError_t e, const char* what) {
   return TLM_EHIP;
 }
 
+int tlm_mla_scratch_setup(int dev);  // tlm_mla.hip
+
 namespace {
 constexpr int kMaxDevices = 64;
 std::once_flag g_dev_once[kMaxDevices];
@@ -67,7 +69,8 @@ extern "C" int tlm_init(int device) {
   }
   hipError_t e = hipSetDevice(device);
   if (e != hipSuccess) return tlm_hip_fail(e, "hipSetDevice");
-  return TLM_OK;
+  // device address of the allocation-free MLA entry point's scratch array (tlm_mla.hip)
+  return tlm_mla_scratch_setup(device);
 }
 
 extern "C" int tlm_num_cus(void) {

@@ -27,6 +27,7 @@
 #include "tlm_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace {
 
@@ -496,6 +497,75 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
   return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
                  block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, page, max_pages, num_split,
                  sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype, stream);
+}
+
+// ---- allocation-free variant ------------------------------------------------------------------
+// The scratch of tlm_mla_decode_noalloc: a file-scope device array, one instance per GPU (each
+// device that loads this code object holds its own copy at its own address until the process
+// ends). In host code `scratch` only names the symbol: its device address is looked up once per
+// device with hipGetSymbolAddress and kept in g_scratch_ptr, which is what kernels receive.
+static __device__ __align__(256) uint8_t scratch[TLM_MLA_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_err[kScratchDevices];
+}  // namespace
+
+// Resolve this device's scratch address (device `dev` must be current). Called from tlm_init and,
+// for callers that skip tlm_init, from the entry point's first call on a device.
+int tlm_mla_scratch_setup(int dev) {
+  if (dev < 0 || dev >= kScratchDevices) {
+    tlm_set_error("tlm_mla_decode_noalloc: device index %d out of range", dev);
+    return TLM_EINVAL;
+  }
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess)
+    return tlm_hip_fail(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+  return TLM_OK;
+}
+
+extern "C" size_t tlm_mla_scratch_bytes(void) { return TLM_MLA_SCRATCH_BYTES; }
+
+extern "C" int tlm_mla_decode_noalloc(const void* q, const void* q_pe, int64_t q_stride,
+                                      int64_t q_pe_stride, const void* kv, const void* k_pe,
+                                      int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                                      const int32_t* block_table, const int32_t* seqlens, void* o,
+                                      int64_t B, int64_t Hq, int64_t dv, int64_t dpe,
+                                      int64_t page, int64_t max_pages, int num_split,
+                                      float sm_scale, const float* kv_scale, int q_dtype,
+                                      int kv_dtype, int o_dtype, void* stream) {
+  const char* fn = "tlm_mla_decode_noalloc";
+  int rc = mla_validate(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride,
+                        kv_rows, block_table, seqlens, o, B, Hq, dv, dpe, page, max_pages,
+                        num_split, q_dtype, kv_dtype, o_dtype);
+  if (rc) return rc;
+  // the path taken must fit the scratch (checked before any HIP call)
+  const bool fp8 = kv_dtype == TLM_F8E4M3 &&
+                   tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride);
+  const size_t need = fp8 ? tlm_mla_fp8_workspace_bytes(B, Hq, num_split)
+                          : mla_split_workspace_bytes(B, Hq, dv, num_split);
+  if (need > TLM_MLA_SCRATCH_BYTES) {
+    tlm_set_error("%s: this call needs %zu bytes of scratch, more than the library's %zu "
+                  "(lower num_split or the batch, or use tlm_mla_decode with a workspace)", fn,
+                  need, (size_t)TLM_MLA_SCRATCH_BYTES);
+    return TLM_EWORKSPACE;
+  }
+  if (B == 0) return TLM_OK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return tlm_hip_fail(e, "hipGetDevice");
+  rc = tlm_mla_scratch_setup(dev);
+  if (rc) return rc;
+  return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
+                 block_table, seqlens, o, g_scratch_ptr[dev], TLM_MLA_SCRATCH_BYTES, B, Hq, dv,
+                 page, max_pages, num_split, sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype,
+                 stream);
 }
 
 extern "C" int tlm_paged_gather(const void* kv_bytes, int64_t row_bytes, int64_t kv_rows,

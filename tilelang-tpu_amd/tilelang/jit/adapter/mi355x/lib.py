@@ -53,6 +53,11 @@ _SIGNATURES = {
                         c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
                        [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int, c_void_p], c_int),
     "tlm_mla_workspace_bytes": ([c_int64, c_int64, c_int64, c_int], c_size_t),
+    "tlm_mla_decode_noalloc": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                c_int64, c_int64, c_void_p, c_void_p, c_void_p] +
+                               [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int,
+                                                c_void_p], c_int),
+    "tlm_mla_scratch_bytes": ([], c_size_t),
     "tlm_paged_gather": ([c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int64, c_int64, c_int64, c_void_p], c_int),
     "tlm_kv_append_fp8": ([c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p,
