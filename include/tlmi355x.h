@@ -169,7 +169,10 @@ int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o, int
  *   out_dtype: in_dtype or F32. The fp32 demo program
  *         (tpu_demo/flashattn/tpu_test_flashattn_fp32.py:14-135) multiplies fp16 copies of its
  *         fp32 Q/K/V tiles and of P but keeps acc_o and the output in fp32: tlm_cast Q, K, V to
- *         F16, then this with in_dtype F16, out_dtype F32. */
+ *         F16, then this with in_dtype F16, out_dtype F32.
+ *   in_dtype F32 (out_dtype F32, D a multiple of 4): all-fp32 attention with no 16-bit
+ *         rounding, the program tpu_demo/ppl/flashattn/fa_fp32.py:10-125 (fp32 tiles into
+ *         ppl_gemm, fp32 P); a per-query correctness kernel, not a tuned one. */
 int tlm_flash_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, int64_t B,
                           int64_t S, int64_t H, int64_t H_kv, int64_t D, int causal,
                           float sm_scale, int in_dtype, int out_dtype, void* stream);
@@ -206,6 +209,50 @@ int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void* v, void* o
                             int causal, float sm_scale, int in_dtype, int out_dtype,
                             void* stream);
 
+/* Elementwise tile programs: the stand-alone T.ppl_* elementwise programs of the TPU demos
+ * (tpu_demo/ppl/test/exp.py:6-16, mul_N_1.py:9-22, elementwise_c.py:9-22,
+ * tpu_demo/ppl/elementwise_add_kernel/elementwise_add.py:9-35; ops language/customize.py:238-339,
+ * 377-472), compiled by the recogniser into a register program run for every element (i, j) of
+ * the [rows, cols] output domain (replaces the PPL codegen of those programs).
+ *   in[k]   input k (in_dtype F32 | F16 | BF16), read at i * cols + j (TLM_EW_FULL), i
+ *           (TLM_EW_ROW: an [rows, 1] tensor broadcast along the row, the (M, 1) operand of
+ *           ppl_add / ppl_mul, codegen_ppl.cc:874-883), j (TLM_EW_COL) or 0 (TLM_EW_SCALAR);
+ *   out[k]  output k (out_dtype), written at i * cols + j, rounded to nearest even;
+ *   code    n_code instruction words: op | dst << 8 | a << 12 | b << 16 | imm << 20, slots
+ *           0..TLM_EW_SLOTS-1 holding fp32 values (initially 0). LOAD dst <- in[imm];
+ *           CONST dst <- consts[imm]; ADD / SUB / MUL / DIV dst <- a op b; EXP dst <- e^a;
+ *           RSQRT dst <- 1 / sqrt(a); SIGMOID dst <- 1 / (1 + e^-a); ROUND dst <- a rounded to
+ *           dtype imm (F16 / BF16 / F32: the value a 16-bit tile holds); STORE out[imm] <- a.
+ * Outputs may alias inputs only element for element (the in-place exp.py). */
+#define TLM_EW_MAX_IN 8
+#define TLM_EW_MAX_OUT 4
+#define TLM_EW_MAX_CODE 64
+#define TLM_EW_MAX_CONST 16
+#define TLM_EW_SLOTS 8
+enum tlm_ew_op {
+  TLM_EW_LOAD = 0,
+  TLM_EW_CONST = 1,
+  TLM_EW_ADD = 2,
+  TLM_EW_SUB = 3,
+  TLM_EW_MUL = 4,
+  TLM_EW_DIV = 5,
+  TLM_EW_EXP = 6,
+  TLM_EW_RSQRT = 7,
+  TLM_EW_SIGMOID = 8,
+  TLM_EW_ROUND = 9,
+  TLM_EW_STORE = 10,
+};
+enum tlm_ew_bcast {
+  TLM_EW_FULL = 0,
+  TLM_EW_ROW = 1,
+  TLM_EW_COL = 2,
+  TLM_EW_SCALAR = 3,
+};
+int tlm_elementwise(const void* const* in, const int* in_dtype, const int* in_bcast, int n_in,
+                    void* const* out, const int* out_dtype, int n_out, const int32_t* code,
+                    int n_code, const float* consts, int n_const, int64_t rows, int64_t cols,
+                    void* stream);
+
 /* MLA paged decode (one query token per sequence, one shared latent KV head).
  * Reference: examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split kernel :100-183,
  * LSE combine :186-221, params :224-256), torch oracle :259-308.
@@ -228,6 +275,12 @@ int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void* v, void* o
  *   a multiple of 64 and Hq a multiple of 64 the decode runs on the fp8 matrix cores with the
  *   sequences' tiles balanced over B*num_split/(Hq/64) ranges (num_split then only sets the
  *   parallelism); other cases use one workgroup per (sequence, split, 64 heads).
+ * dv = 512, dpe = 64, Hq a multiple of 64 and 16-byte aligned Q / KV rows take those
+ *   matrix-core kernels; any other dv <= 1024, dpe <= 256, Hq <= 4096 (e.g. the TPU program
+ *   tpu_demo/ppl/deepseek_mla/mla_decode.py at dim 32 + rope 4 over 8 heads) runs a generic
+ *   per-(sequence, head) kernel that needs no workspace.
+ * A non-paged cache [B, S, 1, d] (examples/deepseek_mla/example_mla_decode.py) is the paged
+ *   layout with page = S, max_pages = 1 and block_table[b, 0] = b.
  * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned; the larger of
  *   the two paths' layouts). */
 int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,

@@ -91,6 +91,29 @@ def row_reduce_ref(x: torch.Tensor, op: str, out_dtype=None) -> torch.Tensor:
     return r.to(out_dtype or x.dtype)
 
 
+# Stand-alone elementwise programs (tpu_demo/ppl/test, elementwise_add_kernel), fp32 math with
+# one rounding per tile write, as the programs' tile dtypes hold the values.
+# exp.py:6-16 / exp_bf16.py: in-place ppl_exp2 (natural exponential, customize.py:313-339).
+def ppl_exp_ref(x: torch.Tensor) -> torch.Tensor:
+    return torch.exp(x.float()).to(x.dtype)
+
+
+# mul_N_1.py:9-22: C = A * B, B [M, 1] broadcast along each row (codegen_ppl.cc:874-883).
+def ppl_mul_rows_ref(a: torch.Tensor, b_col: torch.Tensor) -> torch.Tensor:
+    return (a.float() * b_col.float().reshape(-1, 1)).to(a.dtype)
+
+
+# elementwise_c.py:9-22: B = A * C1 + C2 (ppl_mul_C, then ppl_add_C; the tile holds the product).
+def ppl_scale_shift_ref(a: torch.Tensor, scale: float, shift: float) -> torch.Tensor:
+    t = (a.float() * scale).to(a.dtype).float()
+    return (t + shift).to(a.dtype)
+
+
+# elementwise_add.py:37-38 (ref_add = torch.add(a, b)), cast to C's dtype.
+def ppl_add_ref(a: torch.Tensor, b: torch.Tensor, out_dtype=None) -> torch.Tensor:
+    return (a.float() + b.float()).to(out_dtype or a.dtype)
+
+
 # ------------------------------------------------------------------------------------------------
 # RoPE — tables per tpu_demo/tpu_test_rope_bf16.py:53-74 (make_rope_cos_sin), computed in fp32;
 # rotation per rope_ref_torch (:76-92).
@@ -282,7 +305,29 @@ def mla_decode_ref(q, q_pe, kv, k_pe, block_table, seqlens, page: int, sm_scale:
     return (o, lse) if return_lse else o
 
 
-# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial
+def mla_decode_nopage_ref(q, q_pe, kv, k_pe, sm_scale: Optional[float] = None,
+                          out_dtype=None):
+    """Non-paged MLA decode, examples/deepseek_mla/example_mla_decode.py:230-265 (ref_program):
+    query = [q, q_pe], key = [kv, k_pe] of one shared KV head, softmax(query key^T / sqrt(dv +
+    dpe)) kv in fp32; also the TPU program tpu_demo/ppl/deepseek_mla/mla_decode.py:9-121 (same
+    math with the natural-exp softmax and a singleton query axis). q [B, H, dv] or
+    [B, H, 1, dv], q_pe likewise with dpe; kv [B, S, 1, dv], k_pe [B, S, 1, dpe]. Returns the
+    shape of q in out_dtype (default q's dtype)."""
+    shape = q.shape
+    B, H = shape[0], shape[1]
+    dv, dpe = q.shape[-1], q_pe.shape[-1]
+    S = kv.shape[1]
+    scale = (1.0 / math.sqrt(dv + dpe)) if sm_scale is None else sm_scale
+    qq = torch.cat([q.reshape(B, H, dv).float(), q_pe.reshape(B, H, dpe).float()], dim=-1)
+    kk = torch.cat([kv.reshape(B, S, dv).float(), k_pe.reshape(B, S, dpe).float()], dim=-1)
+    vv = kv.reshape(B, S, dv).float()
+    out = torch.empty(B, H, dv, dtype=torch.float32)
+    for b in range(B):
+        out[b] = torch.softmax((qq[b] @ kk[b].t()) * scale, dim=-1) @ vv[b]
+    return out.reshape(shape).to(out_dtype or q.dtype)
+
+
+# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial
 # outputs with log2-domain LSE, then the LSE-weighted combine. Restated over explicit splits of
 # the token range (the kernel's partition, example_mla_decode_paged.py:140-144: blocks of
 # block_N tokens, the first `total % num_split` splits take one extra block).

@@ -141,13 +141,17 @@ def test_flash_attn_validation():
     assert L.tlm_flash_attn_fwd(None, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.BF16, None) == -1
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 100, 0, 0.1, lib.BF16, None) == -2  # D % 8
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 264, 0, 0.1, lib.BF16, None) == -2  # > 256
-    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.F32, None) == -2
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 128, 0, 0.1, lib.F8E4M3, None) == -2
+    # fp32 attention takes head dims that are multiples of 4 and an fp32 output only
+    assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 16, 1, 22, 0, 0.1, lib.F32, None) == -2
+    assert L.tlm_flash_attn_fwd_ex(p, p, p, p, 1, 16, 1, 1, 20, 0, 0.1, lib.F32, lib.BF16,
+                                   None) == -2
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 128, 0, 0.1, lib.BF16, None) == 0
     assert L.tlm_flash_attn_fwd(p, p, p, p, 1, 0, 1, 8, 0, 0.1, lib.BF16, None) == 0
     ex = L.tlm_flash_attn_fwd_ex
     assert ex(p, p, p, p, 1, 0, 1, 1, 8, 0, 0.1, lib.F16, lib.F32, None) == 0
     assert ex(p, p, p, p, 1, 16, 1, 1, 8, 0, 0.1, lib.F16, lib.BF16, None) == -2
-    assert ex(p, p, p, p, 1, 16, 1, 1, 8, 0, 0.1, lib.F32, lib.F32, None) == -2
+    assert ex(p, p, p, p, 1, 0, 1, 1, 8, 0, 0.1, lib.F32, lib.F32, None) == 0  # fp32: valid
     assert ex(p, p, p, p, 1, 16, 8, 3, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1  # 8 % 3
     assert ex(p, p, p, p, 1, 16, 8, 0, 128, 0, 0.1, lib.BF16, lib.BF16, None) == -1
     assert ex(p, p, p, p, 1, 0, 8, 2, 128, 0, 0.1, lib.BF16, lib.BF16, None) == 0
@@ -167,7 +171,7 @@ def test_flash_attn_validation():
               None) == -1  # 8 % 3
     assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 100, 0, 0.1, lib.F16, lib.F16,
               None) == -2  # D % 8
-    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F32, lib.F32,
+    assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 128, 0, 0.1, lib.F8E5M2, lib.F32,
               None) == -2
     assert vl(p, p, p, p, cu, cu, 2, 64, 100, 90, 8, 2, 128, 0, -1.0, lib.F16, lib.F16,
               None) == -1
@@ -197,10 +201,18 @@ def test_mla_validation_and_workspace():
     rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 16, 2, 128, 512, 64,
                           64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
     assert rc == -4 and "workspace" in _err()
-    # unsupported head dims
-    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 1 << 30, 2, 128, 256,
-                          64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    # head dims beyond the generic kernel's (dv <= 1024, dpe <= 256)
+    rc = L.tlm_mla_decode(p, p, 2048, 576, p, p, 2048, 576, 1000, p, p, p, p, 1 << 30, 2, 128,
+                          2048, 64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
     assert rc == -2
+    rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, p, p, p, p, 1 << 30, 2, 128, 512,
+                          512, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
+    assert rc == -2
+    # misaligned (odd) pointer for 16-bit Q
+    rc = L.tlm_mla_decode(ctypes.c_void_p(0x1001), p, 576, 576, p, p, 576, 576, 1000, p, p, p, p,
+                          1 << 30, 2, 128, 512, 64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3,
+                          lib.BF16, None)
+    assert rc == -1
     # null block table
     rc = L.tlm_mla_decode(p, p, 576, 576, p, p, 576, 576, 1000, None, p, p, p, 1 << 30, 2, 128,
                           512, 64, 64, 4, 2, 0.07, None, lib.BF16, lib.F8E4M3, lib.BF16, None)
@@ -228,7 +240,7 @@ def test_mla_noalloc_validation():
                                         dv, 64, page, 128, splits, 0.07, None, lib.BF16, kv_dt,
                                         lib.BF16, None)
     assert call(bt=None) == -1
-    assert call(dv=256) == -2
+    assert call(dv=2048) == -2
     assert call(kv_dt=lib.F16) == -2  # fp16 KV with bf16 Q
     # the FP8 config with 64 splits needs far more than the scratch
     assert call(splits=64) == -4 and "scratch" in _err()
@@ -271,3 +283,31 @@ def test_kv_append_validation():
     assert L.tlm_kv_append_fp8(*args(D=570, ks=576)) == -2
     assert L.tlm_kv_append_fp8(*args(ks=100)) == -1  # kv row stride smaller than D
     assert L.tlm_kv_append_fp8(*args(B=0)) == 0
+
+
+def test_elementwise_validation():
+    L = lib.load()
+    P, I = ctypes.c_void_p, ctypes.c_int
+    p = P(0x1000)
+    ins = (P * 1)(p)
+    dts = (I * 1)(lib.F32)
+    bc = (I * 1)(lib.EW_FULL)
+    outs = (P * 1)(p)
+    odt = (I * 1)(lib.F32)
+    cf = (ctypes.c_float * 1)(1.0)
+
+    def run(code, n_in=1, bcast=bc, rows=4, cols=4, n_const=1):
+        cw = (ctypes.c_int32 * len(code))(*code)
+        return L.tlm_elementwise(ins, dts, bcast, n_in, outs, odt, 1, cw, len(code), cf, n_const,
+                                 rows, cols, None)
+    load0, store0 = lib.EW_LOAD, lib.EW_STORE
+    assert run([load0, store0], rows=0) == 0
+    assert run([load0 | 1 << 20, store0]) == -1          # input 1 of 1
+    assert run([lib.EW_CONST | 1 << 20, store0]) == -1    # constant 1 of 1
+    assert run([load0, store0 | 1 << 20]) == -1          # output 1 of 1
+    assert run([load0 | 8 << 8, store0]) == -1           # slot 8 of 8
+    assert run([11, store0]) == -1                       # no such opcode
+    assert run([lib.EW_ROUND | 7 << 20, store0]) == -1    # rounding to a non-float dtype
+    assert run([load0, store0], bcast=(I * 1)(9)) == -1  # broadcast kind
+    assert run([]) == -1
+    assert run([load0] * 65) == -1

@@ -79,15 +79,49 @@ def test_symbolic_branch_is_traced():
 def test_unsupported_program_rejected():
 
     @T.prim_func
-    def sig(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+    def mix(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 1), "float32")):
+        with T.Kernel(1, is_cpu=True) as (bx,):
+            a = T.alloc_shared((64, 64), "float32")
+            m = T.alloc_shared((64, 1), "float32")
+            T.ppl_copy(A[0, 0], a)
+            T.ppl_exp2(a)  # an exponential feeding a row max: no kernel family
+            T.ppl_reduce_max(a, m, dim=1)
+            T.ppl_copy(m, B[0, 0])
+
+    with pytest.raises(UnsupportedProgram, match="no gfx950 kernel"):
+        tilelang.compile(mix, out_idx=-1)
+
+
+def test_elementwise_programs_are_recognised():
+    """The stand-alone elementwise demos compile into register programs; an rsqrt alone is
+    one too; a tile copy that does not cover its tensor is rejected."""
+    k = tilelang.compile(programs.ppl_mul_rows(8192, 8192, 64), out_idx=[0])
+    a = k.plan.attrs
+    assert k.plan.family == "elementwise" and a["inputs"] == [1, 2] and a["bcast"] == [0, 1]
+    assert (a["rows"], a["cols"]) == (8192, 8192)
+    k = tilelang.compile(programs.ppl_scale_shift(16, 4, 4, 2), out_idx=-1)
+    assert k.plan.attrs["consts"] == [1 / 8192, 1e-12]
+
+    @T.prim_func
+    def rs(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
         with T.Kernel(1, is_cpu=True) as (bx,):
             a = T.alloc_shared((64, 64), "float32")
             T.ppl_copy(A[0, 0], a)
-            T.ppl_rsqrt(a, a)  # an elementwise rsqrt alone is no kernel family
+            T.ppl_rsqrt(a, a)
             T.ppl_copy(a, B[0, 0])
 
-    with pytest.raises(UnsupportedProgram, match="no gfx950 kernel"):
-        tilelang.compile(sig, out_idx=-1)
+    assert tilelang.compile(rs, out_idx=-1).plan.family == "elementwise"
+
+    @T.prim_func
+    def part(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+        with T.Kernel(1, is_cpu=True) as (bx,):
+            a = T.alloc_shared((32, 64), "float32")  # one 32-row tile of a 64-row tensor
+            T.ppl_copy(A[0, 0], a)
+            T.ppl_rsqrt(a, a)
+            T.ppl_copy(a, B[0, 0])
+
+    with pytest.raises(UnsupportedProgram, match="grid"):
+        tilelang.compile(part, out_idx=-1)
 
 
 def test_unsupported_variants_have_clear_errors():
@@ -95,9 +129,23 @@ def test_unsupported_variants_have_clear_errors():
     with pytest.raises(UnsupportedProgram, match="tiles"):
         tilelang.compile(programs.matmul(64, 64, 64, 32, 32, 32, dtype="float32",
                                          out_dtype="float32"), out_idx=-1)
-    with pytest.raises(UnsupportedProgram, match="tiles"):
-        tilelang.compile(programs.flashattn(1, 2, 4, 8, False, 2, 2, dtype="float32"),
+    # fp32 attention tiles are the all-fp32 program tpu_demo/ppl/flashattn/fa_fp32.py
+    k = tilelang.compile(programs.flashattn(1, 2, 4, 8, False, 2, 2, dtype="float32"),
                          out_idx=-1)
+    assert k.plan.attrs["dtype"] == "float32" and k.plan.attrs["operand_dtype"] is None
+    # fp32 attention tiles with a 16-bit output are not a program of the reference
+    with pytest.raises(UnsupportedProgram):
+        tilelang.compile(_fa_fp32_tiles_bf16_out(), out_idx=-1)
+
+
+def _fa_fp32_tiles_bf16_out():
+    import copy
+    from tilelang.language import ir
+    base = programs.flashattn(1, 2, 4, 8, False, 2, 2, dtype="float32")
+    bad = copy.copy(base)
+    o = base.params[3]
+    bad.params = list(base.params[:3]) + [ir.Buffer(o.name, o.shape, "bfloat16", "global")]
+    return bad
 
 
 @pytest.mark.parametrize("name,prog,attrs", [
@@ -324,3 +372,21 @@ def test_flashattn_with_extra_parameter_is_rejected():
                                                       "global")] + list(base.params[3:])
     with pytest.raises(UnsupportedProgram, match="Extra"):
         recognize(extra)
+
+
+def test_nonpaged_mla_programs_are_recognised():
+    """example_mla_decode.py (split / no-split) and the TPU program mla_decode.py (ppl ops,
+    natural exp, [batch, heads, 1, dim]) map to the MLA family in non-paged mode, with the
+    program's own softmax scale; a 3-gemm program without int32 parameters is no longer sent to
+    the SwiGLU matcher."""
+    k = tilelang.compile(programs.mla_decode_nopage(2, 128, 512, 512, 64, num_split=4),
+                         out_idx=[6])
+    a = k.plan.attrs
+    assert k.plan.family == "mla" and not a["paged"] and a["seqlen_kv"] == 512
+    assert a["num_split"] == 4 and (a["glse"], a["o_partial"], a["o"]) == (4, 5, 6)
+    assert math.isclose(a["sm_scale"], 1 / math.sqrt(576), rel_tol=1e-9)
+    t = tilelang.compile(programs.mla_decode_tpu(4, 8, 512, 32, 4, 4, 4), out_idx=-1)
+    a = t.plan.attrs
+    assert t.plan.family == "mla" and not a["paged"] and (a["dv"], a["dpe"], a["Hq"]) == (32, 4, 8)
+    assert math.isclose(a["sm_scale"], 1 / 6, rel_tol=1e-12)
+    assert t.plan.out_idx == [4]

@@ -168,3 +168,21 @@ def test_flashattn_fp32_output(D, causal):
     torch_assert_close(o, exp, atol=2e-3, rtol=2e-3)
     # the output is not rounded to fp16: it differs from its own fp16 rounding
     assert not torch.equal(o, o.half().float())
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [(1, 2, 4, 8, False), (1, 2, 4, 8, True),
+                                            (2, 3, 300, 64, True), (1, 2, 257, 128, False),
+                                            (2, 2, 65, 20, False)])
+def test_flashattn_all_fp32_program(B, H, S, D, causal):
+    """tpu_demo/ppl/flashattn/fa_fp32.py: fp32 Q, K, V, score and P tiles multiplied by ppl_gemm
+    in fp32 (no 16-bit rounding anywhere), fp32 output; its own shape is flashattn(1, 2, 4, 8,
+    False) with block 2 x 2. TPU convention (CPU tensors, all params, in place). Tolerance
+    1e-4: fp32 throughout, against the fp32 oracle."""
+    g = _gen(69 + S)
+    q, kk, v = (torch.randn(B, S, H, D, generator=g) for _ in range(3))
+    k = tilelang.compile(programs.flashattn(B, H, S, D, causal, 2, 2, dtype="float32"),
+                         out_idx=-1, target="tpu")
+    assert k.plan.attrs["operand_dtype"] is None and k.plan.attrs["dtype"] == "float32"
+    out = torch.zeros(B, S, H, D, dtype=torch.float32)
+    assert k(q, kk, v, out) == 0
+    torch_assert_close(out, ref.flashattn_ref(q, kk, v, causal), atol=1e-4, rtol=1e-4)

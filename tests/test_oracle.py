@@ -554,3 +554,48 @@ def test_flashattn_rows_ref_equals_full_oracle_rows():
         if causal:
             assert torch.allclose(sub[:, 0], v[:, 0].float().repeat_interleave(2, dim=1),
                                   atol=1e-6)
+
+
+def test_mla_nopage_ref_is_the_paged_oracle_on_an_identity_table():
+    """Non-paged MLA (example_mla_decode.py ref_program) equals the paged oracle when the cache
+    is laid out sequence by sequence (one page of S tokens per sequence, table row b = [b]),
+    for the upstream [B, H, d] and the TPU demo's [B, H, 1, d] query layouts; a one-token cache
+    returns its latent row."""
+    g = torch.Generator().manual_seed(11)
+    B, H, S, dv, dpe = 3, 8, 40, 32, 4
+    q = torch.randn(B, H, dv, generator=g).half()
+    qpe = torch.randn(B, H, dpe, generator=g).half()
+    kv = torch.randn(B, S, 1, dv, generator=g).half()
+    kpe = torch.randn(B, S, 1, dpe, generator=g).half()
+    got = ref.mla_decode_nopage_ref(q, qpe, kv, kpe).float()
+    bt = torch.arange(B, dtype=torch.int32).view(B, 1)
+    sl = torch.full((B,), S, dtype=torch.int32)
+    exp = ref.mla_decode_ref(q, qpe, kv.reshape(B * S, dv), kpe.reshape(B * S, dpe), bt, sl, S,
+                             1 / math.sqrt(dv + dpe), out_dtype=torch.float32)
+    assert torch.allclose(got, exp, atol=2e-3, rtol=2e-3)
+    got4 = ref.mla_decode_nopage_ref(q.unsqueeze(2), qpe.unsqueeze(2), kv, kpe)
+    assert got4.shape == (B, H, 1, dv)
+    assert torch.equal(got4.squeeze(2), ref.mla_decode_nopage_ref(q, qpe, kv, kpe))
+    one = ref.mla_decode_nopage_ref(q, qpe, kv[:, :1], kpe[:, :1]).float()
+    assert torch.allclose(one, kv[:, 0].float().expand(B, H, dv), atol=1e-3)
+
+
+def test_elementwise_program_refs_against_float64_numpy():
+    """exp / row-broadcast product / scale-shift / add oracles against float64 numpy (and the
+    closed forms e^0 = 1, e^1 = e), with fp32 rounding as the only difference."""
+    g = torch.Generator().manual_seed(12)
+    a = torch.randn(7, 5, generator=g)
+    b = torch.randn(7, 1, generator=g)
+    c = torch.randn(7, 5, generator=g)
+    an, bn, cn = (x.double().numpy() for x in (a, b, c))
+    assert np.allclose(ref.ppl_exp_ref(a).numpy(), np.exp(an), rtol=2e-7)
+    assert float(ref.ppl_exp_ref(torch.tensor([0.0]))) == 1.0
+    assert abs(float(ref.ppl_exp_ref(torch.tensor([1.0]))) - math.e) < 3e-7
+    assert np.allclose(ref.ppl_mul_rows_ref(a, b).numpy(), an * bn, rtol=2e-7)
+    assert np.allclose(ref.ppl_scale_shift_ref(a, 1 / 8192, 1e-12).numpy(), an / 8192 + 1e-12,
+                       rtol=2e-7, atol=1e-18)
+    assert np.allclose(ref.ppl_add_ref(a, c).numpy(), an + cn, rtol=2e-7)
+    # bf16 tiles: the product is rounded before the shift is added
+    ab = a.to(torch.bfloat16)
+    t = (ab.double() / 8192).to(torch.bfloat16).double() + 1e-12
+    assert torch.equal(ref.ppl_scale_shift_ref(ab, 1 / 8192, 1e-12), t.to(torch.bfloat16))

@@ -947,6 +947,93 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
   }
 }
 
+// All-fp32 attention (tpu_demo/ppl/flashattn/fa_fp32.py: fp32 Q, K, V, fp32 score and P tiles,
+// fp32 output): the generic per-query kernel with fp32 operands and no rounding of P. One query
+// per lane, q and O in VGPRs (DC chunks of 4 floats), keys read with wave-uniform addresses.
+template <bool CAUSAL, int DC>  // DC = capacity in 4-element chunks
+__global__ __launch_bounds__(256) void fa_fwd_generic_f32(const float* __restrict__ Q,
+                                                          const float* __restrict__ K,
+                                                          const float* __restrict__ V,
+                                                          float* __restrict__ O, int H, int Hkv,
+                                                          int D, float sc, SeqMap sm) {
+  const int bh = blockIdx.y, b = bh / H, h = bh % H;
+  const SeqRange sr = seq_range(sm, b);
+  const int S = sr.nq, Sk = sr.nk, coff = Sk - S;
+  if ((int)blockIdx.x * 256 >= S) return;
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  const int nc = D / 4;
+  const int64_t rs = sm.tq, rs_kv = sm.tk;
+  const int64_t head = sr.q0 * H * D + h * sm.hq;
+  const int64_t head_kv = sr.k0 * Hkv * D + (h / (H / Hkv)) * sm.hk;
+  f32x4 qv[DC], o[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    qv[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    o[c] = qv[c];
+    if (c < nc && q < S) qv[c] = *(const f32x4*)(Q + head + (int64_t)q * rs + 4 * c);
+  }
+  float m = -INFINITY, l = 0.f;
+  const int wq_last = min(S - 1, (int)(blockIdx.x * 256 + (threadIdx.x & ~63) + 63));
+  const int kend = CAUSAL ? max(0, min(Sk, wq_last + coff + 1)) : Sk;
+  for (int j = 0; j < kend; ++j) {
+    const float* kr = K + head_kv + (int64_t)j * rs_kv;
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c < nc) {
+        const f32x4 kc = *(const f32x4*)(kr + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s = fmaf(qv[c][e], kc[e], s);
+      }
+    }
+    s *= sc;
+    if (CAUSAL && j > q + coff) s = -INFINITY;
+    const float m_new = fmaxf(m, s);
+    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+    const float p = m_new == -INFINITY ? 0.f : fast_exp2(s - m_new);
+    l = fmaf(l, alpha, p);
+    m = m_new;
+    const float* vr = V + head_kv + (int64_t)j * rs_kv;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c < nc) {
+        const f32x4 vc = *(const f32x4*)(vr + 4 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[c][e] = fmaf(o[c][e], alpha, p * vc[e]);
+      }
+    }
+  }
+  if (q >= S) return;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int c = 0; c < DC; ++c)
+    if (c < nc) *(f32x4*)(O + head + (int64_t)q * rs + 4 * c) = o[c] * inv;
+}
+
+template <bool CAUSAL>
+int launch_generic_f32(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
+                       int Hkv, int D, float sc, const SeqMap& sm, hipStream_t st) {
+  if ((int64_t)B * H > 65535) {
+    tlm_set_error("tlm_flash_attn_fwd: fp32 attention needs batch * heads <= 65535");
+    return TLM_EUNSUPPORTED;
+  }
+  const dim3 grid((unsigned)((S + 255) / 256), (unsigned)(B * H));
+  auto go = [&](auto kern) {
+    kern<<<grid, 256, 0, st>>>((const float*)q, (const float*)k, (const float*)v, (float*)o, H,
+                               Hkv, D, sc, sm);
+  };
+  if (D <= 16)
+    go(fa_fwd_generic_f32<CAUSAL, 4>);
+  else if (D <= 64)
+    go(fa_fwd_generic_f32<CAUSAL, 16>);
+  else if (D <= 128)
+    go(fa_fwd_generic_f32<CAUSAL, 32>);
+  else
+    go(fa_fwd_generic_f32<CAUSAL, 64>);
+  TLM_LAUNCH_CHECK("tlm_flash_attn_fwd (fp32)");
+  return TLM_OK;
+}
+
 template <bool BF16, bool CAUSAL, bool OUT32>
 int launch_generic(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
                    int Hkv, int D, float sc, const SeqMap& sm, hipStream_t st) {
@@ -1002,13 +1089,13 @@ int check_common(const char* fn, const void* q, const void* k, const void* v, co
                   (long long)H, (long long)H_kv);
     return TLM_EINVAL;
   }
-  if (D <= 0 || D > 256 || D % 8 != 0) {
-    tlm_set_error("%s: head dim %lld unsupported (a multiple of 8, at most 256)", fn,
-                  (long long)D);
+  if (D <= 0 || D > 256 || D % (in_dtype == TLM_F32 ? 4 : 8) != 0) {
+    tlm_set_error("%s: head dim %lld unsupported (a multiple of 8, or of 4 for fp32, at most "
+                  "256)", fn, (long long)D);
     return TLM_EUNSUPPORTED;
   }
-  if (in_dtype != TLM_BF16 && in_dtype != TLM_F16) {
-    tlm_set_error("%s: dtype %d unsupported (BF16 or F16)", fn, in_dtype);
+  if (in_dtype != TLM_BF16 && in_dtype != TLM_F16 && in_dtype != TLM_F32) {
+    tlm_set_error("%s: dtype %d unsupported (BF16, F16 or F32)", fn, in_dtype);
     return TLM_EUNSUPPORTED;
   }
   if (out_dtype != in_dtype && out_dtype != TLM_F32) {
@@ -1030,6 +1117,9 @@ int dispatch(const void* q, const void* k, const void* v, void* o, int B, int S,
              int D, bool causal, float sm_scale, int in_dtype, int out_dtype, const SeqMap& sm,
              hipStream_t st) {
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  if (in_dtype == TLM_F32)
+    return causal ? launch_generic_f32<true>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st)
+                  : launch_generic_f32<false>(q, k, v, o, B, S, H, Hkv, D, sc, sm, st);
   const bool bf = in_dtype == TLM_BF16, f32o = out_dtype == TLM_F32;
   if (bf)
     return f32o ? by_shape<true, true>(q, k, v, o, B, S, H, Hkv, D, causal, sc, sm, st)

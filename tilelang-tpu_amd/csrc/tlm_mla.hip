@@ -318,6 +318,115 @@ __global__ __launch_bounds__(256) void paged_gather_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Generic decode for the shapes the matrix-core kernels do not take (head dims other than 512 +
+// 64, head counts that are not a multiple of 64; e.g. the TPU demo's dim 32 + rope 4 over 8
+// heads). Workgroup = one (sequence, head); 256 keys at a time: one thread per key for the
+// score (dot product over dv + dpe), the online softmax in the exp2 domain with the workgroup's
+// chunk maximum, P rounded to Q's dtype as the programs' P tiles are, then O accumulated with
+// the threads spread over the dims. Correctness path for small shapes, not tuned.
+constexpr int MLA_GEN_DV = 1024, MLA_GEN_DQK = MLA_GEN_DV + 256;
+
+template <bool BF16, int KV_KIND, bool O_BF16>
+__global__ __launch_bounds__(256) void mla_generic_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ q_pe, int64_t qs, int64_t qpes,
+    const uint8_t* __restrict__ kv, const uint8_t* __restrict__ k_pe, int64_t kvs_b,
+    int64_t kpes_b, int64_t kv_rows, const int32_t* __restrict__ bt,
+    const int32_t* __restrict__ sl, uint16_t* __restrict__ out, int Hq, int dv, int dpe,
+    int page, int max_pages, float sc, const float* kv_scale) {
+  __shared__ float qf[MLA_GEN_DQK];
+  __shared__ float pt[256];
+  __shared__ int64_t rt[256];
+  __shared__ float red[256];
+  using HQ = h16<BF16>;
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  const int b = (int)(bh / Hq);
+  const int dqk = dv + dpe;
+  for (int d = tid; d < dqk; d += 256)
+    qf[d] = HQ::to_f32(d < dv ? q[bh * qs + d] : q_pe[bh * qpes + (d - dv)]);
+  const float kvs = (KV_KIND == 0 && kv_scale) ? kv_scale[0] : 1.0f;
+  auto kv_val = [&](const uint8_t* row, int d) {
+    if constexpr (KV_KIND == 0) {
+      return __builtin_amdgcn_cvt_f32_fp8((int)row[d], 0);
+    } else {
+      return HQ::to_f32(((const uint16_t*)row)[d]);
+    }
+  };
+  const int64_t lmax = (int64_t)max_pages * page;
+  const int L = (int)max((int64_t)0, min((int64_t)sl[b], lmax));
+  float m = -INFINITY, l = 0.f;
+  float o[MLA_GEN_DV / 256] = {};
+  auto block_reduce = [&](float v, bool is_max) {
+    red[tid] = v;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+      if (tid < off) red[tid] = is_max ? fmaxf(red[tid], red[tid + off]) : red[tid] + red[tid + off];
+      __syncthreads();
+    }
+    const float r = red[0];
+    __syncthreads();
+    return r;
+  };
+  __syncthreads();
+  for (int c0 = 0; c0 < L; c0 += 256) {
+    const int t = c0 + tid;
+    float s = -INFINITY;
+    int64_t row = -1;
+    if (t < L) {
+      row = (int64_t)bt[(int64_t)b * max_pages + t / page] * page + t % page;
+      float acc = 0.f;
+      if (row >= 0 && row < kv_rows) {  // rows outside the pool read as zeros
+        const uint8_t* kr = kv + row * kvs_b;
+        const uint8_t* pr = k_pe + row * kpes_b;
+        for (int d = 0; d < dv; ++d) acc = fmaf(qf[d], kv_val(kr, d), acc);
+        for (int d = 0; d < dpe; ++d) acc = fmaf(qf[dv + d], kv_val(pr, d), acc);
+      } else {
+        row = -1;
+      }
+      s = acc * kvs * sc;
+    }
+    const float m_new = fmaxf(m, block_reduce(s, true));
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    const float p = t < L ? HQ::to_f32(HQ::from_f32(__builtin_amdgcn_exp2f(s - m_new))) : 0.f;
+    pt[tid] = p;
+    rt[tid] = row;
+    l = l * alpha + block_reduce(p, false);
+    m = m_new;
+    const int n = min(256, L - c0);
+#pragma unroll
+    for (int k = 0; k < MLA_GEN_DV / 256; ++k) {
+      const int d = tid + 256 * k;
+      if (d >= dv) break;
+      float acc = o[k] * alpha;
+      for (int j = 0; j < n; ++j)
+        if (rt[j] >= 0) acc = fmaf(pt[j], kv_val(kv + rt[j] * kvs_b, d), acc);
+      o[k] = acc;
+    }
+    __syncthreads();
+  }
+  using HO = h16<O_BF16>;
+  const float w = l > 0.f ? kvs / l : 0.f;
+#pragma unroll
+  for (int k = 0; k < MLA_GEN_DV / 256; ++k) {
+    const int d = tid + 256 * k;
+    if (d < dv) out[bh * dv + d] = (uint16_t)HO::from_f32(o[k] * w);
+  }
+}
+
+template <bool BF16, int KV_KIND, bool O_BF16>
+int launch_generic(const void* q, const void* q_pe, int64_t qs, int64_t qpes, const void* kv,
+                   const void* k_pe, int64_t kvs_b, int64_t kpes_b, int64_t kv_rows,
+                   const int32_t* bt, const int32_t* sl, void* o, int B, int Hq, int dv, int dpe,
+                   int page, int max_pages, float sc, const float* kv_scale, hipStream_t st) {
+  mla_generic_kernel<BF16, KV_KIND, O_BF16><<<(unsigned)((int64_t)B * Hq), 256, 0, st>>>(
+      (const uint16_t*)q, (const uint16_t*)q_pe, qs, qpes, (const uint8_t*)kv,
+      (const uint8_t*)k_pe, kvs_b, kpes_b, kv_rows, bt, sl, (uint16_t*)o, Hq, dv, dpe, page,
+      max_pages, sc, kv_scale);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (generic)");
+  return TLM_OK;
+}
+
 template <bool BF16, int KV_KIND>
 int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, const void* kv,
                  const void* k_pe, int64_t kvs_b, int64_t kpes_b, int64_t kv_rows, const int32_t* bt,
@@ -359,6 +468,19 @@ extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int
                   tlm_mla_fp8_workspace_bytes(B, Hq, num_split));
 }
 
+// The matrix-core kernels take dv = 512, dpe = 64, Hq a multiple of 64 and 16-byte aligned Q / KV
+// rows; every other valid request runs the generic kernel.
+static bool mla_fast_shape(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                           const void* kv, const void* k_pe, int64_t kv_stride,
+                           int64_t kpe_stride, const void* o, int64_t Hq, int64_t dv, int64_t dpe,
+                           int kv_dtype) {
+  const int64_t kv_elt = kv_dtype == TLM_F8E4M3 ? 1 : 2;
+  return dv == MLA_DV && dpe == MLA_DPE && Hq % MLA_HEADS == 0 && tlm_aligned(q, 16) &&
+         tlm_aligned(q_pe, 16) && tlm_aligned(kv, 16) && tlm_aligned(k_pe, 16) &&
+         q_stride % 8 == 0 && q_pe_stride % 8 == 0 && (kv_stride * kv_elt) % 16 == 0 &&
+         (kpe_stride * kv_elt) % 16 == 0 && tlm_aligned(o, 8);
+}
+
 // Argument checks shared by tlm_mla_decode and tlm_mla_decode_noalloc (no HIP call).
 static int mla_validate(const char* fn, const void* q, const void* q_pe, int64_t q_stride,
                         int64_t q_pe_stride, const void* kv, const void* k_pe, int64_t kv_stride,
@@ -380,10 +502,10 @@ static int mla_validate(const char* fn, const void* q, const void* q_pe, int64_t
     tlm_set_error("%s: max_pages * page exceeds the int32 token range", fn);
     return TLM_EINVAL;
   }
-  if (dv != MLA_DV || dpe != MLA_DPE || Hq % MLA_HEADS != 0 || Hq > 4096) {
-    tlm_set_error("%s: kernels exist for dv=512, dpe=64, Hq a multiple of 64 "
-                  "(got dv=%lld dpe=%lld Hq=%lld)", fn, (long long)dv, (long long)dpe,
-                  (long long)Hq);
+  if (dv < 1 || dv > MLA_GEN_DV || dpe < 0 || dpe > MLA_GEN_DQK - MLA_GEN_DV || Hq > 4096) {
+    tlm_set_error("%s: head dims dv in [1, %d], dpe in [0, %d] and at most 4096 heads "
+                  "(got dv=%lld dpe=%lld Hq=%lld)", fn, MLA_GEN_DV, MLA_GEN_DQK - MLA_GEN_DV,
+                  (long long)dv, (long long)dpe, (long long)Hq);
     return TLM_EUNSUPPORTED;
   }
   if (q_stride < dv || q_pe_stride < dpe || kv_stride < dv || kpe_stride < dpe || kv_rows < 0) {
@@ -396,13 +518,11 @@ static int mla_validate(const char* fn, const void* q, const void* q_pe, int64_t
                   "fp8 e4m3 or Q's dtype)", fn, q_dtype, kv_dtype, o_dtype);
     return TLM_EUNSUPPORTED;
   }
-  const int64_t kv_elt = kv_dtype == TLM_F8E4M3 ? 1 : 2;
-  // every 16-byte chunk of Q and KV rows must be aligned
-  if (!tlm_aligned(q, 16) || !tlm_aligned(q_pe, 16) || !tlm_aligned(kv, 16) ||
-      !tlm_aligned(k_pe, 16) || q_stride % 8 || q_pe_stride % 8 || (kv_stride * kv_elt) % 16 ||
-      (kpe_stride * kv_elt) % 16 || !tlm_aligned(o, 8)) {
-    tlm_set_error("%s: Q/KV rows must start on 16-byte boundaries", fn);
-    return TLM_EUNSUPPORTED;
+  const size_t kv_elt = kv_dtype == TLM_F8E4M3 ? 1 : 2;
+  if (!tlm_aligned(q, 2) || !tlm_aligned(q_pe, 2) || !tlm_aligned(kv, kv_elt) ||
+      !tlm_aligned(k_pe, kv_elt) || !tlm_aligned(o, 2)) {
+    tlm_set_error("%s: misaligned Q/KV/O pointer", fn);
+    return TLM_EINVAL;
   }
   if (B > 0 && kv_rows < 1) {
     tlm_set_error("%s: empty KV pool", fn);
@@ -417,11 +537,29 @@ static int mla_run(const char* fn, const void* q, const void* q_pe, int64_t q_st
                    int64_t q_pe_stride, const void* kv, const void* k_pe, int64_t kv_stride,
                    int64_t kpe_stride, int64_t kv_rows, const int32_t* block_table,
                    const int32_t* seqlens, void* o, void* ws, size_t ws_bytes, int64_t B,
-                   int64_t Hq, int64_t dv, int64_t page, int64_t max_pages, int num_split,
-                   float sm_scale, const float* kv_scale, int q_dtype, int kv_dtype, int o_dtype,
-                   void* stream) {
+                   int64_t Hq, int64_t dv, int64_t dpe, int64_t page, int64_t max_pages,
+                   int num_split, float sm_scale, const float* kv_scale, int q_dtype,
+                   int kv_dtype, int o_dtype, void* stream) {
   if (B == 0) return TLM_OK;
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  if (!mla_fast_shape(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, o, Hq,
+                      dv, dpe, kv_dtype)) {
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t kb = kv_dtype == TLM_F8E4M3 ? 1 : 2;
+    const int b = (int)B, h = (int)Hq, pg = (int)page, mp = (int)max_pages;
+    const int v = (int)dv, pe = (int)dpe;
+    const bool bq = q_dtype == TLM_BF16, bo = o_dtype == TLM_BF16;
+#define TLM_MLA_GEN(BQ, KK, BO)                                                                    \
+  launch_generic<BQ, KK, BO>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride * kb,            \
+                             kpe_stride * kb, kv_rows, block_table, seqlens, o, b, h, v, pe, pg,  \
+                             mp, sc, kv_scale, st)
+    if (kv_dtype == TLM_F8E4M3)
+      return bq ? (bo ? TLM_MLA_GEN(true, 0, true) : TLM_MLA_GEN(true, 0, false))
+                : (bo ? TLM_MLA_GEN(false, 0, true) : TLM_MLA_GEN(false, 0, false));
+    return bq ? (bo ? TLM_MLA_GEN(true, 1, true) : TLM_MLA_GEN(true, 1, false))
+              : (bo ? TLM_MLA_GEN(false, 1, true) : TLM_MLA_GEN(false, 1, false));
+#undef TLM_MLA_GEN
+  }
   if (kv_dtype == TLM_F8E4M3) {
     const size_t need = tlm_mla_fp8_workspace_bytes(B, Hq, num_split);
     if (need > 0 && need <= ws_bytes) {
@@ -495,7 +633,7 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
     return TLM_EUNSUPPORTED;
   }
   return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
-                 block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, page, max_pages, num_split,
+                 block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, dpe, page, max_pages, num_split,
                  sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype, stream);
 }
 
@@ -546,10 +684,13 @@ extern "C" int tlm_mla_decode_noalloc(const void* q, const void* q_pe, int64_t q
                         num_split, q_dtype, kv_dtype, o_dtype);
   if (rc) return rc;
   // the path taken must fit the scratch (checked before any HIP call)
-  const bool fp8 = kv_dtype == TLM_F8E4M3 &&
+  const bool fast = mla_fast_shape(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                   kpe_stride, o, Hq, dv, dpe, kv_dtype);
+  const bool fp8 = fast && kv_dtype == TLM_F8E4M3 &&
                    tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride);
-  const size_t need = fp8 ? tlm_mla_fp8_workspace_bytes(B, Hq, num_split)
-                          : mla_split_workspace_bytes(B, Hq, dv, num_split);
+  const size_t need = !fast ? 0
+                      : fp8 ? tlm_mla_fp8_workspace_bytes(B, Hq, num_split)
+                            : mla_split_workspace_bytes(B, Hq, dv, num_split);
   if (need > TLM_MLA_SCRATCH_BYTES) {
     tlm_set_error("%s: this call needs %zu bytes of scratch, more than the library's %zu "
                   "(lower num_split or the batch, or use tlm_mla_decode with a workspace)", fn,
@@ -564,7 +705,7 @@ extern "C" int tlm_mla_decode_noalloc(const void* q, const void* q_pe, int64_t q
   if (rc) return rc;
   return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
                  block_table, seqlens, o, g_scratch_ptr[dev], TLM_MLA_SCRATCH_BYTES, B, Hq, dv,
-                 page, max_pages, num_split, sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype,
+                 dpe, page, max_pages, num_split, sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype,
                  stream);
 }
 

@@ -62,9 +62,27 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
             workspace_cache[dev] = ws
         kvs = None if a["kv_scale"] is None else t[a["kv_scale"]]
-        ops.mla_decode(q, t[a["q_pe"]], t[a["kv"]], t[a["k_pe"]], t[a["block_table"]],
-                       t[a["seqlens"]], t[a["o"]], ws, a["page"], a["num_split"], a["sm_scale"],
-                       kvs)
+        B, Hq, dv, dpe = a["B"], a["Hq"], a["dv"], a["dpe"]
+        if a["paged"]:
+            bt, sl = t[a["block_table"]], t[a["seqlens"]]
+            qq, qpe, o = q, t[a["q_pe"]], t[a["o"]]
+        else:
+            # non-paged cache [B, S, 1, d]: token t of sequence b is row b * S + t, i.e. one page
+            # of S tokens per sequence under the identity table (kept per device and shape)
+            key = (dev, "identity", B, a["seqlen_kv"])
+            if key not in workspace_cache:
+                workspace_cache[key] = (
+                    torch.arange(B, dtype=torch.int32, device=dev).view(B, 1),
+                    torch.full((B,), a["seqlen_kv"], dtype=torch.int32, device=dev))
+            bt, sl = workspace_cache[key]
+            qq = q.view(B, Hq, dv)
+            qpe = t[a["q_pe"]].view(B, Hq, dpe)
+            o = t[a["o"]].view(B, Hq, dv)
+        ops.mla_decode(qq, qpe, t[a["kv"]], t[a["k_pe"]], bt, sl, o, ws, a["page"],
+                       a["num_split"], a["sm_scale"], kvs)
+    elif f == "elementwise":
+        ops.elementwise([t[i] for i in a["inputs"]], a["bcast"], [t[i] for i in a["outputs"]],
+                        a["code"], a["consts"], a["rows"], a["cols"])
     else:  # pragma: no cover - recognizer only emits the families above
         raise RuntimeError(f"no runner for family {f}")
 

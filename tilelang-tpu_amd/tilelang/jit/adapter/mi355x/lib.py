@@ -60,12 +60,22 @@ _SIGNATURES = {
     "tlm_mla_scratch_bytes": ([], c_size_t),
     "tlm_paged_gather": ([c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int64, c_int64, c_int64, c_void_p], c_int),
+    "tlm_elementwise": ([ctypes.POINTER(c_void_p), ctypes.POINTER(c_int),
+                         ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_void_p),
+                         ctypes.POINTER(c_int), c_int, ctypes.POINTER(ctypes.c_int32), c_int,
+                         ctypes.POINTER(c_float), c_int, c_int64, c_int64, c_void_p], c_int),
     "tlm_kv_append_fp8": ([c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                            c_int64, c_int64, c_void_p] + [c_int64] * 5 + [c_void_p, c_void_p],
                           c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)
+
+# enum tlm_ew_op / tlm_ew_bcast (include/tlmi355x.h)
+EW_LOAD, EW_CONST, EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_EXP, EW_RSQRT, EW_SIGMOID, EW_ROUND, \
+    EW_STORE = range(11)
+EW_FULL, EW_ROW, EW_COL, EW_SCALAR = range(4)
+EW_SLOTS, EW_MAX_IN, EW_MAX_OUT, EW_MAX_CODE, EW_MAX_CONST = 8, 8, 4, 64, 16
 
 
 def library_path() -> str:

@@ -396,3 +396,36 @@ def kv_append_fp8(x: torch.Tensor, start: torch.Tensor, count: torch.Tensor,
              _ptr(start), _ptr(count), _ptr(block_table), block_table.shape[1], page, _ptr(kv),
              kv.stride(0), kv.shape[0], B, T, D, _ptr(scale), _stream(dev))
     return kv
+
+
+def elementwise(inputs, bcast, outputs, code, consts, rows: int, cols: int):
+    """Run an elementwise register program (include/tlmi355x.h: tlm_elementwise) over the
+    [rows, cols] output domain. inputs: tensors (F32 / F16 / BF16) with their broadcast kinds
+    (lib.EW_FULL, EW_ROW for an [rows, 1] tensor, EW_COL, EW_SCALAR); outputs: tensors of
+    rows * cols elements; code: instruction words; consts: fp32 constants."""
+    import ctypes
+    dev = _dev(*inputs, *outputs)
+    for t in list(inputs) + list(outputs):
+        _contig("operand", t)
+    for t in outputs:
+        if t.numel() != rows * cols:
+            raise ValueError(f"output of {t.numel()} elements for a {rows} x {cols} domain")
+    if len(bcast) != len(inputs):
+        raise ValueError("one broadcast kind per input")
+    need = {lib.EW_FULL: rows * cols, lib.EW_ROW: rows, lib.EW_COL: cols, lib.EW_SCALAR: 1}
+    for t, bc in zip(inputs, bcast):
+        if bc not in need or t.numel() < need[bc]:
+            raise ValueError(f"input of {t.numel()} elements for broadcast kind {bc} over a "
+                             f"{rows} x {cols} domain")
+    n_in, n_out = len(inputs), len(outputs)
+    P, I = ctypes.c_void_p, ctypes.c_int
+    in_p = (P * max(1, n_in))(*[t.data_ptr() for t in inputs])
+    in_dt = (I * max(1, n_in))(*[dtype_code(t.dtype) for t in inputs])
+    in_bc = (I * max(1, n_in))(*bcast)
+    out_p = (P * n_out)(*[t.data_ptr() for t in outputs])
+    out_dt = (I * n_out)(*[dtype_code(t.dtype) for t in outputs])
+    cw = (ctypes.c_int32 * len(code))(*[(c if c < 2 ** 31 else c - 2 ** 32) for c in code])
+    cf = (ctypes.c_float * max(1, len(consts)))(*consts)
+    lib.call("tlm_elementwise", in_p, in_dt, in_bc, n_in, out_p, out_dt, n_out, cw, len(code),
+             cf, len(consts), int(rows), int(cols), _stream(dev))
+    return outputs

@@ -17,16 +17,21 @@ Families and the reference programs they accept:
   rope     tpu_demo/tpu_test_rope_bf16.py:5-51 (4 params; fp16 / fp32 twins and tpu_test_rope.py)
            and a fused q+k form (6 params)
   swiglu   tpu_demo/tpu_test_swiglu_bf16.py:5-54 (+ tpu_test_swiglu_fp32.py)
-  flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, and fp32 with fp16
-           matrix tiles) and the upstream examples/flash_attention/example_mha_fwd_bshd.py:30-151
-           structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178), and the
+  flashattn tpu_demo/flashattn/tpu_test_flashattn_bf16.py:14-135 (+ fp16, fp32 with fp16
+           matrix tiles, and the all-fp32 tpu_demo/ppl/flashattn/fa_fp32.py) and the upstream
+           examples/flash_attention/example_mha_fwd_bshd.py:30-151 structure, with grouped K/V heads (example_gqa_fwd_bshd.py:62-178), and the
            non-causal variable-length program example_mha_fwd_varlen.py:222-358
   sigmoid  tpu_demo/tpu_test_sigmoid_fp32.py:6-31 (ppl_sigmoid)
   gather   tpu_demo/tpu_test_gather_fp32.py:8-18 (ppl_gather)
   topk     tpu_demo/tpu_test_topk_fp32.py:6-18 (ppl_topk)
   row_reduce tpu_demo/tpu_test_reduce_max.py, tpu_test_reduce_sum.py
+  elementwise tpu_demo/ppl/test/{exp,mul_N_1,elementwise_c}.py and tpu_demo/ppl/
+           elementwise_add_kernel/elementwise_add.py: any chain of elementwise ppl ops between
+           tile copies, evaluated into a register program
   mla      examples/deepseek_mla/example_mla_decode_paged.py:10-256 (split and no-split forms),
-           with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV
+           with fp16/bf16 or fp8-e4m3 (+ fp32 scale parameter) KV; the non-paged
+           examples/deepseek_mla/example_mla_decode.py:10-227 and the TPU program
+           tpu_demo/ppl/deepseek_mla/mla_decode.py:9-121
 """
 from __future__ import annotations
 
@@ -172,12 +177,16 @@ _ALLOWED_OPS = {
     "flashattn": _COPY + _FILL_OPS + _GEMM + ("store", "ppl_add", "ppl_sub", "ppl_mul",
                                               "ppl_div", "ppl_exp", "ppl_mul_C", "ppl_reduce_max",
                                               "ppl_reduce_sum", "reduce_max", "reduce_sum"),
-    "mla": _COPY + _FILL_OPS + _GEMM + ("store", "reduce_max", "reduce_sum"),
+    "mla": _COPY + _FILL_OPS + _GEMM + ("store", "reduce_max", "reduce_sum", "ppl_add",
+                                        "ppl_sub", "ppl_mul", "ppl_div", "ppl_exp", "ppl_mul_C",
+                                        "ppl_reduce_max", "ppl_reduce_sum"),
     "sigmoid": _COPY + ("ppl_sigmoid",),
     "gather": ("ppl_gather",),
     "topk": ("ppl_topk",),
     "row_reduce": _COPY + _FILL_OPS + ("ppl_reduce_max", "ppl_reduce_sum", "reduce_max",
                                        "reduce_sum"),
+    "elementwise": _COPY + _FILL_OPS + ("ppl_add", "ppl_sub", "ppl_mul", "ppl_div", "ppl_add_C",
+                                        "ppl_mul_C", "ppl_exp", "ppl_rsqrt", "ppl_sigmoid"),
 }
 
 
@@ -192,6 +201,8 @@ def _audit(pf, plan: "Plan", used: Optional[List] = None) -> "Plan":
                    f"elementwise step would be dropped), so the program is not compiled")
     if used is None:
         idx = {plan.attrs[k] for k in _PARAM_ATTRS[fam] if plan.attrs.get(k) is not None}
+        if fam == "elementwise":
+            idx = set(plan.attrs["inputs"]) | set(plan.attrs["outputs"])
         used = [pf.params[i] for i in sorted(idx)]
     unused = [getattr(p, "name", repr(p)) for p in pf.params if all(p is not u for u in used)]
     if unused:
@@ -212,6 +223,7 @@ _PARAM_ATTRS = {
     "gather": ("param", "index", "out"),
     "topk": ("src", "values", "indices"),
     "row_reduce": ("x", "y"),
+    "elementwise": (),
 }
 
 
@@ -443,9 +455,12 @@ def _flashattn(pf, names) -> Plan:
     # tiles the two gemms multiply: the fp32 program copies Q, K, V and P to fp16 tiles first
     tile_dts = {_buf(qk[0].args[0]).dtype, _buf(qk[0].args[1]).dtype, _buf(pv[0].args[0]).dtype,
                 _buf(pv[0].args[1]).dtype}
-    if len(tile_dts) != 1 or next(iter(tile_dts)) not in ("bfloat16", "float16"):
-        _fail(fam, f"the gemm tiles must all be bfloat16 or all float16, got {tile_dts}")
+    if len(tile_dts) != 1 or next(iter(tile_dts)) not in ("bfloat16", "float16", "float32"):
+        _fail(fam, f"the gemm tiles must all be bfloat16, all float16 or all float32, got "
+                   f"{tile_dts}")
     tile_dt = next(iter(tile_dts))
+    if tile_dt == "float32" and not (Q.dtype == K.dtype == V.dtype == O.dtype == "float32"):
+        _fail(fam, "fp32 gemm tiles need fp32 Q, K, V and Output")
     if not (Q.dtype == K.dtype == V.dtype == O.dtype):
         _fail(fam, "Q, K, V and Output must share a dtype")
     if Q.dtype not in (tile_dt, "float32"):
@@ -495,7 +510,7 @@ def _flashattn(pf, names) -> Plan:
         q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=S, H=H,
         H_kv=kshp[2], D=D,
         causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
-        operand_dtype=tile_dt if Q.dtype == "float32" else None))
+        operand_dtype=tile_dt if Q.dtype == "float32" and tile_dt != "float32" else None))
 
 
 def _seq_dim(pf, Q: Buffer) -> Optional[int]:
@@ -606,17 +621,23 @@ def _page_size_from_trace(pf, bt: Buffer) -> Optional[int]:
 
 
 def _mla(pf, names) -> Plan:
+    """Paged (int32 BLOCK_TABLE [b, pages] + CACHE_SEQLENS [b]; example_mla_decode_paged.py) or
+    non-paged (KV [b, seqlen_kv, 1, dv]; example_mla_decode.py and the TPU program
+    tpu_demo/ppl/deepseek_mla/mla_decode.py, whose Q / Output carry a singleton query axis)
+    MLA decode."""
     fam = "mla"
     ints = [p for p in pf.params if p.dtype == "int32"]
     bt = [p for p in ints if len(p.shape) == 2]
     sl = [p for p in ints if len(p.shape) == 1]
-    if len(bt) != 1 or len(sl) != 1:
+    paged = bool(ints)
+    if paged and (len(bt) != 1 or len(sl) != 1 or len(ints) != 2):
         _fail(fam, "expected int32 BLOCK_TABLE [b, pages] and CACHE_SEQLENS [b]")
-    bt, sl = bt[0], sl[0]
-    kernels = {op.kernel for op in _ops(pf, _GEMM)}
+    bt = bt[0] if paged else None
+    sl = sl[0] if paged else None
     g = [op for op in _ops(pf, _GEMM)]
     qk = [op for op in g if op.kwargs.get("transpose_B")]
     pv = [op for op in g if not op.kwargs.get("transpose_B")]
+    kernels = {op.kernel for op in g}
     if len(qk) != 2 or len(pv) != 1 or len(kernels) != 1:
         _fail(fam, "expected Q@KV^T + Q_pe@K_pe^T and P@KV in one kernel")
     Q = _source_param(pf, _buf(qk[0].args[0]))
@@ -626,41 +647,55 @@ def _mla(pf, names) -> Plan:
     V = _source_param(pf, _buf(pv[0].args[1]))
     if None in (Q, KV, Qpe, Kpe) or V is not KV:
         _fail(fam, "could not trace Q, Q_pe, KV, K_pe (V must be the latent KV)")
-    out_params = _written_params(pf)
-    # Output = the [b, hq, dv] parameter written by the last kernel
-    O = None
-    glse = opart = None
-    b, hq, dv = _shape(Q)
+    qshape = _shape(Q)
+    if len(qshape) == 4 and qshape[2] == 1:  # TPU layout [b, hq, 1, d]
+        b, hq, dv = qshape[0], qshape[1], qshape[3]
+    elif len(qshape) == 3:
+        b, hq, dv = qshape
+    else:
+        _fail(fam, f"Q must be [batch, heads, dim] or [batch, heads, 1, dim], got {qshape}")
     dpe = _shape(Qpe)[-1]
-    for p in out_params:
+    O = glse = opart = None
+    for p in _written_params(pf):
         s = _shape(p)
-        if s == (b, hq, dv):
+        if s == qshape:
             O = p
         elif len(s) == 3:
             glse = p
         elif len(s) == 4:
             opart = p
     if O is None:
-        _fail(fam, "no [batch, heads, dv] output")
+        _fail(fam, "no Output parameter of Q's shape")
     for p in pf.params:  # glse / Output_partial may only be read (no-split form)
         s = _shape(p)
         if p in (Q, Qpe, KV, Kpe, bt, sl, O):
             continue
         if len(s) == 3 and glse is None and s[:2] == (b, hq):
             glse = p
-        elif len(s) == 4 and opart is None and s[:2] == (b, hq):
+        elif len(s) == 4 and opart is None and s[:2] == (b, hq) and s != qshape:
             opart = p
     kv_shape = _shape(KV)
-    if len(kv_shape) != 3 or kv_shape[1] != 1 or kv_shape[2] != dv or _shape(Kpe)[-1] != dpe:
-        _fail(fam, "KV must be [rows, 1, dv] and K_pe [rows, 1, dpe] (one latent KV head)")
-    if _shape(Qpe)[:2] != (b, hq) or _shape(sl) != (b,) or _shape(bt)[0] != b:
-        _fail(fam, "batch/head dims disagree")
-    max_pages = _shape(bt)[1]
-    page = _page_size_from_trace(pf, bt)
-    if page is None:
-        page = kv_shape[0] // b // max_pages
+    if paged:
+        if len(kv_shape) != 3 or kv_shape[1] != 1 or kv_shape[2] != dv or \
+                _shape(Kpe)[-1] != dpe:
+            _fail(fam, "KV must be [rows, 1, dv] and K_pe [rows, 1, dpe] (one latent KV head)")
+        if _shape(Qpe)[:2] != (b, hq) or _shape(sl) != (b,) or _shape(bt)[0] != b:
+            _fail(fam, "batch/head dims disagree")
+        max_pages = _shape(bt)[1]
+        page = _page_size_from_trace(pf, bt)
+        if page is None:
+            page = kv_shape[0] // b // max_pages
+        seqlen_kv = None
+    else:
+        if len(kv_shape) != 4 or kv_shape[0] != b or kv_shape[2] != 1 or kv_shape[3] != dv or \
+                _shape(Kpe) != (b, kv_shape[1], 1, dpe) or _shape(Qpe)[:2] != (b, hq):
+            _fail(fam, "non-paged KV must be [batch, seqlen_kv, 1, dv] and K_pe "
+                       "[batch, seqlen_kv, 1, dpe] (one latent KV head)")
+        seqlen_kv = kv_shape[1]
+        page, max_pages = seqlen_kv, 1
     num_split = _shape(glse)[-1] if glse is not None else 1
-    # scale: exp2(acc_s * c - max * c), c = sm_scale * log2(e)
+    # scale: exp2(acc_s * c - max * c) with c = sm_scale * log2(e) (upstream programs), or the
+    # TPU program's ppl_mul_C(scores, scores, sm_scale) before its natural-exp ppl_exp2
     sm_scale = None
     for op in _ops(pf, ("store",)):
         v = op.args[2]
@@ -669,6 +704,11 @@ def _mla(pf, names) -> Plan:
             if cs:
                 sm_scale = cs[0] / LOG2E_REF
                 break
+    if sm_scale is None and "ppl_exp" in names:
+        acc_s = _buf(qk[0].args[2])
+        cands = [op for op in _ops(pf, ("ppl_mul_C",)) if _buf(op.args[0]) is acc_s]
+        if cands:
+            sm_scale = _const(cands[0].args[2])
     if sm_scale is None:
         _fail(fam, "could not read the softmax scale")
     kv_scale = None
@@ -685,11 +725,12 @@ def _mla(pf, names) -> Plan:
         _fail(fam, f"Output dtype {O.dtype}")
     return Plan(fam, pf.params, [_index(pf, O)], dict(
         q=_index(pf, Q), q_pe=_index(pf, Qpe), kv=_index(pf, KV), k_pe=_index(pf, Kpe),
-        block_table=_index(pf, bt), seqlens=_index(pf, sl), o=_index(pf, O),
+        block_table=None if bt is None else _index(pf, bt),
+        seqlens=None if sl is None else _index(pf, sl), o=_index(pf, O),
         glse=None if glse is None else _index(pf, glse),
         o_partial=None if opart is None else _index(pf, opart), kv_scale=kv_scale, B=b, Hq=hq,
         dv=dv, dpe=dpe, page=page, max_pages=max_pages, num_split=num_split, sm_scale=sm_scale,
-        q_dtype=Q.dtype, kv_dtype=KV.dtype, o_dtype=O.dtype))
+        paged=paged, seqlen_kv=seqlen_kv, q_dtype=Q.dtype, kv_dtype=KV.dtype, o_dtype=O.dtype))
 
 
 def _sigmoid(pf, names) -> Plan:
@@ -765,13 +806,227 @@ def _row_reduce(pf, names) -> Plan:
         rows=math.prod(xs[:-1]), cols=xs[-1], in_dtype=x.dtype, out_dtype=y.dtype))
 
 
+# ------------------------------------------------------------------------------------------------
+# elementwise tile programs: symbolic evaluation of the tile ops into a register program
+
+
+_EW_BINARY = {"ppl_add": "add", "ppl_sub": "sub", "ppl_mul": "mul", "ppl_div": "div"}
+_EW_CONSTOP = {"ppl_add_C": "add", "ppl_mul_C": "mul"}
+_EW_OPCODE = {"load": 0, "const": 1, "add": 2, "sub": 3, "mul": 4, "div": 5, "exp": 6, "rsqrt": 7,
+              "sigmoid": 8, "round": 9, "store": 10}
+_EW_DTYPE = {"float32": 2, "float16": 0, "bfloat16": 1}  # enum tlm_dtype
+_EW_BCAST = {"full": 0, "row": 1, "col": 2, "scalar": 3}
+
+
+def _grid_var_extent(pf, e) -> Optional[int]:
+    """Extent of the kernel grid dimension whose variable is ``e`` (None if it is not one)."""
+    if not isinstance(e, Expr) or e.op != "var" or not pf.kernels:
+        return None
+    k = pf.kernels[0]
+    for v, ext in zip(k.vars, k.extents):
+        if v is e or (isinstance(v, Expr) and v.args[0] == e.args[0]):
+            try:
+                return int(ir.const_value(ext))
+            except (TypeError, ValueError):
+                return None
+    return None
+
+
+def _tiles_cover(pf, access, tile: Buffer) -> bool:
+    """Whether the tile copy ``access`` (of a global parameter) takes the (i, j)-th tile of a
+    grid that covers the parameter exactly: per dimension either the whole (or unit) dimension,
+    or a start of grid_var * t with extent t and a grid extent of ceil(dim / t)."""
+    buf = access.buffer if isinstance(access, BufferAccess) else access
+    dims = _shape(buf)
+    if isinstance(access, Buffer):
+        return True
+    starts, exts = access.region(tile.shape)
+    for d, (st, ex) in enumerate(zip(starts, exts)):
+        try:
+            t = int(ir.const_value(ex))
+        except (TypeError, ValueError):
+            t = None
+        try:
+            s0 = int(ir.const_value(st))
+        except (TypeError, ValueError):
+            s0 = None
+        if s0 == 0 and (t == dims[d] or dims[d] == 1):
+            continue
+        if not (isinstance(st, Expr) and st.op == "mul"):
+            return False
+        a, b = st.args
+        var, c = (a, b) if isinstance(b, Expr) and b.op == "const" else (b, a)
+        if not (isinstance(c, Expr) and c.op == "const"):
+            return False
+        c = int(c.args[0])
+        if t is None:
+            tdims = list(tile.shape)
+            t = int(ir.const_value(tdims[d - (len(dims) - len(tdims))])) if len(tdims) else 1
+        if t != c or _grid_var_extent(pf, var) != -(-dims[d] // c):
+            return False
+    return True
+
+
+def _elementwise(pf, names) -> Plan:
+    fam = "elementwise"
+    if len(pf.kernels) != 1:
+        _fail(fam, "expected one kernel")
+    writes = _written_params(pf)
+    if not writes:
+        _fail(fam, "no output parameter")
+    full = _shape(writes[0])
+    if any(_shape(w) != full for w in writes):
+        _fail(fam, "outputs of different shapes")
+    rows = math.prod(full[:-1]) if len(full) > 1 else 1
+    cols = full[-1]
+    nodes: List[tuple] = []  # (kind, a, b, imm)
+    memo: Dict[tuple, int] = {}
+
+    def node(kind, a=-1, b=-1, imm=0):
+        key = (kind, a, b, imm)
+        if key not in memo:
+            memo[key] = len(nodes)
+            nodes.append(key)
+        return memo[key]
+
+    def rounded(n, dtype):
+        return n if dtype == "float32" else node("round", n, imm=_EW_DTYPE[dtype])
+
+    inputs: List[Buffer] = []
+    kinds: List[str] = []
+    consts: List[float] = []
+    value: Dict[int, int] = {}  # id(tile) -> node
+    stores: List[tuple] = []    # (output parameter, node)
+
+    def load(p):
+        s = _shape(p)
+        n = math.prod(s)
+        if s == full:
+            kind = "full"
+        elif n == 1:
+            kind = "scalar"
+        elif n == rows and s[-1] == 1:
+            kind = "row"
+        elif n == cols and len(s) >= 1 and s[-1] == cols:
+            kind = "col"
+        else:
+            _fail(fam, f"parameter {p!r} does not broadcast onto the {full} output")
+        for k, q in enumerate(inputs):
+            if q is p:
+                return node("load", imm=k)
+        inputs.append(p)
+        kinds.append(kind)
+        return node("load", imm=len(inputs) - 1)
+
+    def const(v, dtype):
+        v = float(v)
+        if v not in consts:
+            consts.append(v)
+        return rounded(node("const", imm=consts.index(v)), dtype)
+
+    def get(b):
+        b = _buf(b)
+        if b is None or id(b) not in value:
+            _fail(fam, f"tile {b!r} is read before it is written")
+        return value[id(b)]
+
+    for op in _ops(pf):
+        n = op.name
+        if n in _COPY:
+            src, dst = op.args[0], op.args[1]
+            sb, db = _buf(src), _buf(dst)
+            if sb is None or db is None:
+                _fail(fam, "copy operands must be buffers")
+            if sb.scope == "global" and db.scope != "global":
+                if not _tiles_cover(pf, src, db):
+                    _fail(fam, f"the copy from {sb!r} is not one tile of a grid covering it")
+                value[id(db)] = rounded(load(sb), db.dtype)
+            elif sb.scope != "global" and db.scope == "global":
+                if not _tiles_cover(pf, dst, sb):
+                    _fail(fam, f"the copy to {db!r} is not one tile of a grid covering it")
+                stores.append((db, get(sb)))
+            elif sb.scope != "global" and db.scope != "global":
+                value[id(db)] = rounded(get(sb), db.dtype)
+            else:
+                _fail(fam, "global-to-global copies are not tile programs")
+        elif n in _FILL_OPS:
+            b = _buf(op.args[0])
+            value[id(b)] = const(_const(op.args[1]), b.dtype)
+        elif n in _EW_BINARY:
+            out, x, y = (_buf(a) for a in op.args[:3])
+            value[id(out)] = rounded(node(_EW_BINARY[n], get(x), get(y)), out.dtype)
+        elif n in _EW_CONSTOP:
+            out, x = _buf(op.args[0]), _buf(op.args[1])
+            c = const(_const(op.args[2]), x.dtype)
+            value[id(out)] = rounded(node(_EW_CONSTOP[n], get(x), c), out.dtype)
+        elif n == "ppl_exp":
+            out = _buf(op.args[0])
+            value[id(out)] = rounded(node("exp", get(out)), out.dtype)
+        elif n in ("ppl_rsqrt", "ppl_sigmoid"):
+            out, x = _buf(op.args[0]), _buf(op.args[1])
+            value[id(out)] = rounded(node(n[4:], get(x)), out.dtype)
+        else:
+            _fail(fam, f"op {n} is not an elementwise tile op")
+    if not stores:
+        _fail(fam, "nothing is stored")
+    outs: List[Buffer] = []
+    for p, _ in stores:
+        if all(p is not q for q in outs):
+            outs.append(p)
+    if len(inputs) > 8 or len(outs) > 4 or len(consts) > 16:
+        _fail(fam, "more than 8 inputs, 4 outputs or 16 constants")
+    # register allocation over the nodes the stores need, in program (topological) order
+    need = set()
+
+    def mark(i):
+        if i in need or i < 0:
+            return
+        need.add(i)
+        mark(nodes[i][1])
+        mark(nodes[i][2])
+
+    for _, i in stores:
+        mark(i)
+    last_use: Dict[int, int] = {}
+    order = sorted(need)
+    for pos, i in enumerate(order):
+        for a in nodes[i][1:3]:
+            if a >= 0:
+                last_use[a] = pos
+    final = {i: len(order) + k for k, (_, i) in enumerate(stores)}
+    for i, pos in final.items():
+        last_use[i] = max(last_use.get(i, -1), pos)
+    slot: Dict[int, int] = {}
+    free = list(range(8))
+    code: List[int] = []
+    for pos, i in enumerate(order):
+        kind, a, b, imm = nodes[i]
+        sa, sb = slot.get(a, 0), slot.get(b, 0)
+        for x in (a, b):  # operands whose last use is here free their slot for the result
+            if x >= 0 and last_use.get(x) == pos and x in slot and slot[x] not in free:
+                free.append(slot[x])
+        if not free:
+            _fail(fam, "the program needs more than 8 live values")
+        d = min(free)
+        free.remove(d)
+        slot[i] = d
+        code.append(_EW_OPCODE[kind] | d << 8 | sa << 12 | sb << 16 | imm << 20)
+    for p, i in stores:
+        code.append(_EW_OPCODE["store"] | slot[i] << 12 | outs.index(p) << 20)
+    if len(code) > 64:
+        _fail(fam, "more than 64 instructions")
+    return Plan(fam, pf.params, [_index(pf, p) for p in outs], dict(
+        inputs=[_index(pf, p) for p in inputs], bcast=[_EW_BCAST[k] for k in kinds],
+        outputs=[_index(pf, p) for p in outs], code=code, consts=consts, rows=rows, cols=cols))
+
+
 def recognize(pf) -> Plan:
     """Return the :class:`Plan` for ``pf`` or raise :class:`UnsupportedProgram`."""
     names = set(_op_names(pf))
     ints = [p for p in pf.params if p.dtype == "int32"]
     n_gemm = sum(1 for op in _ops(pf, _GEMM))
     try:
-        if ints and n_gemm >= 3:
+        if n_gemm >= 3:
             return _audit(pf, _mla(pf, names))
         if n_gemm == 2 and names & {"ppl_reduce_max", "reduce_max"}:
             return _audit(pf, _flashattn(pf, names))
@@ -781,10 +1036,17 @@ def recognize(pf) -> Plan:
             return _audit(pf, _rope(pf, names))
         if {"ppl_reduce_sum", "ppl_rsqrt"} <= names:
             return _audit(pf, _rmsnorm(pf, names))
-        if {"ppl_exp", "ppl_div"} <= names:
-            return _audit(pf, _swiglu(pf, names))
-        if "ppl_sigmoid" in names:
-            return _audit(pf, _sigmoid(pf, names))
+        ew = n_gemm == 0 and names <= set(_ALLOWED_OPS["elementwise"]) and \
+            bool(names & set(_ALLOWED_OPS["elementwise"]) - set(_COPY) - set(_FILL_OPS))
+        if {"ppl_exp", "ppl_div"} <= names or "ppl_sigmoid" in names:
+            # the dedicated SwiGLU / sigmoid kernels, else the general elementwise program
+            try:
+                fam = _swiglu if "ppl_sigmoid" not in names else _sigmoid
+                return _audit(pf, fam(pf, names))
+            except UnsupportedProgram:
+                if not ew:
+                    raise
+                return _audit(pf, _elementwise(pf, names))
         if "ppl_gather" in names:
             return _audit(pf, _gather(pf, names))
         if "ppl_topk" in names:
@@ -793,6 +1055,8 @@ def recognize(pf) -> Plan:
                                         "reduce_sum"}) == 1 and \
                 not names & {"ppl_exp", "ppl_rsqrt", "ppl_div", "ppl_mul"}:
             return _audit(pf, _row_reduce(pf, names))
+        if ew:
+            return _audit(pf, _elementwise(pf, names))
     except UnsupportedProgram:
         raise
     except (TypeError, ValueError, IndexError) as e:  # malformed trace
@@ -800,4 +1064,4 @@ def recognize(pf) -> Plan:
     raise UnsupportedProgram(
         f"{pf.name}: no gfx950 kernel matches this program (ops: {sorted(names)}). Supported "
         f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla, sigmoid, gather, topk, "
-        f"row_reduce")
+        f"row_reduce, elementwise")

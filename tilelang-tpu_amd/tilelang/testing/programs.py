@@ -772,3 +772,245 @@ def mla_decode(batch, h_q, h_kv, max_seqlen_pad, dv, dpe, block_N, block_H, num_
         combine(glse, Output_partial, Output)
 
     return mla
+
+
+def mla_decode_nopage(batch, heads, seqlen_kv, dim, pe_dim, block_N=64, block_H=64,
+                      num_split=1, dtype="float16"):
+    """examples/deepseek_mla/example_mla_decode.py:10-227: non-paged MLA decode, Q [batch,
+    heads, dim], KV [batch, seqlen_kv, 1, dim], exp2 softmax with scale 1/sqrt(dim + pe_dim) *
+    log2(e); main_split (num_split > 1: per-split partial outputs and log2 sum-exp in glse /
+    Output_partial, then the LSE combine) or main_no_split. Output is parameter 6."""
+    scale = (1.0 / (dim + pe_dim)) ** 0.5 * 1.44269504
+    acc = "float"
+    VB = min(block_H, heads)
+
+    def attn(Q, Q_pe, KV, K_pe, Out, glse=None, Opart=None):
+        grid = (batch, heads // VB) + ((num_split,) if glse is not None else ())
+        with T.Kernel(*grid, threads=256) as ids:
+            bx, by = ids[0], ids[1]
+            bz = ids[2] if glse is not None else None
+            q_s = T.alloc_shared([block_H, dim], dtype)
+            s_s = T.alloc_shared([block_H, block_N], dtype)
+            qpe_s = T.alloc_shared([block_H, pe_dim], dtype)
+            kv_s = T.alloc_shared([block_N, dim], dtype)
+            kpe_s = T.alloc_shared([block_N, pe_dim], dtype)
+            o_s = T.alloc_shared([block_H, dim], dtype)
+            s = T.alloc_fragment([block_H, block_N], acc)
+            o = T.alloc_fragment([block_H, dim], acc)
+            m = T.alloc_fragment([block_H], acc)
+            m_prev = T.alloc_fragment([block_H], acc)
+            alpha = T.alloc_fragment([block_H], acc)
+            rsum = T.alloc_fragment([block_H], acc)
+            l = T.alloc_fragment([block_H], acc)
+            T.use_swizzle(10)
+            T.copy(Q[bx, by * VB:(by + 1) * VB, :], q_s)
+            T.copy(Q_pe[bx, by * VB:(by + 1) * VB, :], qpe_s)
+            T.fill(o, 0)
+            T.fill(l, 0)
+            T.fill(m, -T.infinity(acc))
+            per = seqlen_kv // num_split
+            n_iter = T.ceildiv(per if glse is not None else seqlen_kv, block_N)
+            for k in T.Pipelined(n_iter, num_stages=2):
+                start = (per * bz if glse is not None else 0) + k * block_N
+                T.copy(KV[bx, start:start + block_N, 0, :], kv_s)
+                T.copy(K_pe[bx, start:start + block_N, 0, :], kpe_s)
+                T.clear(s)
+                T.gemm(q_s, kv_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullCol)
+                T.gemm(qpe_s, kpe_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullCol)
+                T.copy(m, m_prev)
+                T.fill(m, -T.infinity(acc))
+                T.reduce_max(s, m, dim=1, clear=False)
+                for i in T.Parallel(block_H):
+                    alpha[i] = T.exp2(m_prev[i] * scale - m[i] * scale)
+                for i, j in T.Parallel(block_H, block_N):
+                    s[i, j] = T.exp2(s[i, j] * scale - m[i] * scale)
+                T.reduce_sum(s, rsum, dim=1)
+                T.copy(s, s_s)
+                for i in T.Parallel(block_H):
+                    l[i] = l[i] * alpha[i] + rsum[i]
+                for i, j in T.Parallel(block_H, dim):
+                    o[i, j] *= alpha[i]
+                T.gemm(s_s, kv_s, o, policy=T.GemmWarpPolicy.FullCol)
+            for i, j in T.Parallel(block_H, dim):
+                o[i, j] /= l[i]
+            if glse is not None:
+                for i in T.Parallel(block_H):
+                    l[i] = T.log2(l[i]) + m[i] * scale
+                T.copy(l, glse[bx, by * VB:(by + 1) * VB, bz])
+                T.copy(o, o_s)
+                T.copy(o_s, Opart[bx, by * VB:(by + 1) * VB, bz, :])
+            else:
+                T.copy(o, o_s)
+                T.copy(o_s, Out[bx, by * VB:(by + 1) * VB, :])
+
+    def combine(glse, Opart, Out):
+        with T.Kernel(heads, batch, threads=128) as (by, bz):
+            part = T.alloc_fragment([dim], dtype)
+            acc_o = T.alloc_fragment([dim], acc)
+            lse_max = T.alloc_local([1], acc)
+            lse_sum = T.alloc_local([1], acc)
+            w = T.alloc_local([1], acc)
+            T.clear(lse_sum)
+            T.clear(acc_o)
+            lse_max[0] = -T.infinity(acc)
+            for k in T.serial(num_split):
+                lse_max[0] = T.max(lse_max[0], glse[bz, by, k])
+            for k in T.serial(num_split):
+                lse_sum[0] += T.exp2(glse[bz, by, k] - lse_max[0])
+            lse_sum[0] = T.log2(lse_sum[0]) + lse_max[0]
+            for k in T.serial(num_split):
+                for i in T.Parallel(dim):
+                    part[i] = Opart[bz, by, k, i]
+                w[0] = T.exp2(glse[bz, by, k] - lse_sum[0])
+                for i in T.Parallel(dim):
+                    acc_o[i] += part[i] * w[0]
+            for i in T.Parallel(dim):
+                Out[bz, by, i] = acc_o[i]
+
+    @T.prim_func
+    def main(Q: T.Tensor([batch, heads, dim], dtype), Q_pe: T.Tensor([batch, heads, pe_dim], dtype),
+             KV: T.Tensor([batch, seqlen_kv, 1, dim], dtype),
+             K_pe: T.Tensor([batch, seqlen_kv, 1, pe_dim], dtype),
+             glse: T.Tensor([batch, heads, num_split], dtype),
+             Output_partial: T.Tensor([batch, heads, num_split, dim], dtype),
+             Output: T.Tensor([batch, heads, dim], dtype)):
+        if num_split > 1:
+            attn(Q, Q_pe, KV, K_pe, None, glse, Output_partial)
+            combine(glse, Output_partial, Output)
+        else:
+            attn(Q, Q_pe, KV, K_pe, Output)
+
+    return main
+
+
+def mla_decode_tpu(batch, heads, seqlen_kv, dim, pe_dim, block_N, block_H):
+    """tpu_demo/ppl/deepseek_mla/mla_decode.py:9-121: the TPU program written with T.ppl_* ops.
+    Q [batch, heads, 1, dim], KV [batch, seqlen_kv, 1, dim], fp16; scores scaled by
+    1/sqrt(dim + pe_dim) with ppl_mul_C and exponentiated with ppl_exp2 (natural exp); P copied to
+    an fp16 tile before the P @ KV gemm."""
+    scale = (1.0 / (dim + pe_dim)) ** 0.5
+    dtype, acc = "float16", "float"
+    VB = min(block_H, heads)
+
+    @T.prim_func
+    def main(Q: T.Tensor([batch, heads, 1, dim], dtype),
+             Q_pe: T.Tensor([batch, heads, 1, pe_dim], dtype),
+             KV: T.Tensor([batch, seqlen_kv, 1, dim], dtype),
+             K_pe: T.Tensor([batch, seqlen_kv, 1, pe_dim], dtype),
+             Output: T.Tensor([batch, heads, 1, dim], dtype)):
+        with T.Kernel(batch, T.ceildiv(heads, VB), is_cpu=True) as (bx, by):
+            q_s = T.alloc_shared([VB, dim], dtype)
+            qpe_s = T.alloc_shared([VB, pe_dim], dtype)
+            kv_s = T.alloc_shared([block_N, dim], dtype)
+            kpe_s = T.alloc_shared([block_N, pe_dim], dtype)
+            p_s = T.alloc_shared([VB, block_N], dtype)
+            o_s = T.alloc_shared([VB, dim], dtype)
+            s = T.alloc_shared([VB, block_N], acc)
+            s_pe = T.alloc_shared([VB, block_N], acc)
+            o = T.alloc_shared([VB, dim], acc)
+            m = T.alloc_shared([VB, 1], acc)
+            m_prev = T.alloc_shared([VB, 1], acc)
+            alpha = T.alloc_shared([VB, 1], acc)
+            rsum = T.alloc_shared([VB, 1], acc)
+            l = T.alloc_shared([VB, 1], acc)
+            T.ppl_copy(Q[bx, by * VB:(by + 1) * VB, :, :], q_s)
+            T.ppl_copy(Q_pe[bx, by * VB:(by + 1) * VB, :, :], qpe_s)
+            T.ppl_fill(o, T.float32(0))
+            T.ppl_fill(l, T.float32(0))
+            T.ppl_fill(m, -T.infinity(acc))
+            for k in T.Pipelined(T.ceildiv(seqlen_kv, block_N), num_stages=2):
+                T.ppl_copy(KV[bx, k * block_N:(k + 1) * block_N, 0, :], kv_s)
+                T.ppl_copy(K_pe[bx, k * block_N:(k + 1) * block_N, 0, :], kpe_s)
+                T.ppl_clear(s)
+                T.ppl_gemm(q_s, kv_s, s, transpose_B=True)
+                T.ppl_clear(s_pe)
+                T.ppl_gemm(qpe_s, kpe_s, s_pe, transpose_B=True)
+                T.ppl_add(s, s, s_pe)
+                T.ppl_copy(m, m_prev)
+                T.ppl_fill(m, -T.infinity(acc))
+                T.ppl_reduce_max(s, m, dim=1, clear=False)
+                prev_scaled = T.alloc_shared([VB, 1], acc)
+                curr_scaled = T.alloc_shared([VB, 1], acc)
+                T.ppl_mul_C(prev_scaled, m_prev, scale)
+                T.ppl_mul_C(curr_scaled, m, scale)
+                T.ppl_subtract(alpha, prev_scaled, curr_scaled)
+                T.ppl_exp2(alpha)
+                m_scaled = T.alloc_shared([VB, 1], acc)
+                T.ppl_mul_C(s, s, scale)
+                T.ppl_mul_C(m_scaled, m, scale)
+                T.ppl_subtract(s, s, m_scaled)
+                T.ppl_exp2(s)
+                T.ppl_reduce_sum(s, rsum, dim=1)
+                T.ppl_copy(s, p_s)
+                T.ppl_mul(l, l, alpha)
+                T.ppl_add(l, l, rsum)
+                T.ppl_mul(o, o, alpha)
+                T.ppl_gemm(p_s, kv_s, o)
+            T.ppl_div(o, o, l)
+            T.ppl_copy(o, o_s)
+            T.ppl_copy(o_s, Output[bx, by * VB:(by + 1) * VB, :, :])
+
+    return main
+
+
+def ppl_exp(M, N, block_M, block_N, dtype="float32"):
+    """tpu_demo/ppl/test/exp.py:6-16 (and exp_bf16.py): in-place natural exp of [M, N]."""
+
+    @T.prim_func
+    def main(scores_scale: T.Tensor([M, N], dtype)):
+        with T.Kernel(T.ceildiv(N, block_N), T.ceildiv(M, block_M), is_cpu=True) as (bx, by):
+            t = T.alloc_shared([block_M, block_N], dtype)
+            T.ppl_copy(scores_scale[by * block_M, bx * block_N], t)
+            T.ppl_exp2(t, block_M, block_N, dtype)
+            T.ppl_copy(t, scores_scale[by * block_M, bx * block_N])
+
+    return main
+
+
+def ppl_mul_rows(M, N, blk_m, dtype="float32"):
+    """tpu_demo/ppl/test/mul_N_1.py:9-22: C = A * B with B [M, 1] broadcast along each row."""
+
+    @T.prim_func
+    def main(C: T.Tensor((M, N), dtype), A: T.Tensor((M, N), dtype), B: T.Tensor((M, 1), dtype)):
+        with T.Kernel(T.ceildiv(M, blk_m), is_cpu=True) as (bx,):
+            a_s = T.alloc_shared((blk_m, N), dtype)
+            b_s = T.alloc_shared((blk_m, 1), dtype)
+            T.ppl_copy(A[bx * blk_m:(bx + 1) * blk_m, :], a_s)
+            T.ppl_copy(B[bx * blk_m:(bx + 1) * blk_m, 0], b_s)
+            T.ppl_mul(a_s, a_s, b_s)
+            T.ppl_copy(a_s, C[bx * blk_m:(bx + 1) * blk_m, :])
+
+    return main
+
+
+def ppl_scale_shift(M, N, blk_m, blk_n, dtype="float32", scale=1 / 8192, shift=1e-12):
+    """tpu_demo/ppl/test/elementwise_c.py:9-22: B = A * (1/8192) + 1e-12 (ppl_mul_C, ppl_add_C)."""
+
+    @T.prim_func
+    def main(A: T.Tensor((M, N), dtype), B: T.Tensor((M, N), dtype)):
+        with T.Kernel(T.ceildiv(M, blk_m), T.ceildiv(N, blk_n), is_cpu=True) as (bx, by):
+            a_s = T.alloc_shared((blk_m, blk_n), dtype)
+            T.ppl_copy(A[bx * blk_m, by * blk_n], a_s)
+            T.ppl_mul_C(a_s, a_s, T.float32(scale))
+            T.ppl_add_C(a_s, a_s, T.float32(shift))
+            T.ppl_copy(a_s, B[bx * blk_m, by * blk_n])
+
+    return main
+
+
+def ppl_add(M, N, block_M, block_N, in_dtype="float32", out_dtype="float32"):
+    """tpu_demo/ppl/elementwise_add_kernel/elementwise_add.py:9-35: C = A + B."""
+
+    @T.prim_func
+    def main(A: T.Tensor((M, N), in_dtype), B: T.Tensor((M, N), in_dtype),
+             C: T.Tensor((M, N), out_dtype)):
+        with T.Kernel(T.ceildiv(N, block_N), T.ceildiv(M, block_M), is_cpu=True) as (bx, by):
+            a_s = T.alloc_shared((block_M, block_N), in_dtype)
+            b_s = T.alloc_shared((block_M, block_N), in_dtype)
+            c_s = T.alloc_shared((block_M, block_N), out_dtype)
+            T.ppl_copy(A[by * block_M, bx * block_N], a_s)
+            T.ppl_copy(B[by * block_M, bx * block_N], b_s)
+            T.ppl_add(c_s, a_s, b_s)
+            T.ppl_copy(c_s, C[by * block_M, bx * block_N])
+
+    return main
