@@ -24,7 +24,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-fPIC",
-    "-std=c++17",
+    "-std=c++20",
     "-Wall",
     "-Wno-unused-function",
     # Packed fp32 VALU forms are kept out of every kernel (hipcc would otherwise emit them
@@ -62,7 +62,7 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -781,26 +781,50 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
   auto start = [&](int64_t g) { return g * T / G; };
   auto slot_of = [&](int64_t g) { return g * F8_SLOTS + ((g == g0 && c0 != start(g0)) ? 1 : 0); };
-  float mx = -INFINITY;
-  for (int64_t g = g0; g <= g1; ++g) {
-    if (start(g) == start(g + 1)) continue;
-    mx = fmaxf(mx, a.part_lse[slot_of(g) * a.Hq + head]);
-  }
-  float sum = 0.f;
-  for (int64_t g = g0; g <= g1; ++g) {
-    if (start(g) == start(g + 1)) continue;
-    sum += __builtin_amdgcn_exp2f(a.part_lse[slot_of(g) * a.Hq + head] - mx);
-  }
-  const float lse = mx + __log2f(sum);
+  // Online merge over the ranges in batches of F8_CMB: the lse values and partial outputs of a
+  // batch are all requested before any is used, so a call waits for about one memory latency
+  // per batch (a sequence spans at most a few ranges at the usual split counts).
+  constexpr int F8_CMB = 8;
+  float m = -INFINITY, l = 0.f;
   f32x4 acc[4] = {};
-  for (int64_t g = g0; g <= g1; ++g) {
-    if (start(g) == start(g + 1)) continue;
-    const int64_t sb = slot_of(g);
-    const float w = __builtin_amdgcn_exp2f(a.part_lse[sb * a.Hq + head] - lse);
-    const u32x2* src = a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
+  for (int64_t gb = g0; gb <= g1; gb += F8_CMB) {
+    float lv[F8_CMB];
+    u32x2 pv[F8_CMB][4];
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) acc[q4] += bf16x4_to_f32(src[q4 * 64]) * w;
+    for (int i = 0; i < F8_CMB; ++i) {
+      const int64_t g = gb + i;  // wave-uniform
+      lv[i] = -INFINITY;
+      if (g <= g1 && start(g) != start(g + 1)) {
+        const int64_t sb = slot_of(g);
+        lv[i] = a.part_lse[sb * a.Hq + head];
+        const u32x2* src =
+            a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) pv[i][q4] = src[q4 * 64];
+      } else {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) pv[i][q4] = u32x2{0u, 0u};
+      }
+    }
+    float mb = m;
+#pragma unroll
+    for (int i = 0; i < F8_CMB; ++i) mb = fmaxf(mb, lv[i]);
+    const float r = __builtin_amdgcn_exp2f(m - mb);  // m = -inf on the first batch: r = 0
+    l *= r;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) acc[q4] *= r;
+#pragma unroll
+    for (int i = 0; i < F8_CMB; ++i) {
+      const float w = __builtin_amdgcn_exp2f(lv[i] - mb);  // 0 for an absent range
+      l += w;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) acc[q4] += bf16x4_to_f32(pv[i][q4]) * w;
+    }
+    m = mb;
   }
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) acc[q4] *= inv;
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4)
     *(u32x2*)(o + 8 * q4) = u32x2{H::pack(acc[q4][0], acc[q4][1]), H::pack(acc[q4][2], acc[q4][3])};
