@@ -278,6 +278,58 @@ def flashattn_bhsd_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None):
 # KV rows, shared latent head (h_kv = 1), value = first dv columns of the key rows.
 # The rows are gathered through the block table: token j -> BT[b, j // page] * page + j % page
 # (the kernel's addressing, :62-63, 147-148). fp8 KV is dequantised as decode(byte) * kv_scale.
+def mha_inference_ref(Q, K, V, sm_scale: Optional[float] = None):
+    """examples/flash_attention/example_mha_inference.py ref_program (:206-213): sequence-major
+    Q [B, S_q, H, D], K, V [B, S_kv, H, D], fp32 softmax(Q K^T / sqrt(D)) V over all keys (the
+    program is non-causal). Returns fp32 [B, S_q, H, D]."""
+    o = flashattn_bhsd_ref(Q.permute(0, 2, 1, 3), K.permute(0, 2, 1, 3), V.permute(0, 2, 1, 3),
+                           False, sm_scale)
+    return o.permute(0, 2, 1, 3).contiguous()
+
+
+def mha_split_combine_ref(Q, K, V, num_split: int, block_N: int, store_dtype=torch.float16):
+    """The split-KV algorithm of example_mha_inference.py (flash_split_ref :230-275, reduce_ref
+    :216-227): each split s covers keys [s per, (s + 1) per), per = S_kv // num_split, in tiles of
+    block_N with the online softmax in the exp2 domain; its normalised output and
+    lse = log2(l) + m * scale are stored in store_dtype (the program's glse / Output_partial);
+    the merge weights each split by 2^(lse_s - log2 sum_s 2^lse_s). Returns fp32 [B, S_q, H, D]
+    and the stored (glse [B, H, num_split, S_q], partial [B, S_q, H, num_split, D])."""
+    B, Sq, H, D = Q.shape
+    Skv = K.shape[1]
+    per = Skv // num_split
+    scale = (1.0 / D) ** 0.5 * 1.44269504
+    q = Q.float() * scale
+    glse = torch.empty(B, H, num_split, Sq, dtype=torch.float32)
+    part = torch.empty(B, Sq, H, num_split, D, dtype=torch.float32)
+    for s in range(num_split):
+        m = torch.full((B, H, Sq), float("-inf"))
+        l = torch.zeros(B, H, Sq)
+        o = torch.zeros(B, Sq, H, D)
+        for t in range(per // block_N):
+            k0 = s * per + t * block_N
+            kk = K[:, k0:k0 + block_N].float()
+            vv = V[:, k0:k0 + block_N].float()
+            sc = torch.einsum("bqhd,bkhd->bhqk", q, kk)
+            m_prev, m = m, torch.maximum(m, sc.amax(-1))
+            alpha = torch.exp2(m_prev - m)
+            p = torch.exp2(sc - m[..., None])
+            l = l * alpha + p.sum(-1)
+            o = o * alpha.permute(0, 2, 1)[..., None] + torch.einsum(
+                "bhqk,bkhd->bqhd", p.to(Q.dtype).float(), vv)
+        o = o / l.permute(0, 2, 1)[..., None]
+        glse[:, :, s] = torch.log2(l) + m
+        part[:, :, :, s] = o
+    glse = glse.to(store_dtype).float()
+    part = part.to(store_dtype).float()
+    lmax = glse.amax(2)
+    lsum = torch.log2(torch.exp2(glse - lmax[:, :, None]).sum(2)) + lmax
+    out = torch.zeros(B, Sq, H, D)
+    for s in range(num_split):
+        w = torch.exp2(glse[:, :, s] - lsum)  # [B, H, S_q]
+        out += part[:, :, :, s] * w.permute(0, 2, 1)[..., None]
+    return out, (glse, part)
+
+
 def paged_rows(block_table: torch.Tensor, seqlen: int, b: int, page: int) -> torch.Tensor:
     j = torch.arange(seqlen, dtype=torch.int64)
     return block_table[b, j // page].to(torch.int64) * page + j % page

@@ -390,3 +390,18 @@ def test_nonpaged_mla_programs_are_recognised():
     assert t.plan.family == "mla" and not a["paged"] and (a["dv"], a["dpe"], a["Hq"]) == (32, 4, 8)
     assert math.isclose(a["sm_scale"], 1 / 6, rel_tol=1e-12)
     assert t.plan.out_idx == [4]
+
+
+def test_splitkv_inference_program_recognised():
+    """example_mha_inference.py: recognised as sequence-major attention with seq_q != seq_kv;
+    splits that drop or overlap keys and the program's causal form are rejected."""
+    k = tilelang.compile(programs.mha_inference(1, 32, 128, 8192, 128), out_idx=[5])
+    a = k.plan.attrs
+    assert k.plan.family == "flashattn" and a["layout"] == "bshd_kv"
+    assert (a["S"], a["S_kv"], a["num_split"], a["o"]) == (128, 8192, 4, 5)
+    assert abs(a["sm_scale"] - 128 ** -0.5) < 1e-6
+    with pytest.raises(UnsupportedProgram, match="whole 64-key tiles"):
+        tilelang.compile(programs.mha_inference(1, 32, 128, 8000, 128), out_idx=[5])
+    with pytest.raises(UnsupportedProgram, match="causal"):
+        tilelang.compile(programs.mha_inference(1, 32, 128, 8192, 128, is_causal=True),
+                         out_idx=[5])

@@ -599,3 +599,31 @@ def test_elementwise_program_refs_against_float64_numpy():
     ab = a.to(torch.bfloat16)
     t = (ab.double() / 8192).to(torch.bfloat16).double() + 1e-12
     assert torch.equal(ref.ppl_scale_shift_ref(ab, 1 / 8192, 1e-12), t.to(torch.bfloat16))
+
+
+def test_mha_inference_ref_and_split_combine():
+    """Split-KV inference oracle: the full-softmax reference equals SDPA on the head-major view
+    (S_q != S_kv, non-causal); the restated split + combine algorithm of the program, with fp32
+    intermediates, equals it to fp32 rounding for any split count, and with the program's fp16
+    glse / Output_partial to fp16 rounding. A plausible slip (a split weight without the lse
+    offset, a dropped alpha rescale, a missing scale) breaks one of these."""
+    g = torch.Generator().manual_seed(45)
+    B, Sq, Skv, H, D = 2, 5, 64, 3, 16
+    q = torch.randn(B, Sq, H, D, generator=g).half()
+    k = torch.randn(B, Skv, H, D, generator=g).half()
+    v = torch.randn(B, Skv, H, D, generator=g).half()
+    full = ref.mha_inference_ref(q, k, v)
+    sdpa = F.scaled_dot_product_attention(*(t.float().transpose(1, 2) for t in (q, k, v)))
+    torch.testing.assert_close(full, sdpa.transpose(1, 2), rtol=1e-5, atol=1e-5)
+    for ns, bn in ((1, 64), (2, 16), (4, 8), (8, 8)):
+        got, (glse, part) = ref.mha_split_combine_ref(q, k, v, ns, bn, store_dtype=torch.float32)
+        # P rounded to fp16 before P V (the program's acc_s_cast): ~1e-3 of the output
+        torch.testing.assert_close(got, full, rtol=2e-3, atol=2e-3)
+        assert glse.shape == (B, H, ns, Sq) and part.shape == (B, Sq, H, ns, D)
+        got16, _ = ref.mha_split_combine_ref(q, k, v, ns, bn)
+        torch.testing.assert_close(got16, full, rtol=5e-3, atol=5e-3)
+    # one split: its stored output is the attention output, its lse the log2 sum-exp
+    got, (glse, part) = ref.mha_split_combine_ref(q, k, v, 1, 64, store_dtype=torch.float32)
+    s = torch.einsum("bqhd,bkhd->bhqk", q.float(), k.float()) / math.sqrt(D)
+    torch.testing.assert_close(glse[:, :, 0], torch.logsumexp(s, -1) / math.log(2), rtol=1e-5,
+                               atol=1e-5)

@@ -216,7 +216,7 @@ _PARAM_ATTRS = {
     "gemm": ("a", "b", "c"),
     "rope": ("q", "k", "cos", "sin", "q_out", "k_out"),
     "swiglu": ("gate", "up", "out"),
-    "flashattn": ("q", "k", "v", "o", "cu_q", "cu_k", "max_q"),
+    "flashattn": ("q", "k", "v", "o", "cu_q", "cu_k", "max_q", "glse", "partial"),
     "mla": ("q", "q_pe", "kv", "k_pe", "block_table", "seqlens", "o", "glse", "o_partial",
             "kv_scale"),
     "sigmoid": ("x", "y"),
@@ -439,6 +439,8 @@ def _flashattn(pf, names) -> Plan:
     kshp = _shape(K)
     if len(shp) == 3:
         return _flashattn_varlen(pf, qk[0], pv[0], Q, K, V, O)
+    if len(_shape(O)) == 5:
+        return _flashattn_splitkv(pf, qk[0], pv[0], Q, K, V, O)
     bhsd = _seq_dim(pf, Q) == 2
     if bhsd:
         if len(shp) != 4 or shp != _shape(O) or kshp != _shape(V) or len(kshp) != 4:
@@ -511,6 +513,62 @@ def _flashattn(pf, names) -> Plan:
         H_kv=kshp[2], D=D,
         causal=causal, sm_scale=sm_scale, dtype=Q.dtype,
         operand_dtype=tile_dt if Q.dtype == "float32" and tile_dt != "float32" else None))
+
+
+def _flashattn_splitkv(pf, qk, pv, Q, K, V, Opart) -> Plan:
+    """examples/flash_attention/example_mha_inference.py:98-203: the query block's online softmax
+    over each of num_split key ranges (flash_attn_split) writes normalised partial outputs to
+    Output_partial [batch, seq_q, heads, num_split, dim] and log2 sum-exp to glse [batch, heads,
+    num_split, seq_q]; combine merges them into Output [batch, seq_q, heads, dim]. The merge of
+    the splits equals attention over all keys when every split covers whole key tiles, so the
+    program runs as one attention pass with seq_q != seq_kv (glse and Output_partial are the
+    program's intermediates and are not written)."""
+    fam = "flashattn"
+    shp, kshp, pshp = _shape(Q), _shape(K), _shape(Opart)
+    if len(shp) != 4 or len(kshp) != 4 or kshp != _shape(V):
+        _fail(fam, "split-KV Q must be [batch, seq_q, heads, dim] and K, V [batch, seq_kv, heads, "
+                   "dim]")
+    B, Sq, H, D = shp
+    Skv, Hkv = kshp[1], kshp[2]
+    if (kshp[0], kshp[3]) != (B, D) or Hkv == 0 or H % Hkv:
+        _fail(fam, f"K/V {kshp} do not match Q {shp}")
+    if len(pshp) != 5 or (pshp[0], pshp[1], pshp[2], pshp[4]) != (B, Sq, H, D):
+        _fail(fam, f"Output_partial {pshp} is not [batch, seq_q, heads, num_split, dim]")
+    ns = pshp[3]
+    outs = [p for p in pf.params if isinstance(p, Buffer) and p not in (Q, K, V, Opart) and
+            _shape(p) == shp]
+    lses = [p for p in pf.params if isinstance(p, Buffer) and list(_shape(p)) == [B, H, ns, Sq]]
+    if len(outs) != 1 or len(lses) != 1 or len(pf.kernels) != 2:
+        _fail(fam, "split-KV attention needs glse [batch, heads, num_split, seq_q], "
+                   "Output_partial and one Output [batch, seq_q, heads, dim] written by a second "
+                   "(combine) kernel")
+    O = outs[0]
+    if not (Q.dtype == K.dtype == V.dtype == O.dtype) or Q.dtype not in ("bfloat16", "float16"):
+        _fail(fam, "split-KV attention takes bfloat16 or float16 Q, K, V and Output")
+    tile_dts = {_buf(qk.args[0]).dtype, _buf(qk.args[1]).dtype, _buf(pv.args[0]).dtype,
+                _buf(pv.args[1]).dtype}
+    if tile_dts != {Q.dtype}:
+        _fail(fam, f"the gemms multiply {tile_dts} tiles of {Q.dtype} parameters")
+    block_N = _shape(_buf(qk.args[1]))[0]
+    if Skv % ns or (Skv // ns) % block_N:
+        _fail(fam, f"seq_kv {Skv} does not split into {ns} ranges of whole {block_N}-key tiles "
+                   "(the program would drop or overlap keys there)")
+    if any(isinstance(e, Expr) and e.has_op("min") for e in _pipelined_extents(pf)):
+        _fail(fam, "the split program's causal form (loop bound without the split offset) is not "
+                   "causal attention")
+    acc_s = _buf(qk.args[2])
+    sm_scale = None
+    for op in _ops(pf, ("store",)):
+        if op.args[0] is acc_s and isinstance(op.args[2], Expr) and op.args[2].has_op("exp2"):
+            cs = [c for c in op.args[2].consts() if isinstance(c, float) and c > 0]
+            if cs:
+                sm_scale = cs[0] / LOG2E_REF
+    if sm_scale is None:
+        _fail(fam, "could not read the softmax scale")
+    return Plan(fam, pf.params, [_index(pf, O)], dict(
+        q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=Sq, S_kv=Skv,
+        H=H, H_kv=Hkv, D=D, causal=False, sm_scale=sm_scale, dtype=Q.dtype, operand_dtype=None,
+        layout="bshd_kv", num_split=ns, glse=_index(pf, lses[0]), partial=_index(pf, Opart)))
 
 
 def _seq_dim(pf, Q: Buffer) -> Optional[int]:

@@ -554,6 +554,155 @@ def flashattn_bhsd(batch, heads, seq_q, seq_kv, dim, is_causal, block_M=128, blo
     return main
 
 
+def mha_inference(batch, heads, seqlen_q, seqlen_kv, dim, is_causal=False, block_M=128,
+                  block_N=64, num_split=4, dtype="float16"):
+    """The program structure of examples/flash_attention/example_mha_inference.py:11-203:
+    split-KV attention for short query blocks over long key ranges. Kernel 1 (flash_attn_split,
+    grid [ceil(seqlen_q / block_M), heads * batch, num_split]) runs the online softmax of one
+    query block over the split's seqlen_kv // num_split keys and stores the normalised partial
+    output in Output_partial [batch, seqlen_q, heads, num_split, dim] and its log2 sum-exp in
+    glse [batch, heads, num_split, seqlen_q]; kernel 2 (combine) merges the splits into Output.
+    Q, Output [batch, seqlen_q, heads, dim]; K, V [batch, seqlen_kv, heads, dim]; Output is
+    parameter 5."""
+    scale = (1.0 / dim) ** 0.5 * 1.44269504
+    shape_q = [batch, seqlen_q, heads, dim]
+    shape_kv = [batch, seqlen_kv, heads, dim]
+    part_shape = [batch, seqlen_q, heads, num_split, dim]
+    acc = "float"
+    per = seqlen_kv // num_split
+
+    @T.macro
+    def scores(K: T.Tensor(shape_kv, dtype), q_s: T.SharedBuffer([block_M, dim], dtype),
+               k_s: T.SharedBuffer([block_N, dim], dtype),
+               s: T.FragmentBuffer([block_M, block_N], acc), k: T.int32, mid: T.int32,
+               hid: T.int32, bid: T.int32, sid: T.int32):
+        T.copy(K[bid, per * sid + k * block_N:per * sid + (k + 1) * block_N, hid, :], k_s)
+        if is_causal:
+            for i, j in T.Parallel(block_M, block_N):
+                s[i, j] = T.if_then_else(mid * block_M + i >= k * block_N + j, 0,
+                                         -T.infinity(acc))
+        else:
+            T.clear(s)
+        T.gemm(q_s, k_s, s, transpose_B=True, policy=T.GemmWarpPolicy.FullRow)
+
+    @T.macro
+    def pv(V: T.Tensor(shape_kv, dtype), v_s: T.SharedBuffer([block_M, dim], dtype),
+           s_cast: T.FragmentBuffer([block_M, block_N], dtype),
+           o: T.FragmentBuffer([block_M, dim], acc), k: T.int32, hid: T.int32, bid: T.int32,
+           sid: T.int32):
+        T.copy(V[bid, per * sid + k * block_N:per * sid + (k + 1) * block_N, hid, :], v_s)
+        T.gemm(s_cast, v_s, o, policy=T.GemmWarpPolicy.FullRow)
+
+    @T.macro
+    def softmax(s: T.FragmentBuffer([block_M, block_N], acc),
+                s_cast: T.FragmentBuffer([block_M, block_N], dtype),
+                m: T.FragmentBuffer([block_M], acc), m_prev: T.FragmentBuffer([block_M], acc),
+                alpha: T.FragmentBuffer([block_M], acc), rsum: T.FragmentBuffer([block_M], acc),
+                l: T.FragmentBuffer([block_M], acc)):
+        T.copy(m, m_prev)
+        T.fill(m, -T.infinity(acc))
+        T.reduce_max(s, m, dim=1, clear=False)
+        for i in T.Parallel(block_M):
+            alpha[i] = T.exp2(m_prev[i] * scale - m[i] * scale)
+        for i, j in T.Parallel(block_M, block_N):
+            s[i, j] = T.exp2(s[i, j] * scale - m[i] * scale)
+        T.reduce_sum(s, rsum, dim=1)
+        for i in T.Parallel(block_M):
+            l[i] = l[i] * alpha[i] + rsum[i]
+        T.copy(s, s_cast)
+
+    @T.macro
+    def rescale(o: T.FragmentBuffer([block_M, dim], acc), alpha: T.FragmentBuffer([block_M], acc)):
+        for i, j in T.Parallel(block_M, dim):
+            o[i, j] *= alpha[i]
+
+    @T.macro
+    def flash_attn_split(Q: T.Tensor(shape_q, dtype), K: T.Tensor(shape_kv, dtype),
+                         V: T.Tensor(shape_kv, dtype),
+                         glse: T.Tensor([batch, heads, num_split, seqlen_q], dtype),
+                         Output_partial: T.Tensor(part_shape, dtype)):
+        with T.Kernel(T.ceildiv(seqlen_q, block_M), heads * batch, num_split,
+                      threads=128) as (bx, by, bz):
+            q_s = T.alloc_shared([block_M, dim], dtype)
+            k_s = T.alloc_shared([block_N, dim], dtype)
+            v_s = T.alloc_shared([block_N, dim], dtype)
+            o_s = T.alloc_shared([block_M, dim], dtype)
+            s = T.alloc_fragment([block_M, block_N], acc)
+            s_cast = T.alloc_fragment([block_M, block_N], dtype)
+            o = T.alloc_fragment([block_M, dim], acc)
+            m = T.alloc_fragment([block_M], acc)
+            m_prev = T.alloc_fragment([block_M], acc)
+            alpha = T.alloc_fragment([block_M], acc)
+            rsum = T.alloc_fragment([block_M], acc)
+            l = T.alloc_fragment([block_M], acc)
+            mid = bx
+            hid = by % heads
+            bid = by // heads
+            sid = bz
+            T.copy(Q[bid, mid * block_M:(mid + 1) * block_M, hid, :], q_s)
+            T.fill(o, 0)
+            T.fill(l, 0)
+            T.fill(m, -T.infinity(acc))
+            n_kv = (T.min(T.ceildiv(seqlen_kv, block_N), T.ceildiv((mid + 1) * block_M, block_N))
+                    if is_causal else T.ceildiv(per, block_N))
+            for k in T.Pipelined(n_kv, num_stages=2):
+                scores(K, q_s, k_s, s, k, mid, hid, bid, sid)
+                softmax(s, s_cast, m, m_prev, alpha, rsum, l)
+                rescale(o, alpha)
+                pv(V, v_s, s_cast, o, k, hid, bid, sid)
+            for i, j in T.Parallel(block_M, dim):
+                o[i, j] /= l[i]
+            for i in T.Parallel(block_M):
+                l[i] = T.log2(l[i]) + m[i] * scale
+            T.copy(l, glse[bid, hid, sid, mid * block_M:(mid + 1) * block_M])
+            T.copy(o, o_s)
+            T.copy(o_s, Output_partial[bid, mid * block_M:(mid + 1) * block_M, hid, sid, :])
+
+    @T.macro
+    def combine(glse: T.Tensor([batch, heads, num_split, seqlen_q], dtype),
+                Output_partial: T.Tensor(part_shape, dtype), Output: T.Tensor(shape_q, dtype)):
+        with T.Kernel(T.ceildiv(seqlen_q, block_M), heads, batch, threads=128) as (bx, by, bz):
+            po = T.alloc_fragment([block_M, dim], dtype)
+            po_s = T.alloc_shared([block_M, dim], dtype)
+            o_acc = T.alloc_fragment([block_M, dim], acc)
+            o_s = T.alloc_shared([block_M, dim], dtype)
+            lse = T.alloc_fragment([num_split, block_M], dtype)
+            lse_k = T.alloc_fragment([block_M], acc)
+            lse_sum = T.alloc_fragment([block_M], acc)
+            lse_max = T.alloc_fragment([block_M], acc)
+            w = T.alloc_fragment([block_M], acc)
+            T.clear(lse_sum)
+            T.clear(o_acc)
+            T.copy(glse[bz, by, :, bx * block_M:(bx + 1) * block_M], lse)
+            T.reduce_max(lse, lse_max, dim=0, clear=False)
+            for k in T.Pipelined(num_split):
+                T.copy(lse[k, :], lse_k)
+                for i in T.Parallel(block_M):
+                    lse_sum[i] += T.exp2(lse_k[i] - lse_max[i])
+            for i in T.Parallel(block_M):
+                lse_sum[i] = T.log2(lse_sum[i]) + lse_max[i]
+            for k in T.Pipelined(num_split, num_stages=2):
+                T.copy(Output_partial[bz, bx * block_M:(bx + 1) * block_M, by, k, :], po_s)
+                T.copy(po_s, po)
+                T.copy(lse[k, :], lse_k)
+                for i in T.Parallel(block_M):
+                    w[i] = T.exp2(lse_k[i] - lse_sum[i])
+                for i, j in T.Parallel(block_M, dim):
+                    o_acc[i, j] += po[i, j] * w[i]
+            T.copy(o_acc, o_s)
+            T.copy(o_s, Output[bz, bx * block_M:(bx + 1) * block_M, by, :])
+
+    @T.prim_func
+    def main(Q: T.Tensor(shape_q, dtype), K: T.Tensor(shape_kv, dtype),
+             V: T.Tensor(shape_kv, dtype),
+             glse: T.Tensor([batch, heads, num_split, seqlen_q], dtype),
+             Output_partial: T.Tensor(part_shape, dtype), Output: T.Tensor(shape_q, dtype)):
+        flash_attn_split(Q, K, V, glse, Output_partial)
+        combine(glse, Output_partial, Output)
+
+    return main
+
+
 def flashattn_varlen(batch, UQ, UKV, heads, dim, is_causal=False, groups=1, block_M=64,
                      block_N=64, dtype="float16"):
     """The program structure of examples/flash_attention/example_mha_fwd_varlen.py:222-358:
