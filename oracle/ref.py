@@ -151,6 +151,18 @@ def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return (up.float() * F.silu(gate.float())).to(gate.dtype)
 
 
+def mlp_ref(x, gate_weight, up_weight, down_weight):
+    """tpu_demo/ppl/mlp/mlp_bf16.py:98-131 with whole blocks: gate = x Wg^T and up = x Wu^T
+    (fp32 accumulation, stored as the 16-bit dtype), SiLU(gate) * up in fp32 rounded to the
+    16-bit dtype, out = gated Wd^T (fp32 accumulation, 16-bit result)."""
+    dt = x.dtype
+    gate = (x.float() @ gate_weight.float().t()).to(dt)
+    up = (x.float() @ up_weight.float().t()).to(dt)
+    g = gate.float()
+    h = (g / (1.0 + torch.exp(-g)) * up.float()).to(dt)
+    return (h.float() @ down_weight.float().t()).to(dt)
+
+
 # ------------------------------------------------------------------------------------------------
 # FlashAttention — tpu_demo/flashattn/tpu_test_flashattn_bf16.py:171-182 (ref_program):
 #   scores = einsum('bqhd,bkhd->bhqk', Q.float(), K.float()) / sqrt(dim); causal tril mask;

@@ -405,3 +405,12 @@ def test_splitkv_inference_program_recognised():
     with pytest.raises(UnsupportedProgram, match="causal"):
         tilelang.compile(programs.mha_inference(1, 32, 128, 8192, 128, is_causal=True),
                          out_idx=[5])
+
+
+def test_mlp_program_recognised_with_whole_blocks_only():
+    k = tilelang.compile(programs.deepseek_mlp(64, 256, 512, 128, 256, 512), out_idx=[0])
+    a = k.plan.attrs
+    assert k.plan.family == "mlp" and (a["x"], a["wg"], a["wu"], a["wd"], a["out"]) == (1, 2, 3, 4, 0)
+    assert (a["M"], a["hidden"], a["inter"]) == (128, 256, 512)
+    with pytest.raises(UnsupportedProgram, match="whole blocks"):
+        tilelang.compile(programs.deepseek_mlp(8, 8, 8, 16, 16, 16), out_idx=[0])

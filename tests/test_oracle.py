@@ -627,3 +627,29 @@ def test_mha_inference_ref_and_split_combine():
     s = torch.einsum("bqhd,bkhd->bhqk", q.float(), k.float()) / math.sqrt(D)
     torch.testing.assert_close(glse[:, :, 0], torch.logsumexp(s, -1) / math.log(2), rtol=1e-5,
                                atol=1e-5)
+
+
+def test_mlp_ref_composition_and_loops():
+    """MLP oracle: equals the pinned gemm / SwiGLU oracles composed (matmul_ref with trans_b,
+    swiglu_ref), and a scalar-loop evaluation of the program's steps on a tiny case (gate/up
+    rounded to bf16, SiLU(g) = g / (1 + e^-g) in fp32, one rounding of the product)."""
+    g = torch.Generator().manual_seed(46)
+    M, Hd, I = 6, 8, 12
+    x = torch.randn(M, Hd, generator=g).bfloat16()
+    wg, wu = (torch.randn(I, Hd, generator=g).bfloat16() for _ in range(2))
+    wd = torch.randn(Hd, I, generator=g).bfloat16()
+    got = ref.mlp_ref(x, wg, wu, wd)
+    gate = ref.matmul_ref(x, wg, torch.bfloat16, trans_b=True)
+    up = ref.matmul_ref(x, wu, torch.bfloat16, trans_b=True)
+    exp = ref.matmul_ref(ref.swiglu_ref(gate, up), wd, torch.bfloat16, trans_b=True)
+    torch.testing.assert_close(got.float(), exp.float(), rtol=0, atol=0)
+    xf, wgf, wuf, wdf = (t.float().tolist() for t in (x, wg, wu, wd))
+    for r in range(M):
+        h = []
+        for i in range(I):
+            gv = float(torch.tensor(sum(xf[r][k] * wgf[i][k] for k in range(Hd))).bfloat16())
+            uv = float(torch.tensor(sum(xf[r][k] * wuf[i][k] for k in range(Hd))).bfloat16())
+            h.append(float(torch.tensor(gv / (1.0 + math.exp(-gv)) * uv).bfloat16()))
+        for c in range(Hd):
+            o = float(torch.tensor(sum(h[i] * wdf[c][i] for i in range(I))).bfloat16())
+            assert abs(o - float(got[r, c])) <= 2 ** -7 * abs(o) + 1e-6

@@ -59,6 +59,16 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     elif f == "flashattn":
         ops.flash_attn_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"], a["sm_scale"],
                            operand_dtype=odt)
+    elif f == "mlp":
+        # gate / up projections into 16-bit temporaries, SiLU(gate) * up, down projection
+        x, out = t[a["x"]], t[a["out"]]
+        M, I = a["M"], a["inter"]
+        gate = torch.empty(M, I, dtype=x.dtype, device=x.device)
+        up = torch.empty_like(gate)
+        ops.gemm(x, t[a["wg"]], gate, True)
+        ops.gemm(x, t[a["wu"]], up, True)
+        ops.swiglu(gate, up, gate)
+        ops.gemm(gate, t[a["wd"]], out, True)
     elif f == "sigmoid":
         ops.sigmoid(t[a["x"]], t[a["y"]])
     elif f == "gather":

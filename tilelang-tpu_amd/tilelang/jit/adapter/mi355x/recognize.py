@@ -187,6 +187,7 @@ _ALLOWED_OPS = {
                                        "reduce_sum"),
     "elementwise": _COPY + _FILL_OPS + ("ppl_add", "ppl_sub", "ppl_mul", "ppl_div", "ppl_add_C",
                                         "ppl_mul_C", "ppl_exp", "ppl_rsqrt", "ppl_sigmoid"),
+    "mlp": _COPY + _FILL_OPS + _GEMM + ("ppl_exp", "ppl_mul_C", "ppl_add", "ppl_div", "ppl_mul"),
 }
 
 
@@ -224,6 +225,7 @@ _PARAM_ATTRS = {
     "topk": ("src", "values", "indices"),
     "row_reduce": ("x", "y"),
     "elementwise": (),
+    "mlp": ("x", "wg", "wu", "wd", "out"),
 }
 
 
@@ -569,6 +571,65 @@ def _flashattn_splitkv(pf, qk, pv, Q, K, V, Opart) -> Plan:
         q=_index(pf, Q), k=_index(pf, K), v=_index(pf, V), o=_index(pf, O), B=B, S=Sq, S_kv=Skv,
         H=H, H_kv=Hkv, D=D, causal=False, sm_scale=sm_scale, dtype=Q.dtype, operand_dtype=None,
         layout="bshd_kv", num_split=ns, glse=_index(pf, lses[0]), partial=_index(pf, Opart)))
+
+
+def _mlp(pf, names) -> Plan:
+    """tpu_demo/ppl/mlp/mlp_bf16.py:10-141 (DeepSeek-V3 MLP): gate / up projections
+    x W^T (ppl_gemm transpose_B into 16-bit tiles), SiLU(gate) * up in fp32 rounded once to
+    the 16-bit type, down projection gated Wd^T. Every workgroup reduces over one hidden block
+    and one intermediate block and overwrites its output block, so the program is the MLP only
+    when those blocks are whole (Block_h = hidden_size, Block_i = intermediate_size); other
+    blockings store a partial, order-dependent result that is not compiled."""
+    fam = "mlp"
+    g = list(_ops(pf, _GEMM))
+    if len(g) != 3 or not all(op.kwargs.get("transpose_B") for op in g):
+        _fail(fam, "expected three ppl_gemm with transpose_B (gate, up, down)")
+    a = [_buf(op.args[0]) for op in g]
+    shared = [(i, j) for i in range(3) for j in range(i + 1, 3) if a[i] is a[j]]
+    if len(shared) != 1:
+        _fail(fam, "gate and up projections must multiply the same x tile")
+    i, j = shared[0]
+    down = g[3 - i - j]
+    divs = list(_ops(pf, ("ppl_div",)))
+    if len(divs) != 1:
+        _fail(fam, "expected one ppl_div (SiLU)")
+    num = _buf(divs[0].args[1])  # SiLU numerator: the fp32 copy of the gate tile
+
+    def feeds(tile, target):
+        return any(_buf(op.args[0]) is tile and _buf(op.args[1]) is target
+                   for op in _ops(pf, _COPY)) or tile is target
+    gate = [op for op in (g[i], g[j]) if feeds(_buf(op.args[2]), num)]
+    if len(gate) != 1:
+        _fail(fam, "could not tell the gate projection (the SiLU input) from the up projection")
+    gate = gate[0]
+    up = g[i] if gate is g[j] else g[j]
+    x = _source_param(pf, a[i])
+    wg, wu = _source_param(pf, _buf(gate.args[1])), _source_param(pf, _buf(up.args[1]))
+    wd = _source_param(pf, _buf(down.args[1]))
+    out = _sink_param(pf, _buf(down.args[2]))
+    if None in (x, wg, wu, wd, out) or len({id(p) for p in (x, wg, wu, wd, out)}) != 5:
+        _fail(fam, "could not trace x, gate_weight, up_weight, down_weight and output")
+    M, Hd = _shape(x)
+    I = _shape(wg)[0]
+    if list(_shape(out)) != [M, Hd] or list(_shape(wg)) != [I, Hd] or \
+            list(_shape(wu)) != [I, Hd] or list(_shape(wd)) != [Hd, I]:
+        _fail(fam, "shapes must be x, output [rows, hidden], gate / up weights [inter, hidden], "
+                   "down weight [hidden, inter]")
+    dt = x.dtype
+    if dt not in ("bfloat16", "float16") or any(p.dtype != dt for p in (wg, wu, wd, out)):
+        _fail(fam, "parameters must all be bfloat16 or all float16")
+    for op in g:
+        if {_buf(op.args[0]).dtype, _buf(op.args[1]).dtype, _buf(op.args[2]).dtype} != {dt}:
+            _fail(fam, "the projections must multiply and store 16-bit tiles of the parameter "
+                       "dtype")
+    bh, bi = _shape(a[i])[1], _shape(_buf(gate.args[1]))[0]
+    if bh != Hd or bi != I:
+        _fail(fam, f"blocks of {bh} hidden / {bi} intermediate columns: each workgroup reduces "
+                   f"over one block and overwrites its output block, which is the MLP only for "
+                   f"whole blocks (Block_h = {Hd}, Block_i = {I})")
+    return Plan(fam, pf.params, [_index(pf, out)], dict(
+        x=_index(pf, x), wg=_index(pf, wg), wu=_index(pf, wu), wd=_index(pf, wd),
+        out=_index(pf, out), M=M, hidden=Hd, inter=I, dtype=dt))
 
 
 def _seq_dim(pf, Q: Buffer) -> Optional[int]:
@@ -1084,6 +1145,8 @@ def recognize(pf) -> Plan:
     ints = [p for p in pf.params if p.dtype == "int32"]
     n_gemm = sum(1 for op in _ops(pf, _GEMM))
     try:
+        if n_gemm == 3 and "ppl_div" in names and not names & {"ppl_reduce_max", "reduce_max"}:
+            return _audit(pf, _mlp(pf, names))
         if n_gemm >= 3:
             return _audit(pf, _mla(pf, names))
         if n_gemm == 2 and names & {"ppl_reduce_max", "reduce_max"}:
@@ -1121,5 +1184,5 @@ def recognize(pf) -> Plan:
         raise UnsupportedProgram(f"{pf.name}: could not analyse program: {e}") from e
     raise UnsupportedProgram(
         f"{pf.name}: no gfx950 kernel matches this program (ops: {sorted(names)}). Supported "
-        f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla, sigmoid, gather, topk, "
+        f"families: rmsnorm, gemm, rope, swiglu, flashattn, mla, mlp, sigmoid, gather, topk, "
         f"row_reduce, elementwise")

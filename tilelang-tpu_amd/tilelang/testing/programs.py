@@ -330,6 +330,71 @@ def swi_glu(Block_w, Block_c, C, W, dtype="bfloat16"):
     return swiglu
 
 
+def deepseek_mlp(Block_bs, Block_h, Block_i, batch_seq, hidden_size, intermediate_size,
+                 dtype="bfloat16"):
+    """The program structure of tpu_demo/ppl/mlp/mlp_bf16.py:10-141 (DeepSeek-V3 MLP): per
+    (row block, hidden block, intermediate block) the gate and up projections
+    x_blk @ W_blk^T are ppl_gemm into 16-bit tiles, converted to fp32; SiLU(gate) = gate /
+    (1 + exp(-gate)) times up in fp32, rounded to the 16-bit type; the down projection
+    gated @ Wd_blk^T is stored to the output block. Parameters: output [batch_seq, hidden],
+    x [batch_seq, hidden], gate_weight, up_weight [intermediate, hidden], down_weight
+    [hidden, intermediate]."""
+    acc = "float32"
+
+    @T.macro
+    def silu(g: T.Tensor((Block_bs, Block_i), acc), out: T.Tensor((Block_bs, Block_i), acc),
+             neg: T.Tensor((Block_bs, Block_i), acc), ones: T.Tensor((Block_bs, Block_i), acc),
+             den: T.Tensor((Block_bs, Block_i), acc)):
+        T.ppl_mul_C(neg, g, T.float32(-1.0))
+        T.ppl_exp2(neg)  # natural exp on BM1690 (customize.py:328-329)
+        T.ppl_add(den, neg, ones)
+        T.ppl_div(out, g, den)
+
+    @T.prim_func
+    def main(output: T.Tensor((batch_seq, hidden_size), dtype),
+             x: T.Tensor((batch_seq, hidden_size), dtype),
+             gate_weight: T.Tensor((intermediate_size, hidden_size), dtype),
+             up_weight: T.Tensor((intermediate_size, hidden_size), dtype),
+             down_weight: T.Tensor((hidden_size, intermediate_size), dtype)):
+        with T.Kernel(T.ceildiv(batch_seq, Block_bs), T.ceildiv(hidden_size, Block_h),
+                      T.ceildiv(intermediate_size, Block_i), is_cpu=True) as (bx, by, bz):
+            xb = T.alloc_shared((Block_bs, Block_h), dtype)
+            wg = T.alloc_shared((Block_i, Block_h), dtype)
+            wu = T.alloc_shared((Block_i, Block_h), dtype)
+            wd = T.alloc_shared((Block_h, Block_i), dtype)
+            g16 = T.alloc_shared((Block_bs, Block_i), dtype)
+            u16 = T.alloc_shared((Block_bs, Block_i), dtype)
+            d16 = T.alloc_shared((Block_bs, Block_h), dtype)
+            g32 = T.alloc_shared((Block_bs, Block_i), acc)
+            u32 = T.alloc_shared((Block_bs, Block_i), acc)
+            s32 = T.alloc_shared((Block_bs, Block_i), acc)
+            h32 = T.alloc_shared((Block_bs, Block_i), acc)
+            h16 = T.alloc_shared((Block_bs, Block_i), dtype)
+            neg = T.alloc_shared((Block_bs, Block_i), acc)
+            ones = T.alloc_shared((Block_bs, Block_i), acc)
+            den = T.alloc_shared((Block_bs, Block_i), acc)
+            T.ppl_fill(ones, T.float32(1.0))
+            T.ppl_copy(x[bx * Block_bs:(bx + 1) * Block_bs, by * Block_h:(by + 1) * Block_h], xb)
+            T.ppl_copy(gate_weight[bz * Block_i:(bz + 1) * Block_i,
+                                   by * Block_h:(by + 1) * Block_h], wg)
+            T.ppl_copy(up_weight[bz * Block_i:(bz + 1) * Block_i,
+                                 by * Block_h:(by + 1) * Block_h], wu)
+            T.ppl_copy(down_weight[by * Block_h:(by + 1) * Block_h,
+                                   bz * Block_i:(bz + 1) * Block_i], wd)
+            T.ppl_gemm(xb, wg, g16, transpose_B=True)
+            T.ppl_copy(g16, g32)
+            silu(g32, s32, neg, ones, den)
+            T.ppl_gemm(xb, wu, u16, transpose_B=True)
+            T.ppl_copy(u16, u32)
+            T.ppl_mul(h32, s32, u32)
+            T.ppl_copy(h32, h16)
+            T.ppl_gemm(h16, wd, d16, transpose_B=True)
+            T.ppl_copy(d16, output[bx * Block_bs:(bx + 1) * Block_bs,
+                                   by * Block_h:(by + 1) * Block_h])
+
+    return main
+
+
 def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
               dtype="bfloat16", gemm_dtype=None):
     """tpu_test_flashattn_bf16.py:14-135 (fp16 twin); dtype float32 with gemm_dtype float16
