@@ -3,6 +3,8 @@
 // rounding per output, 16-byte non-temporal stores.
 #include "tlm_common.h"
 
+#include <algorithm>
+
 namespace {
 
 // ------------------------------------------------------------------------------------------------
@@ -128,6 +130,49 @@ __global__ __launch_bounds__(kRopeThreads) void rope_vec(
       o[j] = H::pack(fmaf(xe, ce, -(xo * so)), fmaf(xo, co, xe * se));
     }
     st_nt(dst, o);
+  }
+}
+
+// One token per workgroup iteration: the token's cos / sin vector is loaded once per lane and
+// applied to all its q and k heads (LPR lanes per head row, 256 / LPR rows in flight per pass,
+// four passes' loads issued before any store).
+template <bool IS_BF16, int LPR>
+__global__ __launch_bounds__(kRopeThreads) void rope_tok(
+    const u32x4* __restrict__ q, const u32x4* __restrict__ k, const u32x4* __restrict__ cos_t,
+    const u32x4* __restrict__ sin_t, u32x4* __restrict__ q_out, u32x4* __restrict__ k_out,
+    int64_t tokens, int hq, int hk) {
+  using H = h16<IS_BF16>;
+  constexpr int SLOTS = kRopeThreads / LPR;  // head rows per pass
+  constexpr int U = 4;                        // passes in flight
+  const int htot = hq + hk;
+  const int sub = threadIdx.x % LPR, slot = threadIdx.x / LPR;
+  for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+    const u32x4 c = cos_t[t * LPR + sub], s = sin_t[t * LPR + sub];
+    for (int h0 = slot; h0 < htot; h0 += U * SLOTS) {
+      u32x4 xs[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int h = h0 + u * SLOTS;
+        if (h < htot)
+          xs[u] = ld_nt(h < hq ? q + (t * hq + h) * LPR + sub : k + (t * hk + (h - hq)) * LPR + sub);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int h = h0 + u * SLOTS;
+        if (h >= htot) break;
+        const u32x4 x = xs[u];
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float xe = H::lo(x[j]), xo = H::hi(x[j]);
+          const float ce = H::lo(c[j]), co = H::hi(c[j]);
+          const float se = H::lo(s[j]), so = H::hi(s[j]);
+          o[j] = H::pack(fmaf(xe, ce, -(xo * so)), fmaf(xo, co, xe * se));
+        }
+        st_nt(h < hq ? q_out + (t * hq + h) * LPR + sub : k_out + (t * hk + (h - hq)) * LPR + sub,
+              o);
+      }
+    }
   }
 }
 
@@ -308,6 +353,12 @@ template <bool IS_BF16, int LPR>
 void launch_rope_vec(const void* q, const void* k, const void* c, const void* s, void* qo,
                      void* ko, int64_t tokens, int hq, int hk, hipStream_t st) {
   constexpr int RPP = kRopeThreads / LPR;
+  if (hq + hk >= RPP) {  // a token fills at least one pass: one token per workgroup iteration
+    rope_tok<IS_BF16, LPR><<<(unsigned)std::min<int64_t>(tokens, 1 << 20), kRopeThreads, 0,
+                             st>>>((const u32x4*)q, (const u32x4*)k, (const u32x4*)c,
+                                   (const u32x4*)s, (u32x4*)qo, (u32x4*)ko, tokens, hq, hk);
+    return;
+  }
   const int64_t nrows = tokens * (hq + hk);
   unsigned grid = grid_for(nrows, RPP * kRopeRowsPerThread, INT32_MAX);
   rope_vec<IS_BF16, LPR><<<grid, kRopeThreads, 0, st>>>(
