@@ -354,7 +354,41 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
     }
   }
 
-  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i
+  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i.
+  // 16-bit C with N % 8 == 0: the wave's 128 x 64 sub-tile is rounded into its own 16 KB of
+  // LDS (the operand stages are free: the last barrier ended every operand read and no LDS-DMA
+  // is in flight) and written back as 16-byte row vectors, full 128-byte lines per 8 lanes,
+  // instead of 2-byte stores. Stage row r holds 64 columns (128 bytes); its 16-byte chunk c sits
+  // at c ^ ((r / 4) % 8), so the four row groups of one 2-byte write and the two rows of one
+  // 16-lane read hit distinct banks.
+  if constexpr (OUT != TLM_F32) {
+    if (N % 8 == 0) {
+      uint16_t* stg = (uint16_t*)smem + wave * (128 * 64);
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = mt * 16 + 4 * (lane >> 4) + i, c = nt * 16 + (lane & 15);
+            const float v = acc[mt][nt][i];
+            stg[r * 64 + 8 * ((c >> 3) ^ ((r >> 2) & 7)) + (c & 7)] =
+                (uint16_t)(OUT == TLM_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+          }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint16_t* Cb = (uint16_t*)C;
+#pragma unroll
+      for (int it = 0; it < 16; ++it) {
+        const int idx = it * 64 + lane, r = idx >> 3, c8 = idx & 7;
+        const u32x4 v = *(const u32x4*)(stg + r * 64 + 8 * (c8 ^ ((r >> 2) & 7)));
+        const int row = m0 + wm * 128 + r, col = n0 + wn * 64 + 8 * c8;
+        if (row < M && col < N) *(u32x4*)(Cb + (int64_t)row * N + col) = v;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
