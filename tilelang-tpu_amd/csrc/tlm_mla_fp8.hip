@@ -15,22 +15,25 @@
 //     one or more sequences: a sequence entirely inside one range is written to the output
 //     directly; the pieces of a longer one go to partial slots (bf16 O, fp32 lse; one for the
 //     range's first piece, one for its last) merged by the combine kernel;
-//   * workgroup = 64 heads x one range = 2 wave pairs x 32 heads. The two waves of a pair split a
-//     64-token tile by tokens for S^T = K Q^T (one 32-token block each, all 576 dims) and by V
-//     dims for O^T = V^T P^T (256 dims each, all 64 tokens), exchanging block maxima and the e4m3
-//     P^T block through LDS: no work is duplicated and each wave holds only 128 O accumulators;
-//   * Q^T stays in VGPRs for the whole piece, split per head into two e4m3 terms
+//   * workgroup = 64 heads x one range, 8 waves (two per SIMD) = 2 head blocks of 32 x 4 waves.
+//     For S^T = K Q^T the four waves of a head block split a 64-token tile into 2 token blocks x
+//     2 halves of the 576 QK dims, and each wave keeps half of its block's tokens, adding the
+//     other half's partial scores received through LDS; for O^T = V^T P^T they split the 512 V
+//     dims four ways over all 64 tokens. No work is duplicated; a wave holds 64 O accumulators;
+//   * Q^T stays in VGPRs for the whole piece (72 per wave), split per head into two e4m3 terms
 //     q / s = hi + lo (s a power of two putting max|q| at <= 448), which keeps bf16-level accuracy
 //     while S^T runs on v_mfma_f32_32x32x64_f8f6f4 straight from the fp8 cache bytes (2 MFMAs per
-//     64 dims: the cost of one bf16 MFMA and no K conversion);
+//     64 dims: the cost of one bf16 MFMA and no K conversion; the rope dims take the hi term on
+//     one dim half and the lo term on the other, so both halves run 9 MFMAs);
 //   * O^T = V^T P^T on the MX-scaled fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): V^T comes
 //     straight from the row-major fp8 tile through ds_read_b64_tr_b8 (8 tokens of one dim per
 //     lane); P^T is rounded once to e4m3 on a power-of-two scale per (head, 32-token block),
 //     passed to the MFMA as its E8M0 block scale (one e4m3 term: relative RMS error ~1.3% of the
 //     output against the exact softmax, against ~0.2% for two terms at one more MFMA per dim
 //     block). K rows are fed to the S^T MFMA in the order tau (bits 2 and 3 of the row index
-//     swapped) so S^T accumulator element i of lane l is token 16(i/8) + 8(l/32) + i%8, the
-//     order of the P^T blocks exchanged through LDS;
+//     swapped; bit 4 flipped on dim half 1) so that accumulator elements 0..7 of lane l are the 8
+//     consecutive tokens 16 dq + 8(l/32) + 0..7 that the wave keeps, the byte order of the P^T
+//     blocks exchanged through LDS;
 //   * softmax without accumulator rescaling: a segment fixes its reference max m from its first
 //     tile and accumulates 2^(x - m); only when a tile's max exceeds m by more than 64 (log2
 //     units) does the segment end (its normalised partial is merged into a scratch slot) and a new
@@ -42,7 +45,11 @@
 //     stale NaN bytes); an explicit vmcnt wait plus s_barrier hands a stage over;
 //   * LDS layout per stage: latent rows of 512 B then rope rows of 64 B, 16-byte chunks XOR-
 //     swizzled so that the row reads of S^T (ds_read_b128) and the transposed reads of V^T
-//     (ds_read_b64_tr_b8) are both bank-conflict free.
+//     (ds_read_b64_tr_b8) are both bank-conflict free;
+//   * the softmax of tile t runs as short levels of independent instructions between the S^T
+//     MFMAs of tile t + 1 (a wave issues in order; a long dependent chain there would hold back
+//     the MFMAs), and nothing in the tile loop may be spilled: a scratch reload there costs a
+//     vmcnt(0) wait on the ring's in-flight LDS-DMA loads.
 #include "tlm_common.h"
 
 #include <algorithm>
@@ -61,32 +68,17 @@ constexpr int F8_TILE = 64;                          // tokens per ring stage
 constexpr int F8_LAT = F8_TILE * F8_DV;              // latent bytes per stage
 constexpr int F8_STAGE = F8_LAT + F8_TILE * F8_DPE;  // + rope bytes
 constexpr int F8_NSTAGE = 3;
-constexpr int F8_HEADS = 64;                         // heads per workgroup (2 pairs x 32)
-constexpr int F8_LOADS = 9;                          // LDS-DMA loads per thread per stage
+constexpr int F8_HEADS = 64;                         // heads per workgroup (2 blocks x 32)
+constexpr int F8_LAT_LOADS = 4;                      // latent LDS-DMA loads per thread per stage
 constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
-constexpr int F8_WAVE_F4 = 8 * 4 * 64;               // 4-element groups per wave in a partial slot
-constexpr int F8_QREG = 4;                           // Q k-steps held in VGPRs; the rest in LDS
-#ifndef F8_DMA_STEPS
-#define F8_DMA_STEPS 3
-#endif
-// The refill of the ring (F8_LOADS LDS-DMA instructions per thread) is spread over the first
-// F8_DMA_STEPS k-steps of the S^T MFMAs, so the tile two ahead is requested early in the step.
-constexpr int F8_DMA_PER_STEP = (F8_LOADS + F8_DMA_STEPS - 1) / F8_DMA_STEPS;
 
 // swizzled 16-byte chunk index of latent row r / rope row r
 TLM_DEV int swz_lat(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 TLM_DEV int swz_rope(int r) { return (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 // K-row order fed to the S^T MFMA (bits 2 and 3 swapped)
 TLM_DEV int tau(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
-
-TLM_DEV void wait_vm(int n) {  // s_waitcnt vmcnt(n), other counters untouched
-  if (n == 0)
-    __builtin_amdgcn_s_waitcnt(0x3f70);
-  else
-    __builtin_amdgcn_s_waitcnt(0x3f70 | F8_LOADS);
-}
 
 // Workgroup barrier that leaves the LDS-DMA loads of the ring in flight: waits for this wave's
 // LDS (and scalar) accesses only, so its LDS writes are visible to the other waves afterwards.
@@ -106,10 +98,10 @@ TLM_DEV T ldc(const T* p) {
 
 TLM_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// LDS reads of the ring issued as inline asm. Compiler-generated reads may be made to wait
-// (vmcnt(0)) for every outstanding LDS-DMA load, including the prefetch of the next stages, when
-// the compiler cannot prove they touch another stage. The caller waits with lds_wait() before
-// using the result.
+// LDS accesses issued as inline asm. Compiler-generated reads may be made to wait (vmcnt(0)) for
+// every outstanding LDS-DMA load, including the prefetch of the next stages, when the compiler
+// cannot prove they touch another stage; asm accesses also keep the lgkmcnt accounting of the
+// kernel exact. The caller waits (lgkm<N>()) and then orders the uses (order_after) itself.
 TLM_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -127,39 +119,38 @@ TLM_DEV i32x8 lds_2xb128(const void* p0, const void* p1) {
   const i32x4 a = lds_b128(p0), b = lds_b128(p1);
   return i32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
-// LDS write issued as inline asm, for the same reason (a compiler-generated write may be made to
-// wait for the ring's LDS-DMA loads); wg_barrier() waits for it (lgkmcnt(0)) before publishing.
 TLM_DEV void lds_write_b64(void* p, u32x2 v) {
   asm volatile("ds_write_b64 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
 }
-// s_waitcnt lgkmcnt(0) that also orders the uses of the given asm-loaded operands after it
-TLM_DEV void lds_wait(i32x8& a) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a) : : "memory"); }
+TLM_DEV void lds_write_b32(void* p, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
 // s_waitcnt lgkmcnt(n): all but the n most recent LDS accesses of this wave have completed (LDS
 // accesses complete in order; no scalar loads may be outstanding). n is a compile-time constant
 // after unrolling.
+template <int N>
+TLM_DEV void lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0xc07f | (N << 8));
+}
 TLM_DEV void lgkm_wait(int n) {
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0xc07f); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0xc27f); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0xc47f); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0xc67f); break;
-    default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+    case 0: lgkm<0>(); break;
+    case 1: lgkm<1>(); break;
+    case 2: lgkm<2>(); break;
+    case 3: lgkm<3>(); break;
+    case 4: lgkm<4>(); break;
+    case 5: lgkm<5>(); break;
+    case 6: lgkm<6>(); break;
+    default: lgkm<0>(); break;
   }
 }
+// makes later uses of an asm-loaded value depend on a preceding wait
 TLM_DEV void order_after(i32x8& a) { asm volatile("" : "+v"(a) : : "memory"); }
-TLM_DEV void lds_wait(i32x8& a, i32x8& b) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b) : : "memory");
-}
-TLM_DEV void lds_wait(i32x8& a, i32x8& b, i32x8& c) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c) : : "memory");
-}
-// s_waitcnt lgkmcnt(0) that also orders the uses of eight asm-loaded operands after it
-TLM_DEV void lds_wait(i32x2 (&r)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
-                 "+v"(r[6]), "+v"(r[7])
-               :
-               : "memory");
+TLM_DEV void order_after(i32x4& a) { asm volatile("" : "+v"(a) : : "memory"); }
+TLM_DEV f32x4 as_f32x4(i32x4 v) {
+  return f32x4{__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]),
+               __int_as_float(v[3])};
 }
 
 TLM_DEV f32x16 mfma_fp8(i32x8 a, i32x8 b, f32x16 c) {
@@ -207,7 +198,7 @@ struct F8Args {
   uint8_t* qsplit;  // [B * Hq][2][576] e4m3 hi and lo terms of q / 2^qexp (written by prep)
   int32_t* qexp;    // [B * Hq] power-of-two exponent of each head's Q scale
   float* part_lse;
-  u32x2* part_o;  // bf16 partial outputs, four per element
+  uint16_t* part_o;  // bf16 partial outputs [slot][head][512]
   uint16_t* out;
   int B, Hq, page, max_pages, G;
   int lmax;           // seqlens are clamped to [0, lmax = max_pages * page]
@@ -301,24 +292,20 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
   if (lane == 0) a.qexp[row] = ex;
 }
 
-// Q^T operand of one head for S^T = K Q^T, from the prep kernel's split: k-step s (64 dims: 0..7
-// latent, 8 rope), lane half hf holds dims 64 s + 32 hf + j at byte j. k-steps >= F8_QREG go to
-// the pair's LDS copy (written by one wave of the pair). Returns the scale 2^e of the head.
-TLM_DEV float load_q(const F8Args& a, int64_t row, int hf, i32x8 (&qhi)[F8_QREG],
-                     i32x8 (&qlo)[F8_QREG], i32x8* qt, bool write_qt) {
+// Q^T operand of one head for one dim half dq of S^T = K Q^T, from the prep kernel's split. Latent
+// k-step s (0..3) covers dims 256 dq + 64 s .. +63; lane half hf holds dims 32 hf .. 32 hf + 31 of
+// a k-step at bytes 0..31 (the byte order of the K operand read from the ring). The rope k-step
+// takes the hi term on dim half 0 and the lo term on dim half 1, so both halves run 9 MFMAs.
+// Returns the head's scale 2^e.
+TLM_DEV float load_q(const F8Args& a, int64_t row, int dq, int hf, i32x8 (&qhi)[4],
+                     i32x8 (&qlo)[4], i32x8& qpe) {
   const uint8_t* qs = a.qsplit + row * F8_QROW;
 #pragma unroll
-  for (int k = 0; k < F8_QREG; ++k) {
-    qhi[k] = *(const i32x8*)(qs + 64 * k + 32 * hf);
-    qlo[k] = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * k + 32 * hf);
+  for (int s = 0; s < 4; ++s) {
+    qhi[s] = *(const i32x8*)(qs + 256 * dq + 64 * s + 32 * hf);
+    qlo[s] = *(const i32x8*)(qs + F8_DV + F8_DPE + 256 * dq + 64 * s + 32 * hf);
   }
-  if (write_qt) {
-#pragma unroll
-    for (int k = F8_QREG; k < 9; ++k) {
-      qt[(2 * (k - F8_QREG)) * 64] = *(const i32x8*)(qs + 64 * k + 32 * hf);
-      qt[(2 * (k - F8_QREG) + 1) * 64] = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * k + 32 * hf);
-    }
-  }
+  qpe = *(const i32x8*)(qs + dq * (F8_DV + F8_DPE) + F8_DV + 32 * hf);
   return ldexpf(1.0f, a.qexp[row]);
 }
 
@@ -333,28 +320,44 @@ TLM_DEV F8Work f8_work(int x, int HG) {
   return F8Work{(k / HG) * 8 + xcd, k % HG};
 }
 
+// s_waitcnt vmcnt(N) with the other counters untouched
+template <int N>
+TLM_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x3f70 | N);
+}
+
+// Workgroup = 64 heads x one range, 8 waves (two per SIMD). Wave w: head block hb = w / 4 (32
+// heads) and q = w % 4, with token block tq = q % 2 and dim half dq = q / 2:
+//   * S^T: the wave computes the partial scores of the 32-token block tq over its half dq of the
+//     576 QK dims (9 MFMAs with Q in registers), keeps tokens 16 dq .. 16 dq + 15 of the block and
+//     adds the other half's partial for them, received through LDS;
+//   * O^T: the wave accumulates dims 128 q .. 128 q + 127 of the head block's 32 heads over all 64
+//     tokens (4 MFMAs) from the e4m3 P^T blocks that the head block's four waves publish.
+// Every wave runs the same barriers per tile (A: tile t + 1 landed and the partial scores of tile
+// t published, B: 16-token maxima, C: P^T blocks and sums).
 template <bool O_BF16>
-__global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
+__global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
   __shared__ __attribute__((aligned(1024))) uint8_t ring[F8_NSTAGE * F8_STAGE];
-  __shared__ float xmax[2][2][32];  // [pair][token block][head]: block maxima
-  __shared__ float xsum[2][2][32];  // [pair][token block][head]: block sums of P
-  // P^T blocks as e4m3: [pair][token block][head][32 tokens], and the E8M0 scale of each
-  // (block, head)
-  __shared__ __attribute__((aligned(16))) uint8_t xq[2][2][32][32];
-  __shared__ int xsc[2][2][32];
-  // Q^T k-steps F8_QREG..8 of each pair: [pair][(k - F8_QREG) * 2 + hi/lo][lane]
-  __shared__ __attribute__((aligned(16))) i32x8 qt[2][(9 - F8_QREG) * 2][64];
+  // partial S^T exchange: [head block][token block][receiving dim half][4-element group][lane]
+  __shared__ f32x4 xs[2][2][2][2][64];
+  // [head block][head], component q: 16-token maxima (log2 units) / sums of the rounded P
+  __shared__ f32x4 xmax[2][32];
+  __shared__ f32x4 xsum[2][32];
+  // P^T in e4m3: [head block][token block][16-token half][head][16 tokens]
+  __shared__ __attribute__((aligned(16))) uint8_t xq[2][2][2][32][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int pr = wave >> 1, dh = wave & 1;  // pair (32 heads), token block / dim half
+  const int hb = wave >> 2, q = wave & 3, tq = q & 1, dq = q >> 1;
   const int hh = lane & 31, hf = lane >> 5;
   const int HG = a.Hq / F8_HEADS;
   const F8Work wk = f8_work(blockIdx.x, HG);
   if (wk.g >= a.G) return;
   const int g = wk.g, hgi = wk.hgi;
-  const int head = hgi * F8_HEADS + pr * 32 + hh;
-  const int64_t T = ldc(a.cu + a.B);
-  const int64_t t_lo = (int64_t)g * T / a.G, t_hi = (int64_t)(g + 1) * T / a.G;
+  const int head = hgi * F8_HEADS + hb * 32 + hh;
+  // tile indices fit int32 (the tile prefix is int32)
+  const int T = ldc(a.cu + a.B);
+  const int t_lo = (int)((int64_t)g * T / a.G), t_hi = (int)((int64_t)(g + 1) * T / a.G);
   if (t_lo >= t_hi) return;
   const float kvs = a.kv_scale ? ldc(a.kv_scale) : 1.0f;
 
@@ -371,12 +374,12 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
 
   // ---- per-tile page table: lane j holds the first KV row of tile tb + j and the number of its
   // rows to load (the sequence's valid tokens that lie inside the pool; the rest read as zeros)
-  int64_t tb = INT64_MIN / 2;
+  int tb = INT32_MIN / 2;
   uint32_t tab_lo = 0, tab_hi = 0;
   int tab_n = 0;
-  auto build_table = [&](int64_t base) {
+  auto build_table = [&](int base) {
     tb = base;
-    const int64_t tj = base + lane;
+    const int tj = base + lane;
     tab_lo = tab_hi = 0;
     tab_n = 0;
     if (tj < t_hi) {
@@ -386,7 +389,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         if (a.cu[mid] <= tj) blo = mid; else bhi = mid - 1;
       }
       const int L = max(0, min(a.seqlens[blo], a.lmax));
-      const int tok0 = (int)(tj - a.cu[blo]) * F8_TILE;
+      const int tok0 = (tj - a.cu[blo]) * F8_TILE;
       const int valid = min(F8_TILE, L - tok0);
       const int64_t row0 =
           (int64_t)a.bt[(int64_t)blo * a.max_pages + tok0 / a.page] * a.page + tok0 % a.page;
@@ -399,36 +402,46 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   };
   build_table(t_lo);
 
-  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 3
+  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 3; every wave loads 8 latent rows
+  // (F8_LAT_LOADS instructions), waves 0..3 also 16 rope rows each
   struct Dma {  // one tile's source rows (base, byte count) and ring stage
     const uint8_t* bkv;
     const uint8_t* bpe;
     int nkv, npe;
     uint8_t* st;
   };
-  auto issue_setup = [&](int64_t t) {
+  auto stage = [&](int si) { return ring + si * F8_STAGE; };
+  auto next_stage = [](int si) { return si == F8_NSTAGE - 1 ? 0 : si + 1; };
+  int s_issue = 0;  // ring stage of the next tile to request
+  auto issue_setup = [&](int t) {
     if (t >= tb + 64) build_table(t);
-    const int j = (int)(t - tb);
+    const int j = t - tb;
     const int64_t row0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)tab_hi, j) << 32) |
                                    (uint32_t)__builtin_amdgcn_readlane((int)tab_lo, j));
     const int64_t nrow = __builtin_amdgcn_readlane(tab_n, j);
     const uint8_t* bkv = nrow > 0 ? a.kv + row0 * a.kv_stride : a.kv;
     const uint8_t* bpe = nrow > 0 ? a.k_pe + row0 * a.kpe_stride : a.k_pe;
-    return Dma{bkv, bpe, (int)(nrow * a.kv_stride), (int)(nrow * a.kpe_stride),
-               ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE};
+    const Dma d{bkv, bpe, (int)(nrow * a.kv_stride), (int)(nrow * a.kpe_stride), stage(s_issue)};
+    s_issue = next_stage(s_issue);
+    return d;
   };
-  // LDS-DMA instruction k (0..8) of this thread for a tile: 0..7 latent, 8 rope
+  const bool rope_loader = wave < 4;  // wave-uniform
+  // LDS-DMA instruction k of this thread for a tile: 0..F8_LAT_LOADS-1 latent, then rope
+  // latent instruction k of lane (c, h) = (lane % 32, lane / 32) reads row r = 8 w + 2 k + h at
+  // swizzled chunk c ^ swz_lat(r) = (c ^ (2 h + (w & 1))) ^ 4 k
+  const int lat_off = (2 * F8_LAT_LOADS * wave + hf) * (int)a.kv_stride;
+  const int lat_x16 = 16 * (hh ^ (2 * hf + (wave & 1)));
   auto issue_dma = [&](const Dma& d, int k) {
-    int ln = lane;
-    asm volatile("" : "+v"(ln));  // offsets recomputed per use, not hoisted into live registers
-    if (k < 8) {  // latent: 2 rows x 32 chunks per wave-instruction
-      const int r = 2 * (8 * wave + k) + (ln >> 5);
-      const int off = r * (int)a.kv_stride + 16 * ((ln & 31) ^ swz_lat(r));
+    if (k < F8_LAT_LOADS) {  // latent: 2 rows x 32 chunks per wave-instruction
+      const int ki = F8_LAT_LOADS * wave + k;
+      const int off = lat_off + 2 * k * (int)a.kv_stride + (lat_x16 ^ (64 * k));
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + (8 * wave + k) * 1024), 16,
-                                               off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + ki * 1024), 16, off, 0, 0,
+                                               0);
     } else {  // rope: 16 rows x 4 chunks per wave-instruction
+      int ln;  // lane id computed here, not kept in a register across the tile
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
       const int r = 16 * wave + (ln >> 2);
       const int off = r * (int)a.kpe_stride + 16 * ((ln & 3) ^ swz_rope(r));
       const __amdgpu_buffer_rsrc_t rp =
@@ -437,18 +450,31 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
                                                off, 0, 0, 0);
     }
   };
-  auto issue = [&](int64_t t) {
+  auto issue = [&](int t) {
     const Dma d = issue_setup(t);
 #pragma unroll
-    for (int k = 0; k < F8_LOADS; ++k) issue_dma(d, k);
+    for (int k = 0; k < F8_LAT_LOADS; ++k) issue_dma(d, k);
+    if (rope_loader) issue_dma(d, F8_LAT_LOADS);
+  };
+  // this wave's loads of all tiles but the last one issued have landed (or of all of them)
+  auto wait_ring = [&](bool keep_last) {
+    if (!keep_last)
+      wait_vmcnt<0>();
+    else if (rope_loader)
+      wait_vmcnt<F8_LAT_LOADS + 1>();
+    else
+      wait_vmcnt<F8_LAT_LOADS>();
   };
   issue(t_lo);
   if (t_lo + 1 < t_hi) issue(t_lo + 1);
 
   // ---- per-lane LDS read offsets
-  const int th = tau(hh);                  // K row of this lane within its 32-token block
-  const int fk = (2 * hf) ^ swz_lat(th);   // latent chunk of k-step s: (4 s) ^ fk
-  const int fr = (2 * hf) ^ swz_rope(th);  // rope chunks: fr, fr ^ 1
+  // K row of this lane: the MFMA row order tau within the 32-token block, with the block's halves
+  // swapped on dim half 1, so that accumulator elements 0..7 of lane (head, half h) are tokens
+  // 16 dq + 8 h + 0..7 on both dim halves and elements 8..15 the tokens the other half keeps
+  const int kr = 32 * tq + (tau(hh) ^ (16 * dq));
+  const int fk = (2 * hf) ^ swz_lat(kr);   // latent chunk of k-step s: (4 s) ^ fk (+ 16 dq)
+  const int fr = (2 * hf) ^ swz_rope(kr);  // rope chunks: fr, fr ^ 1
   // V^T operand of a 32-dim block: lane (dim l % 32, half h) holds tokens 16 h + 0..15 and
   // 32 + 16 h + 0..15, read as four 8-token transposes r = 0..3 at rows
   // 16 h + 8 (r & 1) + 32 (r >> 1) + (lane % 16) / 2; the swizzle depends on r & 1 only
@@ -458,25 +484,22 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
   for (int par = 0; par < 2; ++par) {
     const int vrow = 16 * (gq >> 1) + 8 * par + (i16 >> 1);
     const int vu = (gq & 1) ^ swz_lat(vrow);
-    vbase[par] = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1) + 256 * dh;
+    vbase[par] = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1);
     vx[par] = vu >> 1;
   }
 
-  // ---- software pipeline over the tiles of a piece: the S^T MFMAs of tile t + 1 run with the
-  // softmax of tile t (and its two block exchanges) interleaved between their k-steps, then the
-  // O^T MFMAs of tile t. Every wave executes the same barriers per tile (A: tile t + 1 landed,
-  // B: block maxima, C: P^T blocks), whatever its own tokens or segment state.
-  i32x8 qhi[F8_QREG], qlo[F8_QREG];
-  int64_t t = t_lo;
-  int64_t issued = t_lo + 1 < t_hi ? t_lo + 2 : t_lo + 1;  // tiles [t_lo, issued) requested
+  i32x8 qhi[4], qlo[4], qpe;
+  int t = t_lo;
+  int issued = t_lo + 1 < t_hi ? t_lo + 2 : t_lo + 1;  // tiles [t_lo, issued) requested
+  int s_cur = 0;  // ring stage of tile t
   int cb = b_first;
-  int64_t cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
+  int cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
 
   // Tile x becomes visible: this thread's loads of it have landed (only tile x + 1's may still
   // be in flight), then the workgroup barrier, after which every wave is also done with the
   // stage of tile x - 2. Returns whether tile x + 1 is to be loaded now (into that stage).
-  auto visible = [&](int64_t x, Dma& dma) {
-    wait_vm(issued > x + 1 ? F8_LOADS : 0);
+  auto visible = [&](int x, Dma& dma) {
+    wait_ring(issued > x + 1);
     wg_barrier();
     if (issued == x + 1 && issued < t_hi) {
       dma = issue_setup(issued);
@@ -485,55 +508,57 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     }
     return false;
   };
-  // S^T = K Q^T of tile x for this wave's 32 tokens (rows past the sequence read as zeros and
-  // are masked later), the LDS-DMA instructions of the refill in the first k-steps (REFILL) and
-  // the work hook(k) after the k-step k MFMAs. No branches inside: the k-steps form one block.
-  auto qk_body = [&](int64_t x, f32x16& so, const Dma& dma, auto REFILLc, auto&& hook) {
+  // Partial S^T of tile x for this wave's 32 tokens and dim half (rows past the sequence read as
+  // zeros and are masked later), the LDS-DMA instructions of the refill spread over the first
+  // k-steps (REFILL) and the work hook(i) after MFMA i (0..8). No branches inside.
+  // Per-step waits: before k-step s, all but the LDS accesses issued by the hooks after the K read
+  // of step s (W[s] of them) must have completed; the hooks of the softmax issue, after the K
+  // read of step 1: 3 reads (hook 0); step 2: a write and, after a barrier, 1 read; step 4: a
+  // write and, after a barrier, 2 reads.
+  auto qk_body = [&](const uint8_t* st, f32x16& so, const Dma& dma, auto REFILLc, auto HOOKEDc,
+                     auto&& hook) {
     constexpr bool REFILL = decltype(REFILLc)::value;
-    const uint8_t* st = ring + (int)((x - t_lo) % F8_NSTAGE) * F8_STAGE;
-    const uint8_t* krow = st + (32 * dh + th) * F8_DV;
-    const uint8_t* prow = st + F8_LAT + (32 * dh + th) * F8_DPE;
-    // operands of k-step k: K (32 bytes of this lane's row) and, past F8_QREG, Q^T hi/lo
-    i32x8 kop[3], qop[3][2];
-    auto nreads = [](int k) { return k < F8_QREG ? 2 : 6; };  // LDS reads of k-step k
-    auto kread = [&](int k) {
-      kop[k % 3] = k < 8 ? lds_2xb128(krow + 16 * ((4 * k) ^ fk), krow + 16 * (((4 * k) ^ fk) ^ 1))
+    constexpr bool HOOKED = decltype(HOOKEDc)::value;
+    constexpr int W[5] = {0, HOOKED ? 3 : 0, HOOKED ? 1 : 0, 0, HOOKED ? 2 : 0};
+    const uint8_t* krow = st + kr * F8_DV + 256 * dq;
+    const uint8_t* prow = st + F8_LAT + kr * F8_DPE;
+    i32x8 kop[2];
+    auto kread = [&](int s) {  // s = 0..3 latent, 4 rope
+      kop[s & 1] = s < 4 ? lds_2xb128(krow + 16 * ((4 * s) ^ fk), krow + 16 * (((4 * s) ^ fk) ^ 1))
                          : lds_2xb128(prow + 16 * fr, prow + 16 * (fr ^ 1));
-      if (k >= F8_QREG) {
-        const i32x8* q = &qt[pr][2 * (k - F8_QREG)][lane];
-        qop[k % 3][0] = lds_2xb128(q, (const i32x4*)q + 1);
-        qop[k % 3][1] = lds_2xb128(q + 64, (const i32x4*)(q + 64) + 1);
-      }
     };
     kread(0);
-    kread(1);
     so = f32x16{};
 #pragma unroll
-    for (int k = 0; k < 9; ++k) {
-      // reads of k-step k done (later LDS accesses only make the wait stricter)
-      lgkm_wait(k + 1 < 9 ? nreads(k + 1) : 0);
-      order_after(kop[k % 3]);
-      if (k >= F8_QREG) {
-        order_after(qop[k % 3][0]);
-        order_after(qop[k % 3][1]);
-      }
-      if (k + 2 < 9) kread(k + 2);
+    for (int s = 0; s < 5; ++s) {
+      lgkm_wait(W[s]);  // the K read of k-step s has completed
+      order_after(kop[s & 1]);
+      if (s + 1 < 5) kread(s + 1);
       if constexpr (REFILL) {
-#pragma unroll
-        for (int j = 0; j < F8_DMA_PER_STEP; ++j)
-          if (k * F8_DMA_PER_STEP + j < F8_LOADS) issue_dma(dma, k * F8_DMA_PER_STEP + j);
+        if (s < F8_LAT_LOADS / 2) {
+          issue_dma(dma, 2 * s);
+          issue_dma(dma, 2 * s + 1);
+        }
+        if (s == F8_LAT_LOADS / 2 && rope_loader) issue_dma(dma, F8_LAT_LOADS);
       }
-      so = mfma_fp8(kop[k % 3], k < F8_QREG ? qhi[k] : qop[k % 3][0], so);
-      so = mfma_fp8(kop[k % 3], k < F8_QREG ? qlo[k] : qop[k % 3][1], so);
-      hook(k);
+      if (s < 4) {
+        so = mfma_fp8(kop[s & 1], qhi[s], so);
+        hook(2 * s);
+        so = mfma_fp8(kop[s & 1], qlo[s], so);
+        hook(2 * s + 1);
+      } else {
+        so = mfma_fp8(kop[s & 1], qpe, so);
+        hook(8);
+      }
       sched_fence();
     }
   };
-  auto qk = [&](int64_t x, f32x16& so, bool refill, const Dma& dma, auto&& hook) {
+  auto qk = [&](const uint8_t* st, f32x16& so, bool refill, const Dma& dma, auto HOOKEDc,
+                auto&& hook) {
     if (refill)
-      qk_body(x, so, dma, std::true_type{}, hook);
+      qk_body(st, so, dma, std::true_type{}, HOOKEDc, hook);
     else
-      qk_body(x, so, dma, std::false_type{}, hook);
+      qk_body(st, so, dma, std::false_type{}, HOOKEDc, hook);
   };
 
   while (t < t_hi) {  // one iteration per sequence piece
@@ -544,19 +569,20 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
     }
     const int L = max(0, min(ldc(a.seqlens + cb), a.lmax));
     const int64_t qr = (int64_t)cb * a.Hq + head;
-    const float ch = a.score_scale * kvs * load_q(a, qr, hf, qhi, qlo, &qt[pr][0][lane], dh == 0);
-    const int64_t p_lo = t, p_hi = min(t_hi, cb_hi);
+    const float ch = a.score_scale * kvs * load_q(a, qr, dq, hf, qhi, qlo, qpe);
+    const int p_lo = t, p_hi = min(t_hi, cb_hi);
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
     const int slot = p_lo == t_lo ? 0 : 1;
     bool have_scr = false, first = true;
     float lse_scr = 0.f, mref = 0.f, lsum = 0.f;
-    f32x16 oacc[8];
+    f32x16 oacc[4];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
+    for (int d = 0; d < 4; ++d) oacc[d] = f32x16{};
+    const int dbase = 128 * q + 4 * hf;  // first output dim of this lane
 
     // Segment end: normalise, merge with an earlier segment (scratch slot), store this wave's
-    // 256 dims: to the output for a complete sequence, else to the piece's partial slot (a cut
-    // segment goes to the scratch slot)
+    // 128 dims: to the output for a complete sequence, else to the piece's partial slot (a cut
+    // segment goes to the scratch slot). Partial slots are [slot][head][512] bf16.
     auto flush = [&](bool cut, float m_seg) {
       const float lse_seg = m_seg + __log2f(lsum);
       float w_seg = kvs / lsum, w_old = 0.f, lse_out = lse_seg;
@@ -569,35 +595,38 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         w_old = e_old / tot;
         w_seg *= e_seg / tot;
       }
-      const int64_t scr_slot = (int64_t)g * F8_SLOTS + 2;
-      const u32x2* scr = a.part_o + ((scr_slot * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
-      // value of output group (dt, q4) of this wave (four consecutive dims)
+      auto slot_row = [&](int64_t sb) {
+        return (u32x2*)(a.part_o + (sb * a.Hq + head) * F8_DV + dbase);
+      };
+      const u32x2* scr = slot_row((int64_t)g * F8_SLOTS + 2);
+      // value of output group (dt, q4) of this lane: dims 32 dt + 8 q4 + 0..3 past dbase
       auto val = [&](int dt, int q4, auto merge) {
         f32x4 v = {oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
                    oacc[dt][4 * q4 + 3]};
         v *= w_seg;
-        if constexpr (decltype(merge)::value) v += bf16x4_to_f32(scr[(dt * 4 + q4) * 64]) * w_old;
+        if constexpr (decltype(merge)::value) v += bf16x4_to_f32(scr[8 * dt + 2 * q4]) * w_old;
         return v;
       };
       auto store = [&](auto merge) {
         if (cut || !complete) {
           const int64_t sb = (int64_t)g * F8_SLOTS + (cut ? 2 : slot);
-          u32x2* dst = a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + lane;
+          u32x2* dst = slot_row(sb);
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
+          for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
               const f32x4 v = val(dt, q4, merge);
-              dst[(dt * 4 + q4) * 64] = u32x2{h16<true>::pack(v[0], v[1]), h16<true>::pack(v[2], v[3])};
+              dst[8 * dt + 2 * q4] =
+                  u32x2{h16<true>::pack(v[0], v[1]), h16<true>::pack(v[2], v[3])};
             }
             sched_fence();
           }
-          if (dh == 0 && hf == 0) a.part_lse[sb * a.Hq + head] = lse_out;
+          if (q == 0 && hf == 0) a.part_lse[sb * a.Hq + head] = lse_out;
         } else {
           using H = h16<O_BF16>;
-          uint16_t* o = a.out + qr * F8_DV + 256 * dh + 4 * hf;
+          uint16_t* o = a.out + qr * F8_DV + dbase;
 #pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
+          for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
               const f32x4 v = val(dt, q4, merge);
@@ -611,169 +640,219 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode(const F8Args a) {
         store(std::true_type{});
       else
         store(std::false_type{});
-      wait_vm(0);  // stores retire before the ring's vmcnt accounting resumes
+      wait_vmcnt<0>();  // stores retire before the ring's vmcnt accounting resumes
       if (cut) {
         have_scr = true;
         lse_scr = lse_out;
       }
     };
 
-    // prologue: S^T of the piece's first tile
-    f32x16 s;
+    // partial scores: elements 8..15 go to the other dim half, 0..7 are kept (raw, unmasked)
+    float s8[8];
+    auto publish = [&](const f32x16& sv) {
+      xs[hb][tq][dq ^ 1][0][lane] = f32x4{sv[8], sv[9], sv[10], sv[11]};
+      xs[hb][tq][dq ^ 1][1][lane] = f32x4{sv[12], sv[13], sv[14], sv[15]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s8[i] = sv[i];
+    };
+
+    // prologue: partial S^T of the piece's first tile
     {
       Dma dma{};
       const bool refill = visible(t, dma);
-      qk(t, s, refill, dma, [](int) {});
+      f32x16 s0;
+      qk(stage(s_cur), s0, refill, dma, std::false_type{}, [](int) {});
+      publish(s0);
     }
-    for (; t < p_hi; ++t) {
-      const uint8_t* st = ring + (int)((t - t_lo) % F8_NSTAGE) * F8_STAGE;
-      const int own = L - (int)(t - cb_lo) * F8_TILE - 32 * dh;  // this wave's valid tokens
+    for (; t < p_hi; ++t, s_cur = next_stage(s_cur)) {
+      const uint8_t* st = stage(s_cur);
+      // valid tokens of this wave's 16 (kept element i of lane half h is token 8 h + i of them)
+      const int own = L - (t - cb_lo) * F8_TILE - 32 * tq - 16 * dq;
       const bool nxt = t + 1 < p_hi;
-      // softmax of tile t, in pieces placed after the k-steps of the next tile's S^T:
-      //   0: block max -> LDS; 2: barrier; 3: tile max, segment check, block scale; 3..6: P^T
-      //   in e4m3, 4 elements per step; 6: P^T blocks -> LDS; 7: block sums and scales -> LDS,
-      //   barrier; 8: row sums, B operand
-      float mb = -INFINITY, ps = 0.f, sh = 0.f, m_old = 0.f, tsum = 0.f;
-      int es = 0;
+      // Softmax of tile t as short levels of independent instructions, one after each MFMA of
+      // the next tile's S^T (the wave issues in order, so a dependent chain between two MFMAs
+      // would hold back the second). LDS accesses are inline asm with explicit waits.
+      //   0: other half's partial scores, and the previous tile's row sums
+      //   1: add, mask, 8-element max; previous tile's row sum into lsum
+      //   2: lane-half max -> LDS (16-token maxima)
+      //   3: barrier B, read the head block's four maxima
+      //   4: tile max, segment check, block scales
+      //   5: exponentials
+      //   6: P^T in e4m3 -> LDS, rounded P back to float
+      //   7: barrier C, read the B operand (both token blocks); pairwise sums
+      //   8: 16-token sum of the rounded P -> LDS (read with the next tile)
+      float sh = 0.f, m_old = 0.f, mb = 0.f;
+      int es_me = 0, psc = 0;
       bool cut = false;  // a new segment starts at this tile (flushed before its O^T update)
-      int phi4[4];
+      int phi[2];
+      float pr[8], a4[4];
       i32x8 pbh;
-      int psc = 0;
-      auto hook = [&](int k) {
+      i32x4 xin0, xin1, x4, m4;
+      auto hook = [&](int k, auto HOOKEDc) {
+        constexpr bool HOOKED = decltype(HOOKEDc)::value;
         if (k == 0) {
-          // raw scores (the log2-domain scale ch > 0 is applied inside exp2); element i is token
-          // 16 (i / 8) + 8 hf + i % 8 of the block
-          if (own < 32) {  // wave-uniform: the sequence ends inside this wave's block
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int tok = 16 * (i >> 3) + 8 * hf + (i & 7);
-              s[i] = tok >= own ? -INFINITY : s[i];
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[i]);
-          mb = xhalf_max(mb) * ch;
-          xmax[pr][dh][hh] = mb;  // both lane halves write the same value
+          xin0 = lds_b128(&xs[hb][tq][dq][0][lane]);
+          xin1 = lds_b128(&xs[hb][tq][dq][1][lane]);
+          x4 = lds_b128(&xsum[hb][hh]);
         }
-        if (k == 2) wg_barrier();
+        if (k == 1) {
+          lgkm<0>();
+          order_after(xin0);
+          order_after(xin1);
+          order_after(x4);
+          const f32x4 p0 = as_f32x4(xin0), p1 = as_f32x4(xin1), pv = as_f32x4(x4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s8[e] += p0[e];
+            s8[4 + e] += p1[e];
+          }
+          if (own < 16) {  // wave-uniform: the sequence ends inside this wave's tokens
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s8[i] = 8 * hf + i >= own ? -INFINITY : s8[i];
+          }
+          mb = fmaxf(fmaxf(fmaxf(s8[0], s8[1]), fmaxf(s8[2], s8[3])),
+                     fmaxf(fmaxf(s8[4], s8[5]), fmaxf(s8[6], s8[7])));
+          // the previous tile's sum (same order on the four waves), unless this tile starts
+          // the piece
+          if (t > p_lo) lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+        }
+        if (k == 2) {
+          // raw scores; the log2-domain scale ch > 0 is applied inside exp2
+          mb = xhalf_max(mb) * ch;
+          lds_write_b32((float*)&xmax[hb][hh] + q, __float_as_uint(mb));
+        }
         if (k == 3) {
-          const float mt = fmaxf(mb, xmax[pr][dh ^ 1][hh]);  // tile max of the head
+          wg_barrier();
+          m4 = lds_b128(&xmax[hb][hh]);
+        }
+        if (k == 4) {
+          if constexpr (HOOKED)
+            lgkm<2>();  // the K read issued after it may still be in flight
+          else
+            lgkm<0>();
+          order_after(m4);
+          const f32x4 mx = as_f32x4(m4);
+          const float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));  // tile max
           // a tile whose max exceeds the reference by more than the headroom ends the segment;
           // P of this tile then uses the new reference and the old segment is flushed after the
-          // S^T k-steps (wave-uniform decision, no branch here)
+          // S^T MFMAs (wave-uniform decision, the same on the head block's four waves)
           cut = !first && __ballot(mt > mref + F8_RESET) != 0;
           m_old = mref;
           mref = (first || cut) ? mt : mref;
           first = false;
-          // P^T of this wave's block in e4m3 on a per-head power-of-two scale 2^es (es =
-          // exponent of the block's largest P minus 8, so scaled values are below 256), folded
-          // into the exp2 argument. The row sums add the rounded P, so the weights applied to V
-          // sum to one (a one-token sequence returns its V row exactly) and the largest P of a
-          // segment, 2^0, is exact
-          int e2 = 0;
-          (void)frexpf(__builtin_amdgcn_exp2f(mb - mref), &e2);
-          es = mb == -INFINITY ? 0 : max(-127, min(127, e2 - 8));
-          sh = -(mref + (float)es);
+          // P^T of a 32-token block in e4m3 on a per-head power-of-two scale 2^es, es =
+          // floor(block max - reference) - 7, so the block's largest scaled P lies in [128, 256);
+          // folded into the exp2 argument and passed to the O^T MFMA as the block's E8M0 scale.
+          // The row sums add the rounded P, so the weights applied to V sum to one and the
+          // largest P of a segment, 2^0, is exact
+          auto bscale = [&](float mblk) {
+            const int e = (int)floorf(mblk - mref) - 7;
+            return mblk == -INFINITY ? 0 : max(-127, min(127, e));
+          };
+          const int es0 = bscale(fmaxf(mx[0], mx[2])), es1 = bscale(fmaxf(mx[1], mx[3]));
+          es_me = tq ? es1 : es0;
+          psc = (hf ? es1 : es0) + 127;  // the scale of k block h comes from lane half h
+          sh = -(mref + (float)es_me);
         }
-        if (k >= 3 && k <= 6) {
-          const int q4 = k - 3;
-          float y[4];
+        if (k == 5) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = __builtin_amdgcn_exp2f(fmaf(s[4 * q4 + e], ch, sh));
-          phi4[q4] = pack_fp8x4(y[0], y[1], y[2], y[3]);
-          typedef float f2 __attribute__((ext_vector_type(2)));
-          const f2 r01 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], false);
-          const f2 r23 = __builtin_amdgcn_cvt_pk_f32_fp8(phi4[q4], true);
-          ps += (r01[0] + r01[1]) + (r23[0] + r23[1]);
+          for (int i = 0; i < 8; ++i) pr[i] = fmaf(s8[i], ch, sh);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
         }
         if (k == 6) {
-          // element i is token 16 (i / 8) + 8 hf + i % 8 of the block
-          uint8_t* rh = &xq[pr][dh][hh][8 * hf];
-          lds_write_b64(rh, u32x2{(uint32_t)phi4[0], (uint32_t)phi4[1]});
-          lds_write_b64(rh + 16, u32x2{(uint32_t)phi4[2], (uint32_t)phi4[3]});
+          phi[0] = pack_fp8x4(pr[0], pr[1], pr[2], pr[3]);
+          phi[1] = pack_fp8x4(pr[4], pr[5], pr[6], pr[7]);
+          lds_write_b64(&xq[hb][tq][dq][hh][8 * hf], u32x2{(uint32_t)phi[0], (uint32_t)phi[1]});
+          typedef float f2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(phi[w], false);
+            const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(phi[w], true);
+            pr[4 * w] = lo[0];
+            pr[4 * w + 1] = lo[1];
+            pr[4 * w + 2] = hi[0];
+            pr[4 * w + 3] = hi[1];
+          }
         }
         if (k == 7) {
-          ps = xhalf_sum(ldexpf(ps, es));
-          xsum[pr][dh][hh] = ps;  // both lane halves write the same values
-          xsc[pr][dh][hh] = es + 127;
           wg_barrier();
+          // B operand: lane (head hh, half h) holds tokens 16 h + 0..15 of both token blocks
+          pbh = lds_2xb128(&xq[hb][0][hf][hh][0], &xq[hb][1][hf][hh][0]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a4[i] = pr[2 * i] + pr[2 * i + 1];
         }
         if (k == 8) {
-          tsum = dh == 0 ? ps + xsum[pr][1][hh] : xsum[pr][0][hh] + ps;
-          // B operand: lane (head hh, half hf) holds tokens 16 hf + 0..15 of both blocks; its
-          // scale is that of block hf
-          pbh = lds_2xb128(&xq[pr][0][hh][16 * hf], &xq[pr][1][hh][16 * hf]);
-          psc = xsc[pr][hf][hh];
+          const float ps = xhalf_sum(ldexpf((a4[0] + a4[1]) + (a4[2] + a4[3]), es_me));
+          lds_write_b32((float*)&xsum[hb][hh] + q, __float_as_uint(ps));
         }
       };
       f32x16 sn;
       if (nxt) {
         Dma dma{};
         const bool refill = visible(t + 1, dma);
-        qk(t + 1, sn, refill, dma, hook);
+        qk(stage(next_stage(s_cur)), sn, refill, dma, std::true_type{},
+           [&](int k) { hook(k, std::true_type{}); });
       } else {
+        wg_barrier();  // the partial scores of tile t are published
 #pragma unroll
-        for (int k = 0; k < 9; ++k) hook(k);
+        for (int k = 0; k < 9; ++k) hook(k, std::false_type{});
       }
       if (cut) {  // wave-uniform; rare
         flush(true, m_old);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) oacc[d] = f32x16{};
+        for (int d = 0; d < 4; ++d) oacc[d] = f32x16{};
         lsum = 0.f;
       }
-      lsum += tsum;
-      // O^T (this wave's 256 dims) += V^T P^T over the tile's 64 tokens: 8 dim blocks
+      // O^T (this wave's 128 dims) += V^T P^T over the tile's 64 tokens: 4 dim blocks
       auto vread = [&](int dt) {
         i32x2 r[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-          r[rr] = lds_tr8(st + vbase[rr & 1] + 32 * F8_DV * (rr >> 1) + 32 * (dt ^ vx[rr & 1]));
+          r[rr] = lds_tr8(st + vbase[rr & 1] + 32 * F8_DV * (rr >> 1) +
+                          32 * ((4 * q + dt) ^ vx[rr & 1]));
         return i32x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
       };
-      i32x8 vop[2][2];
-      vop[0][0] = vread(0);
-      vop[0][1] = vread(1);
-      lds_wait(pbh);
+      i32x8 vop[2];
+      vop[0] = vread(0);
 #pragma unroll
-      for (int g2 = 0; g2 < 4; ++g2) {
-        lds_wait(vop[g2 & 1][0], vop[g2 & 1][1]);
-        if (g2 + 1 < 4) {
-          vop[(g2 + 1) & 1][0] = vread(2 * g2 + 2);
-          vop[(g2 + 1) & 1][1] = vread(2 * g2 + 3);
+      for (int dt = 0; dt < 4; ++dt) {
+        if (dt + 1 < 4) {
+          vop[(dt + 1) & 1] = vread(dt + 1);
+          lgkm_wait(4);  // all but the 4 reads just issued
+        } else {
+          lgkm_wait(0);
         }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int dt = 2 * g2 + u;
-          oacc[dt] = mfma_fp8_bscaled(vop[g2 & 1][u], pbh, oacc[dt], psc);
-        }
+        order_after(vop[dt & 1]);
+        if (dt == 0) order_after(pbh);
+        oacc[dt] = mfma_fp8_bscaled(vop[dt & 1], pbh, oacc[dt], psc);
         sched_fence();
       }
-      if (nxt) s = sn;
+      if (nxt) publish(sn);
+    }
+    // the last tile's row sums
+    wg_barrier();
+    {
+      const f32x4 pv = xsum[hb][hh];
+      lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
     }
     flush(false, mref);
   }
 }
 
 // Merge the partial slots of every sequence that spans more than one range; zero-length
-// sequences produce zeros. Workgroup = (sequence, 64-head group, 32-dim block of each half);
-// wave w reads what decode wave w stored, in the same lane layout.
+// sequences produce zeros. Thread = (sequence, head, 8 dims); a workgroup covers 4 heads.
 template <bool O_BF16>
 __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
-  const int HG = a.Hq / F8_HEADS;
-  const int dt = blockIdx.x & 7;
-  const int bh = blockIdx.x >> 3;
-  const int hgi = bh % HG, b = bh / HG;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int pr = wave >> 1, dh = wave & 1;
-  const int hh = lane & 31, hf = lane >> 5;
-  const int head = hgi * F8_HEADS + pr * 32 + hh;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // sequence * Hq + head
+  if (row >= (int64_t)a.B * a.Hq) return;
+  const int b = (int)(row / a.Hq), head = (int)(row % a.Hq);
+  const int d0 = 8 * (threadIdx.x & 63);
   using H = h16<O_BF16>;
-  uint16_t* o = a.out + ((int64_t)b * a.Hq + head) * F8_DV + 256 * dh + 32 * dt + 4 * hf;
+  uint16_t* o = a.out + row * F8_DV + d0;
   const int64_t T = a.cu[a.B], c0 = a.cu[b], c1 = a.cu[b + 1];
   if (c0 == c1) {
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) *(u32x2*)(o + 8 * q4) = u32x2{0u, 0u};
+    *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
     return;
   }
   const int64_t G = a.G;
@@ -786,24 +865,19 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   // per batch (a sequence spans at most a few ranges at the usual split counts).
   constexpr int F8_CMB = 8;
   float m = -INFINITY, l = 0.f;
-  f32x4 acc[4] = {};
+  f32x4 acc[2] = {};
   for (int64_t gb = g0; gb <= g1; gb += F8_CMB) {
     float lv[F8_CMB];
-    u32x2 pv[F8_CMB][4];
+    u32x4 pv[F8_CMB];
 #pragma unroll
     for (int i = 0; i < F8_CMB; ++i) {
       const int64_t g = gb + i;  // wave-uniform
       lv[i] = -INFINITY;
+      pv[i] = u32x4{0u, 0u, 0u, 0u};
       if (g <= g1 && start(g) != start(g + 1)) {
         const int64_t sb = slot_of(g);
         lv[i] = a.part_lse[sb * a.Hq + head];
-        const u32x2* src =
-            a.part_o + ((sb * HG + hgi) * 4 + wave) * F8_WAVE_F4 + dt * 4 * 64 + lane;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) pv[i][q4] = src[q4 * 64];
-      } else {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) pv[i][q4] = u32x2{0u, 0u};
+        pv[i] = *(const u32x4*)(a.part_o + (sb * a.Hq + head) * F8_DV + d0);
       }
     }
     float mb = m;
@@ -811,23 +885,22 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
     for (int i = 0; i < F8_CMB; ++i) mb = fmaxf(mb, lv[i]);
     const float r = __builtin_amdgcn_exp2f(m - mb);  // m = -inf on the first batch: r = 0
     l *= r;
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) acc[q4] *= r;
+    acc[0] *= r;
+    acc[1] *= r;
 #pragma unroll
     for (int i = 0; i < F8_CMB; ++i) {
       const float w = __builtin_amdgcn_exp2f(lv[i] - mb);  // 0 for an absent range
       l += w;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) acc[q4] += bf16x4_to_f32(pv[i][q4]) * w;
+      acc[0] += bf16x4_to_f32(u32x2{pv[i][0], pv[i][1]}) * w;
+      acc[1] += bf16x4_to_f32(u32x2{pv[i][2], pv[i][3]}) * w;
     }
     m = mb;
   }
   const float inv = 1.0f / l;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) acc[q4] *= inv;
-#pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4)
-    *(u32x2*)(o + 8 * q4) = u32x2{H::pack(acc[q4][0], acc[q4][1]), H::pack(acc[q4][2], acc[q4][3])};
+  acc[0] *= inv;
+  acc[1] *= inv;
+  *(u32x4*)o = u32x4{H::pack(acc[0][0], acc[0][1]), H::pack(acc[0][2], acc[0][3]),
+                     H::pack(acc[1][0], acc[1][1]), H::pack(acc[1][2], acc[1][3])};
 }
 
 size_t f8_align(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -886,7 +959,7 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.qsplit = (uint8_t*)ws + f8_cu_bytes(B);
   a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
   a.part_lse = (float*)((char*)ws + f8_cu_bytes(B) + f8_q_bytes(B, Hq));
-  a.part_o = (u32x2*)(a.part_lse + G * F8_SLOTS * Hq);
+  a.part_o = (uint16_t*)(a.part_lse + G * F8_SLOTS * Hq);
   a.out = (uint16_t*)o;
   a.B = (int)B;
   a.Hq = (int)Hq;
@@ -906,11 +979,11 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 prep)");
   const dim3 grid((unsigned)(((G + 7) / 8) * 8 * HG));
   if (o_bf16)
-    mla_fp8_decode<true><<<grid, 256, 0, st>>>(a);
+    mla_fp8_decode<true><<<grid, 512, 0, st>>>(a);
   else
-    mla_fp8_decode<false><<<grid, 256, 0, st>>>(a);
+    mla_fp8_decode<false><<<grid, 512, 0, st>>>(a);
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
-  const dim3 cgrid((unsigned)(B * HG * 8));
+  const dim3 cgrid((unsigned)((B * Hq + 3) / 4));
   if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
   else mla_fp8_combine<false><<<cgrid, 256, 0, st>>>(a);
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 combine)");
