@@ -118,7 +118,7 @@ def test_pages_outside_the_pool_read_as_zero():
     _check(got, _oracle(T2, a))
 
 
-@pytest.mark.parametrize("Hq", [64, 256])
+@pytest.mark.parametrize("Hq", [64, 192, 256])
 def test_head_counts(Hq):
     w = workloads.mla(B=5, Hq=Hq, max_pages=20, min_len=100, max_len=1280, seed=75)
     _check(_run(w.tensors, w.attrs, 4), _oracle(w.tensors, w.attrs))
@@ -138,6 +138,13 @@ def test_large_q_magnitude():
     T = dict(w.tensors)
     T["q"] = (T["q"].float() * 300.0).to(torch.bfloat16)
     _check(_run(T, w.attrs, 2), _oracle(T, w.attrs))
+
+
+def test_page_size_128():
+    """Pages of two 64-token tiles: a tile's rows start at an odd half of a page for every
+    second tile; the fp8 matrix-core path takes it."""
+    w = workloads.mla(B=6, page=128, max_pages=10, min_len=60, max_len=1280, seed=80)
+    _check(_run(w.tensors, w.attrs, 3), _oracle(w.tensors, w.attrs))
 
 
 def test_page_size_16_uses_split_kernel():
