@@ -844,13 +844,15 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
 // sequences produce zeros. Thread = (sequence, head, 8 dims); a workgroup covers 4 heads.
 template <bool O_BF16>
 __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // sequence * Hq + head
+  // the wave's (sequence, head) row is wave-uniform: its range bookkeeping runs on the scalar
+  // unit once per wave
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= (int64_t)a.B * a.Hq) return;
   const int b = (int)(row / a.Hq), head = (int)(row % a.Hq);
   const int d0 = 8 * (threadIdx.x & 63);
   using H = h16<O_BF16>;
   uint16_t* o = a.out + row * F8_DV + d0;
-  const int64_t T = a.cu[a.B], c0 = a.cu[b], c1 = a.cu[b + 1];
+  const int64_t T = ldc(a.cu + a.B), c0 = ldc(a.cu + b), c1 = ldc(a.cu + b + 1);
   if (c0 == c1) {
     *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
     return;
@@ -858,8 +860,19 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   const int64_t G = a.G;
   const int64_t g0 = ((c0 + 1) * G - 1) / T, g1 = (c1 * G - 1) / T;
   if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
-  auto start = [&](int64_t g) { return g * T / G; };
-  auto slot_of = [&](int64_t g) { return g * F8_SLOTS + ((g == g0 && c0 != start(g0)) ? 1 : 0); };
+  // range starts floor(g T / G) stepped incrementally: floor(g T / G) + T / G, plus one when the
+  // remainder (g T) mod G wraps
+  const int64_t tq = T / G, tr = T % G;
+  int64_t s_cur = g0 * T / G, r_cur = g0 * T % G;  // start of range g and its remainder
+  auto step = [&](int64_t& st, int64_t& rm) {
+    st += tq;
+    rm += tr;
+    if (rm >= G) {
+      rm -= G;
+      ++st;
+    }
+  };
+  const bool first_is_piece = c0 != s_cur;  // the sequence starts inside range g0: slot 1 there
   // Online merge over the ranges in batches of F8_CMB: the lse values and partial outputs of a
   // batch are all requested before any is used, so a call waits for about one memory latency
   // per batch (a sequence spans at most a few ranges at the usual split counts).
@@ -874,10 +887,16 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
       const int64_t g = gb + i;  // wave-uniform
       lv[i] = -INFINITY;
       pv[i] = u32x4{0u, 0u, 0u, 0u};
-      if (g <= g1 && start(g) != start(g + 1)) {
-        const int64_t sb = slot_of(g);
-        lv[i] = a.part_lse[sb * a.Hq + head];
-        pv[i] = *(const u32x4*)(a.part_o + (sb * a.Hq + head) * F8_DV + d0);
+      if (g <= g1) {
+        int64_t s_next = s_cur, r_next = r_cur;
+        step(s_next, r_next);
+        if (s_cur != s_next) {  // the range holds tiles
+          const int64_t sb = g * F8_SLOTS + ((g == g0 && first_is_piece) ? 1 : 0);
+          lv[i] = a.part_lse[sb * a.Hq + head];
+          pv[i] = *(const u32x4*)(a.part_o + (sb * a.Hq + head) * F8_DV + d0);
+        }
+        s_cur = s_next;
+        r_cur = r_next;
       }
     }
     float mb = m;
