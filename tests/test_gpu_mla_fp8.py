@@ -61,23 +61,35 @@ def _check(got, exp):
     assert _rel_rms(got, exp) < REL_RMS_MAX
 
 
-@pytest.mark.parametrize("num_split", [1, 3])
-def test_segment_restarts(num_split):
-    """Tile scores rise by ~30-480 log2 units from tile to tile (then fall), so segments end and
-    merge through the scratch slot several times per sequence; the result must still equal the
+# key offsets per run of tokens: score jumps of ~30-1200 log2 units up and down
+LEVELS = {64: [0.0, 1.0, 2.0, 4.0, 8.0, 16.0, 3.0, 0.5, 12.0, 16.0, 1.0, 6.0],
+          32: [0.0, 8.0, 2.0, 16.0, 3.0, 0.5, 12.0, 20.0, 1.0, 6.0, 4.0, 4.5]}
+
+
+@pytest.mark.parametrize("Hq,run,num_split", [(128, 64, 1), (128, 64, 3), (128, 32, 1),
+                                              (128, 32, 3), (64, 64, 3), (64, 32, 1)])
+def test_segment_restarts(Hq, run, num_split):
+    """Keys rise and fall by a whole level every `run` tokens (a 64-token tile, or each 32-token
+    half of one), so scores jump by more than the 2^64 headroom many times per sequence, also
+    between the two halves of a tile and within the first tile of a sequence. The 128-head
+    kernel (Hq = 128) moves its reference and rescales what it holds; the 64-head kernel ends a
+    segment and merges it through the scratch slot. Either way the result must equal the
     single-pass softmax."""
-    w = workloads.mla(B=3, max_pages=12, min_len=700, max_len=768, seed=71)
+    w = workloads.mla(B=3, Hq=Hq, max_pages=12, min_len=700, max_len=768, seed=71)
     T, a = dict(w.tensors), dict(w.attrs)
     g = torch.Generator().manual_seed(72)
     rows = T["kv"].shape[0]
     n_pages = rows // 64
-    level = torch.tensor([0.0, 1.0, 2.0, 4.0, 8.0, 16.0, 3.0, 0.5, 12.0, 16.0, 1.0, 6.0])
+    level = torch.tensor(LEVELS[run])
     latent = torch.randn(rows, 576, generator=g) * 0.25
     bt = T["block_table"]
+    per_page = 64 // run
     for b in range(a["B"]):
         for p in range(a["max_pages"]):
             page = int(bt[b, p])
-            latent[page * 64:(page + 1) * 64] += level[p % len(level)]
+            for r in range(per_page):
+                lo = page * 64 + r * run
+                latent[lo:lo + run] += level[(p * per_page + r) % len(level)]
     T["kv"] = latent.clamp(-448, 448).to(torch.float8_e4m3fn)
     T["kv_scale"] = torch.tensor([1.0], dtype=torch.float32)
     T["q"] = (torch.rand(a["B"], a["Hq"], 576, generator=g) + 0.5).to(torch.bfloat16)

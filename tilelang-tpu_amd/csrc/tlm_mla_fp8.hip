@@ -54,6 +54,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace {
 
@@ -98,6 +99,16 @@ TLM_DEV T ldc(const T* p) {
 
 TLM_DEV void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// f(std::integral_constant<int, i>{}) for i = 0 .. N-1, unrolled at compile time
+template <typename F, int... I>
+TLM_DEV void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+TLM_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // LDS accesses issued as inline asm. Compiler-generated reads may be made to wait (vmcnt(0)) for
 // every outstanding LDS-DMA load, including the prefetch of the next stages, when the compiler
 // cannot prove they touch another stage; asm accesses also keep the lgkmcnt accounting of the
@@ -110,9 +121,23 @@ TLM_DEV i32x2 lds_tr8(const uint8_t* p) {
   asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
   return r;
 }
+template <int OFF>
+TLM_DEV i32x2 lds_tr8_off(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
 TLM_DEV i32x4 lds_b128(const void* p) {
   i32x4 r;
   asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)) : "memory");
+  return r;
+}
+template <int OFF>
+TLM_DEV i32x4 lds_b128_off(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
   return r;
 }
 TLM_DEV i32x8 lds_2xb128(const void* p0, const void* p1) {
@@ -142,6 +167,12 @@ TLM_DEV void lgkm_wait(int n) {
     case 4: lgkm<4>(); break;
     case 5: lgkm<5>(); break;
     case 6: lgkm<6>(); break;
+    case 7: lgkm<7>(); break;
+    case 8: lgkm<8>(); break;
+    case 9: lgkm<9>(); break;
+    case 10: lgkm<10>(); break;
+    case 11: lgkm<11>(); break;
+    case 12: lgkm<12>(); break;
     default: lgkm<0>(); break;
   }
 }
@@ -156,6 +187,19 @@ TLM_DEV f32x4 as_f32x4(i32x4 v) {
 TLM_DEV f32x16 mfma_fp8(i32x8 a, i32x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
+// The same product with its accumulator held in VGPRs, for a kernel whose AGPRs all hold other
+// accumulators (the builtin's register form is chosen for the whole kernel). As inline asm it is
+// outside the compiler's hazard checks, which the caller takes over: an s_nop 1 ahead of each
+// MFMA covers a VALU write of an operand just before it, and xdl_settle() goes between the last
+// MFMA of a chain and the first VALU read of its result (the product is 16 passes). Operands
+// loaded from LDS by inline asm are waited for by the caller as with every asm load here.
+TLM_DEV void mfma_fp8_v0(f32x16& d, const i32x8& a, const i32x8& b) {  // d = a b
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+}
+TLM_DEV void mfma_fp8_v(f32x16& d, const i32x8& a, const i32x8& b) {  // d += a b
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+TLM_DEV void xdl_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 // A unscaled (E8M0 127 = 1), B scaled by 2^(sb - 127). Operand k order: byte j of lane half h is
 // k = 32 (j / 16) + 16 h + j % 16; the scale of B's k-block kb (32 values) for column n comes
 // from lane 32 kb + n.
@@ -840,6 +884,448 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// 128 heads per workgroup (Hq a multiple of 128): 4 waves, one per SIMD, each owning 32 heads for
+// the whole tile: S^T = K Q^T, the softmax and O^T = V^T P^T with no exchange between waves, so
+// the only barrier per tile hands over the ring, and each KV tile goes from L2 to LDS once for all
+// 128 heads.
+//   * registers: the 32 heads' O^T (512 dims, 256 fp32 accumulators per lane) and the hi term of
+//     Q (72 VGPRs); the lo term of Q is kept in LDS (one wave's 32 heads: 18 KB) and read with K;
+//   * a 64-token tile is two 32-token blocks b; K rows are fed to the S^T MFMA in the order rho
+//     (row m -> token (m & 3) | ((m >> 3) & 3) << 2 | ((m >> 2) & 1) << 4), so accumulator element
+//     i of lane half h is token 16 h + i of the block: packed to e4m3 they are exactly bytes
+//     16 b .. 16 b + 15 of the P^T operand of lane half h, with no exchange between lanes;
+//   * the softmax of block 0 runs between the S^T MFMAs of block 1; block 1's after them, its row
+//     sums between the O^T MFMAs. Segments (the reference max fixed per segment) may now end at a
+//     block: a block whose max exceeds the reference by more than the headroom starts a new one,
+//     and a tile cut between its blocks is multiplied in two halves;
+//   * 2-stage ring: the tile is consumed (S^T then O^T) within one iteration, and the next tile
+//     is loaded meanwhile (9 LDS-DMA instructions per wave, one per k-step of block 0);
+//   * the ring's 16-byte chunks are swizzled with row bits 0..2 and 4 (the rows read together
+//     under the order rho differ there), which keeps the K row reads, the rope reads and the
+//     transposed V reads free of bank conflicts.
+constexpr int W_HEADS = 128;
+constexpr int W_NSTAGE = 2;
+constexpr int W_QLO = 9 * 64 * 32;  // one wave's Q lo operands: [k-step][16-byte half][lane]
+
+TLM_DEV int w_rho(int m) { return (m & 3) | (((m >> 3) & 3) << 2) | (((m >> 2) & 1) << 4); }
+TLM_DEV int w_swz(int r) { return ((r & 7) << 1) | ((r >> 4) & 1); }
+TLM_DEV int w_swz_rope(int r) { return (((r >> 2) & 1) << 1) | ((r >> 4) & 1); }
+
+template <bool O_BF16>
+__global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[W_NSTAGE * F8_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t qlo_lds[4][W_QLO];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
+  const int hh = lane & 31, hf = lane >> 5;
+  const int HG = a.Hq / W_HEADS;
+  const F8Work wk = f8_work(blockIdx.x, HG);
+  if (wk.g >= a.G) return;
+  const int g = wk.g, hgi = wk.hgi;
+  const int head = hgi * W_HEADS + 32 * wave + hh;
+  // tile indices fit int32 (the tile prefix is int32)
+  const int T = ldc(a.cu + a.B);
+  const int t_lo = (int)((int64_t)g * T / a.G), t_hi = (int)((int64_t)(g + 1) * T / a.G);
+  if (t_lo >= t_hi) return;
+  const float kvs = a.kv_scale ? ldc(a.kv_scale) : 1.0f;
+
+  // first sequence with a tile in [t_lo, t_hi): largest b with cu[b] <= t_lo
+  int b_first = 0;
+  {
+    int lo = 0, hi = a.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (ldc(a.cu + mid) <= t_lo) lo = mid; else hi = mid - 1;
+    }
+    b_first = lo;
+  }
+
+  // ---- per-tile page table: lane j holds the first KV row of tile tb + j and the number of its
+  // rows to load (the sequence's valid tokens that lie inside the pool; the rest read as zeros)
+  int tb = INT32_MIN / 2;
+  uint32_t tab_lo = 0, tab_hi = 0;
+  int tab_n = 0;
+  auto build_table = [&](int base) {
+    tb = base;
+    const int tj = base + lane;
+    tab_lo = tab_hi = 0;
+    tab_n = 0;
+    if (tj < t_hi) {
+      int blo = 0, bhi = a.B - 1;  // largest b with cu[b] <= tj
+      while (blo < bhi) {
+        const int mid = (blo + bhi + 1) >> 1;
+        if (a.cu[mid] <= tj) blo = mid; else bhi = mid - 1;
+      }
+      const int L = max(0, min(a.seqlens[blo], a.lmax));
+      const int tok0 = (tj - a.cu[blo]) * F8_TILE;
+      const int valid = min(F8_TILE, L - tok0);
+      const int64_t row0 =
+          (int64_t)a.bt[(int64_t)blo * a.max_pages + tok0 / a.page] * a.page + tok0 % a.page;
+      int64_t nrow = min((int64_t)valid, a.kv_rows - row0);
+      if (row0 < 0 || nrow < 0) nrow = 0;
+      tab_lo = (uint32_t)row0;
+      tab_hi = (uint32_t)((uint64_t)row0 >> 32);
+      tab_n = (int)nrow;
+    }
+  };
+  build_table(t_lo);
+
+  // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 2; wave w loads latent rows
+  // 16 w .. 16 w + 15 (8 instructions) and rope rows 16 w .. 16 w + 15 (1 instruction)
+  struct Dma {  // one tile's source rows (base, byte count) and ring stage
+    const uint8_t* bkv;
+    const uint8_t* bpe;
+    int nkv, npe;
+    uint8_t* st;
+  };
+  auto stage = [&](int si) { return ring + si * F8_STAGE; };
+  int s_issue = 0;  // ring stage of the next tile to request
+  auto issue_setup = [&](int t) {
+    if (t >= tb + 64) build_table(t);
+    const int j = t - tb;
+    const int64_t row0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)tab_hi, j) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)tab_lo, j));
+    const int64_t nrow = __builtin_amdgcn_readlane(tab_n, j);
+    const uint8_t* bkv = nrow > 0 ? a.kv + row0 * a.kv_stride : a.kv;
+    const uint8_t* bpe = nrow > 0 ? a.k_pe + row0 * a.kpe_stride : a.k_pe;
+    const Dma d{bkv, bpe, (int)(nrow * a.kv_stride), (int)(nrow * a.kpe_stride), stage(s_issue)};
+    s_issue ^= 1;
+    return d;
+  };
+  // latent instruction k (0..7) of lane (c, h) = (lane % 32, lane / 32) reads row r = 16 w + 2 k + h
+  // at swizzled chunk c ^ w_swz(r) = (c ^ (2 h + (w & 1))) ^ 4 (k % 4)
+  const int lat_off = (16 * wave + hf) * (int)a.kv_stride;
+  const int lat_x16 = 16 * (hh ^ (2 * hf + (wave & 1)));
+  auto issue_dma = [&](const Dma& d, int k) {
+    if (k < 8) {  // latent: 2 rows x 32 chunks per wave-instruction
+      int lo = lat_off, lx = lat_x16;
+      asm volatile("" : "+v"(lo), "+v"(lx));  // per use: the 9 offsets are not kept live
+      const int off = lo + 2 * k * (int)a.kv_stride + (lx ^ (64 * (k & 3)));
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + (8 * wave + k) * 1024), 16,
+                                               off, 0, 0, 0);
+    } else {  // rope: 16 rows x 4 chunks per wave-instruction
+      int ln;  // lane id computed here, not kept in a register across the tile
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      const int r = 16 * wave + (ln >> 2);
+      const int off = r * (int)a.kpe_stride + 16 * ((ln & 3) ^ w_swz_rope(r));
+      const __amdgpu_buffer_rsrc_t rp =
+          __builtin_amdgcn_make_buffer_rsrc((void*)d.bpe, (short)0, d.npe, F8_RSRC_WORD3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(d.st + F8_LAT + wave * 1024), 16,
+                                               off, 0, 0, 0);
+    }
+  };
+  {
+    const Dma d = issue_setup(t_lo);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) issue_dma(d, k);
+  }
+
+  // ---- per-lane LDS read offsets within a ring stage (stages are 1024-byte aligned, so adding a
+  // stage base leaves bits 4..9 of an offset as they are and a swizzle step is one XOR there).
+  // K row of this lane in block b: 32 b + rho(lane % 32); its latent 32-byte chunk of k-step s
+  // is (kofs[b] ^ 64 s) and (kofs[b] ^ 64 s ^ 16), its rope chunk at pofs[b]
+  const int kr0 = w_rho(hh);
+  int kofs[2], pofs[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int r = 32 * b + kr0;
+    kofs[b] = r * F8_DV + 16 * ((2 * hf) ^ w_swz(r));
+    pofs[b] = F8_LAT + r * F8_DPE + 16 * ((2 * hf) ^ w_swz_rope(r));
+  }
+  // V^T operand of a 32-dim block dt: lane (dim l % 32, half h) holds tokens 16 h + 0..15 and
+  // 32 + 16 h + 0..15, read as four 8-token transposes r = 0..3 at rows
+  // 16 h + 8 (r & 1) + 32 (r >> 1) + (lane % 16) / 2, i.e. at (vofs[r & 1] ^ 32 dt) and 32 rows
+  // (16 KB) further; the swizzle depends on r & 1 only
+  const int i16 = lane & 15, gq = lane >> 4;
+  int vofs[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int vrow = 16 * (gq >> 1) + 8 * par + (i16 >> 1);
+    const int vu = (gq & 1) ^ w_swz(vrow);
+    vofs[par] = vrow * F8_DV + 16 * (vu & 1) + 8 * (i16 & 1) + 32 * (vu >> 1);
+  }
+  uint8_t* const qlo_w = qlo_lds[wave];
+  // Q lo of k-step s: bytes 0..15 of every lane, then bytes 16..31 (1 KB each, read whole)
+  const uint32_t qlo_a = lds_addr(qlo_w) + 16 * lane;
+
+  i32x8 qhi[9];
+  int t = t_lo;
+  int s_cur = 0;  // ring stage of tile t
+  int cb = b_first;
+  int cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
+
+  // S^T of block b of the tile in stage st (rows past the sequence read as zeros and are masked
+  // later), the LDS-DMA instructions of a refill (one per k-step, DMA) and the work hook(i) after
+  // MFMA i (0..17). No branches inside: the k-steps form one block.
+  auto qk_body = [&](const uint8_t* st, int b, f32x16& so, const Dma& dma, auto DMAc,
+                     auto&& hook) {
+    constexpr bool DMA = decltype(DMAc)::value;
+    const uint32_t ka = lds_addr(st) + kofs[b], pa = lds_addr(st) + pofs[b];
+    // reads run KD k-steps ahead: an LDS read shared by the four waves and the ring refill
+    // takes longer than the two MFMAs of one k-step
+    constexpr int KD = 3;
+    i32x8 kop[KD + 1], qop[KD + 1];
+    auto kread = [&](auto Sc) {  // s = 0..7 latent, 8 rope; K bytes and this lane's Q lo bytes
+      constexpr int s = decltype(Sc)::value;
+      const uint32_t a0 = s < 8 ? ka ^ (64 * s) : pa, a1 = a0 ^ 16;
+      const i32x4 k0 = lds_b128_off<0>(a0), k1 = lds_b128_off<0>(a1);
+      const i32x4 q0 = lds_b128_off<s * 64 * 32>(qlo_a);
+      const i32x4 q1 = lds_b128_off<s * 64 * 32 + 64 * 16>(qlo_a);
+      kop[s % (KD + 1)] = i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+      qop[s % (KD + 1)] = i32x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+    };
+    static_for<KD>([&](auto Sc) { kread(Sc); });
+    static_for<9>([&](auto Sc) {
+      constexpr int s = decltype(Sc)::value;
+      constexpr int u = s % (KD + 1);
+      // the 4 reads of k-step s have completed; those of up to KD - 1 later k-steps may be
+      // outstanding (the hooks issue no LDS accesses)
+      lgkm<4 * (KD - 1 < 8 - s ? KD - 1 : 8 - s)>();
+      order_after(kop[u]);
+      order_after(qop[u]);
+      if constexpr (s + KD < 9) kread(std::integral_constant<int, s + KD>{});
+      if constexpr (DMA) issue_dma(dma, s);
+      if constexpr (s == 0)
+        mfma_fp8_v0(so, kop[0], qhi[0]);
+      else
+        mfma_fp8_v(so, kop[u], qhi[s]);
+      hook(2 * s);
+      mfma_fp8_v(so, kop[u], qop[u]);
+      hook(2 * s + 1);
+      sched_fence();
+    });
+    xdl_settle();  // before the softmax reads so
+  };
+  auto qk = [&](const uint8_t* st, int b, f32x16& so, bool dma_on, const Dma& dma, auto&& hook) {
+    if (dma_on)
+      qk_body(st, b, so, dma, std::true_type{}, hook);
+    else
+      qk_body(st, b, so, dma, std::false_type{}, hook);
+  };
+
+  while (t < t_hi) {  // one iteration per sequence piece
+    while (t >= cb_hi) {
+      ++cb;
+      cb_lo = cb_hi;
+      cb_hi = ldc(a.cu + cb + 1);
+    }
+    const int L = max(0, min(ldc(a.seqlens + cb), a.lmax));
+    const int64_t qr = (int64_t)cb * a.Hq + head;
+    float ch;
+    {  // Q of the piece: hi term into VGPRs, lo term into this wave's LDS area
+      const uint8_t* qs = a.qsplit + qr * F8_QROW;
+#pragma unroll
+      for (int s = 0; s < 9; ++s) {
+        qhi[s] = *(const i32x8*)(qs + 64 * s + 32 * hf);
+        const i32x8 lo = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * s + 32 * hf);
+        *(i32x4*)(qlo_w + s * 64 * 32 + lane * 16) = i32x4{lo[0], lo[1], lo[2], lo[3]};
+        *(i32x4*)(qlo_w + s * 64 * 32 + 64 * 16 + lane * 16) = i32x4{lo[4], lo[5], lo[6], lo[7]};
+      }
+      ch = a.score_scale * kvs * ldexpf(1.0f, a.qexp[qr]);
+    }
+    const int p_lo = t, p_hi = min(t_hi, cb_hi);
+    const bool complete = p_lo == cb_lo && p_hi == cb_hi;
+    const int slot = p_lo == t_lo ? 0 : 1;
+    bool first = true;
+    float mref = 0.f, lsum = 0.f;
+    f32x16 oacc[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) oacc[d] = f32x16{};
+
+    // Piece end: normalise and store the wave's 32 heads x 512 dims, to the output for a
+    // complete sequence, else to the piece's partial slot ([slot][head][512] bf16) with its lse.
+    auto flush = [&]() {
+      const float w = kvs / lsum;
+      auto store = [&](uint16_t* o, auto H) {
+        using HH = decltype(H);
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {  // dims 32 dt + 8 q4 + 4 hf + 0..3
+            const f32x4 v = f32x4{oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+                                  oacc[dt][4 * q4 + 3]} * w;
+            *(u32x2*)(o + 32 * dt + 8 * q4) = u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])};
+          }
+          sched_fence();
+        }
+      };
+      if (complete) {
+        store(a.out + qr * F8_DV + 4 * hf, h16<O_BF16>{});
+      } else {
+        const int64_t sb = (int64_t)g * F8_SLOTS + slot;
+        store(a.part_o + (sb * a.Hq + head) * F8_DV + 4 * hf, h16<true>{});
+        if (hf == 0) a.part_lse[sb * a.Hq + head] = mref + __log2f(lsum);
+      }
+    };
+
+    // References are whole numbers (log2 domain), so a change of reference is a power of two:
+    // a block whose max exceeds the reference by more than the headroom moves it to the block
+    // max rounded up, and what was accumulated under the old one is scaled by 2^(old - new)
+    // (rare, wave-uniform)
+    while (t < p_hi) {
+      // tile t visible: this wave's loads of it have landed, then every wave's (barrier), after
+      // which the other stage (tile t - 1) is free for tile t + 1
+      wait_vmcnt<0>();
+      wg_barrier();
+      Dma dma{};
+      const bool refill = t + 1 < t_hi;
+      if (refill) dma = issue_setup(t + 1);
+      const uint8_t* st = stage(s_cur);
+      // valid tokens of the tile's two 32-token blocks (element i of lane half h is token
+      // 16 h + i of its block)
+      const int own0 = L - (t - cb_lo) * F8_TILE, own1 = own0 - 32;
+
+      // softmax of one 32-token block, as levels placed after the MFMAs of the next S^T block
+      // (or run back to back): mask and 8-of-16 max; lane-half max and segment check; block
+      // scale; exponentials; e4m3 pack; rounded sums
+      struct Blk {
+        float mb, sh, ps;
+        int es;
+        bool cut;
+        float m_old;
+        float p[16];
+        int w[4];
+      };
+      auto smax = [&](f32x16& sv, int own, Blk& k, int lvl) {
+        if (lvl == 0) {
+          if (own < 32) {  // wave-uniform: the sequence ends inside this block
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sv[i] = 16 * hf + i >= own ? -INFINITY : sv[i];
+          }
+          float m8[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            m8[j] = fmaxf(fmaxf(sv[4 * j], sv[4 * j + 1]), fmaxf(sv[4 * j + 2], sv[4 * j + 3]));
+          k.mb = fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3]));
+        }
+        if (lvl == 1) {
+          // raw scores; the log2-domain scale ch > 0 is applied inside exp2. A head whose block
+          // max exceeds its reference by more than the headroom moves the reference up to the
+          // block max rounded up; the rescale runs when any head of the wave moved (k.cut)
+          k.mb = xhalf_max(k.mb) * ch;
+          const bool over = first || k.mb > mref + F8_RESET;
+          k.cut = !first && __ballot(over) != 0;
+          k.m_old = mref;
+          mref = over ? ceilf(k.mb) : mref;
+          first = false;
+          // P^T in e4m3 on a per-head power-of-two scale 2^es, es = floor(block max - reference)
+          // - 7, so the block's largest scaled P lies in [128, 256): folded into the exp2
+          // argument and passed to the O^T MFMA as the block's E8M0 scale. The row sums add the
+          // rounded P, so the weights applied to V sum to one
+          const int e = (int)floorf(k.mb - mref) - 7;
+          k.es = k.mb == -INFINITY ? 0 : max(-127, min(127, e));
+          k.sh = -(mref + (float)k.es);
+        }
+        if (lvl >= 2 && lvl <= 5) {
+          const int q = lvl - 2;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) k.p[4 * q + e] = fmaf(sv[4 * q + e], ch, k.sh);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) k.p[4 * q + e] = __builtin_amdgcn_exp2f(k.p[4 * q + e]);
+        }
+        if (lvl == 6 || lvl == 7) {
+          const int q = 2 * (lvl - 6);
+          k.w[q] = pack_fp8x4(k.p[4 * q], k.p[4 * q + 1], k.p[4 * q + 2], k.p[4 * q + 3]);
+          k.w[q + 1] = pack_fp8x4(k.p[4 * q + 4], k.p[4 * q + 5], k.p[4 * q + 6], k.p[4 * q + 7]);
+        }
+        if (lvl >= 8 && lvl <= 11) {  // rounded P back to float, pairwise sums
+          typedef float f2 __attribute__((ext_vector_type(2)));
+          const int q = lvl - 8;
+          const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], false);
+          const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], true);
+          k.p[q] = (lo[0] + lo[1]) + (hi[0] + hi[1]);
+        }
+        if (lvl == 12) {
+          k.ps = xhalf_sum(ldexpf((k.p[0] + k.p[1]) + (k.p[2] + k.p[3]), k.es));
+        }
+      };
+      constexpr int NLVL = 13;
+
+      f32x16 s0, s1;
+      Blk k0, k1;
+      // S^T of block 0 (with the refill of tile t + 1), then of block 1 with block 0's softmax
+      qk(st, 0, s0, refill, dma, [](int) {});
+      qk(st, 1, s1, false, dma, [&](int i) {
+        if (i < NLVL) smax(s0, own0, k0, i);
+      });
+#pragma unroll
+      for (int i = 0; i < 8; ++i) smax(s1, own1, k1, i);  // through block 1's e4m3 words
+      // O^T (512 dims) += V^T P^T over the tile's 64 tokens: 16 dim blocks, the rounded-sum
+      // levels of block 1 placed between them
+      const uint32_t va0 = lds_addr(st) + vofs[0], va1 = lds_addr(st) + vofs[1];
+      auto vread = [&](int dt) {
+        const uint32_t p0 = va0 ^ (32 * dt), p1 = va1 ^ (32 * dt);
+        const i32x2 r0 = lds_tr8_off<0>(p0), r1 = lds_tr8_off<0>(p1);
+        const i32x2 r2 = lds_tr8_off<32 * F8_DV>(p0), r3 = lds_tr8_off<32 * F8_DV>(p1);
+        return i32x8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+      };
+      // V^T reads run VD dim blocks ahead
+      constexpr int VD = 3;
+      auto pv = [&](const i32x8& pb, int psc, auto&& hook) {
+        i32x8 vop[VD + 1];
+#pragma unroll
+        for (int dt = 0; dt < VD; ++dt) vop[dt] = vread(dt);
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+          if (dt + VD < 16) vop[(dt + VD) % (VD + 1)] = vread(dt + VD);
+          // the 4 reads of dim block dt have completed; up to VD later blocks' may be outstanding
+          lgkm_wait(4 * min(VD, 15 - dt));
+          order_after(vop[dt % (VD + 1)]);
+          oacc[dt] = mfma_fp8_bscaled(vop[dt % (VD + 1)], pb, oacc[dt], psc);
+          hook(dt);
+          sched_fence();
+        }
+      };
+      if (__builtin_amdgcn_readfirstlane((int)(k0.cut || k1.cut))) {  // the reference moved
+        // earlier tiles were accumulated under the reference before this tile, block 0 under
+        // the one before block 1 (whole numbers no greater than the new one, so the scales are
+        // exact powers of two in (0, 1]; 1 for the heads that kept their reference). In the
+        // first tile of a piece nothing was accumulated before it (the clamp covers the unset
+        // reference there).
+        const int d_o = min(0, max(-200, (int)(k0.m_old - mref)));
+        const int d_0 = min(0, max(-200, (int)(k1.m_old - mref)));
+        const float a_o = ldexpf(1.0f, d_o);
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {  // in place in the AGPRs that hold O^T
+            float x = oacc[d][i], tmp;
+            asm volatile(
+                "v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\ts_nop 1\n\t"
+                "v_accvgpr_write_b32 %0, %1"
+                : "+a"(x), "=&v"(tmp)
+                : "v"(a_o));
+            oacc[d][i] = x;
+          }
+        }
+        asm volatile("s_nop 4" ::: "memory");  // the writes settle before an MFMA reads them
+        lsum *= a_o;
+        k0.ps = ldexpf(k0.ps, d_0);
+        k0.es += d_0;
+        if (k0.es < -127) {  // below the smallest E8M0 scale: weight under 2^-119 of the max
+          k0.es = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) k0.w[j] = 0;
+        }
+      }
+      // B operand: bytes 16 b .. 16 b + 15 of lane half h are tokens 32 b + 16 h + 0..15; the
+      // scale of k block b comes from lane half b
+      const int psc = (hf ? k1.es : k0.es) + 127;
+      pv(i32x8{k0.w[0], k0.w[1], k0.w[2], k0.w[3], k1.w[0], k1.w[1], k1.w[2], k1.w[3]}, psc,
+         [&](int dt) {  // block 1's rounded sums between the MFMAs
+           if (dt < NLVL - 8) smax(s1, own1, k1, 8 + dt);
+         });
+      lsum += k0.ps + k1.ps;
+      ++t;
+      s_cur ^= 1;
+    }
+    flush();
+  }
+}
+
 // Merge the partial slots of every sequence that spans more than one range; zero-length
 // sequences produce zeros. Thread = (sequence, head, 8 dims); a workgroup covers 4 heads.
 template <bool O_BF16>
@@ -928,9 +1414,12 @@ size_t f8_q_bytes(int64_t B, int64_t Hq) {
   return f8_align((size_t)B * Hq * F8_QROW) + f8_align((size_t)B * Hq * 4);
 }
 
-// ranges per call: B * num_split workgroups shared by the Hq / 64 head groups
+// heads per decode workgroup: 128 (mla_fp8_decode_w32) when Hq is a multiple of 128, else 64
+int64_t f8_group_heads(int64_t Hq) { return Hq % W_HEADS == 0 ? W_HEADS : F8_HEADS; }
+
+// ranges per call: B * num_split workgroups shared by the Hq / heads-per-workgroup head groups
 int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
-  return std::max<int64_t>(1, B * num_split / (Hq / F8_HEADS));
+  return std::max<int64_t>(1, B * num_split / (Hq / f8_group_heads(Hq)));
 }
 
 }  // namespace
@@ -989,7 +1478,7 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.score_scale = score_scale;
   a.kv_scale = kv_scale;
   hipStream_t st = (hipStream_t)stream;
-  const int HG = (int)(Hq / F8_HEADS);
+  const int HG = (int)(Hq / f8_group_heads(Hq));
   const int nq = (int)((B * Hq + 3) / 4);
   if (q_bf16)
     mla_fp8_prep<true><<<nq + 1, 256, 0, st>>>(a, nq);
@@ -997,10 +1486,16 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
     mla_fp8_prep<false><<<nq + 1, 256, 0, st>>>(a, nq);
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 prep)");
   const dim3 grid((unsigned)(((G + 7) / 8) * 8 * HG));
-  if (o_bf16)
+  if (f8_group_heads(Hq) == W_HEADS) {
+    if (o_bf16)
+      mla_fp8_decode_w32<true><<<grid, 256, 0, st>>>(a);
+    else
+      mla_fp8_decode_w32<false><<<grid, 256, 0, st>>>(a);
+  } else if (o_bf16) {
     mla_fp8_decode<true><<<grid, 512, 0, st>>>(a);
-  else
+  } else {
     mla_fp8_decode<false><<<grid, 512, 0, st>>>(a);
+  }
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
   const dim3 cgrid((unsigned)((B * Hq + 3) / 4));
   if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
