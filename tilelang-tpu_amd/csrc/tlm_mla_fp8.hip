@@ -147,6 +147,9 @@ TLM_DEV i32x8 lds_2xb128(const void* p0, const void* p1) {
 TLM_DEV void lds_write_b64(void* p, u32x2 v) {
   asm volatile("ds_write_b64 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
 }
+TLM_DEV void lds_write_b64_at(uint32_t addr, u32x2 v) {
+  asm volatile("ds_write_b64 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 TLM_DEV void lds_write_b32(void* p, uint32_t v) {
   asm volatile("ds_write_b32 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
 }
@@ -1137,26 +1140,63 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
 
     // Piece end: normalise and store the wave's 32 heads x 512 dims, to the output for a
     // complete sequence, else to the piece's partial slot ([slot][head][512] bf16) with its lse.
+    // Rows go out whole: each half (256 dims) is staged in this wave's Q lo area, which the
+    // piece no longer reads, as [head][256] with 16-byte chunk c of head h at c ^ h, then
+    // read back as two 512-byte head rows per instruction.
     auto flush = [&]() {
       const float w = kvs / lsum;
-      auto store = [&](uint16_t* o, auto H) {
+      const int64_t sb = (int64_t)g * F8_SLOTS + slot;
+      uint16_t* const rows = complete ? a.out + ((int64_t)cb * a.Hq + head - hh) * F8_DV
+                                      : a.part_o + (sb * a.Hq + head - hh) * F8_DV;
+      // lane terms computed here from an opaque lane id: hoisted out of the piece loop they
+      // would be kept in (spilled) registers across it
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      const int lh = ln & 31, lf = ln >> 5;
+      const uint32_t stage_a = lds_addr(qlo_w);
+      // the wave's 32 rows as one buffer (base wave-uniform, offsets 32-bit)
+      const __amdgpu_buffer_rsrc_t orows =
+          __builtin_amdgcn_make_buffer_rsrc((void*)rows, (short)0, 32 * F8_DV * 2, F8_RSRC_WORD3);
+      auto put = [&](auto H) {
         using HH = decltype(H);
 #pragma unroll
-        for (int dt = 0; dt < 16; ++dt) {
+        for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {  // dims 32 dt + 8 q4 + 4 hf + 0..3
-            const f32x4 v = f32x4{oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
-                                  oacc[dt][4 * q4 + 3]} * w;
-            *(u32x2*)(o + 32 * dt + 8 * q4) = u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])};
+          for (int d8 = 0; d8 < 8; ++d8) {
+            const int dt = 8 * h2 + d8;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {  // dims 32 dt + 8 q4 + 4 hf + 0..3 of head hh
+              const f32x4 v = f32x4{oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+                                    oacc[dt][4 * q4 + 3]} * w;
+              lds_write_b64_at(stage_a + lh * 512 + 16 * ((4 * d8 + q4) ^ lh) + 8 * lf,
+                               u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])});
+            }
+            sched_fence();
           }
-          sched_fence();
+          lgkm<0>();
+#pragma unroll
+          for (int i0 = 0; i0 < 16; i0 += 8) {
+            i32x4 x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {  // heads 2 (i0 + i) + lf, chunk lh
+              const int hr = 2 * (i0 + i) + lf;
+              x[i] = lds_b128_off<0>(stage_a + hr * 512 + 16 * (lh ^ hr));
+            }
+            lgkm<0>();
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              order_after(x[i]);
+              const int hr = 2 * (i0 + i) + lf;
+              __builtin_amdgcn_raw_buffer_store_b128(x[i], orows, hr * 2 * F8_DV + 512 * h2 + 16 * lh,
+                                                     0, 0);
+            }
+          }
         }
       };
       if (complete) {
-        store(a.out + qr * F8_DV + 4 * hf, h16<O_BF16>{});
+        put(h16<O_BF16>{});
       } else {
-        const int64_t sb = (int64_t)g * F8_SLOTS + slot;
-        store(a.part_o + (sb * a.Hq + head) * F8_DV + 4 * hf, h16<true>{});
+        put(h16<true>{});
         if (hf == 0) a.part_lse[sb * a.Hq + head] = mref + __log2f(lsum);
       }
     };
