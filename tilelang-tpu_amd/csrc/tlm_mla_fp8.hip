@@ -370,8 +370,8 @@ TLM_DEV F8Work f8_work(int x, int HG) {
 // s_waitcnt vmcnt(N) with the other counters untouched
 template <int N>
 TLM_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x3f70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (N & 15) | ((N >> 4) << 14));  // vmcnt bits 3:0 and 15:14
 }
 
 // Workgroup = 64 heads x one range, 8 waves (two per SIMD). Wave w: head block hb = w / 4 (32
@@ -926,7 +926,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   const F8Work wk = f8_work(blockIdx.x, HG);
   if (wk.g >= a.G) return;
   const int g = wk.g, hgi = wk.hgi;
-  const int head = hgi * W_HEADS + 32 * wave + hh;
+  const int head0 = hgi * W_HEADS + 32 * wave;  // the wave's first head (uniform)
+  const int head = head0 + hh;
   // tile indices fit int32 (the tile prefix is int32)
   const int T = ldc(a.cu + a.B);
   const int t_lo = (int)((int64_t)g * T / a.G), t_hi = (int)((int64_t)(g + 1) * T / a.G);
@@ -1060,146 +1061,154 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   int cb = b_first;
   int cb_lo = ldc(a.cu + cb), cb_hi = ldc(a.cu + cb + 1);
 
-  // S^T of block b of the tile in stage st (rows past the sequence read as zeros and are masked
-  // later), the LDS-DMA instructions of a refill (one per k-step, DMA) and the work hook(i) after
-  // MFMA i (0..17). No branches inside: the k-steps form one block.
-  auto qk_body = [&](const uint8_t* st, int b, f32x16& so, const Dma& dma, auto DMAc,
-                     auto&& hook) {
+  // S^T of both 32-token blocks of the tile in stage st as one stream of 18 k-steps (rows past
+  // the sequence read as zeros and are masked later): k-step j is k-step j % 9 of block j / 9.
+  // LDS reads run KD k-steps ahead across the block boundary; the last KD k-steps issue the
+  // first KD V^T reads of the O^T update instead (vpre). Block 0's k-steps carry the LDS-DMA
+  // instructions of a refill (DMA); block 1's MFMAs carry the work hook(i) after MFMA i
+  // (0..17). No branches inside: the k-steps form one block.
+  constexpr int KD = 2;
+  auto qk_body = [&](const uint8_t* st, f32x16& s0, f32x16& s1, const Dma& dma, auto DMAc,
+                     auto&& hook, auto&& vpre) {
     constexpr bool DMA = decltype(DMAc)::value;
-    const uint32_t ka = lds_addr(st) + kofs[b], pa = lds_addr(st) + pofs[b];
-    // reads run KD k-steps ahead: an LDS read shared by the four waves and the ring refill
-    // takes longer than the two MFMAs of one k-step
-    constexpr int KD = 3;
+    const uint32_t sa = lds_addr(st);
     i32x8 kop[KD + 1], qop[KD + 1];
-    auto kread = [&](auto Sc) {  // s = 0..7 latent, 8 rope; K bytes and this lane's Q lo bytes
-      constexpr int s = decltype(Sc)::value;
-      const uint32_t a0 = s < 8 ? ka ^ (64 * s) : pa, a1 = a0 ^ 16;
+    auto kread = [&](auto Jc) {  // K bytes and this lane's Q lo bytes of k-step j
+      constexpr int j = decltype(Jc)::value, b = j / 9, s = j % 9;
+      const uint32_t a0 = s < 8 ? (sa + kofs[b]) ^ (64 * s) : sa + pofs[b], a1 = a0 ^ 16;
       const i32x4 k0 = lds_b128_off<0>(a0), k1 = lds_b128_off<0>(a1);
       const i32x4 q0 = lds_b128_off<s * 64 * 32>(qlo_a);
       const i32x4 q1 = lds_b128_off<s * 64 * 32 + 64 * 16>(qlo_a);
-      kop[s % (KD + 1)] = i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
-      qop[s % (KD + 1)] = i32x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+      kop[j % (KD + 1)] = i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+      qop[j % (KD + 1)] = i32x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
     };
-    static_for<KD>([&](auto Sc) { kread(Sc); });
-    static_for<9>([&](auto Sc) {
-      constexpr int s = decltype(Sc)::value;
-      constexpr int u = s % (KD + 1);
-      // the 4 reads of k-step s have completed; those of up to KD - 1 later k-steps may be
-      // outstanding (the hooks issue no LDS accesses)
-      lgkm<4 * (KD - 1 < 8 - s ? KD - 1 : 8 - s)>();
+    static_for<KD>([&](auto Jc) { kread(Jc); });
+    static_for<18>([&](auto Jc) {
+      constexpr int j = decltype(Jc)::value, b = j / 9, s = j % 9, u = j % (KD + 1);
+      f32x16& so = b ? s1 : s0;
+      // the 4 reads of k-step j have completed; the KD - 1 later batches of 4 may be
+      // outstanding (every k-step issues one batch; the hooks issue no LDS accesses)
+      lgkm<4 * (KD - 1)>();
       order_after(kop[u]);
       order_after(qop[u]);
-      if constexpr (s + KD < 9) kread(std::integral_constant<int, s + KD>{});
-      if constexpr (DMA) issue_dma(dma, s);
+      if constexpr (j + KD < 18)
+        kread(std::integral_constant<int, j + KD>{});
+      else
+        vpre(j + KD - 18);
+      if constexpr (DMA && b == 0) issue_dma(dma, s);
       if constexpr (s == 0)
-        mfma_fp8_v0(so, kop[0], qhi[0]);
+        mfma_fp8_v0(so, kop[u], qhi[0]);
       else
         mfma_fp8_v(so, kop[u], qhi[s]);
-      hook(2 * s);
+      if constexpr (b == 1) hook(2 * s);
       mfma_fp8_v(so, kop[u], qop[u]);
-      hook(2 * s + 1);
+      if constexpr (b == 1) hook(2 * s + 1);
+      if constexpr (j == 8) xdl_settle();  // before block 1's hooks read s0
       sched_fence();
     });
-    xdl_settle();  // before the softmax reads so
+    xdl_settle();  // before the softmax reads s1
   };
-  auto qk = [&](const uint8_t* st, int b, f32x16& so, bool dma_on, const Dma& dma, auto&& hook) {
+  auto qk = [&](const uint8_t* st, f32x16& s0, f32x16& s1, bool dma_on, const Dma& dma,
+                auto&& hook, auto&& vpre) {
     if (dma_on)
-      qk_body(st, b, so, dma, std::true_type{}, hook);
+      qk_body(st, s0, s1, dma, std::true_type{}, hook, vpre);
     else
-      qk_body(st, b, so, dma, std::false_type{}, hook);
+      qk_body(st, s0, s1, dma, std::false_type{}, hook, vpre);
   };
 
-  while (t < t_hi) {  // one iteration per sequence piece
+  // Q of the piece starting at tile t: its sequence cb, the hi term into VGPRs, the lo term
+  // straight into this wave's LDS area (LDS-DMA, 18 x 1 KB: lane l's 16 bytes land at l * 16)
+  // and the exponent (asm load: waited for with the rest at the piece's first tile)
+  int L = 0, qe = 0;
+  auto begin_piece = [&]() {
     while (t >= cb_hi) {
       ++cb;
       cb_lo = cb_hi;
       cb_hi = ldc(a.cu + cb + 1);
     }
-    const int L = max(0, min(ldc(a.seqlens + cb), a.lmax));
-    const int64_t qr = (int64_t)cb * a.Hq + head;
-    float ch;
-    {  // Q of the piece: hi term into VGPRs, lo term into this wave's LDS area
-      const uint8_t* qs = a.qsplit + qr * F8_QROW;
+    L = max(0, min(ldc(a.seqlens + cb), a.lmax));
+    const int64_t qr0 = (int64_t)cb * a.Hq + head0;  // the wave's first Q row (uniform)
+    const uint8_t* qs = a.qsplit + (qr0 + hh) * F8_QROW;
 #pragma unroll
-      for (int s = 0; s < 9; ++s) {
-        qhi[s] = *(const i32x8*)(qs + 64 * s + 32 * hf);
-        const i32x8 lo = *(const i32x8*)(qs + F8_DV + F8_DPE + 64 * s + 32 * hf);
-        *(i32x4*)(qlo_w + s * 64 * 32 + lane * 16) = i32x4{lo[0], lo[1], lo[2], lo[3]};
-        *(i32x4*)(qlo_w + s * 64 * 32 + 64 * 16 + lane * 16) = i32x4{lo[4], lo[5], lo[6], lo[7]};
+    for (int s = 0; s < 9; ++s) qhi[s] = *(const i32x8*)(qs + 64 * s + 32 * hf);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.qsplit + qr0 * F8_QROW), (short)0, 32 * F8_QROW, F8_RSRC_WORD3);
+    int ln;  // lane id computed here: a lane offset hoisted out of the piece loop is spilled
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int qoff = (ln & 31) * F8_QROW + F8_DV + F8_DPE + 32 * (ln >> 5);
+    static_for<18>([&](auto Ic) {  // k-step i / 2, 16-byte half i % 2
+      // the step goes in soffset: an instruction offset would also move the LDS destination
+      constexpr int i = decltype(Ic)::value;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(qlo_w + i * 1024), 16, qoff,
+                                               64 * (i / 2) + 16 * (i % 2), 0, 0);
+    });
+    asm volatile("global_load_dword %0, %1, off" : "=v"(qe) : "v"(a.qexp + qr0 + hh) : "memory");
+  };
+  begin_piece();
+
+  // Piece end: the wave's 32 heads x 512 dims, normalised, go to the output for a complete
+  // sequence, else to the piece's partial slot ([slot][head][512] bf16) with its lse. Rows go
+  // out whole: each quarter (128 dims) is staged in this wave's quarter of the ring stage the
+  // piece's last tile used (all waves are past it: barrier), as [head][128] with 16-byte chunk c
+  // of head h at c ^ (h % 16), and read back as four 256-byte head rows per instruction. The
+  // lse store comes first, then exactly FLUSH_STORES row stores.
+  constexpr int FLUSH_STORES = 32;
+  auto flush = [&](const f32x16 (&oacc)[16], uint16_t* rows, float* lse_at, float lse, float w,
+                   const uint8_t* stg, auto H) {
+    using HH = decltype(H);
+    // lane terms computed here from an opaque lane id: hoisted out of the piece loop they
+    // would be kept in (spilled) registers across it
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int lh = ln & 31, lf = ln >> 5, l16 = ln & 15, l4 = ln >> 4;
+    if (lse_at && lf == 0) *lse_at = lse;
+    const uint32_t stage_a = lds_addr(stg) + wave * (F8_STAGE / 4);
+    // the wave's 32 rows as one buffer (base wave-uniform, offsets 32-bit)
+    const __amdgpu_buffer_rsrc_t orows =
+        __builtin_amdgcn_make_buffer_rsrc((void*)rows, (short)0, 32 * F8_DV * 2, F8_RSRC_WORD3);
+#pragma unroll
+    for (int h4 = 0; h4 < 4; ++h4) {
+#pragma unroll
+      for (int d4 = 0; d4 < 4; ++d4) {
+        const int dt = 4 * h4 + d4;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {  // dims 32 dt + 8 q4 + 4 hf + 0..3 of head hh
+          const f32x4 v = f32x4{oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+                                oacc[dt][4 * q4 + 3]} * w;
+          lds_write_b64_at(stage_a + lh * 256 + 16 * ((4 * d4 + q4) ^ (lh & 15)) + 8 * lf,
+                           u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])});
+        }
+        sched_fence();
       }
-      ch = a.score_scale * kvs * ldexpf(1.0f, a.qexp[qr]);
+      lgkm<0>();
+      i32x4 x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // heads 4 i + l4, chunk l16
+        const int hr = 4 * i + l4;
+        x[i] = lds_b128_off<0>(stage_a + hr * 256 + 16 * (l16 ^ (hr & 15)));
+      }
+      lgkm<0>();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        order_after(x[i]);
+        const int hr = 4 * i + l4;
+        __builtin_amdgcn_raw_buffer_store_b128(x[i], orows, hr * 2 * F8_DV + 256 * h4 + 16 * l16,
+                                               0, 0);
+      }
     }
+  };
+
+  while (t < t_hi) {  // one iteration per sequence piece
     const int p_lo = t, p_hi = min(t_hi, cb_hi);
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
     const int slot = p_lo == t_lo ? 0 : 1;
+    const float ch = a.score_scale * kvs;  // times 2^qe, applied at the piece's first tile
+    float chq = 0.f;
     bool first = true;
     float mref = 0.f, lsum = 0.f;
     f32x16 oacc[16];
 #pragma unroll
     for (int d = 0; d < 16; ++d) oacc[d] = f32x16{};
-
-    // Piece end: normalise and store the wave's 32 heads x 512 dims, to the output for a
-    // complete sequence, else to the piece's partial slot ([slot][head][512] bf16) with its lse.
-    // Rows go out whole: each half (256 dims) is staged in this wave's Q lo area, which the
-    // piece no longer reads, as [head][256] with 16-byte chunk c of head h at c ^ h, then
-    // read back as two 512-byte head rows per instruction.
-    auto flush = [&]() {
-      const float w = kvs / lsum;
-      const int64_t sb = (int64_t)g * F8_SLOTS + slot;
-      uint16_t* const rows = complete ? a.out + ((int64_t)cb * a.Hq + head - hh) * F8_DV
-                                      : a.part_o + (sb * a.Hq + head - hh) * F8_DV;
-      // lane terms computed here from an opaque lane id: hoisted out of the piece loop they
-      // would be kept in (spilled) registers across it
-      int ln;
-      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-      const int lh = ln & 31, lf = ln >> 5;
-      const uint32_t stage_a = lds_addr(qlo_w);
-      // the wave's 32 rows as one buffer (base wave-uniform, offsets 32-bit)
-      const __amdgpu_buffer_rsrc_t orows =
-          __builtin_amdgcn_make_buffer_rsrc((void*)rows, (short)0, 32 * F8_DV * 2, F8_RSRC_WORD3);
-      auto put = [&](auto H) {
-        using HH = decltype(H);
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-#pragma unroll
-          for (int d8 = 0; d8 < 8; ++d8) {
-            const int dt = 8 * h2 + d8;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {  // dims 32 dt + 8 q4 + 4 hf + 0..3 of head hh
-              const f32x4 v = f32x4{oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
-                                    oacc[dt][4 * q4 + 3]} * w;
-              lds_write_b64_at(stage_a + lh * 512 + 16 * ((4 * d8 + q4) ^ lh) + 8 * lf,
-                               u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])});
-            }
-            sched_fence();
-          }
-          lgkm<0>();
-#pragma unroll
-          for (int i0 = 0; i0 < 16; i0 += 8) {
-            i32x4 x[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {  // heads 2 (i0 + i) + lf, chunk lh
-              const int hr = 2 * (i0 + i) + lf;
-              x[i] = lds_b128_off<0>(stage_a + hr * 512 + 16 * (lh ^ hr));
-            }
-            lgkm<0>();
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              order_after(x[i]);
-              const int hr = 2 * (i0 + i) + lf;
-              __builtin_amdgcn_raw_buffer_store_b128(x[i], orows, hr * 2 * F8_DV + 512 * h2 + 16 * lh,
-                                                     0, 0);
-            }
-          }
-        }
-      };
-      if (complete) {
-        put(h16<O_BF16>{});
-      } else {
-        put(h16<true>{});
-        if (hf == 0) a.part_lse[sb * a.Hq + head] = mref + __log2f(lsum);
-      }
-    };
 
     // References are whole numbers (log2 domain), so a change of reference is a power of two:
     // a block whose max exceeds the reference by more than the headroom moves it to the block
@@ -1207,9 +1216,19 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
     // (rare, wave-uniform)
     while (t < p_hi) {
       // tile t visible: this wave's loads of it have landed, then every wave's (barrier), after
-      // which the other stage (tile t - 1) is free for tile t + 1
-      wait_vmcnt<0>();
+      // which the other stage (tile t - 1) is free for tile t + 1. At a piece's first tile the
+      // previous piece's row stores (the most recent VMEM operations) may still be in flight;
+      // the piece's Q was requested before them.
+      if (t == p_lo && p_lo != t_lo) {
+        wait_vmcnt<FLUSH_STORES>();
+      } else {
+        wait_vmcnt<0>();
+      }
       wg_barrier();
+      if (t == p_lo) {
+        asm volatile("" : "+v"(qe) : : "memory");  // the exponent is read after the wait
+        chq = ch * ldexpf(1.0f, qe);
+      }
       Dma dma{};
       const bool refill = t + 1 < t_hi;
       if (refill) dma = issue_setup(t + 1);
@@ -1245,7 +1264,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           // raw scores; the log2-domain scale ch > 0 is applied inside exp2. A head whose block
           // max exceeds its reference by more than the headroom moves the reference up to the
           // block max rounded up; the rescale runs when any head of the wave moved (k.cut)
-          k.mb = xhalf_max(k.mb) * ch;
+          k.mb = xhalf_max(k.mb) * chq;
           const bool over = first || k.mb > mref + F8_RESET;
           k.cut = !first && __ballot(over) != 0;
           k.m_old = mref;
@@ -1259,58 +1278,56 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           k.es = k.mb == -INFINITY ? 0 : max(-127, min(127, e));
           k.sh = -(mref + (float)k.es);
         }
-        if (lvl >= 2 && lvl <= 5) {
-          const int q = lvl - 2;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) k.p[4 * q + e] = fmaf(sv[4 * q + e], ch, k.sh);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) k.p[4 * q + e] = __builtin_amdgcn_exp2f(k.p[4 * q + e]);
+        if (lvl >= 2 && lvl <= 9) {  // exponentials, two per level
+          const int e = 2 * (lvl - 2);
+          k.p[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], chq, k.sh));
+          k.p[e + 1] = __builtin_amdgcn_exp2f(fmaf(sv[e + 1], chq, k.sh));
         }
-        if (lvl == 6 || lvl == 7) {
-          const int q = 2 * (lvl - 6);
+        if (lvl == 10 || lvl == 11) {
+          const int q = 2 * (lvl - 10);
           k.w[q] = pack_fp8x4(k.p[4 * q], k.p[4 * q + 1], k.p[4 * q + 2], k.p[4 * q + 3]);
           k.w[q + 1] = pack_fp8x4(k.p[4 * q + 4], k.p[4 * q + 5], k.p[4 * q + 6], k.p[4 * q + 7]);
         }
-        if (lvl >= 8 && lvl <= 11) {  // rounded P back to float, pairwise sums
+        if (lvl >= 12 && lvl <= 15) {  // rounded P back to float, pairwise sums
           typedef float f2 __attribute__((ext_vector_type(2)));
-          const int q = lvl - 8;
+          const int q = lvl - 12;
           const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], false);
           const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], true);
           k.p[q] = (lo[0] + lo[1]) + (hi[0] + hi[1]);
         }
-        if (lvl == 12) {
+        if (lvl == 16) {
           k.ps = xhalf_sum(ldexpf((k.p[0] + k.p[1]) + (k.p[2] + k.p[3]), k.es));
         }
       };
-      constexpr int NLVL = 13;
+      constexpr int NLVL = 17, NWORDS = 12;  // levels; levels through the e4m3 words
 
-      f32x16 s0, s1;
-      Blk k0, k1;
-      // S^T of block 0 (with the refill of tile t + 1), then of block 1 with block 0's softmax
-      qk(st, 0, s0, refill, dma, [](int) {});
-      qk(st, 1, s1, false, dma, [&](int i) {
-        if (i < NLVL) smax(s0, own0, k0, i);
-      });
-#pragma unroll
-      for (int i = 0; i < 8; ++i) smax(s1, own1, k1, i);  // through block 1's e4m3 words
-      // O^T (512 dims) += V^T P^T over the tile's 64 tokens: 16 dim blocks, the rounded-sum
-      // levels of block 1 placed between them
+      // V^T operand of 32-dim block dt; the reads run VD dim blocks ahead of the O^T MFMAs, the
+      // first VD issued by the last k-steps of the S^T stream
+      constexpr int VD = KD;
       const uint32_t va0 = lds_addr(st) + vofs[0], va1 = lds_addr(st) + vofs[1];
+      i32x8 vop[VD + 1];
       auto vread = [&](int dt) {
         const uint32_t p0 = va0 ^ (32 * dt), p1 = va1 ^ (32 * dt);
         const i32x2 r0 = lds_tr8_off<0>(p0), r1 = lds_tr8_off<0>(p1);
         const i32x2 r2 = lds_tr8_off<32 * F8_DV>(p0), r3 = lds_tr8_off<32 * F8_DV>(p1);
-        return i32x8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+        vop[dt % (VD + 1)] = i32x8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
       };
-      // V^T reads run VD dim blocks ahead
-      constexpr int VD = 3;
-      auto pv = [&](const i32x8& pb, int psc, auto&& hook) {
-        i32x8 vop[VD + 1];
+
+      f32x16 s0, s1;
+      Blk k0, k1;
+      // S^T of both blocks (with the refill of tile t + 1 in block 0), block 0's softmax between
+      // block 1's MFMAs, then block 1's through its e4m3 words
+      qk(st, s0, s1, refill, dma, [&](int i) {
+        if (i < NLVL) smax(s0, own0, k0, i);
+      }, vread);
 #pragma unroll
-        for (int dt = 0; dt < VD; ++dt) vop[dt] = vread(dt);
+      for (int i = 0; i < NWORDS; ++i) smax(s1, own1, k1, i);
+      // O^T (512 dims) += V^T P^T over the tile's 64 tokens: 16 dim blocks, the rounded-sum
+      // levels of block 1 placed between them
+      auto pv = [&](const i32x8& pb, int psc, auto&& hook) {
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) {
-          if (dt + VD < 16) vop[(dt + VD) % (VD + 1)] = vread(dt + VD);
+          if (dt + VD < 16) vread(dt + VD);
           // the 4 reads of dim block dt have completed; up to VD later blocks' may be outstanding
           lgkm_wait(4 * min(VD, 15 - dt));
           order_after(vop[dt % (VD + 1)]);
@@ -1356,13 +1373,25 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       const int psc = (hf ? k1.es : k0.es) + 127;
       pv(i32x8{k0.w[0], k0.w[1], k0.w[2], k0.w[3], k1.w[0], k1.w[1], k1.w[2], k1.w[3]}, psc,
          [&](int dt) {  // block 1's rounded sums between the MFMAs
-           if (dt < NLVL - 8) smax(s1, own1, k1, 8 + dt);
+           if (dt < NLVL - NWORDS) smax(s1, own1, k1, NWORDS + dt);
          });
       lsum += k0.ps + k1.ps;
       ++t;
       s_cur ^= 1;
     }
-    flush();
+    // piece end: request the next piece's Q first (this wave's Q lo area is free), then store
+    // this piece's rows through the stage of its last tile
+    const int64_t sb = (int64_t)g * F8_SLOTS + slot;
+    uint16_t* const rows = complete ? a.out + ((int64_t)cb * a.Hq + head0) * F8_DV
+                                    : a.part_o + (sb * a.Hq + head0) * F8_DV;
+    float* const lse_at = complete ? nullptr : a.part_lse + sb * a.Hq + head;
+    const float lse = mref + __log2f(lsum), w = kvs / lsum;
+    if (t < t_hi) begin_piece();
+    wg_barrier();
+    if (complete)
+      flush(oacc, rows, lse_at, lse, w, stage(s_cur ^ 1), h16<O_BF16>{});
+    else
+      flush(oacc, rows, lse_at, lse, w, stage(s_cur ^ 1), h16<true>{});
   }
 }
 
