@@ -202,6 +202,11 @@ TLM_DEV void mfma_fp8_v0(f32x16& d, const i32x8& a, const i32x8& b) {  // d = a 
 TLM_DEV void mfma_fp8_v(f32x16& d, const i32x8& a, const i32x8& b) {  // d += a b
   asm volatile("s_nop 1\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
 }
+// d = a b with b's k-blocks scaled by 2^(sb - 127) (a unscaled), accumulator in VGPRs
+TLM_DEV void mfma_fp8_v0_bscaled(f32x16& d, const i32x8& a, const i32x8& b, int sb) {
+  asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %4 op_sel_hi:[0,0,0]"
+               : "=&v"(d) : "v"(a), "v"(b), "v"(127), "v"(sb));
+}
 TLM_DEV void xdl_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 // A unscaled (E8M0 127 = 1), B scaled by 2^(sb - 127). Operand k order: byte j of lane half h is
 // k = 32 (j / 16) + 16 h + j % 16; the scale of B's k-block kb (32 values) for column n comes
@@ -1153,7 +1158,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   // of head h at c ^ (h % 16), and read back as four 256-byte head rows per instruction. The
   // lse store comes first, then exactly FLUSH_STORES row stores.
   constexpr int FLUSH_STORES = 32;
-  auto flush = [&](const f32x16 (&oacc)[16], uint16_t* rows, float* lse_at, float lse, float w,
+  auto flush = [&](f32x16 (&oacc)[16], uint16_t* rows, float* lse_at, float lse, float w,
                    const uint8_t* stg, auto H) {
     using HH = decltype(H);
     // lane terms computed here from an opaque lane id: hoisted out of the piece loop they
@@ -1178,6 +1183,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           lds_write_b64_at(stage_a + lh * 256 + 16 * ((4 * d4 + q4) ^ (lh & 15)) + 8 * lf,
                            u32x2{HH::pack(v[0], v[1]), HH::pack(v[2], v[3])});
         }
+        oacc[dt] = f32x16{};  // ready for the next piece (before the stores below are issued)
         sched_fence();
       }
       lgkm<0>();
@@ -1198,6 +1204,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
     }
   };
 
+  f32x16 oacc[16];  // O^T of the piece; zero at its start (the flush clears it)
+#pragma unroll
+  for (int d = 0; d < 16; ++d) oacc[d] = f32x16{};
   while (t < t_hi) {  // one iteration per sequence piece
     const int p_lo = t, p_hi = min(t_hi, cb_hi);
     const bool complete = p_lo == cb_lo && p_hi == cb_hi;
@@ -1206,9 +1215,6 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
     float chq = 0.f;
     bool first = true;
     float mref = 0.f, lsum = 0.f;
-    f32x16 oacc[16];
-#pragma unroll
-    for (int d = 0; d < 16; ++d) oacc[d] = f32x16{};
 
     // References are whole numbers (log2 domain), so a change of reference is a power of two:
     // a block whose max exceeds the reference by more than the headroom moves it to the block
@@ -1241,7 +1247,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       // (or run back to back): mask and 8-of-16 max; lane-half max and segment check; block
       // scale; exponentials; e4m3 pack; rounded sums
       struct Blk {
-        float mb, sh, ps;
+        float mb, sh;
         int es;
         bool cut;
         float m_old;
@@ -1250,7 +1256,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       };
       auto smax = [&](f32x16& sv, int own, Blk& k, int lvl) {
         if (lvl == 0) {
-          if (own < 32) {  // wave-uniform: the sequence ends inside this block
+          if (own < 32) {  // wave-uniform: the sequence ends inside this block (a branch, not
+                           // selects on every tile)
+            asm volatile("" ::: "memory");
 #pragma unroll
             for (int i = 0; i < 16; ++i) sv[i] = 16 * hf + i >= own ? -INFINITY : sv[i];
           }
@@ -1288,18 +1296,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           k.w[q] = pack_fp8x4(k.p[4 * q], k.p[4 * q + 1], k.p[4 * q + 2], k.p[4 * q + 3]);
           k.w[q + 1] = pack_fp8x4(k.p[4 * q + 4], k.p[4 * q + 5], k.p[4 * q + 6], k.p[4 * q + 7]);
         }
-        if (lvl >= 12 && lvl <= 15) {  // rounded P back to float, pairwise sums
-          typedef float f2 __attribute__((ext_vector_type(2)));
-          const int q = lvl - 12;
-          const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], false);
-          const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(k.w[q], true);
-          k.p[q] = (lo[0] + lo[1]) + (hi[0] + hi[1]);
-        }
-        if (lvl == 16) {
-          k.ps = xhalf_sum(ldexpf((k.p[0] + k.p[1]) + (k.p[2] + k.p[3]), k.es));
-        }
       };
-      constexpr int NLVL = 17, NWORDS = 12;  // levels; levels through the e4m3 words
+      constexpr int NLVL = 12;  // the row sums of the rounded, scaled P come from an MFMA
 
       // V^T operand of 32-dim block dt; the reads run VD dim blocks ahead of the O^T MFMAs, the
       // first VD issued by the last k-steps of the S^T stream
@@ -1321,10 +1319,15 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         if (i < NLVL) smax(s0, own0, k0, i);
       }, vread);
 #pragma unroll
-      for (int i = 0; i < NWORDS; ++i) smax(s1, own1, k1, i);
+      for (int i = 0; i < NLVL; ++i) smax(s1, own1, k1, i);
       // O^T (512 dims) += V^T P^T over the tile's 64 tokens: 16 dim blocks, the rounded-sum
       // levels of block 1 placed between them
-      auto pv = [&](const i32x8& pb, int psc, auto&& hook) {
+      // and, after the first dim block, the row sums of the tile's scaled P: ones^T P^T (every
+      // output row holds them; the first MFMA has read P^T, so no VALU write precedes it)
+      const i32x8 ones = i32x8{0x38383838, 0x38383838, 0x38383838, 0x38383838,
+                               0x38383838, 0x38383838, 0x38383838, 0x38383838};  // e4m3 1.0
+      auto pv = [&](const i32x8& pb, int psc) {
+        f32x16 rs;
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) {
           if (dt + VD < 16) vread(dt + VD);
@@ -1332,9 +1335,11 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           lgkm_wait(4 * min(VD, 15 - dt));
           order_after(vop[dt % (VD + 1)]);
           oacc[dt] = mfma_fp8_bscaled(vop[dt % (VD + 1)], pb, oacc[dt], psc);
-          hook(dt);
+          if (dt == 0) mfma_fp8_v0_bscaled(rs, ones, pb, psc);
           sched_fence();
         }
+        asm volatile("" : "+v"(rs));  // read 15 MFMAs later: the sum MFMA has completed
+        return rs[0];
       };
       if (__builtin_amdgcn_readfirstlane((int)(k0.cut || k1.cut))) {  // the reference moved
         // earlier tiles were accumulated under the reference before this tile, block 0 under
@@ -1360,7 +1365,6 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         }
         asm volatile("s_nop 4" ::: "memory");  // the writes settle before an MFMA reads them
         lsum *= a_o;
-        k0.ps = ldexpf(k0.ps, d_0);
         k0.es += d_0;
         if (k0.es < -127) {  // below the smallest E8M0 scale: weight under 2^-119 of the max
           k0.es = 0;
@@ -1371,11 +1375,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       // B operand: bytes 16 b .. 16 b + 15 of lane half h are tokens 32 b + 16 h + 0..15; the
       // scale of k block b comes from lane half b
       const int psc = (hf ? k1.es : k0.es) + 127;
-      pv(i32x8{k0.w[0], k0.w[1], k0.w[2], k0.w[3], k1.w[0], k1.w[1], k1.w[2], k1.w[3]}, psc,
-         [&](int dt) {  // block 1's rounded sums between the MFMAs
-           if (dt < NLVL - NWORDS) smax(s1, own1, k1, NWORDS + dt);
-         });
-      lsum += k0.ps + k1.ps;
+      lsum += pv(i32x8{k0.w[0], k0.w[1], k0.w[2], k0.w[3], k1.w[0], k1.w[1], k1.w[2], k1.w[3]},
+                 psc);
       ++t;
       s_cur ^= 1;
     }
