@@ -1278,6 +1278,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           k.m_old = mref;
           mref = over ? ceilf(k.mb) : mref;
           first = false;
+        }
+        if (lvl == 2) {
           // P^T in e4m3 on a per-head power-of-two scale 2^es, es = floor(block max - reference)
           // - 7, so the block's largest scaled P lies in [128, 256): folded into the exp2
           // argument and passed to the O^T MFMA as the block's E8M0 scale. The row sums add the
@@ -1286,18 +1288,21 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
           k.es = k.mb == -INFINITY ? 0 : max(-127, min(127, e));
           k.sh = -(mref + (float)k.es);
         }
-        if (lvl >= 2 && lvl <= 9) {  // exponentials, two per level
-          const int e = 2 * (lvl - 2);
+        if (lvl >= 3 && lvl <= 10) {  // exponentials, two per level
+          const int e = 2 * (lvl - 3);
           k.p[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], chq, k.sh));
           k.p[e + 1] = __builtin_amdgcn_exp2f(fmaf(sv[e + 1], chq, k.sh));
         }
-        if (lvl == 10 || lvl == 11) {
-          const int q = 2 * (lvl - 10);
+        if (lvl == 11 || lvl == 12) {
+          const int q = 2 * (lvl - 11);
           k.w[q] = pack_fp8x4(k.p[4 * q], k.p[4 * q + 1], k.p[4 * q + 2], k.p[4 * q + 3]);
           k.w[q + 1] = pack_fp8x4(k.p[4 * q + 4], k.p[4 * q + 5], k.p[4 * q + 6], k.p[4 * q + 7]);
         }
       };
-      constexpr int NLVL = 12;  // the row sums of the rounded, scaled P come from an MFMA
+      // the row sums of the rounded, scaled P come from an MFMA; level i of block 0 runs after
+      // block 1's MFMA LVL_AT[i] (dependent levels an MFMA apart at least)
+      constexpr int NLVL = 13;
+      constexpr int LVL_AT[NLVL] = {0, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 13, 14};
 
       // V^T operand of 32-dim block dt; the reads run VD dim blocks ahead of the O^T MFMAs, the
       // first VD issued by the last k-steps of the S^T stream
@@ -1316,7 +1321,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       // S^T of both blocks (with the refill of tile t + 1 in block 0), block 0's softmax between
       // block 1's MFMAs, then block 1's through its e4m3 words
       qk(st, s0, s1, refill, dma, [&](int i) {
-        if (i < NLVL) smax(s0, own0, k0, i);
+#pragma unroll
+        for (int l = 0; l < NLVL; ++l)
+          if (LVL_AT[l] == i) smax(s0, own0, k0, l);
       }, vread);
 #pragma unroll
       for (int i = 0; i < NLVL; ++i) smax(s1, own1, k1, i);
