@@ -295,7 +295,7 @@ int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_
 size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split);
 
 /* Bytes of the library-owned scratch of tlm_mla_decode_noalloc (per GPU). */
-#define TLM_MLA_SCRATCH_BYTES ((size_t)64 << 20)
+#define TLM_MLA_SCRATCH_BYTES ((size_t)128 << 20)
 
 /* tlm_mla_decode without a caller workspace and without any allocation: the kernels' scratch
  * (tile prefix, Q terms, partial outputs and log-sum-exps) lives in a library-owned device array
@@ -304,7 +304,7 @@ size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split)
  * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same
  * arguments, validation and results as tlm_mla_decode (ws / ws_bytes dropped). Returns
  * TLM_EWORKSPACE, before any HIP call, when the path taken needs more scratch than
- * TLM_MLA_SCRATCH_BYTES (the FP8 config B 64, Hq 128 with num_split <= 5 fits). Every call on a
+ * TLM_MLA_SCRATCH_BYTES (the FP8 config B 64, Hq 128 with num_split <= 4 fits). Every call on a
  * GPU shares that GPU's array and nothing in it has to start zeroed; calls that overlap in time on
  * one GPU (several streams or host threads) race on it and must be serialised by the caller. */
 int tlm_mla_decode_noalloc(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,

@@ -232,7 +232,7 @@ def test_mla_noalloc_validation():
     """The allocation-free entry point validates like tlm_mla_decode and rejects, before any HIP
     call, a request whose scratch need exceeds the library's array."""
     L = lib.load()
-    assert L.tlm_mla_scratch_bytes() == 64 << 20
+    assert L.tlm_mla_scratch_bytes() == 128 << 20
     p = ctypes.c_void_p(0x1000)
 
     def call(B=64, Hq=128, dv=512, splits=4, bt=p, kv_dt=lib.F8E4M3, page=64):
@@ -244,15 +244,16 @@ def test_mla_noalloc_validation():
     assert call(kv_dt=lib.F16) == -2  # fp16 KV with bf16 Q
     # the FP8 config with 64 splits needs far more than the scratch
     assert call(splits=64) == -4 and "scratch" in _err()
-    # fp8 pages of 16 tokens take the split path, whose 4 splits x 64 sequences need 67 MB
-    assert call(page=16) == -4 and "scratch" in _err()
+    # fp8 pages of 16 tokens take the split path, whose 16 splits x 64 sequences need 269 MB
+    assert call(page=16, splits=16) == -4 and "scratch" in _err()
     # bf16 KV (split path, 4 splits x 4096 sequences) as well
     assert L.tlm_mla_decode_noalloc(p, p, 576, 576, p, p, 576, 576, 1 << 20, p, p, p, 4096, 128,
                                     512, 64, 64, 128, 4, 0.07, None, lib.BF16, lib.BF16,
                                     lib.BF16, None) == -4
     assert call(B=0) == 0
-    # the config's FP8 path fits the scratch at the benchmark's 4 splits
-    assert L.tlm_mla_workspace_bytes(64, 128, 512, 4) > 0
+    # the config's FP8 path fits the scratch at the benchmark's 4 splits, not at 5
+    assert 0 < L.tlm_mla_workspace_bytes(64, 128, 512, 4) <= L.tlm_mla_scratch_bytes()
+    assert L.tlm_mla_workspace_bytes(64, 128, 512, 5) > L.tlm_mla_scratch_bytes()
 
 
 def test_paged_gather_validation():

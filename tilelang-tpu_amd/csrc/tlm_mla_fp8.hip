@@ -15,13 +15,16 @@
 //     one or more sequences: a sequence entirely inside one range is written to the output
 //     directly; the pieces of a longer one go to partial slots (bf16 O, fp32 lse; one for the
 //     range's first piece, one for its last) merged by the combine kernel;
-//   * workgroup = 64 heads x one range, 8 waves (two per SIMD) = 2 head blocks of 32 x 4 waves.
-//     For S^T = K Q^T the four waves of a head block split a 64-token tile into 2 token blocks x
-//     2 halves of the 576 QK dims, and each wave keeps half of its block's tokens, adding the
-//     other half's partial scores received through LDS; for O^T = V^T P^T they split the 512 V
-//     dims four ways over all 64 tokens. No work is duplicated; a wave holds 64 O accumulators;
-//   * Q^T stays in VGPRs for the whole piece (72 per wave), split per head into two e4m3 terms
-//     q / s = hi + lo (s a power of two putting max|q| at <= 448), which keeps bf16-level accuracy
+//   * two decode kernels share the partition, the Q terms, the P rounding and the combine:
+//     mla_fp8_decode_w32 (Hq a multiple of 128, the config) gives a workgroup 128 heads and each
+//     of its 4 waves 32 heads for the whole tile (described at the kernel); mla_fp8_decode (Hq a
+//     multiple of 64 otherwise) gives a workgroup 64 heads in 8 waves (two per SIMD) = 2 head
+//     blocks of 32 x 4 waves. There, for S^T = K Q^T the four waves of a head block split a
+//     64-token tile into 2 token blocks x 2 halves of the 576 QK dims, and each wave keeps half
+//     of its block's tokens, adding the other half's partial scores received through LDS; for
+//     O^T = V^T P^T they split the 512 V dims four ways over all 64 tokens;
+//   * Q^T (in VGPRs; its lo term in LDS in the 128-head kernel) is split per head into two e4m3
+//     terms q / s = hi + lo (s a power of two putting max|q| at <= 448): bf16-level accuracy
 //     while S^T runs on v_mfma_f32_32x32x64_f8f6f4 straight from the fp8 cache bytes (2 MFMAs per
 //     64 dims: the cost of one bf16 MFMA and no K conversion; the rope dims take the hi term on
 //     one dim half and the lo term on the other, so both halves run 9 MFMAs);
@@ -34,22 +37,25 @@
 //     swapped; bit 4 flipped on dim half 1) so that accumulator elements 0..7 of lane l are the 8
 //     consecutive tokens 16 dq + 8(l/32) + 0..7 that the wave keeps, the byte order of the P^T
 //     blocks exchanged through LDS;
-//   * softmax without accumulator rescaling: a segment fixes its reference max m from its first
-//     tile and accumulates 2^(x - m); only when a tile's max exceeds m by more than 64 (log2
-//     units) does the segment end (its normalised partial is merged into a scratch slot) and a new
-//     one start at that tile. fp32 holds 2^64 * 448 * 2^31 without overflow, so the result equals
-//     the rescaling online softmax while the O accumulators are only ever touched by MFMAs;
-//   * KV tiles (64 tokens x 576 bytes) stream into a 3-stage LDS ring with buffer_load ... lds
+//   * softmax without per-tile rescaling: the reference max m of a head is fixed when its
+//     first block is seen and 2^(x - m) accumulates; only a block whose max exceeds m by more
+//     than 64 (log2 units) moves it. fp32 holds 2^64 * 448 * 2^31 without overflow, so the result
+//     equals the rescaling online softmax while the O accumulators are touched by MFMAs only. The
+//     64-head kernel ends a segment there (its normalised partial merges into a scratch slot);
+//     the 128-head kernel keeps whole-number references and scales what it holds by the exact
+//     power of two instead;
+//   * KV tiles (64 tokens x 576 bytes) stream into an LDS ring (3 stages; 2 in the 128-head
+//     kernel) with buffer_load ... lds
 //     (16 bytes per lane, no VGPR round trip); each tile's buffer descriptor bounds the rows to
 //     the sequence's valid tokens and to the KV pool, so rows past either read as zeros (never
 //     stale NaN bytes); an explicit vmcnt wait plus s_barrier hands a stage over;
 //   * LDS layout per stage: latent rows of 512 B then rope rows of 64 B, 16-byte chunks XOR-
 //     swizzled so that the row reads of S^T (ds_read_b128) and the transposed reads of V^T
 //     (ds_read_b64_tr_b8) are both bank-conflict free;
-//   * the softmax of tile t runs as short levels of independent instructions between the S^T
-//     MFMAs of tile t + 1 (a wave issues in order; a long dependent chain there would hold back
-//     the MFMAs), and nothing in the tile loop may be spilled: a scratch reload there costs a
-//     vmcnt(0) wait on the ring's in-flight LDS-DMA loads.
+//   * the softmax runs as short levels of independent instructions between S^T MFMAs (a wave
+//     issues in order; a long dependent chain there would hold back the MFMAs), and nothing in
+//     the tile loop may be spilled: a scratch reload there costs a vmcnt(0) wait on the ring's
+//     in-flight LDS-DMA loads.
 #include "tlm_common.h"
 
 #include <algorithm>
@@ -897,21 +903,27 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
 // the whole tile: S^T = K Q^T, the softmax and O^T = V^T P^T with no exchange between waves, so
 // the only barrier per tile hands over the ring, and each KV tile goes from L2 to LDS once for all
 // 128 heads.
-//   * registers: the 32 heads' O^T (512 dims, 256 fp32 accumulators per lane) and the hi term of
-//     Q (72 VGPRs); the lo term of Q is kept in LDS (one wave's 32 heads: 18 KB) and read with K;
+//   * registers: the 32 heads' O^T (512 dims: 256 fp32 accumulators per lane, all the AGPRs)
+//     and the hi term of Q (72 VGPRs); S^T accumulates in VGPRs (inline-asm MFMA, since the
+//     builtin's AGPR form would take AGPRs from O^T); the lo term of Q is kept in LDS (one wave's
+//     32 heads: 18 KB) and read with K;
 //   * a 64-token tile is two 32-token blocks b; K rows are fed to the S^T MFMA in the order rho
 //     (row m -> token (m & 3) | ((m >> 3) & 3) << 2 | ((m >> 2) & 1) << 4), so accumulator element
 //     i of lane half h is token 16 h + i of the block: packed to e4m3 they are exactly bytes
 //     16 b .. 16 b + 15 of the P^T operand of lane half h, with no exchange between lanes;
-//   * the softmax of block 0 runs between the S^T MFMAs of block 1; block 1's after them, its row
-//     sums between the O^T MFMAs. Segments (the reference max fixed per segment) may now end at a
-//     block: a block whose max exceeds the reference by more than the headroom starts a new one,
-//     and a tile cut between its blocks is multiplied in two halves;
+//   * the S^T MFMAs of both blocks are one stream of 18 k-steps with LDS reads two k-steps ahead;
+//     block 0's softmax runs between block 1's MFMAs, block 1's after them; the row sums of the
+//     rounded, scaled P come from one more MFMA (ones^T P^T) with the O^T update;
+//   * references are whole numbers, so moving one (a block more than 64 above it) scales the
+//     accumulated O^T and row sums by an exact power of two, in place in the AGPRs (rare);
 //   * 2-stage ring: the tile is consumed (S^T then O^T) within one iteration, and the next tile
 //     is loaded meanwhile (9 LDS-DMA instructions per wave, one per k-step of block 0);
 //   * the ring's 16-byte chunks are swizzled with row bits 0..2 and 4 (the rows read together
 //     under the order rho differ there), which keeps the K row reads, the rope reads and the
-//     transposed V reads free of bank conflicts.
+//     transposed V reads free of bank conflicts;
+//   * at a piece end the next piece's Q is requested first, then the normalised rows are staged
+//     through the last tile's ring stage and stored whole; the next piece's first tile waits for
+//     the loads only (the stores are the most recent VMEM operations).
 constexpr int W_HEADS = 128;
 constexpr int W_NSTAGE = 2;
 constexpr int W_QLO = 9 * 64 * 32;  // one wave's Q lo operands: [k-step][16-byte half][lane]
