@@ -77,6 +77,7 @@ constexpr int F8_STAGE = F8_LAT + F8_TILE * F8_DPE;  // + rope bytes
 constexpr int F8_NSTAGE = 3;
 constexpr int F8_HEADS = 64;                         // heads per workgroup (2 blocks x 32)
 constexpr int F8_LAT_LOADS = 4;                      // latent LDS-DMA loads per thread per stage
+constexpr int F8_PIECE_COST = 2;                    // tiles' worth of work of a piece
 constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
@@ -252,7 +253,9 @@ struct F8Args {
   int64_t kv_stride, kpe_stride, kv_rows;  // bytes between token rows; rows in the pool
   const int32_t* bt;
   const int32_t* seqlens;
-  int32_t* cu;  // [B + 1] tile prefix over sequences (written by the prep kernel)
+  int32_t* cu;       // [B + 1] tile prefix over sequences (written by the prep kernel)
+  int32_t* vcu;      // [B + 1] cost prefix: cu plus F8_PIECE_COST per non-empty sequence before
+  int32_t* range_t;  // [G + 1] first tile of each range (range g: [range_t[g], range_t[g + 1]))
   uint8_t* qsplit;  // [B * Hq][2][576] e4m3 hi and lo terms of q / 2^qexp (written by prep)
   int32_t* qexp;    // [B * Hq] power-of-two exponent of each head's Q scale
   float* part_lse;
@@ -271,11 +274,16 @@ constexpr int F8_QROW = 2 * (F8_DV + F8_DPE);  // bytes per (sequence, head) in 
 //     q / 2^e = hi + lo, with 2^e the power of two that puts max|q| at <= 448; hi + lo is exact
 //     for every element within 2^10 of the row maximum (a bf16/fp16 value has at most 8/11
 //     significant bits and the residual of the first rounding fits e4m3's 4);
-//   * workgroup nq: tile prefix over sequences, cu[b] = sum_{b' < b} ceil(L_b' / 64).
+//   * workgroup nq: tile prefix over sequences, cu[b] = sum_{b' < b} ceil(L_b' / 64), and the
+//     ranges: the cost of a sequence is its tiles plus F8_PIECE_COST (the fixed work of a piece:
+//     its Q fetch and its row flush, in tiles), the cost line [0, V) is cut into G equal ranges
+//     and range g starts at the first tile at or after cost position floor(g V / G) (a range
+//     starting inside a sequence's piece cost starts at its first tile). Ranges holding a
+//     sequence start then get fewer tiles.
 template <bool Q_BF16>
 __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
   if ((int)blockIdx.x == nq) {
-    __shared__ int32_t part[256];
+    __shared__ int32_t part[256], vpart[256];
     const int t = threadIdx.x;
     const int per = (a.B + 255) / 256;
     const int b0 = min(a.B, t * per), b1 = min(a.B, b0 + per);
@@ -283,22 +291,46 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
       const int L = max(0, min(a.seqlens[b], a.lmax));
       return (L + F8_TILE - 1) / F8_TILE;
     };
-    int32_t sum = 0;
-    for (int b = b0; b < b1; ++b) sum += tiles(b);
+    auto cost = [&](int n) { return n ? n + F8_PIECE_COST : 0; };
+    int32_t sum = 0, vsum = 0;
+    for (int b = b0; b < b1; ++b) {
+      const int n = tiles(b);
+      sum += n;
+      vsum += cost(n);
+    }
     part[t] = sum;
+    vpart[t] = vsum;
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {
-      const int32_t v = t >= off ? part[t - off] : 0;
+      const int32_t v = t >= off ? part[t - off] : 0, vv = t >= off ? vpart[t - off] : 0;
       __syncthreads();
       part[t] += v;
+      vpart[t] += vv;
       __syncthreads();
     }
-    int32_t run = part[t] - sum;
+    const int64_t V = vpart[255], G = a.G;
+    int32_t run = part[t] - sum, vrun = vpart[t] - vsum;
     for (int b = b0; b < b1; ++b) {
+      const int n = tiles(b), vn = cost(n);
       a.cu[b] = run;
-      run += tiles(b);
+      a.vcu[b] = vrun;
+      // ranges whose cost start floor(g V / G) lies in this sequence's [vrun, vrun + vn)
+      if (vn > 0) {
+        for (int64_t g = (vrun * G + V - 1) / V; g < G && (g * V) / G < vrun + vn; ++g) {
+          const int64_t v = (g * V) / G;
+          a.range_t[g] = run + (int)max((int64_t)0, v - vrun - F8_PIECE_COST);
+        }
+      }
+      run += n;
+      vrun += vn;
     }
-    if (t == 255) a.cu[a.B] = part[255];
+    if (t == 255) {
+      a.cu[a.B] = part[255];
+      a.vcu[a.B] = vpart[255];
+      a.range_t[a.G] = part[255];
+      if (V == 0)  // no tiles at all: every range is empty
+        for (int g = 0; g < a.G; ++g) a.range_t[g] = 0;
+    }
     return;
   }
   using H = h16<Q_BF16>;
@@ -414,8 +446,7 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
   const int g = wk.g, hgi = wk.hgi;
   const int head = hgi * F8_HEADS + hb * 32 + hh;
   // tile indices fit int32 (the tile prefix is int32)
-  const int T = ldc(a.cu + a.B);
-  const int t_lo = (int)((int64_t)g * T / a.G), t_hi = (int)((int64_t)(g + 1) * T / a.G);
+  const int t_lo = ldc(a.range_t + g), t_hi = ldc(a.range_t + g + 1);
   if (t_lo >= t_hi) return;
   const float kvs = a.kv_scale ? ldc(a.kv_scale) : 1.0f;
 
@@ -946,27 +977,15 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   const int head0 = hgi * W_HEADS + 32 * wave;  // the wave's first head (uniform)
   const int head = head0 + hh;
   // tile indices fit int32 (the tile prefix is int32)
-  const int T = ldc(a.cu + a.B);
-  const int t_lo = (int)((int64_t)g * T / a.G), t_hi = (int)((int64_t)(g + 1) * T / a.G);
+  const int t_lo = ldc(a.range_t + g), t_hi = ldc(a.range_t + g + 1);
   if (t_lo >= t_hi) return;
   const float kvs = a.kv_scale ? ldc(a.kv_scale) : 1.0f;
-
-  // first sequence with a tile in [t_lo, t_hi): largest b with cu[b] <= t_lo
-  int b_first = 0;
-  {
-    int lo = 0, hi = a.B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (ldc(a.cu + mid) <= t_lo) lo = mid; else hi = mid - 1;
-    }
-    b_first = lo;
-  }
 
   // ---- per-tile page table: lane j holds the first KV row of tile tb + j and the number of its
   // rows to load (the sequence's valid tokens that lie inside the pool; the rest read as zeros)
   int tb = INT32_MIN / 2;
   uint32_t tab_lo = 0, tab_hi = 0;
-  int tab_n = 0;
+  int tab_n = 0, tab_b = 0;
   auto build_table = [&](int base) {
     tb = base;
     const int tj = base + lane;
@@ -978,6 +997,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         const int mid = (blo + bhi + 1) >> 1;
         if (a.cu[mid] <= tj) blo = mid; else bhi = mid - 1;
       }
+      tab_b = blo;
       const int L = max(0, min(a.seqlens[blo], a.lmax));
       const int tok0 = (tj - a.cu[blo]) * F8_TILE;
       const int valid = min(F8_TILE, L - tok0);
@@ -991,6 +1011,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
     }
   };
   build_table(t_lo);
+  // first sequence with a tile in [t_lo, t_hi): the sequence of lane 0's tile
+  const int b_first = __builtin_amdgcn_readfirstlane(tab_b);
 
   // ---- KV ring: LDS-DMA of tile t into stage (t - t_lo) % 2; wave w loads latent rows
   // 16 w .. 16 w + 15 (8 instructions) and rope rows 16 w .. 16 w + 15 (1 instruction)
@@ -1427,18 +1449,20 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   const int d0 = 8 * (threadIdx.x & 63);
   using H = h16<O_BF16>;
   uint16_t* o = a.out + row * F8_DV + d0;
-  const int64_t T = ldc(a.cu + a.B), c0 = ldc(a.cu + b), c1 = ldc(a.cu + b + 1);
-  if (c0 == c1) {
+  // positions on the cost line (see the prep kernel): the sequence covers [v0, v1), its first
+  // tile at v0 + F8_PIECE_COST; range g starts at cost position floor(g V / G)
+  const int64_t V = ldc(a.vcu + a.B), v0 = ldc(a.vcu + b), v1 = ldc(a.vcu + b + 1);
+  if (v0 == v1) {
     *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
     return;
   }
   const int64_t G = a.G;
-  const int64_t g0 = ((c0 + 1) * G - 1) / T, g1 = (c1 * G - 1) / T;
+  const int64_t g0 = ((v0 + F8_PIECE_COST + 1) * G - 1) / V, g1 = (v1 * G - 1) / V;
   if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
-  // range starts floor(g T / G) stepped incrementally: floor(g T / G) + T / G, plus one when the
-  // remainder (g T) mod G wraps
-  const int64_t tq = T / G, tr = T % G;
-  int64_t s_cur = g0 * T / G, r_cur = g0 * T % G;  // start of range g and its remainder
+  // range starts floor(g V / G) stepped incrementally: floor(g V / G) + V / G, plus one when the
+  // remainder (g V) mod G wraps
+  const int64_t tq = V / G, tr = V % G;
+  int64_t s_cur = g0 * V / G, r_cur = g0 * V % G;  // start of range g and its remainder
   auto step = [&](int64_t& st, int64_t& rm) {
     st += tq;
     rm += tr;
@@ -1447,7 +1471,8 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
       ++st;
     }
   };
-  const bool first_is_piece = c0 != s_cur;  // the sequence starts inside range g0: slot 1 there
+  // range g0 also holds tiles of earlier sequences when it starts before this one: slot 1 there
+  const bool first_is_piece = s_cur < v0;
   // Online merge over the ranges in batches of F8_CMB: the lse values and partial outputs of a
   // batch are all requested before any is used, so a call waits for about one memory latency
   // per batch (a sequence spans at most a few ranges at the usual split counts).
@@ -1498,7 +1523,10 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
 }
 
 size_t f8_align(size_t n) { return (n + 255) & ~(size_t)255; }
-size_t f8_cu_bytes(int64_t B) { return f8_align((size_t)(B + 1) * 4); }
+// tile prefix cu and cost prefix vcu ([B + 1] each), range starts ([G + 1])
+size_t f8_cu_bytes(int64_t B, int64_t G) {
+  return f8_align((size_t)(B + 1) * 8) + f8_align((size_t)(G + 1) * 4);
+}
 size_t f8_q_bytes(int64_t B, int64_t Hq) {
   return f8_align((size_t)B * Hq * F8_QROW) + f8_align((size_t)B * Hq * 4);
 }
@@ -1513,12 +1541,12 @@ int64_t f8_ranges(int64_t B, int64_t Hq, int num_split) {
 
 }  // namespace
 
-// Workspace of the fp8 path: tile prefix, Q terms, then lse (fp32) and O (bf16) partial slots
-// (three 64-head x 512 slots per range and head group).
+// Workspace of the fp8 path: tile and cost prefixes and range starts, Q terms, then lse (fp32)
+// and O (bf16) partial slots (three slots of Hq x 512 per range).
 size_t tlm_mla_fp8_workspace_bytes(int64_t B, int64_t Hq, int num_split) {
   if (Hq % F8_HEADS) return 0;
   const size_t G = (size_t)f8_ranges(B, Hq, num_split);
-  return f8_cu_bytes(B) + f8_q_bytes(B, Hq) +
+  return f8_cu_bytes(B, (int64_t)G) + f8_q_bytes(B, Hq) +
          G * F8_SLOTS * (size_t)Hq * (F8_DV * sizeof(uint16_t) + sizeof(float));
 }
 
@@ -1551,11 +1579,13 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.kv_rows = kv_rows;
   a.bt = block_table;
   a.seqlens = seqlens;
-  a.cu = (int32_t*)ws;
   const int64_t G = f8_ranges(B, Hq, num_split);
-  a.qsplit = (uint8_t*)ws + f8_cu_bytes(B);
+  a.cu = (int32_t*)ws;
+  a.vcu = a.cu + (B + 1);
+  a.range_t = (int32_t*)((char*)ws + f8_align((size_t)(B + 1) * 8));
+  a.qsplit = (uint8_t*)ws + f8_cu_bytes(B, G);
   a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
-  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B) + f8_q_bytes(B, Hq));
+  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B, G) + f8_q_bytes(B, Hq));
   a.part_o = (uint16_t*)(a.part_lse + G * F8_SLOTS * Hq);
   a.out = (uint16_t*)o;
   a.B = (int)B;
