@@ -77,7 +77,7 @@ constexpr int F8_STAGE = F8_LAT + F8_TILE * F8_DPE;  // + rope bytes
 constexpr int F8_NSTAGE = 3;
 constexpr int F8_HEADS = 64;                         // heads per workgroup (2 blocks x 32)
 constexpr int F8_LAT_LOADS = 4;                      // latent LDS-DMA loads per thread per stage
-constexpr int F8_PIECE_COST = 2;                    // tiles' worth of work of a piece
+constexpr int F8_PIECE_COST = 3;                    // tiles' worth of work of a piece
 constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
