@@ -948,7 +948,7 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
 //   * references are whole numbers, so moving one (a block more than 64 above it) scales the
 //     accumulated O^T and row sums by an exact power of two, in place in the AGPRs (rare);
 //   * 2-stage ring: the tile is consumed (S^T then O^T) within one iteration, and the next tile
-//     is loaded meanwhile (9 LDS-DMA instructions per wave, one per k-step of block 0);
+//     is loaded meanwhile (9 LDS-DMA instructions per wave, on the even k-steps of the stream);
 //   * the ring's 16-byte chunks are swizzled with row bits 0..2 and 4 (the rows read together
 //     under the order rho differ there), which keeps the K row reads, the rope reads and the
 //     transposed V reads free of bank conflicts;
@@ -1103,7 +1103,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   // S^T of both 32-token blocks of the tile in stage st as one stream of 18 k-steps (rows past
   // the sequence read as zeros and are masked later): k-step j is k-step j % 9 of block j / 9.
   // LDS reads run KD k-steps ahead across the block boundary; the last KD k-steps issue the
-  // first KD V^T reads of the O^T update instead (vpre). Block 0's k-steps carry the LDS-DMA
+  // first KD V^T reads of the O^T update instead (vpre). The even k-steps carry the LDS-DMA
   // instructions of a refill (DMA); block 1's MFMAs carry the work hook(i) after MFMA i
   // (0..17). No branches inside: the k-steps form one block.
   constexpr int KD = 2;
@@ -1134,7 +1134,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         kread(std::integral_constant<int, j + KD>{});
       else
         vpre(j + KD - 18);
-      if constexpr (DMA && b == 0) issue_dma(dma, s);
+      // the refill, spread over both blocks (even k-steps): the CU takes each 1 KB LDS-DMA
+      // instruction in ~40 cycles, which a burst on block 0 alone turned into issue stalls
+      if constexpr (DMA && j % 2 == 0) issue_dma(dma, j / 2);
       if constexpr (s == 0)
         mfma_fp8_v0(so, kop[u], qhi[0]);
       else
