@@ -1338,7 +1338,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       // the row sums of the rounded, scaled P come from an MFMA; level i of block 0 runs after
       // block 1's MFMA LVL_AT[i] (dependent levels an MFMA apart at least)
       constexpr int NLVL = 13;
-      constexpr int LVL_AT[NLVL] = {0, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 13, 14};
+      constexpr int LVL_AT[NLVL] = {0, 2, 4, 5, 6, 7, 8, 9, 10, 11, 12, 14, 16};
 
       // V^T operand of 32-dim block dt; the reads run VD dim blocks ahead of the O^T MFMAs, the
       // first VD issued by the last k-steps of the S^T stream
