@@ -270,19 +270,30 @@ struct F8Args {
 constexpr int F8_QROW = 2 * (F8_DV + F8_DPE);  // bytes per (sequence, head) in qsplit
 
 // Prep kernel, one launch ahead of the decode kernel:
-//   * workgroups 0 .. nq-1: one wave per (sequence, head) splits that Q row into two e4m3 terms,
+//   * workgroups 1 .. nq: one wave per (sequence, head) splits that Q row into two e4m3 terms,
 //     q / 2^e = hi + lo, with 2^e the power of two that puts max|q| at <= 448; hi + lo is exact
 //     for every element within 2^10 of the row maximum (a bf16/fp16 value has at most 8/11
 //     significant bits and the residual of the first rounding fits e4m3's 4);
-//   * workgroup nq: tile prefix over sequences, cu[b] = sum_{b' < b} ceil(L_b' / 64), and the
+//   * workgroup 0 (dispatched first, so its dependent loads overlap the Q split): tile prefix
+//     over sequences, cu[b] = sum_{b' < b} ceil(L_b' / 64), and the
 //     ranges: the cost of a sequence is its tiles plus F8_PIECE_COST (the fixed work of a piece:
 //     its Q fetch and its row flush, in tiles), the cost line [0, V) is cut into G equal ranges
 //     and range g starts at the first tile at or after cost position floor(g V / G) (a range
 //     starting inside a sequence's piece cost starts at its first tile). Ranges holding a
 //     sequence start then get fewer tiles.
+// floor / ceil of n / d for 0 <= n < 2^53, 0 < d: a double quotient corrected by integer
+// products (a 64-bit integer division is a long software routine on the GPU)
+TLM_DEV int64_t div_floor(int64_t n, int64_t d) {
+  int64_t q = (int64_t)((double)n / (double)d);
+  while (q * d > n) --q;
+  while ((q + 1) * d <= n) ++q;
+  return q;
+}
+TLM_DEV int64_t div_ceil(int64_t n, int64_t d) { return div_floor(n + d - 1, d); }
+
 template <bool Q_BF16>
 __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
-  if ((int)blockIdx.x == nq) {
+  if (blockIdx.x == 0) {
     __shared__ int32_t part[256], vpart[256];
     const int t = threadIdx.x;
     const int per = (a.B + 255) / 256;
@@ -316,8 +327,9 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
       a.vcu[b] = vrun;
       // ranges whose cost start floor(g V / G) lies in this sequence's [vrun, vrun + vn)
       if (vn > 0) {
-        for (int64_t g = (vrun * G + V - 1) / V; g < G && (g * V) / G < vrun + vn; ++g) {
-          const int64_t v = (g * V) / G;
+        for (int64_t g = div_ceil(vrun * G, V); g < G; ++g) {
+          const int64_t v = div_floor(g * V, G);
+          if (v >= vrun + vn) break;
           a.range_t[g] = run + (int)max((int64_t)0, v - vrun - F8_PIECE_COST);
         }
       }
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
   }
   using H = h16<Q_BF16>;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)(blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)a.B * a.Hq) return;
   // lane: latent dims 8 lane .. +7; lanes 0..7 also rope dims 8 lane .. +7
   const u32x4 wl = *(const u32x4*)(a.q + row * a.q_stride + 8 * lane);
@@ -1459,12 +1471,12 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
     return;
   }
   const int64_t G = a.G;
-  const int64_t g0 = ((v0 + F8_PIECE_COST + 1) * G - 1) / V, g1 = (v1 * G - 1) / V;
+  const int64_t g0 = div_floor((v0 + F8_PIECE_COST + 1) * G - 1, V), g1 = div_floor(v1 * G - 1, V);
   if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
   // range starts floor(g V / G) stepped incrementally: floor(g V / G) + V / G, plus one when the
   // remainder (g V) mod G wraps
-  const int64_t tq = V / G, tr = V % G;
-  int64_t s_cur = g0 * V / G, r_cur = g0 * V % G;  // start of range g and its remainder
+  const int64_t tq = div_floor(V, G), tr = V - tq * G;
+  int64_t s_cur = div_floor(g0 * V, G), r_cur = g0 * V - s_cur * G;  // start of range g, remainder
   auto step = [&](int64_t& st, int64_t& rm) {
     st += tq;
     rm += tr;
