@@ -355,14 +355,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
   }
 
   // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i.
-  // 16-bit C with N % 8 == 0: the wave's 128 x 64 sub-tile is rounded into its own 16 KB of
-  // LDS (the operand stages are free: the last barrier ended every operand read and no LDS-DMA
-  // is in flight) and written back as 16-byte row vectors, full 128-byte lines per 8 lanes,
-  // instead of 2-byte stores. Stage row r holds 64 columns (128 bytes); its 16-byte chunk c sits
+  // 16-bit C with N % 8 == 0 and C 16-byte aligned: the wave's 128 x 64 sub-tile is rounded
+  // into its own 16 KB of LDS (the operand stages are free: the last barrier ended every operand
+  // read and no LDS-DMA is in flight) and written back as 16-byte row vectors, full 128-byte
+  // lines per 8 lanes, instead of 2-byte stores. Stage row r holds 64 columns (128 bytes); its 16-byte chunk c sits
   // at c ^ ((r / 4) % 8), so the four row groups of one 2-byte write and the two rows of one
   // 16-lane read hit distinct banks.
   if constexpr (OUT != TLM_F32) {
-    if (N % 8 == 0) {
+    if (N % 8 == 0 && ((uintptr_t)C & 15) == 0) {
       uint16_t* stg = (uint16_t*)smem + wave * (128 * 64);
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt)

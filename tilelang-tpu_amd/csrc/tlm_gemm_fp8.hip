@@ -268,7 +268,47 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
     }
   }
 
-  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i
+  // epilogue: lane holds column (lane & 15) of each 16x16 tile, rows 4 (lane / 16) + i.
+  // fp32 C with N % 4 == 0 and C 16-byte aligned: the wave's 128 x 64 sub-tile goes through its
+  // own 16 KB of LDS in two 64-row halves (the stages are free: the last barrier ended every
+  // operand read and no LDS-DMA is in flight) and leaves as 16-byte row vectors, one 256-byte
+  // row per 16 lanes, instead of 4-byte stores. Stage row r holds 64 floats (16 chunks of 16
+  // bytes); chunk c sits at c ^ 4((r / 4) % 4), so the four row groups of one 4-byte write land
+  // in four different 64-byte bank windows and a 16-lane read covers one row.
+  if constexpr (OUT == TLM_F32) {
+    if (N % 4 == 0 && ((uintptr_t)C & 15) == 0) {
+      float* stg = (float*)smem + wave * (64 * 64);
+      float* Cf = (float*)C;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = m * 16 + 4 * (lane >> 4) + i, c = nt * 16 + (lane & 15);
+              stg[r * 64 + 4 * ((c >> 2) ^ (4 * ((r >> 2) & 3))) + (c & 3)] =
+                  acc[4 * h + m][nt][i];
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+          const int idx = it * 64 + lane, r = idx >> 4, c4 = idx & 15;
+          const u32x4 v = *(const u32x4*)(stg + r * 64 + 4 * (c4 ^ (4 * ((r >> 2) & 3))));
+          const int row = m0 + wm * 128 + 64 * h + r, col = n0 + wn * 64 + 4 * c4;
+          if (row < M && col < N) *(u32x4*)(Cf + (int64_t)row * N + col) = v;
+        }
+        // the second half overwrites the stage only after every lane has read the first
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
