@@ -78,7 +78,11 @@ constexpr int F8_NSTAGE = 3;
 constexpr int F8_HEADS = 64;                         // heads per workgroup (2 blocks x 32)
 constexpr int F8_LAT_LOADS = 4;                      // latent LDS-DMA loads per thread per stage
 constexpr int F8_PIECE_COST = 3;                    // tiles' worth of work of a piece
-constexpr int F8_SLOTS = 3;                          // first piece, last piece, segment scratch
+constexpr int F8_SLOTS = 3;
+// cache policy of the KV-cache LDS-DMA loads: non-temporal (bit 1 on gfx950). The cache is read
+// once per call; streaming it leaves L2 and the Infinity Cache to Q and the partial slots
+// (whole call ~1-2% faster back to back, ~12% after a cache flush).
+constexpr int F8_KV_NT = 2;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
 
@@ -539,7 +543,7 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + ki * 1024), 16, off, 0, 0,
-                                               0);
+                                               F8_KV_NT);
     } else {  // rope: 16 rows x 4 chunks per wave-instruction
       int ln;  // lane id computed here, not kept in a register across the tile
       asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
@@ -548,7 +552,7 @@ __global__ __launch_bounds__(512) void mla_fp8_decode(const F8Args a) {
       const __amdgpu_buffer_rsrc_t rp =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bpe, (short)0, d.npe, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(d.st + F8_LAT + wave * 1024), 16,
-                                               off, 0, 0, 0);
+                                               off, 0, 0, F8_KV_NT);
     }
   };
   auto issue = [&](int t) {
@@ -1060,7 +1064,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bkv, (short)0, d.nkv, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(d.st + (8 * wave + k) * 1024), 16,
-                                               off, 0, 0, 0);
+                                               off, 0, 0, F8_KV_NT);
     } else {  // rope: 16 rows x 4 chunks per wave-instruction
       int ln;  // lane id computed here, not kept in a register across the tile
       asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
@@ -1069,7 +1073,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       const __amdgpu_buffer_rsrc_t rp =
           __builtin_amdgcn_make_buffer_rsrc((void*)d.bpe, (short)0, d.npe, F8_RSRC_WORD3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void*)(d.st + F8_LAT + wave * 1024), 16,
-                                               off, 0, 0, 0);
+                                               off, 0, 0, F8_KV_NT);
     }
   };
   {
