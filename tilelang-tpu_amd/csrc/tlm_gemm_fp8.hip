@@ -274,7 +274,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
   // operand read and no LDS-DMA is in flight) and leaves as 16-byte row vectors, one 256-byte
   // row per 16 lanes, instead of 4-byte stores. Stage row r holds 64 floats (16 chunks of 16
   // bytes); chunk c sits at c ^ 4((r / 4) % 4), so the four row groups of one 4-byte write land
-  // in four different 64-byte bank windows and a 16-lane read covers one row.
+  // in four different 64-byte bank windows and a 16-lane read covers one row. The row stores
+  // are non-temporal (C is not read again; ~1.5% faster per launch at 4096^3).
   if constexpr (OUT == TLM_F32) {
     if (N % 4 == 0 && ((uintptr_t)C & 15) == 0) {
       float* stg = (float*)smem + wave * (64 * 64);
@@ -299,7 +300,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm8_256x256(const uint8_t* __re
           const int idx = it * 64 + lane, r = idx >> 4, c4 = idx & 15;
           const u32x4 v = *(const u32x4*)(stg + r * 64 + 4 * (c4 ^ (4 * ((r >> 2) & 3))));
           const int row = m0 + wm * 128 + 64 * h + r, col = n0 + wn * 64 + 4 * c4;
-          if (row < M && col < N) *(u32x4*)(Cf + (int64_t)row * N + col) = v;
+          if (row < M && col < N) st_nt((u32x4*)(Cf + (int64_t)row * N + col), v);
         }
         // the second half overwrites the stage only after every lane has read the first
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
