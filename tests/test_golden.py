@@ -1,6 +1,9 @@
 """Golden fixtures (tests/golden/golden.npz, written by tests/golden/make_golden.py).
 
-CPU: the oracle re-derives every stored output bit for bit (the fixtures freeze it).
+CPU: the oracle re-derives every stored input and elementwise output bit for bit (the fixtures
+freeze it); outputs of float reductions (GEMM, attention, MLA, RMSNorm) match within one 16-bit rounding at
+the output's scale, since torch's CPU reductions are split by thread count and a host with
+another core count sums in another order.
 GPU: each kernel family reproduces the stored outputs within the family's tolerance.
 """
 import math
@@ -35,8 +38,19 @@ def test_fixtures_match_oracle():
     fresh = make_golden.cases()
     stored = load()
     assert set(fresh) == set(stored)
+    f16, b16 = torch.float16, torch.bfloat16
+    reductions = {"gemm_c": f16, "fa_o": b16, "mla_o": b16, "rmsnorm_y": f16}
     for k in stored:
-        assert np.array_equal(fresh[k], stored[k]), k
+        if k in reductions:
+            # within one 16-bit rounding at the output's scale (an output that cancels to near
+            # zero can differ by many of its own ulps)
+            a = t16(fresh[k], reductions[k]).float()
+            b = t16(stored[k], reductions[k]).float()
+            eps = 2.0 ** -8 if reductions[k] == b16 else 2.0 ** -11
+            tol = eps * float(b.abs().max())
+            assert float((a - b).abs().max()) <= tol, (k, float((a - b).abs().max()), tol)
+        else:
+            assert np.array_equal(fresh[k], stored[k]), k
 
 
 @pytest.mark.gpu
