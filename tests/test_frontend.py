@@ -414,3 +414,49 @@ def test_mlp_program_recognised_with_whole_blocks_only():
     assert (a["M"], a["hidden"], a["inter"]) == (128, 256, 512)
     with pytest.raises(UnsupportedProgram, match="whole blocks"):
         tilelang.compile(programs.deepseek_mlp(8, 8, 8, 16, 16, 16), out_idx=[0])
+
+
+def test_elementwise_tile_at_another_grid_position_is_rejected():
+    """An input tile taken at the transposed grid position of the output tile reads other
+    elements than the ones it is stored to: not an elementwise program."""
+
+    @T.prim_func
+    def swapped(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+        with T.Kernel(2, 2, is_cpu=True) as (bx, by):
+            a = T.alloc_shared((32, 32), "float32")
+            T.ppl_copy(A[by * 32, bx * 32], a)
+            T.ppl_rsqrt(a, a)
+            T.ppl_copy(a, B[bx * 32, by * 32])
+
+    with pytest.raises(UnsupportedProgram, match="grid position"):
+        tilelang.compile(swapped, out_idx=-1)
+
+    @T.prim_func
+    def same(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+        with T.Kernel(2, 2, is_cpu=True) as (bx, by):
+            a = T.alloc_shared((32, 32), "float32")
+            T.ppl_copy(A[by * 32, bx * 32], a)
+            T.ppl_rsqrt(a, a)
+            T.ppl_copy(a, B[by * 32, bx * 32])
+
+    assert tilelang.compile(same, out_idx=-1).plan.family == "elementwise"
+
+
+def test_elementwise_reload_after_store_is_rejected():
+    """A copy from a parameter after the program stored to it would read the stored values;
+    the register program loads each input once, so such a program is rejected."""
+
+    @T.prim_func
+    def reload(A: T.Tensor((64, 64), "float32"), B: T.Tensor((64, 64), "float32")):
+        with T.Kernel(1, is_cpu=True) as (bx,):
+            a = T.alloc_shared((64, 64), "float32")
+            b = T.alloc_shared((64, 64), "float32")
+            T.ppl_copy(A[0, 0], a)
+            T.ppl_add(a, a, a)
+            T.ppl_copy(a, A[0, 0])
+            T.ppl_copy(A[0, 0], b)
+            T.ppl_add(b, b, b)
+            T.ppl_copy(b, B[0, 0])
+
+    with pytest.raises(UnsupportedProgram, match="after the program stores"):
+        tilelang.compile(reload, out_idx=-1)

@@ -951,15 +951,18 @@ def _grid_var_extent(pf, e) -> Optional[int]:
     return None
 
 
-def _tiles_cover(pf, access, tile: Buffer) -> bool:
-    """Whether the tile copy ``access`` (of a global parameter) takes the (i, j)-th tile of a
-    grid that covers the parameter exactly: per dimension either the whole (or unit) dimension,
-    or a start of grid_var * t with extent t and a grid extent of ceil(dim / t)."""
+def _tile_map(pf, access, tile: Buffer):
+    """Grid mapping of the tile copy ``access`` of a global parameter, or None when the copy is
+    not the (i, j)-th tile of a grid that covers the parameter exactly. Per dimension the entry
+    is None (the whole or unit dimension, or a tile as long as the dimension) or (grid variable
+    name, tile extent) for a start of grid_var * t with extent t and a grid extent of
+    ceil(dim / t)."""
     buf = access.buffer if isinstance(access, BufferAccess) else access
     dims = _shape(buf)
     if isinstance(access, Buffer):
-        return True
+        return [None] * len(dims)
     starts, exts = access.region(tile.shape)
+    out = []
     for d, (st, ex) in enumerate(zip(starts, exts)):
         try:
             t = int(ir.const_value(ex))
@@ -970,20 +973,27 @@ def _tiles_cover(pf, access, tile: Buffer) -> bool:
         except (TypeError, ValueError):
             s0 = None
         if s0 == 0 and (t == dims[d] or dims[d] == 1):
+            out.append(None)
             continue
         if not (isinstance(st, Expr) and st.op == "mul"):
-            return False
+            return None
         a, b = st.args
         var, c = (a, b) if isinstance(b, Expr) and b.op == "const" else (b, a)
         if not (isinstance(c, Expr) and c.op == "const"):
-            return False
+            return None
         c = int(c.args[0])
         if t is None:
             tdims = list(tile.shape)
             t = int(ir.const_value(tdims[d - (len(dims) - len(tdims))])) if len(tdims) else 1
         if t != c or _grid_var_extent(pf, var) != -(-dims[d] // c):
-            return False
-    return True
+            return None
+        out.append(None if t >= dims[d] else (var.args[0], t))
+    return out
+
+
+def _tiles_cover(pf, access, tile: Buffer) -> bool:
+    """Whether the tile copy ``access`` takes one tile of a grid covering its parameter."""
+    return _tile_map(pf, access, tile) is not None
 
 
 def _elementwise(pf, names) -> Plan:
@@ -1017,7 +1027,14 @@ def _elementwise(pf, names) -> Plan:
     value: Dict[int, int] = {}  # id(tile) -> node
     stores: List[tuple] = []    # (output parameter, node)
 
+    stored: List[Buffer] = []
+    maps: List[tuple] = []      # (kind, grid map) of every global tile copy
+
     def load(p):
+        if any(p is q for q in stored):
+            # a later copy from a parameter the program has written would read the stored
+            # values; the register program reads each input once, before any store
+            _fail(fam, f"parameter {p!r} is copied from after the program stores to it")
         s = _shape(p)
         n = math.prod(s)
         if s == full:
@@ -1057,13 +1074,18 @@ def _elementwise(pf, names) -> Plan:
             if sb is None or db is None:
                 _fail(fam, "copy operands must be buffers")
             if sb.scope == "global" and db.scope != "global":
-                if not _tiles_cover(pf, src, db):
+                m = _tile_map(pf, src, db)
+                if m is None:
                     _fail(fam, f"the copy from {sb!r} is not one tile of a grid covering it")
                 value[id(db)] = rounded(load(sb), db.dtype)
+                maps.append((kinds[[q is sb for q in inputs].index(True)], m, sb))
             elif sb.scope != "global" and db.scope == "global":
-                if not _tiles_cover(pf, dst, sb):
+                m = _tile_map(pf, dst, sb)
+                if m is None:
                     _fail(fam, f"the copy to {db!r} is not one tile of a grid covering it")
                 stores.append((db, get(sb)))
+                stored.append(db)
+                maps.append(("out", m, db))
             elif sb.scope != "global" and db.scope != "global":
                 value[id(db)] = rounded(get(sb), db.dtype)
             else:
@@ -1088,6 +1110,21 @@ def _elementwise(pf, names) -> Plan:
             _fail(fam, f"op {n} is not an elementwise tile op")
     if not stores:
         _fail(fam, "nothing is stored")
+    # every tile copy must address the same element grid: the kernel applies the program to
+    # element (r, c) of every operand, so an input tile taken at another grid position than
+    # the output tile (a tile transpose, a shifted tile) has no elementwise meaning here
+    out_map = next(m for k, m, _ in maps if k == "out")
+    for kind, m, p in maps:
+        if kind == "scalar":
+            continue
+        if kind in ("out", "full"):
+            ok = m == out_map
+        elif kind == "row":
+            ok = len(m) == len(out_map) and m[:-1] == out_map[:-1] and m[-1] is None
+        else:  # col
+            ok = m[-1] == out_map[-1]
+        if not ok:
+            _fail(fam, f"the tile copy of {p!r} is not at the output tile's grid position")
     outs: List[Buffer] = []
     for p, _ in stores:
         if all(p is not q for q in outs):
