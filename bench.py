@@ -50,6 +50,18 @@ CACHE_EVICT_BYTES = 512 << 20
 METRIC = "TFLOP/s (% MFMA peak) GEMM/FA/FP8-MLA; GB/s (% HBM peak) norm/rope/swiglu"
 
 
+def cpu_model() -> str:
+    """Model name of the host CPU (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -624,10 +636,24 @@ def bench_mla(args, dev, flush, cpu):
     if cpu:
         from oracle import ref
         nb = 4
-        t0 = cpu_time(lambda: ref.mla_decode_ref(
-            w.tensors["q"][:nb, :, :dv], w.tensors["q"][:nb, :, dv:], w.tensors["kv"][:, :dv],
-            w.tensors["kv"][:, dv:], w.tensors["block_table"], w.tensors["seqlens"][:nb],
-            a["page"], a["sm_scale"], float(w.tensors["kv_scale"])), reps=1)
+        got = {}
+
+        def oracle_sample():
+            got["ref"] = ref.mla_decode_ref(
+                w.tensors["q"][:nb, :, :dv], w.tensors["q"][:nb, :, dv:], w.tensors["kv"][:, :dv],
+                w.tensors["kv"][:, dv:], w.tensors["block_table"], w.tensors["seqlens"][:nb],
+                a["page"], a["sm_scale"], float(w.tensors["kv_scale"]), out_dtype=torch.float32)
+
+        t0 = cpu_time(oracle_sample, reps=1)
+        # the error this throughput is bought with: the GPU output of the same sequences against
+        # the dequantised fp32 oracle (the FP8 bound of the config is 3% relative RMS)
+        run(sets[0])
+        o = sets[0]["out"][:nb].float().cpu()
+        e = got["ref"]
+        res["accuracy"] = {
+            "rel_rms": float(((o - e).pow(2).mean() / e.pow(2).mean()).sqrt()),
+            "max_abs": float((o - e).abs().max()),
+            "sample": f"first {nb} of {B} sequences against oracle.ref.mla_decode_ref (fp32)"}
         sl = int(w.tensors["seqlens"][:nb].sum())
         sb = sl * (dv + dpe) + nb * Hq * (dv + dpe) * 2 + nb * Hq * dv * 2 + \
             w.tensors["block_table"][:nb].numel() * 4 + nb * 4
@@ -803,6 +829,8 @@ def main():
         log(f"[bench] {n} ...")
         try:
             results[n] = BENCHES[n](args, dev, flush, not args.no_cpu)
+            if results[n].get("cpu_baseline"):
+                results[n]["cpu_baseline"]["cpu_model"] = cpu_model()
             tb = traffic.get(results[n].get("workload"))
             if tb is not None and results[n].get("roofline"):
                 results[n]["roofline"]["traffic"] = tb
@@ -848,7 +876,8 @@ def main():
         "sclk": head.get("sclk"),
         "cpu_baseline": head.get("cpu_baseline"),
         "configs": [results[n] for n in names],
-        "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()},
+        "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+                 "cpu_model": cpu_model()},
     }
     print(json.dumps(line))
 

@@ -285,11 +285,7 @@ def flashattn_bhsd_ref(Q, K, V, causal: bool, sm_scale: Optional[float] = None):
 
 
 # ------------------------------------------------------------------------------------------------
-# MLA decode — examples/deepseek_mla/example_mla_decode_paged.py:259-308 (run_torch_mla /
-# scaled_dot_product_attention): per sequence, fp32 attention of q [h_q, d] over the sequence's
-# KV rows, shared latent head (h_kv = 1), value = first dv columns of the key rows.
-# The rows are gathered through the block table: token j -> BT[b, j // page] * page + j % page
-# (the kernel's addressing, :62-63, 147-148). fp8 KV is dequantised as decode(byte) * kv_scale.
+# Split-KV inference attention — examples/flash_attention/example_mha_inference.py
 def mha_inference_ref(Q, K, V, sm_scale: Optional[float] = None):
     """examples/flash_attention/example_mha_inference.py ref_program (:206-213): sequence-major
     Q [B, S_q, H, D], K, V [B, S_kv, H, D], fp32 softmax(Q K^T / sqrt(D)) V over all keys (the
@@ -342,6 +338,12 @@ def mha_split_combine_ref(Q, K, V, num_split: int, block_N: int, store_dtype=tor
     return out, (glse, part)
 
 
+# ------------------------------------------------------------------------------------------------
+# MLA decode — examples/deepseek_mla/example_mla_decode_paged.py:259-308 (run_torch_mla /
+# scaled_dot_product_attention): per sequence, fp32 attention of q [h_q, d] over the sequence's
+# KV rows, shared latent head (h_kv = 1), value = first dv columns of the key rows.
+# The rows are gathered through the block table: token j -> BT[b, j // page] * page + j % page
+# (the kernel's addressing, :62-63, 147-148). fp8 KV is dequantised as decode(byte) * kv_scale.
 def paged_rows(block_table: torch.Tensor, seqlen: int, b: int, page: int) -> torch.Tensor:
     j = torch.arange(seqlen, dtype=torch.int64)
     return block_table[b, j // page].to(torch.int64) * page + j % page
@@ -391,7 +393,7 @@ def mla_decode_nopage_ref(q, q_pe, kv, k_pe, sm_scale: Optional[float] = None,
     return out.reshape(shape).to(out_dtype or q.dtype)
 
 
-# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial
+# examples/deepseek_mla/torch_refs.py:6-78 (flash_split_ref + reduce_ref): split-KV partial
 # outputs with log2-domain LSE, then the LSE-weighted combine. Restated over explicit splits of
 # the token range (the kernel's partition, example_mla_decode_paged.py:140-144: blocks of
 # block_N tokens, the first `total % num_split` splits take one extra block).

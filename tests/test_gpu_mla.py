@@ -26,6 +26,7 @@ DEV = "cuda"
 
 
 FP8_REL_RMS = 0.03
+CONFIG_REL_RMS = 0.02
 # share of elements allowed outside atol + rtol |ref| for FP8 KV: e4m3 P^T rounding at a few
 # tokens per sequence (none at the config's lengths)
 FP8_MISMATCH = 0.005
@@ -114,7 +115,9 @@ def test_fp8_config_full(num_split):
     exp = _oracle(w, seqs)
     got = out[seqs]
     torch_assert_close(got, exp, atol=2e-2, rtol=5e-2)
-    assert _rel_rms(got, exp) < FP8_REL_RMS
+    # the config itself runs at ~1.3-1.6% (one e4m3 term for P^T); 2% keeps a precision
+    # regression from hiding under the 3% policy ceiling of the adversarial cases
+    assert _rel_rms(got, exp) < CONFIG_REL_RMS
 
 
 def test_split_invariance_and_page_permutation():

@@ -9,6 +9,12 @@ from ..utils.tensor import TensorSupplyType, get_tensor_supply, torch_assert_clo
 from .bench import do_bench  # noqa: F401
 
 
+def _as_list(outs) -> list:
+    if outs is None:
+        return []
+    return [outs] if isinstance(outs, torch.Tensor) else list(outs)
+
+
 class Profiler:
 
     def __init__(self, params, result_idx, supply_type=TensorSupplyType.Auto, adapter=None):
@@ -33,20 +39,19 @@ class Profiler:
     def assert_allclose(self, reference_program: Callable,
                         input_tensors: Optional[List[torch.Tensor]] = None, atol: float = 1e-2,
                         rtol: float = 1e-2, max_mismatched_ratio=0.01):
-        ins = self._get_inputs() if input_tensors is None else input_tensors
-        ref_outs = reference_program(*ins)
+        """Run the kernel and ``reference_program`` on the same inputs (generated from the
+        parameters unless given) and require every output pair to agree within atol + rtol |ref|
+        on all but ``max_mismatched_ratio`` of the elements."""
+        args = self._get_inputs() if input_tensors is None else input_tensors
+        expected = _as_list(reference_program(*args))
         torch.cuda.synchronize()
-        lib_outs = self.func(*ins)
+        got = _as_list(self.func(*args))
         torch.cuda.synchronize()
-        if isinstance(lib_outs, torch.Tensor):
-            lib_outs = [lib_outs]
-        if isinstance(ref_outs, torch.Tensor):
-            ref_outs = [ref_outs]
-        elif ref_outs is None:
-            ref_outs = []
-        assert len(lib_outs) == len(ref_outs), "len(lib_outs) not equals to len(ref_outs) !"
-        for lhs, rhs in zip(lib_outs, ref_outs):
-            torch_assert_close(lhs, rhs, rtol=rtol, atol=atol,
+        if len(got) != len(expected):
+            raise AssertionError(f"the kernel returned {len(got)} outputs and the reference "
+                                 f"program {len(expected)}")
+        for out, exp in zip(got, expected):
+            torch_assert_close(out, exp, rtol=rtol, atol=atol,
                                max_mismatched_ratio=max_mismatched_ratio)
 
     def assert_consistent(self, repeat=10):
