@@ -586,6 +586,49 @@ def bench_flashattn_bhsd(args, dev, flush, cpu):
     return res
 
 
+def bench_flashattn_inference(args, dev, flush, cpu):
+    """examples/flash_attention/example_mha_inference.py at its own defaults (:279-289): batch 1,
+    32 heads, 128 queries over 8192 keys, dim 128, fp16, 4 key splits; through
+    ``tilelang.compile``, the program's glse / Output_partial written and combined. Algorithmic
+    FLOPs = 4 B H S_q S_kv D (two matmuls)."""
+    import tilelang
+    from tilelang.testing import programs
+    B, H, Sq, Sk, D, ns = 1, 32, 128, 8192, 128, 4
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, Sq, H, D, generator=g).half()
+    kk = torch.randn(B, Sk, H, D, generator=g).half()
+    v = torch.randn(B, Sk, H, D, generator=g).half()
+    k = tilelang.compile(programs.mha_inference(B, H, Sq, Sk, D, num_split=ns), out_idx=[5])
+    flops = 4 * B * H * Sq * Sk * D
+    nbytes = (2 * B * Sq * H * D + 2 * B * Sk * H * D) * 2
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        sets.append([q.to(dev), kk.to(dev), v.to(dev),
+                     torch.empty(B, H, ns, Sq, dtype=torch.half, device=dev),
+                     torch.empty(B, Sq, H, ns, D, dtype=torch.half, device=dev),
+                     torch.empty(B, Sq, H, D, dtype=torch.half, device=dev)])
+    fns = [lambda t=t: k(*t) for t in sets]
+    pmc_launches(args, fns, "flashattn_inference")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 20, flush)
+    res = {"workload": f"flashattn_inference_fp16_b{B}h{H}sq{Sq}skv{Sk}d{D}_split{ns}",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "dtype": "f16",
+           "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                MFMA_PEAK["fp16"]),
+           "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+           "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+           "note": "whole call: the key-part attention kernel plus the split combine"}
+    if cpu:
+        from oracle import ref
+        t = cpu_time(lambda: ref.mha_inference_ref(q[:, :, :1], kk[:, :, :1], v[:, :, :1]),
+                     reps=3)
+        res["cpu_baseline"] = {"value": flops / H / t / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "head 0, oracle.ref.mha_inference_ref"}
+    return res
+
+
 def bench_mla(args, dev, flush, cpu):
     from tilelang.jit.adapter.mi355x import ops
     from tilelang.testing import workloads
@@ -774,6 +817,7 @@ BENCHES = {
     "swiglu": bench_swiglu,
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
+    "flashattn_inference": bench_flashattn_inference,
     "flashattn_gqa": bench_flashattn_gqa,
     "flashattn_varlen": bench_flashattn_varlen,
     "flashattn_bhsd": bench_flashattn_bhsd,
@@ -782,7 +826,8 @@ BENCHES = {
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
-         "flashattn_gqa", "flashattn_varlen", "flashattn_bhsd", "gemm_fp8", "mla", "kv_append"]
+         "flashattn_gqa", "flashattn_varlen", "flashattn_bhsd", "flashattn_inference", "gemm_fp8",
+         "mla", "kv_append"]
 
 
 def main():

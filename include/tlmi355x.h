@@ -209,6 +209,26 @@ int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void* v, void* o
                             int causal, float sm_scale, int in_dtype, int out_dtype,
                             void* stream);
 
+/* Split-KV inference attention: the program's partial outputs and their combine.
+ * Reference: examples/flash_attention/example_mha_inference.py:10-203 (flash_attn_split :98-160,
+ * combine :162-203, main(Q, K, V, glse, Output_partial, Output) :187-203).
+ *   q, o [B, S_q, H, D]; k, v [B, S_kv, H_kv, D]; glse [B, H, num_split, S_q];
+ *   o_partial [B, S_q, H, num_split, D]; all of `dtype` (F16 | BF16), dense.
+ *   Split s covers keys [s P, (s + 1) P), P = S_kv / num_split (S_kv must be a multiple of
+ *   num_split, 1 <= num_split <= 16). o_partial[b, q, h, s] = the split's normalised output and
+ *   glse[b, h, s, q] = log2(l) + m, the split's log2 sum-exp of the scaled scores (exp2 domain,
+ *   scale = sm_scale * log2 e), both rounded to `dtype`; o = the program's combine of those
+ *   stored values. Non-causal (the program's causal form has no split offset).
+ *   ws: caller workspace of at least tlm_flash_attn_splitkv_workspace_bytes() bytes (16-byte
+ *   aligned): the splits are cut into finer key parts so the launch fills every CU, and the parts
+ *   are merged exactly (fp32) before the per-split rounding. */
+size_t tlm_flash_attn_splitkv_workspace_bytes(int64_t B, int64_t S_q, int64_t S_kv, int64_t H,
+                                             int64_t D, int num_split);
+int tlm_flash_attn_splitkv_fwd(const void* q, const void* k, const void* v, void* glse,
+                               void* o_partial, void* o, void* ws, size_t ws_bytes, int64_t B,
+                               int64_t S_q, int64_t S_kv, int64_t H, int64_t H_kv, int64_t D,
+                               int num_split, float sm_scale, int dtype, void* stream);
+
 /* Elementwise tile programs: the stand-alone T.ppl_* elementwise programs of the TPU demos
  * (tpu_demo/ppl/test/exp.py:6-16, mul_N_1.py:9-22, elementwise_c.py:9-22,
  * tpu_demo/ppl/elementwise_add_kernel/elementwise_add.py:9-35; ops language/customize.py:238-339,

@@ -192,6 +192,28 @@ def test_flash_attn_validation():
     assert bh(p, p, p, p, 1, 8, 2, 0, 80, 128, 0, 0.1, lib.F16, lib.F16, None) == 0
 
 
+def test_splitkv_attention_validation_and_workspace():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    wsb = L.tlm_flash_attn_splitkv_workspace_bytes
+    # example_mha_inference.py defaults: B 1, 128 queries, 8192 keys, 32 heads, D 128, 4 splits:
+    # 128 workgroups before the key parts, so each split is cut in two (fp32 O and lse per part)
+    assert wsb(1, 128, 8192, 32, 128, 4) == 1 * 128 * 32 * 4 * 2 * 129 * 4
+    assert wsb(1, 128, 8190, 32, 128, 4) == 0  # S_kv not a multiple of num_split
+    assert wsb(1, 128, 8192, 32, 128, 17) == 0
+    f = L.tlm_flash_attn_splitkv_fwd
+    # q, k, v, glse, o_partial, o, ws, ws_bytes, B, S_q, S_kv, H, H_kv, D, ns, scale, dtype, stream
+    big = 1 << 30
+    assert f(p, p, p, None, p, p, p, big, 1, 128, 8192, 32, 32, 128, 4, 0.1, lib.F16, None) == -1
+    assert f(p, p, p, p, p, p, p, big, 1, 128, 8190, 32, 32, 128, 4, 0.1, lib.F16, None) == -1
+    assert f(p, p, p, p, p, p, p, big, 1, 128, 8192, 32, 32, 128, 17, 0.1, lib.F16, None) == -2
+    assert f(p, p, p, p, p, p, p, big, 1, 128, 8192, 32, 32, 128, 4, 0.1, lib.F32, None) == -2
+    assert f(p, p, p, p, p, p, p, big, 1, 128, 8192, 32, 3, 128, 4, 0.1, lib.F16, None) == -1
+    assert f(p, p, p, p, p, p, p, 64, 1, 128, 8192, 32, 32, 128, 4, 0.1, lib.F16, None) == -4
+    assert "workspace" in _err()
+    assert f(p, p, p, p, p, p, p, 0, 0, 128, 8192, 32, 32, 128, 4, 0.1, lib.F16, None) == 0
+
+
 def test_mla_validation_and_workspace():
     L = lib.load()
     ws = L.tlm_mla_workspace_bytes(64, 128, 512, 4)

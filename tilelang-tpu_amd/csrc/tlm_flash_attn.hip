@@ -29,6 +29,7 @@
 // Softmax runs in the exp2 domain with sm_scale * log2(e) folded into one fma.
 #include "tlm_common.h"
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -70,6 +71,22 @@ TLM_DEV SeqRange seq_range(const SeqMap& m, int b) {
 
 TLM_DEV s16x4 lds_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+// Key split of the split-KV inference program (examples/flash_attention/example_mha_inference.py:
+// 98-160): program split s covers keys [s per, (s + 1) per) of its sequence; each is cut into r
+// internal parts of per_i keys (the last may be shorter or empty) so the launch fills the chip.
+// Internal split si = s r + j writes its normalised fp32 output to O [B][S_q][H][nsi][D] and its
+// log2 sum-exp (scaled-score units; -inf for no keys) to lse [B][S_q][H][nsi].
+struct FaSplit {
+  float* lse;
+  int nsi, r, per, per_i;
+};
+TLM_DEV SeqRange split_keys(SeqRange sr, const FaSplit& sp, int si) {
+  const int s = si / sp.r, j = si % sp.r;
+  sr.k0 += (int64_t)s * sp.per + (int64_t)j * sp.per_i;
+  sr.nk = max(0, min(sp.per_i, sp.per - j * sp.per_i));
+  return sr;
 }
 
 template <bool BF16>
@@ -468,12 +485,13 @@ TLM_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool BF16, bool CAUSAL, bool OUT32>
+template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__ Q,
                                                    const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ V,
                                                    void* __restrict__ O, int B, int S, int H,
-                                                   int Hkv, float sc, SeqMap sm) {
+                                                   int Hkv, float sc, SeqMap sm, FaSplit sp) {
+  static_assert(!SPLIT || (OUT32 && !CAUSAL), "split parts are non-causal with fp32 output");
   using MT = fa_mma16<BF16>;
   using v8 = typename MT::v8;
   using HH = h16<BF16>;
@@ -494,9 +512,13 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int nqt = (S + PP_BQ - 1) / PP_BQ;
   const int nslot = CAUSAL ? (nqt + 1) / 2 : nqt;
   const int G = H / Hkv;
-  const int lin = blockIdx.x;
-  int b, h, slot;
-  if ((B * Hkv) % 8 == 0) {
+  int lin = blockIdx.x;
+  int b, h, slot, si = 0;
+  if constexpr (SPLIT) {  // workgroup = (internal split, batch, head, query tile)
+    si = lin % sp.nsi;
+    lin /= sp.nsi;
+  }
+  if (!SPLIT && (B * Hkv) % 8 == 0) {
     const int xcd = lin & 7, s = lin >> 3;
     const int per = nslot * G;  // workgroups per K/V head
     const int kvh = (s / per) * 8 + xcd, rem = s % per;
@@ -511,7 +533,8 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   }
   // S counts the query tiles of the grid; the sequence's own query and key counts are Sq, Sk.
   // Causal: query i sees keys j <= i + (Sk - Sq) (bottom-right aligned; 0 offset when dense).
-  const SeqRange sr = seq_range(sm, b);
+  SeqRange sr = seq_range(sm, b);
+  if constexpr (SPLIT) sr = split_keys(sr, sp, si);
   const int n_items = CAUSAL && 2 * slot != nqt - 1 ? 2 : 1;
   for (int item = 0; item < n_items; ++item) {
   const int qt = CAUSAL && item == 0 ? nqt - 1 - slot : slot;
@@ -785,21 +808,32 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
 
   // ---- epilogue: lane holds O^T[d = 16 dt + 4 g + i][query my_q[qq]]; the row sums of a query
   // are spread over the four lane groups
-  float inv[2];
+  float inv[2], l_all[2];
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
     float l_tot = l_part[qq] + __shfl_xor(l_part[qq], 16, 64);
     l_tot += __shfl_xor(l_tot, 32, 64);
+    l_all[qq] = l_tot;
     inv[qq] = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   }
-  if constexpr (OUT32) {  // fp32 output (fp32 programs): 16-byte stores straight from registers
-    float* Of = (float*)O + head;
+  if constexpr (OUT32) {  // fp32 output (fp32 programs, split parts): 16-byte stores from registers
+    int64_t ob = head, ors = rs;
+    if constexpr (SPLIT) {  // part si of query q: row ((b S_q + q) H + h) nsi + si
+      ob = ((sr.q0 * H + h) * sp.nsi + si) * PP_D;
+      ors = (int64_t)H * sp.nsi * PP_D;
+    }
+    float* Of = (float*)O + ob;
 #pragma unroll
     for (int qq = 0; qq < 2; ++qq)
       if (my_q[qq] < Sq) {
 #pragma unroll
         for (int dt = 0; dt < PP_D / 16; ++dt)
-          *(f32x4*)(Of + (int64_t)my_q[qq] * rs + 16 * dt + 4 * g) = oacc[dt][qq] * inv[qq];
+          *(f32x4*)(Of + (int64_t)my_q[qq] * ors + 16 * dt + 4 * g) = oacc[dt][qq] * inv[qq];
+        if constexpr (SPLIT) {
+          if (g == 0)
+            sp.lse[ob / PP_D + (int64_t)my_q[qq] * ors / PP_D] =
+                l_all[qq] > 0.f ? m_run[qq] + __log2f(l_all[qq]) : -INFINITY;
+        }
       }
     return;
   }
@@ -829,17 +863,18 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   }
 }
 
-template <bool BF16, bool CAUSAL, bool OUT32>
+template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false>
 int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
-              float sc, const SeqMap& sm, hipStream_t st) {
+              float sc, const SeqMap& sm, hipStream_t st, const FaSplit& sp = FaSplit{}) {
   const int64_t nqt = (S + PP_BQ - 1) / PP_BQ;
-  const int64_t nwg = (CAUSAL ? (nqt + 1) / 2 : nqt) * B * H;  // causal: two tiles per workgroup
+  // causal: two tiles per workgroup; split: one workgroup per internal key split
+  const int64_t nwg = (CAUSAL ? (nqt + 1) / 2 : nqt) * B * H * (SPLIT ? sp.nsi : 1);
   if (nwg > INT32_MAX) {
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
-  fa_fwd_pp<BF16, CAUSAL, OUT32><<<(unsigned)nwg, 512, 0, st>>>(
-      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc, sm);
+  fa_fwd_pp<BF16, CAUSAL, OUT32, SPLIT><<<(unsigned)nwg, 512, 0, st>>>(
+      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc, sm, sp);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
 }
@@ -864,15 +899,19 @@ int launch(const void* q, const void* k, const void* v, void* o, int B, int S, i
 // read with wave-uniform addresses; per key the online softmax of the reference (m = running
 // max, alpha = 2^(m_prev - m), P = 2^(s sc - m) rounded to the input type before P V, l from
 // the fp32 P). No MFMA: for shapes far too small to fill matrix tiles.
-template <bool BF16, bool CAUSAL, bool OUT32, int DC>  // DC = capacity in 8-element chunks
+template <bool BF16, bool CAUSAL, bool OUT32, int DC,  // DC = capacity in 8-element chunks
+          bool SPLIT = false>
 __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict__ Q,
                                                       const uint16_t* __restrict__ K,
                                                       const uint16_t* __restrict__ V,
                                                       void* __restrict__ O, int H, int Hkv,
-                                                      int D, float sc, SeqMap sm) {
+                                                      int D, float sc, SeqMap sm, FaSplit sp) {
+  static_assert(!SPLIT || (OUT32 && !CAUSAL), "split parts are non-causal with fp32 output");
   using HH = h16<BF16>;
-  const int bh = blockIdx.y, b = bh / H, h = bh % H;
-  const SeqRange sr = seq_range(sm, b);
+  const int si = SPLIT ? (int)(blockIdx.y % sp.nsi) : 0;
+  const int bh = SPLIT ? (int)(blockIdx.y / sp.nsi) : (int)blockIdx.y, b = bh / H, h = bh % H;
+  SeqRange sr = seq_range(sm, b);
+  if constexpr (SPLIT) sr = split_keys(sr, sp, si);
   const int S = sr.nq, Sk = sr.nk, coff = Sk - S;  // causal: query i sees keys j <= i + coff
   if ((int)blockIdx.x * 256 >= S) return;  // whole block
   const int q = blockIdx.x * 256 + threadIdx.x;
@@ -930,10 +969,16 @@ __global__ __launch_bounds__(256) void fa_fwd_generic(const uint16_t* __restrict
   }
   if (q >= S) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
+  int64_t ob = head, ors = rs;
+  if constexpr (SPLIT) {  // part si of query q: row ((b S_q + q) H + h) nsi + si
+    ob = ((sr.q0 * H + h) * sp.nsi + si) * D;
+    ors = (int64_t)H * sp.nsi * D;
+    sp.lse[ob / D + (int64_t)q * ors / D] = l > 0.f ? m + __log2f(l) : -INFINITY;
+  }
 #pragma unroll
   for (int c = 0; c < DC; ++c) {
     if (c < nc) {
-      const int64_t off = head + (int64_t)q * rs + 8 * c;
+      const int64_t off = ob + (int64_t)q * ors + 8 * c;
       if constexpr (OUT32) {
         float* Of = (float*)O + off;
         *(f32x4*)Of = f32x4{o[c][0] * inv, o[c][1] * inv, o[c][2] * inv, o[c][3] * inv};
@@ -1034,28 +1079,116 @@ int launch_generic_f32(const void* q, const void* k, const void* v, void* o, int
   return TLM_OK;
 }
 
-template <bool BF16, bool CAUSAL, bool OUT32>
+template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false>
 int launch_generic(const void* q, const void* k, const void* v, void* o, int B, int S, int H,
-                   int Hkv, int D, float sc, const SeqMap& sm, hipStream_t st) {
-  if ((int64_t)B * H > 65535) {
-    tlm_set_error("tlm_flash_attn_fwd: head dim %d needs batch * heads <= 65535", D);
+                   int Hkv, int D, float sc, const SeqMap& sm, hipStream_t st,
+                   const FaSplit& sp = FaSplit{}) {
+  const int64_t ny = (int64_t)B * H * (SPLIT ? sp.nsi : 1);
+  if (ny > 65535) {
+    tlm_set_error("tlm_flash_attn_fwd: head dim %d needs batch * heads%s <= 65535", D,
+                  SPLIT ? " * key parts" : "");
     return TLM_EUNSUPPORTED;
   }
-  const dim3 grid((unsigned)((S + 255) / 256), (unsigned)(B * H));
+  const dim3 grid((unsigned)((S + 255) / 256), (unsigned)ny);
   auto go = [&](auto kern) {
     kern<<<grid, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, H,
-                               Hkv, D, sc, sm);
+                               Hkv, D, sc, sm, sp);
   };
   if (D <= 16)
-    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 2>);
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 2, SPLIT>);
   else if (D <= 64)
-    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 8>);
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 8, SPLIT>);
   else if (D <= 128)
-    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 16>);
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 16, SPLIT>);
   else
-    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 32>);
+    go(fa_fwd_generic<BF16, CAUSAL, OUT32, 32, SPLIT>);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
+}
+
+// Combine of the split-KV inference program (example_mha_inference.py:162-203, reduce_ref
+// :216-227). Thread = (row = (b, q, h), 4 dims). Each program split s first merges its r internal
+// parts exactly (fp32), and its result is stored as the program's partial in the 16-bit dtype:
+// Output_partial[b, q, h, s, :] = O_s and glse[b, h, s, q] = lse_s (log2 domain). Output is then
+// the merge of those stored (rounded) values, as the program's combine reads them back:
+// O = sum_s O_s 2^(lse_s - lse), lse = log2 sum_s 2^(lse_s) (taken here as a running merge).
+constexpr int FA_MAX_PARTS = 8;  // internal parts per program split
+template <bool BF16>
+__global__ __launch_bounds__(256) void fa_split_combine(const float* __restrict__ part,
+                                                        const float* __restrict__ lse,
+                                                        uint16_t* __restrict__ glse,
+                                                        uint16_t* __restrict__ opart,
+                                                        uint16_t* __restrict__ out, int64_t rows,
+                                                        int Sq, int H, int D, int ns, int r) {
+  using HH = h16<BF16>;
+  const int nch = D / 4;
+  const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gt / nch;
+  if (row >= rows) return;
+  const int c = (int)(gt % nch);
+  const int h = (int)(row % H);
+  const int64_t bq = row / H;
+  const int q = (int)(bq % Sq);
+  const int64_t b = bq / Sq;
+  const int nsi = ns * r;
+  float M = -INFINITY, L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < ns; ++sp) {
+    // every part of the split requested before any is used
+    float lv[FA_MAX_PARTS];
+    f32x4 pv[FA_MAX_PARTS];
+#pragma unroll
+    for (int j = 0; j < FA_MAX_PARTS; ++j) {
+      lv[j] = -INFINITY;
+      pv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (j < r) {
+        const int64_t pi = row * nsi + sp * r + j;
+        lv[j] = lse[pi];
+        pv[j] = *(const f32x4*)(part + pi * D + 4 * c);
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < FA_MAX_PARTS; ++j) m = fmaxf(m, lv[j]);
+    float l = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int j = 0; j < FA_MAX_PARTS; ++j) {
+        const float w = fast_exp2(lv[j] - m);  // 0 for an empty or absent part
+        l += w;
+        o += pv[j] * w;
+      }
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const u32x2 pk = u32x2{HH::pack(o[0] * inv, o[1] * inv), HH::pack(o[2] * inv, o[3] * inv)};
+    *(u32x2*)(opart + (row * ns + sp) * D + 4 * c) = pk;
+    const uint32_t lb = HH::from_f32(l > 0.f ? m + __log2f(l) : -INFINITY);
+    if (c == 0) glse[((b * H + h) * ns + sp) * Sq + q] = (uint16_t)lb;
+    // merge the stored values, as read back: running max and sum of 2^lse
+    const float lr = HH::to_f32(lb);
+    if (lr != -INFINITY) {
+      const float Mn = fmaxf(M, lr);
+      const float a = fast_exp2(M - Mn), w = fast_exp2(lr - Mn);  // a = 0 while M = -inf
+      L = L * a + w;
+      acc = acc * a + f32x4{HH::lo(pk[0]), HH::hi(pk[0]), HH::lo(pk[1]), HH::hi(pk[1])} * w;
+      M = Mn;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  *(u32x2*)(out + row * D + 4 * c) =
+      u32x2{HH::pack(acc[0] * inv, acc[1] * inv), HH::pack(acc[2] * inv, acc[3] * inv)};
+}
+
+// Internal key parts per program split: enough workgroups for every CU, each part at least
+// eight 64-key tiles. Shared by the launch and the workspace query.
+int split_parts(int64_t B, int64_t S_q, int64_t S_kv, int64_t H, int64_t D, int ns) {
+  const int64_t per = S_kv / ns;
+  const int64_t qtiles = D == 128 ? (S_q + PP_BQ - 1) / PP_BQ : (S_q + 255) / 256;
+  const int64_t base = std::max<int64_t>(1, B * H * qtiles * ns);
+  int64_t r = (256 + base - 1) / base;
+  r = std::min<int64_t>(r, std::max<int64_t>(1, per / (8 * PP_KV)));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(r, FA_MAX_PARTS));
 }
 
 // S: queries per sequence (dense) or the longest sequence's (variable length); sm: row ranges.
@@ -1189,6 +1322,88 @@ extern "C" int tlm_flash_attn_bhsd_fwd(const void* q, const void* k, const void*
   const SeqMap sm{nullptr, nullptr, (int)S_q, (int)S_kv, D, D, S_q * D, S_kv * D};
   return dispatch(q, k, v, o, (int)B, (int)S_q, (int)H, (int)H_kv, (int)D, causal != 0,
                   sm_scale, in_dtype, out_dtype, sm, (hipStream_t)stream);
+}
+
+extern "C" size_t tlm_flash_attn_splitkv_workspace_bytes(int64_t B, int64_t S_q, int64_t S_kv,
+                                                         int64_t H, int64_t D, int num_split) {
+  if (B <= 0 || S_q <= 0 || S_kv <= 0 || H <= 0 || D <= 0 || num_split <= 0 ||
+      num_split > 16 || S_kv % num_split)
+    return 0;
+  const int r = split_parts(B, S_q, S_kv, H, D, num_split);
+  return (size_t)B * S_q * H * num_split * r * (D + 1) * sizeof(float);
+}
+
+extern "C" int tlm_flash_attn_splitkv_fwd(const void* q, const void* k, const void* v, void* glse,
+                                          void* o_partial, void* o, void* ws, size_t ws_bytes,
+                                          int64_t B, int64_t S_q, int64_t S_kv, int64_t H,
+                                          int64_t H_kv, int64_t D, int num_split, float sm_scale,
+                                          int dtype, void* stream) {
+  const char* fn = "tlm_flash_attn_splitkv_fwd";
+  int rc = check_common(fn, q, k, v, o, H, H_kv, D, sm_scale, dtype, dtype);
+  if (rc != TLM_OK) return rc;
+  if (dtype == TLM_F32) {
+    tlm_set_error("%s: dtype must be F16 or BF16", fn);
+    return TLM_EUNSUPPORTED;
+  }
+  if (!glse || !o_partial || !ws || !tlm_aligned(glse, 2) || !tlm_aligned(o_partial, 16) ||
+      !tlm_aligned(ws, 16)) {
+    tlm_set_error("%s: glse, Output_partial and the workspace must be non-null and aligned (2, "
+                  "16, 16 bytes)", fn);
+    return TLM_EINVAL;
+  }
+  if (num_split < 1 || num_split > 16) {
+    tlm_set_error("%s: num_split %d outside [1, 16]", fn, num_split);
+    return TLM_EUNSUPPORTED;
+  }
+  if (B < 0 || S_q < 0 || S_kv < 0 || B > 65535 || S_q > (1 << 24) || S_kv > (1 << 24) ||
+      S_kv % num_split) {
+    tlm_set_error("%s: bad shape (S_kv must be a multiple of num_split)", fn);
+    return TLM_EINVAL;
+  }
+  if (B == 0 || S_q == 0 || H == 0) return TLM_OK;
+  if (S_kv == 0) {
+    tlm_set_error("%s: no keys", fn);
+    return TLM_EINVAL;
+  }
+  const size_t need = tlm_flash_attn_splitkv_workspace_bytes(B, S_q, S_kv, H, D, num_split);
+  if (ws_bytes < need) {
+    tlm_set_error("%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
+    return TLM_EWORKSPACE;
+  }
+  const int r = split_parts(B, S_q, S_kv, H, D, num_split);
+  const int per = (int)(S_kv / num_split);
+  const int per_i = (per + r - 1) / r;
+  const int64_t rows = B * S_q * H;
+  float* part = (float*)ws;
+  float* lse = part + rows * num_split * r * D;
+  const FaSplit sp{lse, num_split * r, r, per, per_i};
+  const SeqMap sm{nullptr, nullptr, (int)S_q, (int)S_kv, H * D, H_kv * D, D, D};
+  const float sc = (float)((double)sm_scale * 1.4426950408889634);
+  hipStream_t st = (hipStream_t)stream;
+  const bool bf = dtype == TLM_BF16;
+  if (D == 128)
+    rc = bf ? launch_pp<true, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                 (int)H_kv, sc, sm, st, sp)
+            : launch_pp<false, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                  (int)H_kv, sc, sm, st, sp);
+  else
+    rc = bf ? launch_generic<true, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                      (int)H_kv, (int)D, sc, sm, st, sp)
+            : launch_generic<false, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                       (int)H_kv, (int)D, sc, sm, st, sp);
+  if (rc != TLM_OK) return rc;
+  const int64_t nthr = rows * (D / 4);
+  const dim3 grid((unsigned)((nthr + 255) / 256));
+  if (bf)
+    fa_split_combine<true><<<grid, 256, 0, st>>>(part, lse, (uint16_t*)glse,
+                                                 (uint16_t*)o_partial, (uint16_t*)o, rows,
+                                                 (int)S_q, (int)H, (int)D, num_split, r);
+  else
+    fa_split_combine<false><<<grid, 256, 0, st>>>(part, lse, (uint16_t*)glse,
+                                                  (uint16_t*)o_partial, (uint16_t*)o, rows,
+                                                  (int)S_q, (int)H, (int)D, num_split, r);
+  TLM_LAUNCH_CHECK("tlm_flash_attn_splitkv_fwd (combine)");
+  return TLM_OK;
 }
 
 extern "C" int tlm_flash_attn_fwd(const void* q, const void* k, const void* v, void* o,

@@ -40,19 +40,18 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
         ops.flash_attn_varlen_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["cu_q"]], t[a["cu_k"]],
                                   t[a["max_q"]], t[a["o"]], a["causal"], a["sm_scale"])
     elif f == "flashattn" and a.get("layout") == "bshd_kv":
-        # seq_q != seq_kv in the sequence-major layout: the variable-length kernel with every
-        # sequence of seq_q queries and seq_kv keys (prefix tables kept per device and shape)
-        q, k, v, o = t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]]
-        dev, B, Sq, Skv = q.device, a["B"], a["S"], a["S_kv"]
-        key = (dev, "cu", B, Sq, Skv)
-        if key not in workspace_cache:
-            ar = torch.arange(B + 1, dtype=torch.int32, device=dev)
-            workspace_cache[key] = (ar * Sq, ar * Skv)
-        cu_q, cu_k = workspace_cache[key]
-        H, Hkv, D = a["H"], a["H_kv"], a["D"]
-        ops.flash_attn_varlen_fwd(q.view(B * Sq, H, D), k.view(B * Skv, Hkv, D),
-                                  v.view(B * Skv, Hkv, D), cu_q, cu_k, Sq, o.view(B * Sq, H, D),
-                                  False, a["sm_scale"])
+        # split-KV inference program: partial outputs and log2 sum-exp per key split written to
+        # the program's glse / Output_partial, then their combine into Output
+        q = t[a["q"]]
+        need = ops.flash_attn_splitkv_workspace_bytes(a["B"], a["S"], a["S_kv"], a["H"], a["D"],
+                                                      a["num_split"])
+        key = (q.device, "splitkv")
+        ws = workspace_cache.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+            workspace_cache[key] = ws
+        ops.flash_attn_splitkv_fwd(q, t[a["k"]], t[a["v"]], t[a["glse"]], t[a["partial"]],
+                                   t[a["o"]], a["num_split"], a["sm_scale"], ws)
     elif f == "flashattn" and a.get("layout") == "bhsd":
         ops.flash_attn_bhsd_fwd(t[a["q"]], t[a["k"]], t[a["v"]], t[a["o"]], a["causal"],
                                 a["sm_scale"])

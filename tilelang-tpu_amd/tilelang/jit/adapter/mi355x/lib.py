@@ -42,6 +42,9 @@ _SIGNATURES = {
                                   [c_int, c_float, c_int, c_int, c_void_p], c_int),
     "tlm_flash_attn_bhsd_fwd": ([c_void_p] * 4 + [c_int64] * 6 +
                                 [c_int, c_float, c_int, c_int, c_void_p], c_int),
+    "tlm_flash_attn_splitkv_workspace_bytes": ([c_int64] * 5 + [c_int], c_size_t),
+    "tlm_flash_attn_splitkv_fwd": ([c_void_p] * 7 + [c_size_t] + [c_int64] * 6 +
+                                   [c_int, c_float, c_int, c_void_p], c_int),
     "tlm_cast": ([c_void_p, c_int, c_void_p, c_int, c_int64, c_void_p], c_int),
     "tlm_sigmoid": ([c_void_p, c_void_p, c_int64, c_int, c_void_p], c_int),
     "tlm_gather_rows": ([c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p],

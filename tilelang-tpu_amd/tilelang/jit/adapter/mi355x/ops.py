@@ -232,6 +232,39 @@ def flash_attn_varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int
     return o
 
 
+def flash_attn_splitkv_workspace_bytes(B, S_q, S_kv, H, D, num_split) -> int:
+    return int(lib.load().tlm_flash_attn_splitkv_workspace_bytes(B, S_q, S_kv, H, D, num_split))
+
+
+def flash_attn_splitkv_fwd(q, k, v, glse, o_partial, o, num_split: int, sm_scale: float,
+                           workspace: torch.Tensor):
+    """Split-KV inference attention (example_mha_inference.py): q, o [B, S_q, H, D]; k, v
+    [B, S_kv, H_kv, D]; writes glse [B, H, num_split, S_q], o_partial [B, S_q, H, num_split, D]
+    (each split's log2 sum-exp and normalised output, rounded to the dtype) and o, their
+    combine."""
+    dev = _dev(q, k, v, glse, o_partial, o, workspace)
+    for n, t in (("Q", q), ("K", k), ("V", v), ("glse", glse), ("Output_partial", o_partial),
+                 ("Output", o), ("workspace", workspace)):
+        _contig(n, t)
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or o.shape != q.shape:
+        raise ValueError("Q, Output must be [B, S_q, H, D] and K, V [B, S_kv, H_kv, D]")
+    B, Sq, H, D = q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    if k.shape[0] != B or k.shape[3] != D or Hkv == 0 or H % Hkv:
+        raise ValueError(f"K/V {tuple(k.shape)} do not match Q {tuple(q.shape)}")
+    if tuple(glse.shape) != (B, H, num_split, Sq) or \
+            tuple(o_partial.shape) != (B, Sq, H, num_split, D):
+        raise ValueError("glse must be [B, H, num_split, S_q] and Output_partial "
+                         "[B, S_q, H, num_split, D]")
+    if len({q.dtype, k.dtype, v.dtype, glse.dtype, o_partial.dtype, o.dtype}) != 1:
+        raise ValueError("all tensors must share one 16-bit dtype")
+    ws_bytes = workspace.numel() * workspace.element_size()
+    lib.call("tlm_flash_attn_splitkv_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(glse),
+             _ptr(o_partial), _ptr(o), _ptr(workspace), ws_bytes, B, Sq, Skv, H, Hkv, D,
+             int(num_split), float(sm_scale), dtype_code(q.dtype), _stream(dev))
+    return o
+
+
 def sigmoid(x: torch.Tensor, y: torch.Tensor):
     """y = sigmoid(x), fp32 math."""
     dev = _dev(x, y)

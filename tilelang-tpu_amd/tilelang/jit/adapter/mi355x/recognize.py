@@ -522,9 +522,9 @@ def _flashattn_splitkv(pf, qk, pv, Q, K, V, Opart) -> Plan:
     over each of num_split key ranges (flash_attn_split) writes normalised partial outputs to
     Output_partial [batch, seq_q, heads, num_split, dim] and log2 sum-exp to glse [batch, heads,
     num_split, seq_q]; combine merges them into Output [batch, seq_q, heads, dim]. The merge of
-    the splits equals attention over all keys when every split covers whole key tiles, so the
-    program runs as one attention pass with seq_q != seq_kv (glse and Output_partial are the
-    program's intermediates and are not written)."""
+    the splits equals attention over all keys when every split covers whole key tiles. The
+    program's partials (each split's normalised output and log2 sum-exp, in the program's
+    dtype) are written as the program writes them, and Output is their combine."""
     fam = "flashattn"
     shp, kshp, pshp = _shape(Q), _shape(K), _shape(Opart)
     if len(shp) != 4 or len(kshp) != 4 or kshp != _shape(V):
@@ -545,8 +545,12 @@ def _flashattn_splitkv(pf, qk, pv, Q, K, V, Opart) -> Plan:
                    "Output_partial and one Output [batch, seq_q, heads, dim] written by a second "
                    "(combine) kernel")
     O = outs[0]
-    if not (Q.dtype == K.dtype == V.dtype == O.dtype) or Q.dtype not in ("bfloat16", "float16"):
-        _fail(fam, "split-KV attention takes bfloat16 or float16 Q, K, V and Output")
+    if not (Q.dtype == K.dtype == V.dtype == O.dtype == lses[0].dtype == Opart.dtype) or \
+            Q.dtype not in ("bfloat16", "float16"):
+        _fail(fam, "split-KV attention takes one bfloat16 or float16 dtype for Q, K, V, glse, "
+                   "Output_partial and Output")
+    if ns > 16:
+        _fail(fam, f"{ns} splits (at most 16)")
     tile_dts = {_buf(qk.args[0]).dtype, _buf(qk.args[1]).dtype, _buf(pv.args[0]).dtype,
                 _buf(pv.args[1]).dtype}
     if tile_dts != {Q.dtype}:
