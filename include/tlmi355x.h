@@ -311,6 +311,29 @@ int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_
                    int64_t max_pages, int num_split, float sm_scale, const float* kv_scale,
                    int q_dtype, int kv_dtype, int o_dtype, void* stream);
 
+/* tlm_mla_decode for the split programs that keep their partials: the split kernel of
+ * examples/deepseek_mla/example_mla_decode_paged.py:100-183 writes glse [b, h, s] and
+ * Output_partial [b, h, s, :] (:182-184) and its combine (:186-221) reads them back; the non-paged
+ * example_mla_decode.py split form does the same.
+ *   glse [B, Hq, num_split] and o_partial [B, Hq, num_split, dv], dense, of p_dtype (F16 | BF16 |
+ *   F32, the last stored without rounding):
+ *   split s of a sequence holds its blocks of part_block tokens dealt out so that the first
+ *   (blocks % num_split) splits take one extra (the program's block_N; :140-144). o_partial
+ *   receives the split's normalised output (times kv_scale for fp8 KV) and glse its log2
+ *   sum-exp of the scaled scores (exp2 domain), both rounded to p_dtype; o is the combine of the
+ *   stored values. A split without tokens stores -inf and zeros (the reference divides 0 by 0
+ *   there). dv must be a multiple of 4. With glse and o_partial both NULL this is
+ *   tlm_mla_decode. The partials path runs the program's partition on the split kernels (not the
+ *   balanced fp8 path); ws as for tlm_mla_decode. Other arguments as tlm_mla_decode. */
+int tlm_mla_decode_ex(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                      const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                      int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
+                      void* o, void* ws, size_t ws_bytes, int64_t B, int64_t Hq, int64_t dv,
+                      int64_t dpe, int64_t page, int64_t max_pages, int num_split,
+                      float sm_scale, const float* kv_scale, int q_dtype, int kv_dtype,
+                      int o_dtype, void* glse, void* o_partial, int64_t part_block, int p_dtype,
+                      void* stream);
+
 /* Workspace bytes that tlm_mla_decode needs for (B, Hq, dv, num_split). */
 size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split);
 

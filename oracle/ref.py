@@ -409,8 +409,15 @@ def mla_split_partition(seqlen: int, num_split: int, block_n: int):
 
 
 def mla_split_combine_ref(q, q_pe, kv, k_pe, block_table, seqlens, page, sm_scale, num_split,
-                          block_n=64, kv_scale=1.0, out_dtype=torch.bfloat16):
+                          block_n=64, kv_scale=1.0, out_dtype=torch.bfloat16, store_dtype=None):
+    """Split partials (flash_split_ref) and their LSE combine (reduce_ref). With store_dtype the
+    partials are rounded to it before the combine, as the split program stores glse /
+    Output_partial (example_mla_decode_paged.py:182-184) and its combine reads them back
+    (:186-221); then returns (out, (glse [B, Hq, ns], partial [B, Hq, ns, dv])) as floats. A
+    split without tokens has lse -inf and a zero partial."""
     B, Hq, dv = q.shape
+    glse_all = torch.empty(B, Hq, num_split)
+    part_all = torch.empty(B, Hq, num_split, dv)
     kv2 = kv.reshape(kv.shape[0], -1)
     kp2 = k_pe.reshape(k_pe.shape[0], -1)
     out = torch.zeros(B, Hq, dv, dtype=torch.float32)
@@ -436,10 +443,17 @@ def mla_split_combine_ref(q, q_pe, kv, k_pe, block_table, seqlens, page, sm_scal
             parts.append((p @ kvf[r]) / l[:, None])
             lses.append(torch.log2(l) + m)
         g = torch.stack(lses, -1)  # [Hq, ns]
+        if store_dtype is not None:
+            g = g.to(store_dtype).float()
+            parts = [pt.to(store_dtype).float() for pt in parts]
+        glse_all[b] = g
+        part_all[b] = torch.stack(parts, 1)
         gmax = g.max(-1).values
         lse = torch.log2(torch.exp2(g - gmax[:, None]).sum(-1)) + gmax
         for i, part in enumerate(parts):
             out[b] += part * torch.exp2(g[:, i] - lse)[:, None]
+    if store_dtype is not None:
+        return out.to(out_dtype), (glse_all, part_all)
     return out.to(out_dtype)
 
 

@@ -250,6 +250,28 @@ def test_mla_validation_and_workspace():
     assert rc == -1
 
 
+def test_mla_decode_ex_validation():
+    L = lib.load()
+    p = ctypes.c_void_p(0x1000)
+    bt = ctypes.c_void_p(0x2000)
+    f = L.tlm_mla_decode_ex
+    # q, q_pe, qs, qpes, kv, k_pe, kvs, kpes, rows, bt, sl, o, ws, ws_bytes, B, Hq, dv, dpe, page,
+    # max_pages, ns, scale, kv_scale, q_dt, kv_dt, o_dt, glse, o_partial, part_block, p_dt, stream
+    args = [p, p, 576, 576, p, p, 576, 576, 1024, bt, bt, p, p, 1 << 30, 2, 64, 512, 64, 64, 8,
+            4, 0.1, None, lib.F16, lib.F16, lib.F16]
+    assert f(*args, p, None, 64, lib.F16, None) == -1       # o_partial missing
+    assert f(*args, p, p, 0, lib.F16, None) == -1           # part_block
+    assert f(*args, p, p, 64, lib.F8E4M3, None) == -1       # partial dtype
+    assert f(*args, ctypes.c_void_p(0x1001), p, 64, lib.F16, None) == -1  # glse alignment
+    a2 = list(args)
+    a2[16] = 510  # dv not a multiple of 4
+    a2[2] = a2[6] = 574
+    assert f(*a2, p, p, 64, lib.F16, None) == -2
+    a0 = list(args)
+    a0[14] = 0   # no sequences: nothing to do
+    assert f(*a0, p, p, 64, lib.F16, None) == 0
+
+
 def test_mla_noalloc_validation():
     """The allocation-free entry point validates like tlm_mla_decode and rejects, before any HIP
     call, a request whose scratch need exceeds the library's array."""

@@ -80,6 +80,44 @@ def test_reference_program_fp16_split():
     exp = ref.mla_decode_ref(q[..., :dv], q[..., dv:], kvp[..., :dv], kvp[..., dv:], bt, sl, bs,
                              1 / math.sqrt(dv + dpe), out_dtype=torch.float16)
     torch_assert_close(out.cpu(), exp, atol=1e-2, rtol=1e-2)
+    # the split kernel's partials (:182-184), as the program stores them, and the combine of
+    # the stored values (:186-221)
+    comb, (g_ref, p_ref) = ref.mla_split_combine_ref(
+        q[..., :dv], q[..., dv:], kvp[..., :dv], kvp[..., dv:], bt, sl, bs,
+        1 / math.sqrt(dv + dpe), 2, block_n=64, out_dtype=torch.float16,
+        store_dtype=torch.float16)
+    torch_assert_close(glse.cpu().float(), g_ref, atol=2e-2, rtol=0)
+    torch_assert_close(opart.cpu().float(), p_ref, atol=1e-2, rtol=1e-2)
+    torch_assert_close(out.cpu(), comb, atol=1e-2, rtol=1e-2)
+
+
+def test_split_program_partials_with_empty_splits():
+    """Sequences with fewer 64-token blocks than splits (one block over 4 splits): the empty
+    splits store lse -inf and zeros, and the output is the attention over the tokens."""
+    B, Hq, dv, dpe, bs, ns = 2, 64, 512, 64, 64, 4
+    prog = programs.mla_decode(B, Hq, 1, 256, dv, dpe, 64, 64, ns, bs, dtype="bfloat16")
+    k = tilelang.compile(prog, out_idx=[8])
+    g = torch.Generator().manual_seed(33)
+    q = torch.randn(B, Hq, dv + dpe, generator=g).bfloat16()
+    kvp = torch.randn(B * 256, 1, dv + dpe, generator=g).bfloat16()
+    bt = torch.randperm(B * 4, generator=g).view(B, 4).to(torch.int32)
+    sl = torch.tensor([40, 130], dtype=torch.int32)
+    glse = torch.empty(B, Hq, ns, dtype=torch.bfloat16, device=DEV)
+    opart = torch.empty(B, Hq, ns, dv, dtype=torch.bfloat16, device=DEV)
+    out = k(q[..., :dv].contiguous().to(DEV), q[..., dv:].contiguous().to(DEV),
+            kvp[..., :dv].contiguous().to(DEV), kvp[..., dv:].contiguous().to(DEV),
+            bt.to(DEV), sl.to(DEV), glse, opart).cpu()
+    comb, (g_ref, p_ref) = ref.mla_split_combine_ref(
+        q[..., :dv], q[..., dv:], kvp[..., :dv], kvp[..., dv:], bt, sl, bs,
+        1 / math.sqrt(dv + dpe), ns, block_n=64, out_dtype=torch.bfloat16,
+        store_dtype=torch.bfloat16)
+    assert torch.isinf(glse[0, :, 1:].float()).all() and not opart[0, :, 1:].any()
+    torch_assert_close(glse.cpu().float(), g_ref, atol=0.13, rtol=0)
+    torch_assert_close(opart.cpu().float(), p_ref, atol=2e-2, rtol=2e-2)
+    torch_assert_close(out, comb, atol=2e-2, rtol=2e-2)
+    exp = ref.mla_decode_ref(q[..., :dv], q[..., dv:], kvp[..., :dv], kvp[..., dv:], bt, sl, bs,
+                             1 / math.sqrt(dv + dpe), out_dtype=torch.bfloat16)
+    torch_assert_close(out, exp, atol=2e-2, rtol=2e-2)
 
 
 def test_fp8_program_through_compile():
@@ -104,6 +142,15 @@ def test_fp8_program_through_compile():
                              1 / math.sqrt(576), float(T["kv_scale"]))
     torch_assert_close(out.cpu(), exp, atol=2e-2, rtol=5e-2)
     assert _rel_rms(out.cpu(), exp) < FP8_REL_RMS
+    # the program's fp32 partials: each split's output (times kv_scale) and log2 sum-exp
+    _, (g_ref, p_ref) = ref.mla_split_combine_ref(
+        T["q"][..., :512], T["q"][..., 512:], T["kv"][:, :512], T["kv"][:, 512:],
+        T["block_table"], T["seqlens"], page, 1 / math.sqrt(576), 4, block_n=64,
+        kv_scale=float(T["kv_scale"]), store_dtype=torch.float32)
+    live = torch.isfinite(g_ref)
+    assert torch.equal(torch.isfinite(glse.cpu()), live)
+    torch_assert_close(glse.cpu()[live], g_ref[live], atol=1e-3, rtol=1e-4)
+    torch_assert_close(opart.cpu(), p_ref, atol=2e-2, rtol=5e-2)
 
 
 @pytest.mark.parametrize("num_split", [1, 4, 8])

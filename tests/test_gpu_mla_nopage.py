@@ -94,6 +94,16 @@ def test_upstream_program_config_batch():
     opart = torch.empty(B, H, 4, dv, dtype=torch.float16, device=DEV)
     out = k(q.to(DEV), qpe.to(DEV), kv.to(DEV), kpe.to(DEV), glse, opart).cpu()
     torch_assert_close(out, ref.mla_decode_nopage_ref(q, qpe, kv, kpe), atol=1e-2, rtol=1e-2)
+    # the split form's partials (example_mla_decode.py: split s covers tokens
+    # [s S / 4, (s + 1) S / 4)), checked on sequences 0 and 63 through an identity block table
+    sel = [0, 63]
+    bt = torch.arange(2, dtype=torch.int32).view(2, 1)
+    sl = torch.full((2,), S, dtype=torch.int32)
+    _, (g_ref, p_ref) = ref.mla_split_combine_ref(
+        q[sel], qpe[sel], kv[sel].reshape(2 * S, dv), kpe[sel].reshape(2 * S, dpe), bt, sl, S,
+        1 / math.sqrt(dv + dpe), 4, block_n=64, store_dtype=torch.float16)
+    torch_assert_close(glse[sel].cpu().float(), g_ref, atol=2e-2, rtol=0)
+    torch_assert_close(opart[sel].cpu().float(), p_ref, atol=1e-2, rtol=1e-2)
 
 
 def test_upstream_program_generic_heads():

@@ -227,6 +227,37 @@ def test_mla_page_permutation_and_split_invariance():
         assert torch.allclose(sc, base, atol=1e-5)
 
 
+def test_mla_split_partials_are_attention_over_each_split():
+    """The stored partials of mla_split_combine_ref: split s's partial is the attention output
+    over its own tokens and its glse the log2 sum-exp there (natural-log lse of mla_decode_ref
+    over the same tokens, divided by ln 2); a split without tokens holds -inf and zeros."""
+    g = torch.Generator().manual_seed(12)
+    B, Hq, dv, dpe, page = 2, 3, 8, 4, 2
+    q = torch.randn(B, Hq, dv, generator=g)
+    qp = torch.randn(B, Hq, dpe, generator=g)
+    kv = torch.randn(12, dv, generator=g)
+    kp = torch.randn(12, dpe, generator=g)
+    bt = torch.tensor([[3, 0, 5], [1, 4, 2]], dtype=torch.int32)
+    sl = torch.tensor([5, 2], dtype=torch.int32)
+    ns = 3
+    out, (glse, part) = ref.mla_split_combine_ref(q, qp, kv, kp, bt, sl, page, 0.7, ns,
+                                                  block_n=page, out_dtype=torch.float32,
+                                                  store_dtype=torch.float32)
+    assert torch.allclose(out, ref.mla_decode_ref(q, qp, kv, kp, bt, sl, page, 0.7,
+                                                  out_dtype=torch.float32), atol=1e-5)
+    for b in range(B):
+        for s_, (st, en) in enumerate(ref.mla_split_partition(int(sl[b]), ns, page)):
+            if en <= st:
+                assert torch.isinf(glse[b, :, s_]).all() and not part[b, :, s_].any()
+                continue
+            sub_bt = bt[b:b + 1, st // page:]
+            o, lse = ref.mla_decode_ref(q[b:b + 1], qp[b:b + 1], kv, kp, sub_bt,
+                                        torch.tensor([en - st], dtype=torch.int32), page, 0.7,
+                                        out_dtype=torch.float32, return_lse=True)
+            assert torch.allclose(part[b, :, s_], o[0], atol=1e-5)
+            assert torch.allclose(glse[b, :, s_], lse[0] / math.log(2.0), atol=1e-5)
+
+
 def test_split_partition_rule():
     """example_mla_decode_paged.py:140-144: blocks dealt out, first (total % ns) get one more."""
     for L, ns, bn in ((4096, 4, 64), (65, 4, 64), (1, 8, 64), (1000, 3, 64)):

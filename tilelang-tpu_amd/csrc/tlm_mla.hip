@@ -39,7 +39,7 @@ constexpr int MLA_DV = 512, MLA_DPE = 64, MLA_D = MLA_DV + MLA_DPE;
 constexpr int MLA_WAVES = 8;
 constexpr int MLA_HEADS = 64;           // heads per workgroup
 constexpr int MLA_BN = 32;              // tokens per KV tile
-constexpr int MLA_PART_BLOCK = 64;      // split partition granularity (reference block_N)
+constexpr int MLA_PART_BLOCK = 64;      // default split partition granularity (reference block_N)
 constexpr int KVP = MLA_D + 24;         // LDS pitch (halves): 1200 B rows
 constexpr int QK_SUB = MLA_D / 16 / 4;  // 9 k-substeps of S^T per wave
 constexpr int O_DT = MLA_DV / 4 / 32;   // 4 32-wide d tiles of O^T per wave
@@ -83,6 +83,17 @@ TLM_DEV void fp8x16_to_h16(u32x4 in, u32x4& lo, u32x4& hi) {
   hi = out[1];
 }
 
+// Token range [t0, t1) of split s of a sequence of L tokens: its blocks of `blk` tokens are dealt
+// out so the first (blocks % num_split) splits take one extra (example_mla_decode_paged.py:
+// 140-144). Empty when the sequence has fewer blocks than splits.
+TLM_DEV void mla_split_range(int L, int num_split, int s, int blk, int& t0, int& t1) {
+  const int total = (L + blk - 1) / blk;
+  const int per = total / num_split, rem = total % num_split;
+  const int nb = per + (s < rem ? 1 : 0);
+  t0 = (per * s + min(s, rem)) * blk;
+  t1 = min(t0 + nb * blk, L);
+}
+
 // KV_KIND: 0 = fp8 e4m3, 1 = same 16-bit type as Q.
 template <bool BF16, int KV_KIND>
 __global__ __launch_bounds__(64 * MLA_WAVES, 1) void mla_split_kernel(
@@ -92,7 +103,7 @@ __global__ __launch_bounds__(64 * MLA_WAVES, 1) void mla_split_kernel(
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seqlens,
     float* __restrict__ ws_o, float* __restrict__ ws_lse,
     int Hq, int page, int max_pages, int num_split, float score_scale,
-    const float* __restrict__ kv_scale) {
+    const float* __restrict__ kv_scale, int part_block) {
   using MT = mla_mma<BF16>;
   using v8 = typename MT::v8;
   __shared__ __attribute__((aligned(16))) uint16_t sKV[2][MLA_BN * KVP];
@@ -108,12 +119,9 @@ __global__ __launch_bounds__(64 * MLA_WAVES, 1) void mla_split_kernel(
   // clamp to what the block table can address (a larger seqlen would index past the table)
   const int L = max(0, min(seqlens[b], max_pages * page));
 
-  // token range of this split (reference partition over 64-token blocks)
-  const int total = (L + MLA_PART_BLOCK - 1) / MLA_PART_BLOCK;
-  const int per = total / num_split, rem = total % num_split;
-  const int nb64 = per + (split < rem ? 1 : 0);
-  const int t_begin = (per * split + min(split, rem)) * MLA_PART_BLOCK;
-  const int t_end = min(t_begin + nb64 * MLA_PART_BLOCK, L);
+  // token range of this split (reference partition over blocks of part_block tokens)
+  int t_begin, t_end;
+  mla_split_range(L, num_split, split, part_block, t_begin, t_end);
   const int nblk = t_end > t_begin ? (t_end - t_begin + MLA_BN - 1) / MLA_BN : 0;
 
   const float kvs = (KV_KIND == 0 && kv_scale) ? kv_scale[0] : 1.0f;
@@ -299,6 +307,73 @@ __global__ __launch_bounds__(128) void mla_combine_kernel(const float* __restric
   *(u32x2*)(out + bh * MLA_DV + d) = pk;
 }
 
+// Combine of the split programs that keep their partials (example_mla_decode_paged.py:100-221,
+// example_mla_decode.py): split s's normalised output (times kv_scale for fp8 KV) and log2
+// sum-exp are stored rounded to the program's dtype in Output_partial [b, h, s, :] and glse
+// [b, h, s], and Output is the combine of those stored values, as the program's combine kernel
+// reads them back: O = sum_s O_s 2^(lse_s - lse), lse = log2 sum_s 2^(lse_s - max) + max. A split
+// without tokens stores lse -inf and zeros (the reference divides 0 by 0 there). One workgroup
+// per (sequence, head), 4 dims per thread.
+// PK: storage of the partials, 0 fp16, 1 bf16, 2 fp32 (stored unrounded).
+template <int PK>
+struct part_store {
+  static TLM_DEV float round(float x) {
+    if constexpr (PK == 2) return x;
+    else return h16<PK == 1>::to_f32(h16<PK == 1>::from_f32(x));
+  }
+  static TLM_DEV void put_lse(void* g, int64_t i, float x) {
+    if constexpr (PK == 2) ((float*)g)[i] = x;
+    else ((uint16_t*)g)[i] = (uint16_t)h16<PK == 1>::from_f32(x);
+  }
+  // stores four values and returns them as read back
+  static TLM_DEV f32x4 put4(void* p, int64_t i, f32x4 v) {
+    if constexpr (PK == 2) {
+      *(f32x4*)((float*)p + i) = v;
+      return v;
+    } else {
+      using H = h16<PK == 1>;
+      const u32x2 pk = {H::pack(v[0], v[1]), H::pack(v[2], v[3])};
+      *(u32x2*)((uint16_t*)p + i) = pk;
+      return f32x4{H::lo(pk[0]), H::hi(pk[0]), H::lo(pk[1]), H::hi(pk[1])};
+    }
+  }
+};
+
+template <int PK, bool OUT_BF16>
+__global__ __launch_bounds__(256) void mla_partial_combine(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_lse, void* __restrict__ glse,
+    void* __restrict__ opart, uint16_t* __restrict__ out, int num_split, int dv,
+    const float* kv_scale, int kv_is_fp8) {
+  using PS = part_store<PK>;
+  using HO = h16<OUT_BF16>;
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x * 4;
+  const float* lse = ws_lse + bh * num_split;
+  const float kvs = (kv_is_fp8 && kv_scale) ? kv_scale[0] : 1.0f;
+  float M = -INFINITY, L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < num_split; ++s) {
+    const float l0 = lse[s];
+    if (threadIdx.x == 0) PS::put_lse(glse, bh * num_split + s, l0);
+    if (d >= dv) continue;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (l0 != -INFINITY) v = *(const f32x4*)(ws_o + (bh * num_split + s) * dv + d) * kvs;
+    const f32x4 vr = PS::put4(opart, (bh * num_split + s) * dv + d, v);
+    const float lr = PS::round(l0);  // the stored values, as read back
+    if (lr != -INFINITY) {
+      const float Mn = fmaxf(M, lr);
+      const float a = fast_exp2(M - Mn), w = fast_exp2(lr - Mn);  // a = 0 while M = -inf
+      L = L * a + w;
+      acc = acc * a + vr * w;
+      M = Mn;
+    }
+  }
+  if (d >= dv) return;
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  *(u32x2*)(out + bh * dv + d) = u32x2{HO::pack(acc[0] * inv, acc[1] * inv),
+                                       HO::pack(acc[2] * inv, acc[3] * inv)};
+}
+
 // ------------------------------------------------------------------------------------------------
 // Paged gather: one 64-lane wave per token row; rows resolved through the block table exactly
 // as the decode kernel resolves them (example_mla_decode_paged.py:62-63).
@@ -327,20 +402,26 @@ __global__ __launch_bounds__(256) void paged_gather_kernel(
 // the threads spread over the dims. Correctness path for small shapes, not tuned.
 constexpr int MLA_GEN_DV = 1024, MLA_GEN_DQK = MLA_GEN_DV + 256;
 
+// Split mode (ws_o != nullptr, the split programs that keep their partials): workgroup =
+// (sequence, head, split) over the split's token range; the normalised output (without
+// kv_scale) goes to ws_o [b, h, s, :] and the log2 sum-exp to ws_lse [b, h, s].
 template <bool BF16, int KV_KIND, bool O_BF16>
 __global__ __launch_bounds__(256) void mla_generic_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ q_pe, int64_t qs, int64_t qpes,
     const uint8_t* __restrict__ kv, const uint8_t* __restrict__ k_pe, int64_t kvs_b,
     int64_t kpes_b, int64_t kv_rows, const int32_t* __restrict__ bt,
     const int32_t* __restrict__ sl, uint16_t* __restrict__ out, int Hq, int dv, int dpe,
-    int page, int max_pages, float sc, const float* kv_scale) {
+    int page, int max_pages, float sc, const float* kv_scale, float* __restrict__ ws_o,
+    float* __restrict__ ws_lse, int num_split, int part_block) {
   __shared__ float qf[MLA_GEN_DQK];
   __shared__ float pt[256];
   __shared__ int64_t rt[256];
   __shared__ float red[256];
   using HQ = h16<BF16>;
   const int tid = threadIdx.x;
-  const int64_t bh = blockIdx.x;
+  const bool split_mode = ws_o != nullptr;
+  const int64_t bh = split_mode ? blockIdx.x / num_split : blockIdx.x;
+  const int split = split_mode ? (int)(blockIdx.x % num_split) : 0;
   const int b = (int)(bh / Hq);
   const int dqk = dv + dpe;
   for (int d = tid; d < dqk; d += 256)
@@ -354,7 +435,9 @@ __global__ __launch_bounds__(256) void mla_generic_kernel(
     }
   };
   const int64_t lmax = (int64_t)max_pages * page;
-  const int L = (int)max((int64_t)0, min((int64_t)sl[b], lmax));
+  const int L_all = (int)max((int64_t)0, min((int64_t)sl[b], lmax));
+  int c_lo = 0, L = L_all;  // token range [c_lo, L)
+  if (split_mode) mla_split_range(L_all, num_split, split, part_block, c_lo, L);
   float m = -INFINITY, l = 0.f;
   float o[MLA_GEN_DV / 256] = {};
   auto block_reduce = [&](float v, bool is_max) {
@@ -369,7 +452,7 @@ __global__ __launch_bounds__(256) void mla_generic_kernel(
     return r;
   };
   __syncthreads();
-  for (int c0 = 0; c0 < L; c0 += 256) {
+  for (int c0 = c_lo; c0 < L; c0 += 256) {
     const int t = c0 + tid;
     float s = -INFINITY;
     int64_t row = -1;
@@ -405,6 +488,17 @@ __global__ __launch_bounds__(256) void mla_generic_kernel(
     }
     __syncthreads();
   }
+  if (split_mode) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const int64_t slot = bh * num_split + split;
+#pragma unroll
+    for (int k = 0; k < MLA_GEN_DV / 256; ++k) {
+      const int d = tid + 256 * k;
+      if (d < dv) ws_o[slot * dv + d] = o[k] * inv;
+    }
+    if (tid == 0) ws_lse[slot] = l > 0.f ? m + __log2f(l) : -INFINITY;
+    return;
+  }
   using HO = h16<O_BF16>;
   const float w = l > 0.f ? kvs / l : 0.f;
 #pragma unroll
@@ -418,11 +512,14 @@ template <bool BF16, int KV_KIND, bool O_BF16>
 int launch_generic(const void* q, const void* q_pe, int64_t qs, int64_t qpes, const void* kv,
                    const void* k_pe, int64_t kvs_b, int64_t kpes_b, int64_t kv_rows,
                    const int32_t* bt, const int32_t* sl, void* o, int B, int Hq, int dv, int dpe,
-                   int page, int max_pages, float sc, const float* kv_scale, hipStream_t st) {
-  mla_generic_kernel<BF16, KV_KIND, O_BF16><<<(unsigned)((int64_t)B * Hq), 256, 0, st>>>(
+                   int page, int max_pages, float sc, const float* kv_scale, hipStream_t st,
+                   float* ws_o = nullptr, float* ws_lse = nullptr, int num_split = 1,
+                   int part_block = MLA_PART_BLOCK) {
+  const int64_t nwg = (int64_t)B * Hq * (ws_o ? num_split : 1);
+  mla_generic_kernel<BF16, KV_KIND, O_BF16><<<(unsigned)nwg, 256, 0, st>>>(
       (const uint16_t*)q, (const uint16_t*)q_pe, qs, qpes, (const uint8_t*)kv,
       (const uint8_t*)k_pe, kvs_b, kpes_b, kv_rows, bt, sl, (uint16_t*)o, Hq, dv, dpe, page,
-      max_pages, sc, kv_scale);
+      max_pages, sc, kv_scale, ws_o, ws_lse, num_split, part_block);
   TLM_LAUNCH_CHECK("tlm_mla_decode (generic)");
   return TLM_OK;
 }
@@ -431,12 +528,13 @@ template <bool BF16, int KV_KIND>
 int launch_split(const void* q, const void* q_pe, int64_t qs, int64_t qpes, const void* kv,
                  const void* k_pe, int64_t kvs_b, int64_t kpes_b, int64_t kv_rows, const int32_t* bt,
                  const int32_t* sl, float* ws_o, float* ws_lse, int B, int Hq, int page,
-                 int max_pages, int ns, float sc, const float* kv_scale, hipStream_t st) {
+                 int max_pages, int ns, float sc, const float* kv_scale, hipStream_t st,
+                 int part_block = MLA_PART_BLOCK) {
   const int64_t nwg = (int64_t)B * ns * (Hq / MLA_HEADS);
   mla_split_kernel<BF16, KV_KIND><<<(unsigned)nwg, 64 * MLA_WAVES, 0, st>>>(
       (const uint16_t*)q, (const uint16_t*)q_pe, qs, qpes, (const uint8_t*)kv,
       (const uint8_t*)k_pe, kvs_b, kpes_b, kv_rows, bt, sl, ws_o, ws_lse, Hq, page, max_pages, ns, sc,
-      kv_scale);
+      kv_scale, part_block);
   TLM_LAUNCH_CHECK("tlm_mla_decode (split)");
   return TLM_OK;
 }
@@ -539,11 +637,74 @@ static int mla_run(const char* fn, const void* q, const void* q_pe, int64_t q_st
                    const int32_t* seqlens, void* o, void* ws, size_t ws_bytes, int64_t B,
                    int64_t Hq, int64_t dv, int64_t dpe, int64_t page, int64_t max_pages,
                    int num_split, float sm_scale, const float* kv_scale, int q_dtype,
-                   int kv_dtype, int o_dtype, void* stream) {
+                   int kv_dtype, int o_dtype, void* stream, void* glse = nullptr,
+                   void* opart = nullptr, int part_block = MLA_PART_BLOCK,
+                   int p_dtype = TLM_F16) {
   if (B == 0) return TLM_OK;
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
-  if (!mla_fast_shape(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, o, Hq,
-                      dv, dpe, kv_dtype)) {
+  const bool partials = glse != nullptr && opart != nullptr;
+  const bool fast = mla_fast_shape(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                   kpe_stride, o, Hq, dv, dpe, kv_dtype);
+  if (partials) {
+    // the program's own split partition, its partials stored, Output from the stored values
+    if (ws_bytes < mla_split_workspace_bytes(B, Hq, dv, num_split)) {
+      tlm_set_error("%s: %zu bytes of workspace, %zu required", fn, ws_bytes,
+                    mla_split_workspace_bytes(B, Hq, dv, num_split));
+      return TLM_EWORKSPACE;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    float* ws_o = (float*)ws;
+    float* ws_lse = ws_o + (size_t)B * Hq * num_split * dv;
+    const bool bq = q_dtype == TLM_BF16;
+    const bool f8 = kv_dtype == TLM_F8E4M3;
+    const int b = (int)B, h = (int)Hq, pg = (int)page, mp = (int)max_pages;
+    const int64_t kb = f8 ? 1 : 2;
+    int rc;
+    if (fast) {
+      rc = bq ? (f8 ? launch_split<true, 0>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                            kpe_stride, kv_rows, block_table, seqlens, ws_o,
+                                            ws_lse, b, h, pg, mp, num_split, sc, kv_scale, st,
+                                            part_block)
+                    : launch_split<true, 1>(q, q_pe, q_stride, q_pe_stride, kv, k_pe,
+                                            kv_stride * 2, kpe_stride * 2, kv_rows, block_table,
+                                            seqlens, ws_o, ws_lse, b, h, pg, mp, num_split, sc,
+                                            kv_scale, st, part_block))
+              : (f8 ? launch_split<false, 0>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                             kpe_stride, kv_rows, block_table, seqlens, ws_o,
+                                             ws_lse, b, h, pg, mp, num_split, sc, kv_scale, st,
+                                             part_block)
+                    : launch_split<false, 1>(q, q_pe, q_stride, q_pe_stride, kv, k_pe,
+                                             kv_stride * 2, kpe_stride * 2, kv_rows, block_table,
+                                             seqlens, ws_o, ws_lse, b, h, pg, mp, num_split, sc,
+                                             kv_scale, st, part_block));
+    } else {
+#define TLM_MLA_GENS(BQ, KK)                                                                       \
+  launch_generic<BQ, KK, false>(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride * kb,         \
+                                kpe_stride * kb, kv_rows, block_table, seqlens, o, b, h, (int)dv, \
+                                (int)dpe, pg, mp, sc, kv_scale, st, ws_o, ws_lse, num_split,      \
+                                part_block)
+      rc = bq ? (f8 ? TLM_MLA_GENS(true, 0) : TLM_MLA_GENS(true, 1))
+              : (f8 ? TLM_MLA_GENS(false, 0) : TLM_MLA_GENS(false, 1));
+#undef TLM_MLA_GENS
+    }
+    if (rc) return rc;
+    const unsigned nthr = (unsigned)(((dv / 4) + 63) / 64 * 64);
+    const unsigned nwg = (unsigned)(B * Hq);
+    auto comb = [&](auto kern) {
+      kern<<<nwg, nthr, 0, st>>>(ws_o, ws_lse, glse, opart, (uint16_t*)o, num_split, (int)dv,
+                                 kv_scale, f8 ? 1 : 0);
+    };
+    const bool ob = o_dtype == TLM_BF16;
+    if (p_dtype == TLM_F32)
+      ob ? comb(mla_partial_combine<2, true>) : comb(mla_partial_combine<2, false>);
+    else if (p_dtype == TLM_BF16)
+      ob ? comb(mla_partial_combine<1, true>) : comb(mla_partial_combine<1, false>);
+    else
+      ob ? comb(mla_partial_combine<0, true>) : comb(mla_partial_combine<0, false>);
+    TLM_LAUNCH_CHECK("tlm_mla_decode (partial combine)");
+    return TLM_OK;
+  }
+  if (!fast) {
     hipStream_t st = (hipStream_t)stream;
     const int64_t kb = kv_dtype == TLM_F8E4M3 ? 1 : 2;
     const int b = (int)B, h = (int)Hq, pg = (int)page, mp = (int)max_pages;
@@ -635,6 +796,54 @@ extern "C" int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride,
   return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
                  block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, dpe, page, max_pages, num_split,
                  sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype, stream);
+}
+
+extern "C" int tlm_mla_decode_ex(const void* q, const void* q_pe, int64_t q_stride,
+                                 int64_t q_pe_stride, const void* kv, const void* k_pe,
+                                 int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                                 const int32_t* block_table, const int32_t* seqlens, void* o,
+                                 void* ws, size_t ws_bytes, int64_t B, int64_t Hq, int64_t dv,
+                                 int64_t dpe, int64_t page, int64_t max_pages, int num_split,
+                                 float sm_scale, const float* kv_scale, int q_dtype, int kv_dtype,
+                                 int o_dtype, void* glse, void* o_partial, int64_t part_block,
+                                 int p_dtype, void* stream) {
+  const char* fn = "tlm_mla_decode_ex";
+  if (!glse && !o_partial)
+    return tlm_mla_decode(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride,
+                          kv_rows, block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, dpe, page,
+                          max_pages, num_split, sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype,
+                          stream);
+  int rc = mla_validate(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride,
+                        kv_rows, block_table, seqlens, o, B, Hq, dv, dpe, page, max_pages,
+                        num_split, q_dtype, kv_dtype, o_dtype);
+  if (rc) return rc;
+  if (part_block < 1 || part_block > (1 << 20) ||
+      (p_dtype != TLM_F16 && p_dtype != TLM_BF16 && p_dtype != TLM_F32)) {
+    tlm_set_error("%s: part_block %lld must be in [1, 2^20] and p_dtype F16, BF16 or F32", fn,
+                  (long long)part_block);
+    return TLM_EINVAL;
+  }
+  const size_t pe = p_dtype == TLM_F32 ? 4 : 2;
+  if (!glse || !o_partial || !tlm_aligned(glse, pe) || !tlm_aligned(o_partial, 4 * pe)) {
+    tlm_set_error("%s: glse and o_partial must both be given (aligned to 1 and 4 elements)", fn);
+    return TLM_EINVAL;
+  }
+  if (dv % 4) {
+    tlm_set_error("%s: partials need dv a multiple of 4 (got %lld)", fn, (long long)dv);
+    return TLM_EUNSUPPORTED;
+  }
+  if ((int64_t)B * Hq * num_split > INT32_MAX) {
+    tlm_set_error("%s: problem too large", fn);
+    return TLM_EINVAL;
+  }
+  if (B > 0 && (!ws || !tlm_aligned(ws, 16))) {
+    tlm_set_error("%s: workspace must be non-null and 16-byte aligned", fn);
+    return TLM_EINVAL;
+  }
+  return mla_run(fn, q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
+                 block_table, seqlens, o, ws, ws_bytes, B, Hq, dv, dpe, page, max_pages, num_split,
+                 sm_scale, kv_scale, q_dtype, kv_dtype, o_dtype, stream, glse, o_partial,
+                 (int)part_block, p_dtype);
 }
 
 // ---- allocation-free variant ------------------------------------------------------------------

@@ -101,8 +101,15 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
             qq = q.view(B, Hq, dv)
             qpe = t[a["q_pe"]].view(B, Hq, dpe)
             o = t[a["o"]].view(B, Hq, dv)
+        g = op = None
+        if a.get("partials"):  # the split program writes glse / Output_partial
+            g, op = t[a["glse"]], t[a["o_partial"]]
+            if not a["paged"]:
+                g = g.view(B, Hq, a["num_split"])
+                op = op.view(B, Hq, a["num_split"], dv)
         ops.mla_decode(qq, qpe, t[a["kv"]], t[a["k_pe"]], bt, sl, o, ws, a["page"],
-                       a["num_split"], a["sm_scale"], kvs)
+                       a["num_split"], a["sm_scale"], kvs, glse=g, o_partial=op,
+                       part_block=a.get("part_block", 64))
     elif f == "elementwise":
         ops.elementwise([t[i] for i in a["inputs"]], a["bcast"], [t[i] for i in a["outputs"]],
                         a["code"], a["consts"], a["rows"], a["cols"])

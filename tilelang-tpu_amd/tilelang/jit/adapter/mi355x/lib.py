@@ -55,6 +55,10 @@ _SIGNATURES = {
     "tlm_mla_decode": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                         c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
                        [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int, c_void_p], c_int),
+    "tlm_mla_decode_ex": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                           c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t] +
+                          [c_int64] * 6 + [c_int, c_float, c_void_p, c_int, c_int, c_int,
+                                           c_void_p, c_void_p, c_int64, c_int, c_void_p], c_int),
     "tlm_mla_workspace_bytes": ([c_int64, c_int64, c_int64, c_int], c_size_t),
     "tlm_mla_decode_noalloc": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                 c_int64, c_int64, c_void_p, c_void_p, c_void_p] +

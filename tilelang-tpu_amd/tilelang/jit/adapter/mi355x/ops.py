@@ -356,11 +356,16 @@ def _rows_count(kv, dv, k_pe, dpe) -> int:
 
 
 def mla_decode(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, page: int,
-               num_split: int, sm_scale: float, kv_scale: Optional[torch.Tensor] = None):
+               num_split: int, sm_scale: float, kv_scale: Optional[torch.Tensor] = None,
+               glse: Optional[torch.Tensor] = None, o_partial: Optional[torch.Tensor] = None,
+               part_block: int = 64):
     """Paged MLA decode. q [B,Hq,dv], q_pe [B,Hq,dpe], kv [rows,...,dv], k_pe [rows,...,dpe]
     (any uniform row stride), block_table int32 [B, max_pages], seqlens int32 [B],
-    out [B, Hq, dv]. kv_scale: device fp32 scalar for fp8 KV (None -> 1)."""
-    dev = _dev(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, kv_scale)
+    out [B, Hq, dv]. kv_scale: device fp32 scalar for fp8 KV (None -> 1). glse [B, Hq, ns] and
+    o_partial [B, Hq, ns, dv] (both or neither): the split programs' partials, written over
+    the program's partition in blocks of part_block tokens."""
+    dev = _dev(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, kv_scale, glse,
+               o_partial)
     B, Hq, dv = q.shape
     dpe = q_pe.shape[-1]
     if tuple(q_pe.shape[:2]) != (B, Hq) or tuple(out.shape) != (B, Hq, dv):
@@ -386,10 +391,27 @@ def mla_decode(q, q_pe, kv, k_pe, block_table, seqlens, out, workspace, page: in
     if kv_scale is not None and (kv_scale.dtype != torch.float32 or kv_scale.numel() != 1):
         raise ValueError("kv_scale must be a one-element float32 tensor")
     ws_bytes = workspace.numel() * workspace.element_size()
-    lib.call("tlm_mla_decode", q_ptr, qpe_ptr, q_rs, qpe_rs, kv_ptr, kpe_ptr, kv_rs, kpe_rs,
-             _rows_count(kv, dv, k_pe, dpe), _ptr(block_table), _ptr(seqlens), _ptr(out), _ptr(workspace), ws_bytes, B, Hq, dv,
-             dpe, page, block_table.shape[1], num_split, float(sm_scale), _ptr(kv_scale),
-             dtype_code(q.dtype), dtype_code(kv.dtype), dtype_code(out.dtype), _stream(dev))
+    if (glse is None) != (o_partial is None):
+        raise ValueError("glse and Output_partial go together")
+    if glse is None:
+        lib.call("tlm_mla_decode", q_ptr, qpe_ptr, q_rs, qpe_rs, kv_ptr, kpe_ptr, kv_rs, kpe_rs,
+                 _rows_count(kv, dv, k_pe, dpe), _ptr(block_table), _ptr(seqlens), _ptr(out),
+                 _ptr(workspace), ws_bytes, B, Hq, dv, dpe, page, block_table.shape[1],
+                 num_split, float(sm_scale), _ptr(kv_scale), dtype_code(q.dtype),
+                 dtype_code(kv.dtype), dtype_code(out.dtype), _stream(dev))
+        return out
+    _contig("glse", glse)
+    _contig("Output_partial", o_partial)
+    if tuple(glse.shape) != (B, Hq, num_split) or \
+            tuple(o_partial.shape) != (B, Hq, num_split, dv) or glse.dtype != o_partial.dtype:
+        raise ValueError("glse must be [B, Hq, num_split] and Output_partial [B, Hq, num_split, "
+                         "dv], of one dtype")
+    lib.call("tlm_mla_decode_ex", q_ptr, qpe_ptr, q_rs, qpe_rs, kv_ptr, kpe_ptr, kv_rs, kpe_rs,
+             _rows_count(kv, dv, k_pe, dpe), _ptr(block_table), _ptr(seqlens), _ptr(out),
+             _ptr(workspace), ws_bytes, B, Hq, dv, dpe, page, block_table.shape[1], num_split,
+             float(sm_scale), _ptr(kv_scale), dtype_code(q.dtype), dtype_code(kv.dtype),
+             dtype_code(out.dtype), _ptr(glse), _ptr(o_partial), int(part_block),
+             dtype_code(glse.dtype), _stream(dev))
     return out
 
 
