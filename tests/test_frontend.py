@@ -460,3 +460,50 @@ def test_elementwise_reload_after_store_is_rejected():
 
     with pytest.raises(UnsupportedProgram, match="after the program stores"):
         tilelang.compile(reload, out_idx=-1)
+
+
+def test_symbolic_extents_specialise_per_call():
+    """T.symbolic (reference tilelang/language/__init__.py:85-86): the demo's fill program
+    (tpu_demo/ppl/matmul.py:26) compiles with symbolic m, n; each call binds them from the
+    argument shapes and recognises the specialised program (rows / cols from the binding)."""
+    m, n = T.symbolic("m"), T.symbolic("n")
+    prog = programs.fill_tiles(m, n, 128, 128)
+    assert prog.symbolic_vars() == ["m", "n"]
+    k = tilelang.compile(prog, out_idx=-1)
+    assert k.plan.family == "elementwise" and k.adapter.dynamic
+    spec = prog.specialize({"m": 300, "n": 520})
+    assert tuple(spec.params[0].shape) == (300, 520)
+    assert [ir_const(e) for e in spec.kernels[0].extents] == [5, 3]  # ceil(520/128), ceil(300/128)
+    plan = k.adapter._plan_for({"m": 300, "n": 520})
+    assert (plan.attrs["rows"], plan.attrs["cols"]) == (300, 520)
+    assert plan.attrs["consts"] == [0.0] and not plan.attrs["inputs"]
+    # the same binding is recognised once
+    assert k.adapter._plan_for({"m": 300, "n": 520}) is plan
+    # the elementwise add over symbolic m, n: shapes must agree under the binding
+    add = tilelang.compile(programs.add_symbolic(64, 64), out_idx=-1)
+    with pytest.raises(ValueError, match="mismatch"):
+        add.adapter._check(1, torch.zeros(4, 6), {"m": 4, "n": 5})
+
+
+def ir_const(e):
+    from tilelang.language import ir
+    return ir.const_value(e)
+
+
+def test_symbolic_program_still_fails_at_compile_time():
+    """A symbolic program that fits no kernel family is rejected by tilelang.compile, at the
+    trial binding, not at the first call."""
+    m = T.symbolic("m")
+
+    @T.prim_func
+    def mix(A: T.Tensor((m, 64), "float32"), B: T.Tensor((m, 1), "float32")):
+        with T.Kernel(T.ceildiv(m, 64), is_cpu=True) as (bx,):
+            a = T.alloc_shared((64, 64), "float32")
+            r = T.alloc_shared((64, 1), "float32")
+            T.ppl_copy(A[bx * 64, 0], a)
+            T.ppl_exp2(a)
+            T.ppl_reduce_max(a, r, dim=1)
+            T.ppl_copy(r, B[bx * 64, 0])
+
+    with pytest.raises(UnsupportedProgram):
+        tilelang.compile(mix, out_idx=-1)

@@ -101,3 +101,37 @@ def test_register_program_through_the_c_abi():
     e1 = torch.sigmoid(a * row + col) / (1.0 / torch.sqrt(sc)) - 1.0
     torch_assert_close(o1.cpu(), e1, atol=1e-6, rtol=1e-6)
     torch_assert_close(o2.cpu().float(), torch.exp(e1).half().float(), atol=0, rtol=1e-3)
+
+
+def test_symbolic_fill_program_per_binding():
+    """tpu_demo/ppl/matmul.py (:9-26) with symbolic m, n: one compiled kernel, called on
+    tensors of several shapes (including tiles cut by the edge); every element takes the fill
+    value rounded to the tensor's dtype (bit-exact)."""
+    import tilelang.language as T
+    k = tilelang.compile(programs.fill_tiles(T.symbolic("m"), T.symbolic("n"), 128, 128,
+                                             value=0.0), out_idx=-1)
+    for (m, n) in ((300, 520), (128, 64), (1, 1000)):
+        a = torch.full((m, n), 7.0, dtype=torch.float16, device=DEV)
+        assert k(a) == 0
+        assert torch.equal(a.cpu(), torch.zeros(m, n, dtype=torch.float16))
+    k2 = tilelang.compile(programs.fill_tiles(T.symbolic("m"), T.symbolic("n"), 64, 32,
+                                              dtype="bfloat16", value=1.0 / 3), out_idx=-1)
+    a = torch.empty(70, 90, dtype=torch.bfloat16, device=DEV)
+    assert k2(a) == 0  # the only parameter is the output: all parameters, in place
+    exp = torch.full((70, 90), 1.0 / 3, dtype=torch.float32).to(torch.bfloat16)
+    assert torch.equal(a.cpu(), exp)
+    with pytest.raises(ValueError, match="not bound"):
+        k2()  # inputs only: nothing binds m, n
+
+
+def test_symbolic_add_program_shapes():
+    """elementwise_add.py over symbolic m, n: the binding comes from A; B and C must agree."""
+    k = tilelang.compile(programs.add_symbolic(64, 64), out_idx=-1)
+    for (m, n) in ((100, 70), (256, 512)):
+        a = torch.randn(m, n, generator=_g(m)).to(DEV)
+        b = torch.randn(m, n, generator=_g(n)).to(DEV)
+        c = k(a, b)
+        torch_assert_close(c.cpu(), ref.ppl_add_ref(a.cpu(), b.cpu()), atol=0, rtol=0,
+                           max_mismatched_ratio=0)
+    with pytest.raises(ValueError, match="mismatch"):
+        k(torch.zeros(4, 6, device=DEV), torch.zeros(4, 5, device=DEV))

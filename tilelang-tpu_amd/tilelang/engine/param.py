@@ -1,6 +1,6 @@
 """Kernel parameter metadata (reference tilelang/engine/param.py:13-109: dtype + static shape)."""
 from dataclasses import dataclass
-from typing import List
+from typing import Any, List, Union
 
 import torch
 
@@ -10,11 +10,21 @@ from ..utils.tensor import map_torch_type
 @dataclass
 class KernelParam:
     dtype: torch.dtype
-    shape: List[int]
+    shape: List[Union[int, Any]]  # an int, or a symbolic extent (T.symbolic) bound per call
 
     @classmethod
     def from_buffer(cls, buffer) -> "KernelParam":
-        return cls(map_torch_type(buffer.dtype), [int(s) for s in buffer.shape])
+        from ..language import ir
+        shape = []
+        for s in buffer.shape:
+            try:
+                shape.append(int(ir.const_value(s)))
+            except (TypeError, ValueError):
+                shape.append(s)
+        return cls(map_torch_type(buffer.dtype), shape)
+
+    def is_dynamic(self) -> bool:
+        return any(not isinstance(s, int) for s in self.shape)
 
     def is_scalar(self) -> bool:
         return len(self.shape) == 0

@@ -14,11 +14,23 @@ from typing import Any, List
 
 import torch
 
+from ....language import ir
 from ..base import BaseKernelAdapter
 from . import ops
+from .recognize import recognize
 
 
 _TORCH_DT = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+
+
+def _eval_extent(s, env):
+    """Integer value of a tensor extent under the symbolic binding ``env`` (None if unbound)."""
+    if isinstance(s, int):
+        return s
+    if ir.sym_names(s) - set(env):
+        return None
+    v = ir.substitute(s, env)
+    return int(ir.const_value(v))
 
 
 def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
@@ -122,6 +134,10 @@ class MI355XKernelAdapter(BaseKernelAdapter):
     def __init__(self, params, result_idx, plan, prim_func=None):
         self.plan = plan
         self.prim_func = prim_func
+        # symbolic extents: the plan above is the compile-time trial; each call recognises the
+        # program specialised to its argument shapes (cached per binding)
+        self.dynamic = any(p.is_dynamic() for p in params)
+        self._plans = {}
         self._ws = {}
         super().__init__(None, params, result_idx)
         # the recognizer knows which parameters the program writes
@@ -132,7 +148,7 @@ class MI355XKernelAdapter(BaseKernelAdapter):
         return (f"// gfx950 kernel family {self.plan.describe()}\n"
                 f"// dispatched through libtlmi355x.so (include/tlmi355x.h)\n")
 
-    def _check(self, i, t):
+    def _check(self, i, t, env=None):
         p = self.params[i]
         if p.is_scalar():  # a plain Python int, as cython_wrapper.pyx:117-122 passes it
             if isinstance(t, bool) or not isinstance(t, int):
@@ -144,9 +160,39 @@ class MI355XKernelAdapter(BaseKernelAdapter):
         if t.dtype != p.dtype:
             raise ValueError(f"Buffer dtype mismatch for parameter {i}: expected {p.dtype}, "
                              f"got {t.dtype}")
-        if list(t.shape) != [int(s) for s in p.shape]:
-            raise ValueError(f"Static shape mismatch for parameter {i}: expected "
-                             f"{list(p.shape)}, got {list(t.shape)}")
+        if not p.is_dynamic():
+            if list(t.shape) != [int(s) for s in p.shape]:
+                raise ValueError(f"Static shape mismatch for parameter {i}: expected "
+                                 f"{list(p.shape)}, got {list(t.shape)}")
+            return
+        # symbolic extents (T.symbolic): a plain variable is bound by the first argument that
+        # carries it; every other extent must equal its value under the binding
+        if t.dim() != len(p.shape):
+            raise ValueError(f"Dimension mismatch for parameter {i}: expected {len(p.shape)} "
+                             f"dims, got {t.dim()}")
+        for d, (s, n) in enumerate(zip(p.shape, t.shape)):
+            if isinstance(s, ir.Var) and s.name not in env:
+                env[s.name] = int(n)
+        for d, (s, n) in enumerate(zip(p.shape, t.shape)):
+            v = _eval_extent(s, env)
+            if v is not None and v != int(n):
+                raise ValueError(f"Shape mismatch for parameter {i} dim {d}: expected {s!r} = "
+                                 f"{v} under {env}, got {int(n)}")
+
+    def _plan_for(self, env):
+        """The plan of the program specialised to the bound symbolic extents (cached)."""
+        if not self.dynamic:
+            return self.plan
+        names = self.prim_func.symbolic_vars()
+        missing = [n for n in names if n not in env]
+        if missing:
+            raise ValueError(f"symbolic extents {missing} are not bound by any input tensor")
+        key = tuple(env[n] for n in names)
+        plan = self._plans.get(key)
+        if plan is None:
+            plan = recognize(self.prim_func.specialize({n: env[n] for n in names}))
+            self._plans[key] = plan
+        return plan
 
     def _convert_torch_func(self):
 
@@ -163,9 +209,11 @@ class MI355XKernelAdapter(BaseKernelAdapter):
             else:
                 raise ValueError(f"Expected {n} arguments (all parameters, outputs written in "
                                  f"place) or {n - len(outs)} (inputs only), got {len(args)}")
+            env: dict = {}
             for i, t in enumerate(full):
                 if t is not None:
-                    self._check(i, t)
+                    self._check(i, t, env)
+            plan = self._plan_for(env)
             ins = [t for t in full if isinstance(t, torch.Tensor)]
             if not torch.cuda.is_available():
                 raise RuntimeError("no HIP device visible: the mi355x target runs on gfx950 only "
@@ -180,15 +228,18 @@ class MI355XKernelAdapter(BaseKernelAdapter):
             for i, t in enumerate(full):
                 if t is None:
                     p = self.params[i]
-                    dev_t.append(torch.empty([int(s) for s in p.shape], dtype=p.dtype,
-                                             device=gpu))
+                    shape = [_eval_extent(s, env) for s in p.shape]
+                    if any(v is None for v in shape):
+                        raise ValueError(f"the shape {list(p.shape)} of output {i} is not bound "
+                                         f"by the inputs")
+                    dev_t.append(torch.empty(shape, dtype=p.dtype, device=gpu))
                 elif not isinstance(t, torch.Tensor):  # scalar argument
                     dev_t.append(t)
                 elif t.device != gpu:
                     dev_t.append(t.to(gpu))
                 else:
                     dev_t.append(t)
-            _run_plan(self.plan, dev_t, self._ws)
+            _run_plan(plan, dev_t, self._ws)
             if inplace:
                 for i in outs:
                     if full[i].data_ptr() != dev_t[i].data_ptr():

@@ -1214,8 +1214,10 @@ def recognize(pf) -> Plan:
             return _audit(pf, _rope(pf, names))
         if {"ppl_reduce_sum", "ppl_rsqrt"} <= names:
             return _audit(pf, _rmsnorm(pf, names))
+        # tile programs of copies, fills and elementwise ops (a fill-only program, such as the
+        # symbolic-shape fill of tpu_demo/ppl/matmul.py, stores a constant)
         ew = n_gemm == 0 and names <= set(_ALLOWED_OPS["elementwise"]) and \
-            bool(names & set(_ALLOWED_OPS["elementwise"]) - set(_COPY) - set(_FILL_OPS))
+            bool(names & (set(_ALLOWED_OPS["elementwise"]) - set(_COPY)))
         if {"ppl_exp", "ppl_div"} <= names or "ppl_sigmoid" in names:
             # the dedicated SwiGLU / sigmoid kernels, else the general elementwise program
             try:

@@ -8,6 +8,9 @@ from ..utils.tensor import TensorSupplyType
 from .adapter.mi355x import MI355XKernelAdapter, recognize
 
 
+SYMBOLIC_TRIAL = 4096  # trial value of each symbolic extent at compile time
+
+
 class JITKernel:
     """Compiled kernel. Calling it runs the gfx950 kernel chosen for the program."""
 
@@ -33,7 +36,11 @@ class JITKernel:
         if func is None:
             raise ValueError("JITKernel needs a prim_func")
         self.prim_func = func
-        plan = recognize(func)
+        sym = func.symbolic_vars() if hasattr(func, "symbolic_vars") else []
+        # symbolic extents (T.symbolic): the program is recognised here at a trial binding, so
+        # an unsupported program still fails at compile time; each call specialises it to the
+        # argument shapes
+        plan = recognize(func.specialize({n: SYMBOLIC_TRIAL for n in sym}) if sym else func)
         params = [KernelParam.from_buffer(b) for b in func.params]
         self.adapter = MI355XKernelAdapter(params, out_idx, plan, func)
         self.torch_function = self.adapter.func

@@ -52,6 +52,31 @@ class PrimFunc:
         ps = ", ".join(repr(p) for p in self.params)
         return f"PrimFunc {self.name}({ps}) [{len(self.ops)} ops, {len(self.kernels)} kernels]"
 
+    def symbolic_vars(self) -> list:
+        """Names of the symbolic shape variables of the parameters (T.symbolic), in order of
+        first appearance."""
+        names = []
+        for p in self.params:
+            for d in getattr(p, "shape", ()):
+                for n in sorted(ir.sym_names(d)):
+                    if n not in names:
+                        names.append(n)
+        return names
+
+    def specialize(self, env: dict) -> "PrimFunc":
+        """This program with its symbolic shape variables bound to the integers in ``env`` (the
+        trace is re-written with the values folded in; nothing is re-executed)."""
+        memo: dict = {}
+        out = PrimFunc.__new__(PrimFunc)
+        out.name = self.name
+        out.params = [ir.substitute(p, env, memo) for p in self.params]
+        out.ops = [ir.substitute(o, env, memo) for o in self.ops]
+        out.kernels = [ir.substitute(k, env, memo) for k in self.kernels]
+        out.allocs = [ir.substitute(b, env, memo) for b in self.allocs]
+        out.fn = self.fn
+        out.attrs = dict(self.attrs)
+        return out
+
     def script(self) -> str:
         lines = [repr(self)]
         for op in self.ops:
@@ -91,6 +116,13 @@ def prim_func(fn=None, *, private: bool = False, check_well_formed: bool = False
     if fn is None:
         return deco
     return deco(fn)
+
+
+def symbolic(name: str, dtype: str = "int32"):
+    """A symbolic tensor extent (reference tilelang/language/__init__.py:85-86): usable in
+    ``T.Tensor`` shapes and in the body's arithmetic; bound from the arguments' shapes when the
+    compiled kernel is called."""
+    return ir.SymVar(name, canon_dtype(dtype))
 
 
 def macro(fn=None, **kwargs):

@@ -223,6 +223,14 @@ class Var(Expr):
         return iter((self,))
 
 
+class SymVar(Var):
+    """Symbolic shape variable (``T.symbolic``, reference tilelang/language/__init__.py:85-86):
+    a tensor extent bound when the kernel is called (from the argument's shape); the traced
+    program is specialised to the bound values before recognition."""
+
+    __slots__ = ()
+
+
 class ScalarParam(Var):
     """Scalar prim_func parameter (``max_seqlen_q: T.int32``): a symbolic value in the traced
     body and a Python number at call time (the reference passes such parameters as plain
@@ -268,6 +276,80 @@ _FOLD = {
     "min": min,
     "max": max,
 }
+
+
+_FOLD_CALL = dict(_FOLD, ceildiv=lambda a, b: -(-a // b))
+
+
+def sym_names(x) -> set:
+    """Names of the symbolic shape variables in an expression (or a plain value)."""
+    if isinstance(x, Expr):
+        return {e.args[0] for e in x.walk() if isinstance(e, SymVar)}
+    return set()
+
+
+def substitute(x, env: dict, memo: Optional[dict] = None):
+    """``x`` with the symbolic shape variables named in ``env`` replaced by their values and
+    the arithmetic over them folded. Buffers, accesses, loops and launches that mention one are
+    rebuilt (one new object per old one, so identities between trace records are kept); every
+    other object is returned as is."""
+    memo = {} if memo is None else memo
+    key = id(x)
+    if key in memo:
+        return memo[key]
+    out = x
+    if isinstance(x, SymVar):
+        if x.args[0] in env:
+            out = Const(int(env[x.args[0]]), x.dtype)
+    elif isinstance(x, BufferAccess):
+        b = substitute(x.buffer, env, memo)
+        idx = substitute(x.indices, env, memo)
+        if b is not x.buffer or idx is not x.indices:
+            out = BufferAccess(b, idx)
+    elif isinstance(x, Expr):
+        if sym_names(x) & set(env):
+            args = tuple(substitute(a, env, memo) for a in x.args)
+            if all(is_const(a) for a in args) and x.op in _FOLD_CALL and len(args) == 2:
+                out = binop(x.op, args[0], args[1]) if x.op in _FOLD else \
+                    Const(_FOLD_CALL[x.op](*(const_value(a) for a in args)), x.dtype)
+            else:
+                out = Expr(x.op, args, x.dtype)
+    elif isinstance(x, Buffer):
+        shape = substitute(tuple(x.shape), env, memo)
+        if shape is not x.shape and any(a is not b for a, b in zip(shape, x.shape)):
+            out = Buffer.__new__(Buffer)
+            out.__dict__.update(x.__dict__)
+            out.shape = tuple(shape)
+    elif isinstance(x, tuple):
+        items = tuple(substitute(a, env, memo) for a in x)
+        out = x if all(a is b for a, b in zip(items, x)) else items
+    elif isinstance(x, list):
+        items = [substitute(a, env, memo) for a in x]
+        out = x if all(a is b for a, b in zip(items, x)) else items
+    elif isinstance(x, dict):
+        items = {k: substitute(v, env, memo) for k, v in x.items()}
+        out = x if all(items[k] is x[k] for k in x) else items
+    elif isinstance(x, slice):
+        st, sp, se = (substitute(v, env, memo) for v in (x.start, x.stop, x.step))
+        if st is not x.start or sp is not x.stop or se is not x.step:
+            out = slice(st, sp, se)
+    elif isinstance(x, Loop):
+        ext = substitute(x.extents, env, memo)
+        kw = substitute(x.kwargs, env, memo)
+        if ext is not x.extents or kw is not x.kwargs:
+            out = Loop(x.kind, x.vars, ext, kw)
+    elif isinstance(x, KernelLaunch):
+        ext = substitute(x.extents, env, memo)
+        if ext is not x.extents:
+            out = KernelLaunch(x.index, ext, x.threads, x.is_cpu, x.vars)
+    elif isinstance(x, Op):
+        args = substitute(x.args, env, memo)
+        kw = substitute(x.kwargs, env, memo)
+        loops = substitute(x.loops, env, memo)
+        if args is not x.args or kw is not x.kwargs or loops is not x.loops:
+            out = Op(x.name, args, kw, loops, x.kernel)
+    memo[key] = out
+    return out
 
 
 def binop(op: str, a, b):

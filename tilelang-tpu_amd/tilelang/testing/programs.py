@@ -1228,3 +1228,24 @@ def ppl_add(M, N, block_M, block_N, in_dtype="float32", out_dtype="float32"):
             T.ppl_copy(c_s, C[by * block_M, bx * block_N])
 
     return main
+
+
+def fill_tiles(M, N, block_M, block_N, dtype="float16", accum_dtype="float", value=0.0):
+    """tpu_demo/ppl/matmul.py:9-23: every block_M x block_N tile of A [M, N] is filled with a
+    constant in an accum_dtype tile and copied out (cast to dtype). The demo calls it with
+    symbolic extents, matmul(T.symbolic("m"), T.symbolic("n"), 128, 128, 2) (:26)."""
+
+    @T.prim_func
+    def main(A: T.Tensor((M, N), dtype)):
+        with T.Kernel(T.ceildiv(N, block_N), T.ceildiv(M, block_M), is_cpu=True) as (bx, by):
+            a_s = T.alloc_shared((block_M, block_N), accum_dtype)
+            T.ppl_fill(a_s, T.float32(value))
+            T.copy(a_s, A[by * block_M, bx * block_N])
+
+    return main
+
+
+def add_symbolic(block_M, block_N, dtype="float32"):
+    """tpu_demo/ppl/elementwise_add_kernel/elementwise_add.py:9-35 over symbolic extents m, n
+    (T.symbolic, reference tilelang/language/__init__.py:85-86): C = A + B for any [m, n]."""
+    return ppl_add(T.symbolic("m"), T.symbolic("n"), block_M, block_N, dtype, dtype)
