@@ -151,16 +151,21 @@ def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return (up.float() * F.silu(gate.float())).to(gate.dtype)
 
 
-def mlp_ref(x, gate_weight, up_weight, down_weight):
+def mlp_ref(x, gate_weight, up_weight, down_weight, operand_dtype=None):
     """tpu_demo/ppl/mlp/mlp_bf16.py:98-131 with whole blocks: gate = x Wg^T and up = x Wu^T
     (fp32 accumulation, stored as the 16-bit dtype), SiLU(gate) * up in fp32 rounded to the
-    16-bit dtype, out = gated Wd^T (fp32 accumulation, 16-bit result)."""
-    dt = x.dtype
+    16-bit dtype, out = gated Wd^T (fp32 accumulation, 16-bit result). mlp_fp32.py:83-120
+    (operand_dtype bf16): the fp32 x and weights are first rounded to the operand dtype, and
+    the 16-bit down projection is returned as fp32."""
+    dt = operand_dtype or x.dtype
+    x, gate_weight, up_weight, down_weight = (v.to(dt) for v in
+                                              (x, gate_weight, up_weight, down_weight))
     gate = (x.float() @ gate_weight.float().t()).to(dt)
     up = (x.float() @ up_weight.float().t()).to(dt)
     g = gate.float()
     h = (g / (1.0 + torch.exp(-g)) * up.float()).to(dt)
-    return (h.float() @ down_weight.float().t()).to(dt)
+    out = (h.float() @ down_weight.float().t()).to(dt)
+    return out if operand_dtype is None else out.float()
 
 
 # ------------------------------------------------------------------------------------------------

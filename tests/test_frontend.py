@@ -416,6 +416,16 @@ def test_mlp_program_recognised_with_whole_blocks_only():
         tilelang.compile(programs.deepseek_mlp(8, 8, 8, 16, 16, 16), out_idx=[0])
 
 
+def test_fp32_mlp_program_recognised():
+    """tpu_demo/ppl/mlp/mlp_fp32.py: fp32 parameters, bf16 gemm tiles; whole blocks only."""
+    k = tilelang.compile(programs.deepseek_mlp_fp32(16, 16, 16, 16, 16, 16), out_idx=[0])
+    a = k.plan.attrs
+    assert k.plan.family == "mlp" and a["dtype"] == "float32"
+    assert a["operand_dtype"] == "bfloat16"
+    with pytest.raises(UnsupportedProgram, match="whole blocks"):
+        tilelang.compile(programs.deepseek_mlp_fp32(8, 8, 8, 16, 16, 16), out_idx=[0])
+
+
 def test_elementwise_tile_at_another_grid_position_is_rejected():
     """An input tile taken at the transposed grid position of the output tile reads other
     elements than the ones it is stored to: not an elementwise program."""

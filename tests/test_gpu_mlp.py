@@ -57,3 +57,14 @@ def test_deepseek_shapes(M, Hd, I, dtype):
     x, wg, wu, wd = _weights(M, Hd, I, 112 + M, dtype)
     out = k(x.to(DEV), wg.to(DEV), wu.to(DEV), wd.to(DEV)).cpu()
     _check(out, ref.mlp_ref(x, wg, wu, wd))
+
+
+@pytest.mark.parametrize("M,Hd,I", [(16, 16, 16), (96, 512, 1024)])
+def test_fp32_program(M, Hd, I):
+    """tpu_demo/ppl/mlp/mlp_fp32.py with whole blocks: fp32 parameters and output, bf16 gemm
+    tiles (the demo's own 16 x 16 x 16 and a larger shape)."""
+    k = tilelang.compile(programs.deepseek_mlp_fp32(min(M, 64), Hd, I, M, Hd, I), out_idx=[0])
+    x, wg, wu, wd = _weights(M, Hd, I, 113 + M, torch.float32)
+    out = k(x.to(DEV), wg.to(DEV), wu.to(DEV), wd.to(DEV)).cpu()
+    assert out.dtype == torch.float32
+    _check(out, ref.mlp_ref(x, wg, wu, wd, operand_dtype=torch.bfloat16))

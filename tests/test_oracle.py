@@ -684,3 +684,9 @@ def test_mlp_ref_composition_and_loops():
         for c in range(Hd):
             o = float(torch.tensor(sum(h[i] * wdf[c][i] for i in range(I))).bfloat16())
             assert abs(o - float(got[r, c])) <= 2 ** -7 * abs(o) + 1e-6
+    # the all-fp32 program (mlp_fp32.py): fp32 tiles rounded to bf16 before the gemms (RNE,
+    # torch's cast), the bf16 result widened exactly: the bf16 oracle on the rounded inputs
+    x32 = x.float() + torch.randn(M, Hd, generator=g) * 1e-3
+    got32 = ref.mlp_ref(x32, wg.float(), wu.float(), wd.float(), operand_dtype=torch.bfloat16)
+    assert got32.dtype == torch.float32
+    assert torch.equal(got32, ref.mlp_ref(x32.bfloat16(), wg, wu, wd).float())

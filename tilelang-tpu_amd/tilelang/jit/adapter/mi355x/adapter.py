@@ -23,6 +23,14 @@ from .recognize import recognize
 _TORCH_DT = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
 
 
+def _cast_to(v: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    """A copy of ``v`` in dtype ``dt`` made by the library's cast kernel (round to nearest
+    even)."""
+    o = torch.empty(v.shape, dtype=dt, device=v.device)
+    ops.cast(v, o)
+    return o
+
+
 def _eval_extent(s, env):
     """Integer value of a tensor extent under the symbolic binding ``env`` (None if unbound)."""
     if isinstance(s, int):
@@ -73,13 +81,23 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     elif f == "mlp":
         # gate / up projections into 16-bit temporaries, SiLU(gate) * up, down projection
         x, out = t[a["x"]], t[a["out"]]
+        wg, wu, wd = t[a["wg"]], t[a["wu"]], t[a["wd"]]
         M, I = a["M"], a["inter"]
+        if odt is not None:
+            # all-fp32 program: its fp32 tiles are copied to 16-bit tiles for the gemms, whose
+            # 16-bit result of the down projection is copied to the fp32 output
+            x, wg, wu, wd = (_cast_to(v, odt) for v in (x, wg, wu, wd))
         gate = torch.empty(M, I, dtype=x.dtype, device=x.device)
         up = torch.empty_like(gate)
-        ops.gemm(x, t[a["wg"]], gate, True)
-        ops.gemm(x, t[a["wu"]], up, True)
+        ops.gemm(x, wg, gate, True)
+        ops.gemm(x, wu, up, True)
         ops.swiglu(gate, up, gate)
-        ops.gemm(gate, t[a["wd"]], out, True)
+        if odt is None:
+            ops.gemm(gate, wd, out, True)
+        else:
+            d16 = torch.empty(out.shape, dtype=odt, device=out.device)
+            ops.gemm(gate, wd, d16, True)
+            ops.cast(d16, out)
     elif f == "sigmoid":
         ops.sigmoid(t[a["x"]], t[a["y"]])
     elif f == "gather":

@@ -578,7 +578,8 @@ def _flashattn_splitkv(pf, qk, pv, Q, K, V, Opart) -> Plan:
 
 
 def _mlp(pf, names) -> Plan:
-    """tpu_demo/ppl/mlp/mlp_bf16.py:10-141 (DeepSeek-V3 MLP): gate / up projections
+    """tpu_demo/ppl/mlp/mlp_bf16.py:10-141 and mlp_fp32.py:7-120 (DeepSeek-V3 MLP; the fp32
+    program copies its fp32 tiles to bf16 tiles for the gemms): gate / up projections
     x W^T (ppl_gemm transpose_B into 16-bit tiles), SiLU(gate) * up in fp32 rounded once to
     the 16-bit type, down projection gated Wd^T. Every workgroup reduces over one hidden block
     and one intermediate block and overwrites its output block, so the program is the MLP only
@@ -620,12 +621,18 @@ def _mlp(pf, names) -> Plan:
         _fail(fam, "shapes must be x, output [rows, hidden], gate / up weights [inter, hidden], "
                    "down weight [hidden, inter]")
     dt = x.dtype
-    if dt not in ("bfloat16", "float16") or any(p.dtype != dt for p in (wg, wu, wd, out)):
-        _fail(fam, "parameters must all be bfloat16 or all float16")
-    for op in g:
-        if {_buf(op.args[0]).dtype, _buf(op.args[1]).dtype, _buf(op.args[2]).dtype} != {dt}:
-            _fail(fam, "the projections must multiply and store 16-bit tiles of the parameter "
-                       "dtype")
+    if dt not in ("bfloat16", "float16", "float32") or \
+            any(p.dtype != dt for p in (wg, wu, wd, out)):
+        _fail(fam, "parameters must all be bfloat16, all float16 or all float32")
+    # the projections multiply and store 16-bit tiles: of the parameter dtype, or (all-fp32
+    # program, tpu_demo/ppl/mlp/mlp_fp32.py) of one 16-bit operand dtype the fp32 tiles are
+    # copied to
+    tdt = {_buf(op.args[k]).dtype for op in g for k in range(3)}
+    if len(tdt) != 1 or (dt != "float32" and tdt != {dt}) or \
+            not tdt <= {"bfloat16", "float16"}:
+        _fail(fam, "the projections must multiply and store 16-bit tiles of one dtype (the "
+                   "parameter dtype for 16-bit parameters)")
+    operand = next(iter(tdt)) if dt == "float32" else None
     bh, bi = _shape(a[i])[1], _shape(_buf(gate.args[1]))[0]
     if bh != Hd or bi != I:
         _fail(fam, f"blocks of {bh} hidden / {bi} intermediate columns: each workgroup reduces "
@@ -633,7 +640,7 @@ def _mlp(pf, names) -> Plan:
                    f"whole blocks (Block_h = {Hd}, Block_i = {I})")
     return Plan(fam, pf.params, [_index(pf, out)], dict(
         x=_index(pf, x), wg=_index(pf, wg), wu=_index(pf, wu), wd=_index(pf, wd),
-        out=_index(pf, out), M=M, hidden=Hd, inter=I, dtype=dt))
+        out=_index(pf, out), M=M, hidden=Hd, inter=I, dtype=dt, operand_dtype=operand))
 
 
 def _seq_dim(pf, Q: Buffer) -> Optional[int]:

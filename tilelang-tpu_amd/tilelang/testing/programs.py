@@ -395,6 +395,79 @@ def deepseek_mlp(Block_bs, Block_h, Block_i, batch_seq, hidden_size, intermediat
     return main
 
 
+def deepseek_mlp_fp32(Block_bs, Block_h, Block_i, batch_seq, hidden_size, intermediate_size,
+                      gemm_dtype="bfloat16"):
+    """The program structure of tpu_demo/ppl/mlp/mlp_fp32.py:7-120: fp32 parameters and tiles;
+    the x / weight tiles are copied to bf16 tiles for the three ppl_gemm (transpose_B, bf16
+    results, :95-114), gate and up read back as fp32, SiLU(gate) * up in fp32 rounded to bf16
+    for the down projection, whose bf16 result is copied to the fp32 output block (:116-120)."""
+    acc = "float32"
+    gdt = gemm_dtype
+
+    @T.macro
+    def silu(g: T.Tensor((Block_bs, Block_i), acc), out: T.Tensor((Block_bs, Block_i), acc),
+             neg: T.Tensor((Block_bs, Block_i), acc), ones: T.Tensor((Block_bs, Block_i), acc),
+             den: T.Tensor((Block_bs, Block_i), acc)):
+        T.ppl_mul_C(neg, g, T.float32(-1.0))
+        T.ppl_exp2(neg)  # natural exp on BM1690 (customize.py:328-329)
+        T.ppl_add(den, neg, ones)
+        T.ppl_div(out, g, den)
+
+    @T.prim_func
+    def main(output: T.Tensor((batch_seq, hidden_size), acc),
+             x: T.Tensor((batch_seq, hidden_size), acc),
+             gate_weight: T.Tensor((intermediate_size, hidden_size), acc),
+             up_weight: T.Tensor((intermediate_size, hidden_size), acc),
+             down_weight: T.Tensor((hidden_size, intermediate_size), acc)):
+        with T.Kernel(T.ceildiv(batch_seq, Block_bs), T.ceildiv(hidden_size, Block_h),
+                      T.ceildiv(intermediate_size, Block_i), is_cpu=True) as (bx, by, bz):
+            x32 = T.alloc_shared((Block_bs, Block_h), acc)
+            wg32 = T.alloc_shared((Block_i, Block_h), acc)
+            wu32 = T.alloc_shared((Block_i, Block_h), acc)
+            wd32 = T.alloc_shared((Block_h, Block_i), acc)
+            g32 = T.alloc_shared((Block_bs, Block_i), acc)
+            u32 = T.alloc_shared((Block_bs, Block_i), acc)
+            d32 = T.alloc_shared((Block_bs, Block_h), acc)
+            s32 = T.alloc_shared((Block_bs, Block_i), acc)
+            h32 = T.alloc_shared((Block_bs, Block_i), acc)
+            neg = T.alloc_shared((Block_bs, Block_i), acc)
+            ones = T.alloc_shared((Block_bs, Block_i), acc)
+            den = T.alloc_shared((Block_bs, Block_i), acc)
+            T.ppl_fill(ones, T.float32(1.0))
+            T.ppl_copy(x[bx * Block_bs:(bx + 1) * Block_bs, by * Block_h:(by + 1) * Block_h], x32)
+            T.ppl_copy(gate_weight[bz * Block_i:(bz + 1) * Block_i,
+                                   by * Block_h:(by + 1) * Block_h], wg32)
+            T.ppl_copy(up_weight[bz * Block_i:(bz + 1) * Block_i,
+                                 by * Block_h:(by + 1) * Block_h], wu32)
+            T.ppl_copy(down_weight[by * Block_h:(by + 1) * Block_h,
+                                   bz * Block_i:(bz + 1) * Block_i], wd32)
+            xb = T.alloc_shared((Block_bs, Block_h), gdt)
+            wg = T.alloc_shared((Block_i, Block_h), gdt)
+            wu = T.alloc_shared((Block_i, Block_h), gdt)
+            wd = T.alloc_shared((Block_h, Block_i), gdt)
+            g16 = T.alloc_shared((Block_bs, Block_i), gdt)
+            u16 = T.alloc_shared((Block_bs, Block_i), gdt)
+            h16 = T.alloc_shared((Block_bs, Block_i), gdt)
+            d16 = T.alloc_shared((Block_bs, Block_h), gdt)
+            T.ppl_copy(x32, xb)
+            T.ppl_copy(wg32, wg)
+            T.ppl_copy(wu32, wu)
+            T.ppl_copy(wd32, wd)
+            T.ppl_gemm(xb, wg, g16, transpose_B=True)
+            T.ppl_copy(g16, g32)
+            silu(g32, s32, neg, ones, den)
+            T.ppl_gemm(xb, wu, u16, transpose_B=True)
+            T.ppl_copy(u16, u32)
+            T.ppl_mul(h32, s32, u32)
+            T.ppl_copy(h32, h16)
+            T.ppl_gemm(h16, wd, d16, transpose_B=True)
+            T.ppl_copy(d16, d32)
+            T.ppl_copy(d32, output[bx * Block_bs:(bx + 1) * Block_bs,
+                                   by * Block_h:(by + 1) * Block_h])
+
+    return main
+
+
 def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
               dtype="bfloat16", gemm_dtype=None):
     """tpu_test_flashattn_bf16.py:14-135 (fp16 twin); dtype float32 with gemm_dtype float16
