@@ -115,6 +115,35 @@ TLM_DEV float xhalf_sum(float x) {
 TLM_DEV u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
 TLM_DEV void st_nt(u32x4* p, u32x4 v) { __builtin_nontemporal_store(v, p); }
 
+// 16-byte accesses with an explicit cache policy CP (gfx950 bits: sc0 = 1, nt = 2, sc1 = 16)
+// through a raw buffer descriptor at the wave-uniform address `base`; `off` is the lane's byte
+// offset from it (below 2^31). CP_GLOBAL / CP_GLOBAL_NT select a plain / non-temporal global
+// access instead.
+constexpr int CP_GLOBAL_NT = -1, CP_GLOBAL = -2;
+constexpr int CP_PLAIN = 0, CP_NT = 2, CP_SC01 = 17, CP_NT_SC01 = 19;
+TLM_DEV __amdgpu_buffer_rsrc_t stream_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
+}
+template <int CP>
+TLM_DEV void st_cp(void* base, int off, u32x4 v) {
+  if constexpr (CP == CP_GLOBAL_NT)
+    __builtin_nontemporal_store(v, (u32x4*)((char*)base + off));
+  else if constexpr (CP == CP_GLOBAL)
+    *(u32x4*)((char*)base + off) = v;
+  else
+    __builtin_amdgcn_raw_buffer_store_b128(v, stream_rsrc(base), off, 0, CP);
+}
+template <int CP>
+TLM_DEV u32x4 ld_cp(const void* base, int off) {
+  if constexpr (CP == CP_GLOBAL_NT)
+    return __builtin_nontemporal_load((const u32x4*)((const char*)base + off));
+  else if constexpr (CP == CP_GLOBAL)
+    return *(const u32x4*)((const char*)base + off);
+  else
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(stream_rsrc(base), off,
+                                                                           0, CP));
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host-side error plumbing (defined in tlm_capi.hip).
 void tlm_set_error(const char* fmt, ...);
