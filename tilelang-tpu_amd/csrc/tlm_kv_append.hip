@@ -20,12 +20,18 @@
 
 namespace {
 
+// Cache policy of the fp8 page stores (st_cp) when the pool spans less than 2^31 bytes (buffer
+// offsets from the pool base); larger pools store through plain global stores.
+constexpr int kKvStoreCP = CP_NT;
+constexpr int kKvLoadCP = CP_GLOBAL_NT;  // the source rows (read once)
+constexpr int kKvWgCap = 8192;  // workgroups per launch at most
+
 // One workgroup handles `rows` token rows of one sequence at a time (blockIdx.y strides over the
 // sequences, so start[b] / count[b] are uniform loads): thread t owns chunk t % chunks of row
 // t / chunks, both fixed for the whole loop; rows longer than 256 chunks loop over chunks with
 // one row per workgroup. page_shift >= 0: the page size is 2^page_shift (shift and mask instead
 // of a 64-bit division).
-template <bool BF16, int VEC>
+template <bool BF16, int VEC, bool BUF>
 __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_bstride, int64_t x_rstride,
     const int32_t* __restrict__ start, const int32_t* __restrict__ count,
@@ -52,7 +58,7 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
   auto load = [&](int b, int j, int c, u32x4 (&w)[VEC / 8]) {
     const u32x4* src = (const u32x4*)(x + b * x_bstride + j * x_rstride + VEC * c);
 #pragma unroll
-    for (int u = 0; u < VEC / 8; ++u) w[u] = ld_nt(src + u);  // read once
+    for (int u = 0; u < VEC / 8; ++u) w[u] = ld_cp<kKvLoadCP>(src, 16 * u);  // read once
   };
   auto convert = [&](const u32x4 (&w)[VEC / 8], int c, int64_t row) {
     float v[VEC];
@@ -89,7 +95,9 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
       o[h] = (uint32_t)word;
     }
     uint8_t* dst = kv + row * kv_stride + VEC * c;
-    if constexpr (VEC == 16) {
+    if constexpr (VEC == 16 && BUF) {
+      st_cp<kKvStoreCP>(kv, (int)(row * kv_stride + VEC * c), u32x4{o[0], o[1], o[2], o[3]});
+    } else if constexpr (VEC == 16) {
       *(u32x4*)dst = u32x4{o[0], o[1], o[2], o[3]};
     } else {
       *(u32x2*)dst = u32x2{o[0], o[1]};
@@ -128,10 +136,18 @@ void launch(const void* x, int64_t xb, int64_t xr, const int32_t* start, const i
   int shift = -1;
   if ((page & (page - 1)) == 0) shift = __builtin_ctzll((unsigned long long)page);
   const int64_t gy = std::min<int64_t>(B, 65535);
-  const int64_t gx = std::min<int64_t>((T + rows - 1) / rows, std::max<int64_t>(1, 8192 / gy));
-  kv_append_fp8_kernel<BF16, VEC><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, st>>>(
-      (const uint16_t*)x, xb, xr, start, count, bt, max_pages, page, shift, (uint8_t*)kv,
-      kv_stride, kv_rows, (int)B, (int)T, chunks, rows, scale);
+  const int64_t gx =
+      std::min<int64_t>((T + rows - 1) / rows, std::max<int64_t>(1, kKvWgCap / gy));
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  auto go = [&](auto kern) {
+    kern<<<grid, 256, 0, st>>>((const uint16_t*)x, xb, xr, start, count, bt, max_pages, page,
+                               shift, (uint8_t*)kv, kv_stride, kv_rows, (int)B, (int)T, chunks,
+                               rows, scale);
+  };
+  if (kv_rows * kv_stride < ((int64_t)1 << 31))  // buffer offsets from the pool base fit
+    go(kv_append_fp8_kernel<BF16, VEC, true>);
+  else
+    go(kv_append_fp8_kernel<BF16, VEC, false>);
 }
 
 }  // namespace
