@@ -404,6 +404,31 @@ def bench_gemm(args, dev, flush, cpu, M=4096, N=4096, K=4096, dtype=torch.float1
     return res
 
 
+def bench_gemm_library(args, dev, flush, cpu, M=4096, N=4096, K=4096):
+    """Comparator, not this library: torch.matmul on the same fp16 4096^3 operands (ROCm
+    dispatches it to hipBLASLt), timed exactly as the gemm workload (graph of back-to-back
+    launches over rotating copies, HIP events, settled clocks). Not in the default run."""
+    from tilelang.testing import workloads
+    w = workloads.gemm(M, N, K, dtype=torch.float16)
+    flops = 2 * M * N * K
+    nbytes = 2 * (M * K + K * N + M * N)
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        sets.append((w.tensors["a"].to(dev), w.tensors["b"].to(dev),
+                     torch.empty(M, N, dtype=torch.float16, device=dev)))
+    fns = [lambda s=s: torch.matmul(s[0], s[1], out=s[2]) for s in sets]
+    pmc_launches(args, fns, "gemm_library")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 50, flush)
+    return {"workload": f"gemm_torch_matmul_float16_{M}x{N}x{K}",
+            "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+            "dtype": "f16", "note": "comparator: torch.matmul (hipBLASLt), not this library",
+            "roofline": roofline("mfma", flops / (mean_ms * 1e-3) / 1e12, "TFLOP/s",
+                                 MFMA_PEAK["fp16"]),
+            "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+            "algorithmic_flops": flops}
+
+
 def bench_flashattn(args, dev, flush, cpu, S=4096, causal=True):
     import tilelang
     from tilelang.testing import programs, workloads
@@ -818,6 +843,7 @@ BENCHES = {
     "flashattn": bench_flashattn,
     "flashattn_s2048": lambda a, d, f, c: bench_flashattn(a, d, f, c, S=2048, causal=False),
     "flashattn_inference": bench_flashattn_inference,
+    "gemm_library": bench_gemm_library,
     "flashattn_gqa": bench_flashattn_gqa,
     "flashattn_varlen": bench_flashattn_varlen,
     "flashattn_bhsd": bench_flashattn_bhsd,
@@ -835,7 +861,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="all", choices=["all", "copy"] + ORDER)
+    ap.add_argument("--workload", default="all", choices=["all", "copy", "gemm_library"] + ORDER)
     ap.add_argument("--pmc-launches", type=int, default=0,
                     help="only launch the workload's kernel N times (for rocprofv3 --pmc)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

@@ -85,6 +85,10 @@ constexpr int F8_SLOTS = 3;
 constexpr int F8_KV_NT = 2;                          // first piece, last piece, segment scratch
 constexpr float F8_RESET = 64.f;                     // log2 headroom of a segment's reference
 constexpr int F8_RSRC_WORD3 = 0x00020000;            // raw buffer, 32-bit data format
+// cache policies (st_cp / ld_cp bits): the decode's output / partial row stores, the combine's
+// partial loads and output stores
+constexpr int F8_ROW_CP = CP_PLAIN;
+constexpr int F8_CMB_LOAD_CP = CP_GLOBAL, F8_CMB_STORE_CP = CP_GLOBAL;
 
 // swizzled 16-byte chunk index of latent row r / rope row r
 TLM_DEV int swz_lat(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
@@ -1251,7 +1255,7 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         order_after(x[i]);
         const int hr = 4 * i + l4;
         __builtin_amdgcn_raw_buffer_store_b128(x[i], orows, hr * 2 * F8_DV + 256 * h4 + 16 * l16,
-                                               0, 0);
+                                               0, F8_ROW_CP);
       }
     }
   };
@@ -1511,7 +1515,7 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
         if (s_cur != s_next) {  // the range holds tiles
           const int64_t sb = g * F8_SLOTS + ((g == g0 && first_is_piece) ? 1 : 0);
           lv[i] = a.part_lse[sb * a.Hq + head];
-          pv[i] = *(const u32x4*)(a.part_o + (sb * a.Hq + head) * F8_DV + d0);
+          pv[i] = ld_cp<F8_CMB_LOAD_CP>(a.part_o + (sb * a.Hq + head) * F8_DV, 2 * d0);
         }
         s_cur = s_next;
         r_cur = r_next;
@@ -1536,8 +1540,9 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   const float inv = 1.0f / l;
   acc[0] *= inv;
   acc[1] *= inv;
-  *(u32x4*)o = u32x4{H::pack(acc[0][0], acc[0][1]), H::pack(acc[0][2], acc[0][3]),
-                     H::pack(acc[1][0], acc[1][1]), H::pack(acc[1][2], acc[1][3])};
+  st_cp<F8_CMB_STORE_CP>(a.out + row * F8_DV, 2 * d0,
+                         u32x4{H::pack(acc[0][0], acc[0][1]), H::pack(acc[0][2], acc[0][3]),
+                               H::pack(acc[1][0], acc[1][1]), H::pack(acc[1][2], acc[1][3])});
 }
 
 size_t f8_align(size_t n) { return (n + 255) & ~(size_t)255; }
