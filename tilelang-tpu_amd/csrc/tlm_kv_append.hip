@@ -24,7 +24,12 @@ namespace {
 // offsets from the pool base); larger pools store through plain global stores.
 constexpr int kKvStoreCP = CP_NT;
 constexpr int kKvLoadCP = CP_GLOBAL_NT;  // the source rows (read once)
+// Launch shape, measured on the B 64, T 512, D 576 bf16 chunk (back to back): 256 threads and one
+// row group per thread (4,736 workgroups) 4.48 TB/s; two or four row groups per thread with their
+// loads issued together 3.68 / 3.40 TB/s; 128 / 64 / 512 threads 4.31-4.37 / 3.93 / 4.31 TB/s.
 constexpr int kKvWgCap = 8192;  // workgroups per launch at most
+constexpr int KV_U = 1;         // row groups per thread and iteration (loads issued together)
+constexpr int KV_T = 256;       // threads per workgroup
 
 // One workgroup handles `rows` token rows of one sequence at a time (blockIdx.y strides over the
 // sequences, so start[b] / count[b] are uniform loads): thread t owns chunk t % chunks of row
@@ -32,7 +37,7 @@ constexpr int kKvWgCap = 8192;  // workgroups per launch at most
 // one row per workgroup. page_shift >= 0: the page size is 2^page_shift (shift and mask instead
 // of a 64-bit division).
 template <bool BF16, int VEC, bool BUF>
-__global__ __launch_bounds__(256) void kv_append_fp8_kernel(
+__global__ __launch_bounds__(KV_T) void kv_append_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_bstride, int64_t x_rstride,
     const int32_t* __restrict__ start, const int32_t* __restrict__ count,
     const int32_t* __restrict__ block_table, int64_t max_pages, int64_t page, int page_shift,
@@ -50,7 +55,7 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
   // the sign of -0), and NaN inputs are passed through. Other scales divide per element.
   const float y = __fdiv_rn(1.0f, s);
   const bool fast = s >= 0x1p-90f && s <= 0x1p90f;
-  const int r = (int)threadIdx.x / chunks;  // row of the group (0 when chunks > 256)
+  const int r = (int)threadIdx.x / chunks;  // row of the group (0 when chunks > KV_T)
   const int c0 = (int)threadIdx.x - r * chunks;
   if (r >= rows) return;  // threads past the last whole row (no barriers in this kernel)
   const int64_t pool_tokens = max_pages * page;
@@ -107,21 +112,29 @@ __global__ __launch_bounds__(256) void kv_append_fp8_kernel(
   for (int b = blockIdx.y; b < B; b += gridDim.y) {
     const int cnt = min(count[b], T);
     const int64_t st = start[b];
-    for (int j = blockIdx.x * rows + r; j < cnt; j += gridDim.x * rows) {
-      // the source row exists for every j < cnt: its load goes out before the table lookup, so
-      // the two global reads overlap instead of running back to back
-      u32x4 w[VEC / 8];
-      load(b, j, c0, w);
-      const int64_t p = st + j;
-      if (p < 0 || p >= pool_tokens) continue;  // beyond the block table
-      const int64_t pg = page_shift >= 0 ? p >> page_shift : p / page;
-      const int64_t off = page_shift >= 0 ? p & (page - 1) : p % page;
-      const int64_t row = (int64_t)block_table[b * max_pages + pg] * page + off;
-      if (row < 0 || row >= kv_rows) continue;  // a corrupt table entry never writes out of the pool
-      convert(w, c0, row);
-      for (int c = c0 + 256; c < chunks; c += 256) {  // rows of more than 256 chunks
-        load(b, j, c, w);
-        convert(w, c, row);
+    const int step = gridDim.x * rows;
+    for (int j0 = blockIdx.x * rows + r; j0 < cnt; j0 += step * KV_U) {
+      // the source rows exist for every j < cnt: their loads (KV_U rows, step apart) go out
+      // before the table lookups, so the global reads overlap instead of running back to back
+      u32x4 w[KV_U][VEC / 8];
+#pragma unroll
+      for (int u = 0; u < KV_U; ++u)
+        if (j0 + u * step < cnt) load(b, j0 + u * step, c0, w[u]);
+#pragma unroll
+      for (int u = 0; u < KV_U; ++u) {
+        const int j = j0 + u * step;
+        if (j >= cnt) break;
+        const int64_t p = st + j;
+        if (p < 0 || p >= pool_tokens) continue;  // beyond the block table
+        const int64_t pg = page_shift >= 0 ? p >> page_shift : p / page;
+        const int64_t off = page_shift >= 0 ? p & (page - 1) : p % page;
+        const int64_t row = (int64_t)block_table[b * max_pages + pg] * page + off;
+        if (row < 0 || row >= kv_rows) continue;  // a corrupt table entry never writes out of the pool
+        convert(w[u], c0, row);
+        for (int c = c0 + KV_T; c < chunks; c += KV_T) {  // rows of more than KV_T chunks
+          load(b, j, c, w[u]);
+          convert(w[u], c, row);
+        }
       }
     }
   }
@@ -132,15 +145,15 @@ void launch(const void* x, int64_t xb, int64_t xr, const int32_t* start, const i
             const int32_t* bt, int64_t max_pages, int64_t page, void* kv, int64_t kv_stride,
             int64_t kv_rows, int64_t B, int64_t T, int64_t D, const float* scale, hipStream_t st) {
   const int chunks = (int)(D / VEC);
-  const int rows = chunks > 256 ? 1 : 256 / chunks;  // token rows per workgroup
+  const int rows = chunks > KV_T ? 1 : KV_T / chunks;  // token rows per workgroup
   int shift = -1;
   if ((page & (page - 1)) == 0) shift = __builtin_ctzll((unsigned long long)page);
   const int64_t gy = std::min<int64_t>(B, 65535);
   const int64_t gx =
-      std::min<int64_t>((T + rows - 1) / rows, std::max<int64_t>(1, kKvWgCap / gy));
+      std::min<int64_t>((T + rows * KV_U - 1) / (rows * KV_U), std::max<int64_t>(1, kKvWgCap / gy));
   const dim3 grid((unsigned)gx, (unsigned)gy);
   auto go = [&](auto kern) {
-    kern<<<grid, 256, 0, st>>>((const uint16_t*)x, xb, xr, start, count, bt, max_pages, page,
+    kern<<<grid, KV_T, 0, st>>>((const uint16_t*)x, xb, xr, start, count, bt, max_pages, page,
                                shift, (uint8_t*)kv, kv_stride, kv_rows, (int)B, (int)T, chunks,
                                rows, scale);
   };
