@@ -430,11 +430,12 @@ constexpr int PP_VRING = PP_NST * PP_TILE;        // V ring follows the K ring
 constexpr int PP_SMEM = 2 * PP_NST * PP_TILE;     // 128 KB
 constexpr int PP_OP = PP_D + 8;                   // epilogue staging pitch (halves)
 constexpr int PP_RSRC_WORD3 = 0x00020000;         // raw buffer, 32-bit data format
-// Cache policy of the K / V LDS-DMA loads (st_cp bits), causal and full attention. Non-temporal
-// loads for full attention measured 1-2% faster back to back (S 2048: 1,149-1,152 against
-// 1,098-1,128 TFLOP/s; head-major 1,133-1,148 against 1,122-1,132), neutral for grouped-query,
-// and 4-5% slower for causal, whose workgroups re-read a head's K / V tiles from L2.
-constexpr int PP_KV_CP_CAUSAL = CP_PLAIN, PP_KV_CP_FULL = CP_NT;
+// Cache policy of the K / V LDS-DMA loads (st_cp bits). Plain: the query tiles of one K / V head
+// re-read its tiles from L2. Non-temporal loads measured 4-5% slower for causal and, for full
+// attention, 1-2% faster at S 2048, neutral for head-major and grouped-query, 3-4% slower for
+// ragged batches (1,038-1,044 against 1,069-1,084 TFLOP/s), whose counted fetches rose from
+// 1.12 to 1.77 times the algorithmic bytes (grouped-query: 1.88 to 2.45).
+constexpr int PP_KV_CP = CP_PLAIN;
 static_assert(8 * 32 * PP_OP * 2 <= PP_SMEM, "epilogue staging must fit in the rings");
 
 #define TLM_INLINE __attribute__((always_inline))
@@ -599,7 +600,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     for (int r = 0; r < 4; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rsrc, (__attribute__((address_space(3))) void*)(dlds + slot * PP_TILE + r * 1024), 16,
-          doff[r], 0, 0, CAUSAL ? PP_KV_CP_CAUSAL : PP_KV_CP_FULL);
+          doff[r], 0, 0, PP_KV_CP);
   };
 
   // ---- operand read addresses (LDS byte addresses of the current K / V stage; row-block offsets
