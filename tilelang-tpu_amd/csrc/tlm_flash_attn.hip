@@ -506,7 +506,11 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, wl = wave & 3;
-  const int blk = grp == 0 ? 2 * wl : 7 - 2 * wl;  // waves w and w + 4 share a SIMD
+  // query block of the wave (waves w and w + 4 share a SIMD). Causal: the pairs (0, 7), (2, 5),
+  // (4, 3), (6, 1) give every SIMD the same key count. Otherwise wave w takes block w, so a tile
+  // of at most 128 queries (split inference, ragged tails) has all its working waves in group 0:
+  // a step is then one MFMA phase and one softmax phase instead of two of each.
+  const int blk = CAUSAL ? (grp == 0 ? 2 * wl : 7 - 2 * wl) : wave;
 
   // workgroup -> (batch, head, slot). Workgroup ids go round-robin over the 8 XCDs; each XCD
   // takes whole K/V heads: all query tiles of the G = H / Hkv query heads that read one K/V head
