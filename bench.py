@@ -690,7 +690,7 @@ def bench_mla(args, dev, flush, cpu):
     pmc_launches(args, fns, "mla")
     ms, how = time_steps(fns, args.steps, args.warmup)
     mean_ms, med_ms = time_launches(fns, 100, flush)
-    # BASELINE.md bounds this config by HBM (576 B per cached token, Q, O, table, lengths), so
+    # The config is bounded by HBM (576 B per cached token, Q, O, table, lengths), so
     # roofline.frac is against 8 TB/s. The matrix-core rate is reported beside it: algorithmic
     # flops over the bf16-equivalent peak, and the executed e4m3 flops (Q^T runs as two e4m3
     # terms, P^T as one) over the fp8 peak. Durations are whole tlm_mla_decode calls (prep +
