@@ -489,10 +489,34 @@ def test_symbolic_extents_specialise_per_call():
     assert plan.attrs["consts"] == [0.0] and not plan.attrs["inputs"]
     # the same binding is recognised once
     assert k.adapter._plan_for({"m": 300, "n": 520}) is plan
-    # the elementwise add over symbolic m, n: shapes must agree under the binding
+    # the elementwise add over symbolic m, n: shapes must agree under the binding (checked
+    # before any device work, so this runs without a GPU)
     add = tilelang.compile(programs.add_symbolic(64, 64), out_idx=-1)
     with pytest.raises(ValueError, match="mismatch"):
-        add.adapter._check(1, torch.zeros(4, 6), {"m": 4, "n": 5})
+        add(torch.zeros(4, 5), torch.zeros(4, 6))
+    with pytest.raises(ValueError, match="mismatch"):
+        add(torch.zeros(4, 5), torch.zeros(3, 5))
+
+
+def test_symbolic_extent_checked_after_every_binding():
+    """An extent that depends on a variable bound by a later argument (2 * m in the first
+    parameter, m bound by the second) is still compared with the argument's size."""
+    from tilelang.language import ir
+    add = tilelang.compile(programs.add_symbolic(64, 64), out_idx=-1)
+    ad = add.adapter
+    m = next(s for s in ad.params[1].shape if isinstance(s, ir.Var) and s.name == "m")
+    env = {}
+    ad._check(1, torch.zeros(4, 5), env)
+    assert env == {"m": 4, "n": 5}
+    ad.params[0].shape = [m * 2, ad.params[0].shape[1]]
+    try:
+        ad._check_bound(0, torch.zeros(8, 5), env)
+        with pytest.raises(ValueError, match="mismatch"):
+            ad._check_bound(0, torch.zeros(4, 5), env)
+        with pytest.raises(ValueError, match="not bound"):
+            ad._check_bound(0, torch.zeros(8, 5), {"n": 5})
+    finally:
+        ad.params[0].shape = list(ad.params[1].shape)
 
 
 def ir_const(e):

@@ -184,16 +184,25 @@ class MI355XKernelAdapter(BaseKernelAdapter):
                                  f"{list(p.shape)}, got {list(t.shape)}")
             return
         # symbolic extents (T.symbolic): a plain variable is bound by the first argument that
-        # carries it; every other extent must equal its value under the binding
+        # carries it; _check_bound then compares every extent with its value under the binding
         if t.dim() != len(p.shape):
             raise ValueError(f"Dimension mismatch for parameter {i}: expected {len(p.shape)} "
                              f"dims, got {t.dim()}")
-        for d, (s, n) in enumerate(zip(p.shape, t.shape)):
+        for s, n in zip(p.shape, t.shape):
             if isinstance(s, ir.Var) and s.name not in env:
                 env[s.name] = int(n)
+
+    def _check_bound(self, i, t, env):
+        """Every extent of a symbolic-shape parameter equals its value under the binding that
+        all arguments made (so an extent such as 2 * m is checked even when m is bound by a
+        later argument)."""
+        p = self.params[i]
         for d, (s, n) in enumerate(zip(p.shape, t.shape)):
             v = _eval_extent(s, env)
-            if v is not None and v != int(n):
+            if v is None:
+                raise ValueError(f"extent {s!r} of parameter {i} dim {d} is not bound by any "
+                                 f"input tensor")
+            if v != int(n):
                 raise ValueError(f"Shape mismatch for parameter {i} dim {d}: expected {s!r} = "
                                  f"{v} under {env}, got {int(n)}")
 
@@ -231,6 +240,10 @@ class MI355XKernelAdapter(BaseKernelAdapter):
             for i, t in enumerate(full):
                 if t is not None:
                     self._check(i, t, env)
+            if self.dynamic:
+                for i, t in enumerate(full):
+                    if isinstance(t, torch.Tensor) and self.params[i].is_dynamic():
+                        self._check_bound(i, t, env)
             plan = self._plan_for(env)
             ins = [t for t in full if isinstance(t, torch.Tensor)]
             if not torch.cuda.is_available():
