@@ -104,3 +104,33 @@ def test_partials_split_and_part_boundaries(dtype):
     torch_assert_close(part.cpu().float(), p_ref, atol=tol, rtol=tol)
     torch_assert_close(out.cpu().float(), comb, atol=tol, rtol=tol)
     torch_assert_close(out.cpu().float(), ref.mha_inference_ref(q, kk, v), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_grouped_kv_heads_equal_repeated_heads(D):
+    """The C ABI's split-KV call with grouped K/V heads (query head h reads K/V head
+    h // (H / H_kv), example_gqa_fwd_bshd.py:92-100) equals the call on K/V repeated per group,
+    bit for bit: glse, Output_partial and Output (D 128 on the tiled kernel, D 64 on the
+    per-query kernel)."""
+    from tilelang.jit.adapter.mi355x import ops
+    B, H, Hkv, Sq, Skv, ns = 2, 8, 2, 130, 2048, 4
+    g = torch.Generator().manual_seed(113 + D)
+    q = torch.randn(B, Sq, H, D, generator=g).half().to(DEV)
+    kk = torch.randn(B, Skv, Hkv, D, generator=g).half().to(DEV)
+    v = torch.randn(B, Skv, Hkv, D, generator=g).half().to(DEV)
+    rep = lambda t: t.repeat_interleave(H // Hkv, dim=2).contiguous()
+    outs = []
+    for k_, v_ in ((kk, v), (rep(kk), rep(v))):
+        glse = torch.full((B, H, ns, Sq), float("nan"), dtype=torch.half, device=DEV)
+        part = torch.full((B, Sq, H, ns, D), float("nan"), dtype=torch.half, device=DEV)
+        out = torch.full((B, Sq, H, D), float("nan"), dtype=torch.half, device=DEV)
+        ws = torch.empty(ops.flash_attn_splitkv_workspace_bytes(B, Sq, Skv, H, D, ns),
+                         dtype=torch.uint8, device=DEV)
+        ops.flash_attn_splitkv_fwd(q, k_, v_, glse, part, out, ns, D ** -0.5, ws)
+        outs.append((glse.cpu(), part.cpu(), out.cpu()))
+    for a, b in zip(*outs):
+        assert not a.isnan().any()
+        assert torch.equal(a, b)
+    torch_assert_close(outs[0][2].float(),
+                       ref.mha_inference_ref(q.cpu(), rep(kk).cpu(), rep(v).cpu()),
+                       atol=1e-2, rtol=1e-2)
