@@ -60,6 +60,64 @@ def test_gemm_trans_b_and_out_dtypes(M, N, K, out):
     torch_assert_close(c.cpu(), exp, atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 100, 96), (16, 1000, 520), (3, 4104, 4096)])
+def test_gemm_skinny_nonfinite_column_stays_in_its_column(M, N, K):
+    """The skinny kernel reads whole 64-column strips of B; in the last, ragged strip the columns
+    past N hold the next row's leading values. A NaN / inf column 0 of B must reach column 0 of C
+    only: every other column matches the oracle."""
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.rand(M, K, generator=g) * 2 - 1).half()
+    b = (torch.rand(K, N, generator=g) * 2 - 1).half()
+    b[:, 0] = float("nan")
+    b[1::2, 0] = float("inf")
+    c = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    ops.gemm(a.to(DEV), b.to(DEV), c)
+    c = c.cpu()
+    assert not torch.isfinite(c[:, 0]).any()
+    torch_assert_close(c[:, 1:], ref.matmul_ref(a, b)[:, 1:], atol=1e-2, rtol=1e-2)
+
+
+def test_gemm_skinny_split_repeatable():
+    """M <= 16 with row-major B splits K over several workgroups per column strip; the partial
+    tiles are summed in split order by whichever workgroup arrives last, and the arrival counters
+    are left at zero: reruns are bitwise equal, also after calls of other shapes in between."""
+    g = torch.Generator().manual_seed(21)
+    a = (torch.rand(16, 4096, generator=g) * 2 - 1).half().to(DEV)
+    b = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(DEV)
+    c0 = torch.empty(16, 4096, dtype=torch.float16, device=DEV)
+    ops.gemm(a, b, c0)
+    torch_assert_close(c0.cpu(), ref.matmul_ref(a.cpu(), b.cpu()), atol=1e-2, rtol=1e-2)
+    for m, n, k in [(3, 1000, 520), (16, 512, 4096), (16, 4096, 4096)]:
+        x = torch.randn(m, k, device=DEV).half()
+        y = torch.randn(k, n, device=DEV).half()
+        ops.gemm(x, y, torch.empty(m, n, dtype=torch.float16, device=DEV))
+        c = torch.empty_like(c0)
+        ops.gemm(a, b, c)
+        assert torch.equal(c, c0)
+
+
+def test_gemm_skinny_concurrent_streams():
+    """Each stream owns one workspace slot of the split skinny kernel (4 per device); further
+    streams take the unsplit kernel. Six streams run skinny GEMMs at the same time, twice over,
+    and every result matches the oracle."""
+    g = torch.Generator().manual_seed(22)
+    shapes = [(16, 4096, 4096), (8, 6144, 2048), (16, 2048, 8192), (1, 4096, 4096),
+              (5, 3000, 1000), (16, 4096, 4096)]
+    ins = [((torch.rand(m, k, generator=g) * 2 - 1).half(),
+            (torch.rand(k, n, generator=g) * 2 - 1).half()) for m, n, k in shapes]
+    dev_ins = [(x.to(DEV), y.to(DEV)) for x, y in ins]
+    outs = [torch.empty(m, n, dtype=torch.float16, device=DEV) for m, n, _ in shapes]
+    streams = [torch.cuda.Stream() for _ in shapes]
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for (x, y), c, st in zip(dev_ins, outs, streams):
+            with torch.cuda.stream(st):
+                ops.gemm(x, y, c)
+    torch.cuda.synchronize()
+    for (x, y), c in zip(ins, outs):
+        torch_assert_close(c.cpu(), ref.matmul_ref(x, y), atol=1e-2, rtol=1e-2)
+
+
 def test_gemm_generic_path_odd_k():
     """K not a multiple of 8 takes the scalar fallback kernel."""
     g = torch.Generator().manual_seed(14)

@@ -1,5 +1,5 @@
 """GPU parity over seeded random shapes for the tiled MFMA kernels (16x16 operand layouts, LDS
-swizzles, edge masking): GEMM (both B layouts, fp16 / bf16, ragged M, N, K), FP8 GEMM and
+swizzles, edge masking): GEMM (both B layouts, fp16 / bf16, ragged M, N, K, skinny M <= 16), FP8 GEMM and
 FlashAttention (causal or not, grouped K/V heads, head dim 64 and 128, ragged S), and the other
 attention layouts over random shapes and head dims 8-256: head-major with independent query and
 key lengths, variable length, split-KV inference with its partials. Each case prints its shape
@@ -43,6 +43,24 @@ def test_gemm_random(M, N, K, trans_b, dt):
     ops.gemm(a.to(DEV), b.to(DEV), c, trans_b=trans_b)
     torch_assert_close(c.cpu().float(), ref.matmul_ref(a, b, torch.float32, trans_b),
                        atol=1e-2, rtol=1e-2)
+
+
+def _skinny_cases(n, seed):
+    r = random.Random(seed)
+    out = []
+    for _ in range(n):
+        M = r.randint(1, 16)
+        N = 8 * r.randint(1, 300)
+        K = r.choice([8 * r.randint(1, 64), 32 * r.randint(1, 128), 8 * r.randint(500, 700)])
+        out.append((M, N, K, r.random() < 0.25, r.choice([torch.float16, torch.bfloat16])))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,trans_b,dt", _skinny_cases(16, seed=77))
+def test_gemm_skinny_random(M, N, K, trans_b, dt):
+    """M <= 16 takes the skinny kernels: A staged in LDS for row-major B and K <= 4096, A read
+    per block otherwise (K past 4096, B^T); ragged N and K not a multiple of 32 included."""
+    test_gemm_random(M, N, K, trans_b, dt)
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 520, 640), (256, 256, 128), (1000, 264, 2048),

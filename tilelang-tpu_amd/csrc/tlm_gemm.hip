@@ -20,9 +20,12 @@
 //   * workgroup -> tile order is XCD-aware: consecutive workgroup ids land on different XCDs
 //     (round-robin dispatch), so ids are regrouped to give each XCD a compact block of tiles
 //     that shares A row-panels and B column-panels in that XCD's L2.
-// Skinny kernel (M <= 16): see gemm_skinny below.
+// Skinny kernels (M <= 16): gemm_skinny_split for row-major B, gemm_skinny for B^T and the shapes
+// or streams the split kernel does not take; see below.
 #include "tlm_common.h"
 
+#include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -405,7 +408,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
 }
 
 // ------------------------------------------------------------------------------------------------
-// Skinny GEMM (M <= 16): the whole of A fits one MFMA row block, so the kernel streams B.
+// Skinny GEMM (M <= 16) for B^T and the row-major cases gemm_skinny_split does not take: the
+// whole of A fits one MFMA row block, so the kernel streams B.
 // Workgroup = 8 waves on a 64-column strip of C; the waves split K into interleaved 32-row
 // blocks, each block is one v_mfma_f32_16x16x32 per 16 columns. A operand (row m = lane%16,
 // k = 8*(lane/16)..+7) is a direct 16-byte global load. Row-major B goes through a wave-private
@@ -506,6 +510,202 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Split skinny GEMM (M <= 16, row-major B): the preferred form of the M <= 16 stream. B is read
+// in 256-byte row segments (a 128-column strip per workgroup), and the k range is split over
+// `nsplit` workgroups per strip so that about one workgroup runs per CU. Measured on the bare
+// read pattern of a 4096 x 14336 fp16 B: 128-byte segments over all of K stream at 5.7 TB/s,
+// 256-byte segments over half of K at 6.3 TB/s, and a workgroup per CU is needed (one CU alone
+// streams about 38 GB/s). Within a workgroup the 8 waves take interleaved 16-row blocks (16 x
+// 128 halves = 4 KB, one block in flight per wave), each one v_mfma_f32_16x16x16 per 16 columns.
+// The workgroup's part of A (16 rows x at most 2048 k) is staged in LDS once, after the first B
+// block is requested: per-block A fragments read from the cache were measured to cost 2.5 us of
+// 24 at 16 x 14336 x 4096.
+//
+// The nsplit partial 16 x 128 tiles of a strip meet in a workspace: every workgroup stores its
+// tile and counts itself in with an atomic on the strip's arrival counter; the last to arrive
+// adds the tiles in split order (the result does not depend on arrival order), writes C and
+// resets the counter to zero. The workspace is a file-scope device array with SS_SLOTS slots;
+// each stream that runs this kernel on a device owns one slot, so calls that overlap are on
+// different streams and never share a slot. A further stream takes gemm_skinny.
+constexpr int SS_WAVES = 8;
+constexpr int SS_NT = 128;
+constexpr int SS_BK = 16;
+constexpr int SS_AMAX_K = 2048;  // k range of one workgroup: its A is 64 KB of LDS
+constexpr int SS_MAX_SPLIT = 16;
+constexpr int SS_SLOTS = 4;
+constexpr int SS_MAX_WG = 512;   // workgroups of one call that publish a partial tile
+constexpr int SS_PART = 16 * SS_NT;
+
+template <bool BF16>
+struct mfma16k16_t;
+template <>
+struct mfma16k16_t<false> {
+  static TLM_DEV f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct mfma16k16_t<true> {
+  static TLM_DEV f32x4 mma(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+};
+
+template <bool BF16, int OUT>
+__global__ __launch_bounds__(64 * SS_WAVES) void gemm_skinny_split(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, int M,
+    int N, int K, int nsplit, float* __restrict__ part, unsigned* __restrict__ arrivals) {
+  using MT = mfma16k16_t<BF16>;
+  constexpr int AL = SS_AMAX_K * 16 * 2;
+  constexpr int WB = SS_BK * SS_NT * 2;
+  constexpr int LDS = AL + SS_WAVES * WB;
+  static_assert(LDS >= SS_WAVES * 16 * (SS_NT + 1) * 4 + 4, "reduction and flag alias the LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const int nstrips = (N + SS_NT - 1) / SS_NT;
+  const int strip = blockIdx.x % nstrips, split = blockIdx.x / nstrips;
+  const int n0 = strip * SS_NT;
+  const int KB = (K + SS_BK - 1) / SS_BK;
+  const int kb_lo = (int)((int64_t)split * KB / nsplit);
+  const int nbk = (int)((int64_t)(split + 1) * KB / nsplit) - kb_lo;  // <= SS_AMAX_K / SS_BK
+
+  // B rows past K read as zero (past the descriptor's end), and so does a block index of KB,
+  // which a wave with no block left loads; the columns past N of a ragged last strip hold
+  // whatever follows and only reach output columns that are not stored.
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)B, (short)0, (int)((int64_t)K * N * 2), RSRC_WORD3);
+  const int boff = g * N * 2 + (n0 + 8 * j) * 2;  // row 4p + lane/16, 16-byte chunk lane%16
+  auto load = [&](u32x4 (&rb)[4], int kb) {
+    const int k0 = kb * SS_BK;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      rb[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rsb, boff + (k0 + 4 * p) * N * 2, 0, CP_NT));
+  };
+  // the wave's first two blocks are requested before A, so that B keeps streaming while A
+  // is staged; after that one block is in flight per wave
+  u32x4 rb0[4], rn[4];
+  load(rb0, wave < nbk ? kb_lo + wave : KB);
+  load(rn, wave + SS_WAVES < nbk ? kb_lo + wave + SS_WAVES : KB);
+
+  // A columns 16 kb_lo .. as 16 rows of SS_AMAX_K halves, 16-byte chunk c of row m stored at
+  // c ^ m: row-contiguous 1 KB loads and LDS writes, and the fragment reads of 16 rows x one
+  // chunk are free of bank conflicts. The fragment of local block b (row lane%16, k 4g .. + 3)
+  // is in chunk 2b + g/2 at byte 8 (g%2). Rows past M and k past K read as zero.
+  constexpr int AROW = SS_AMAX_K * 2;
+  {
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)A, (short)0, (int)((int64_t)M * K * 2), RSRC_WORD3);
+    constexpr int NA = SS_AMAX_K * 2 / (64 * SS_WAVES);
+    const int kc0 = 2 * kb_lo, ncw = 2 * nbk, kc_end = K / 8;
+    u32x4 t[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int q = i * 64 * SS_WAVES + tid, m = q / (AROW / 16), c = q % (AROW / 16);
+      const int off = (m < M && c < ncw && kc0 + c < kc_end) ? (m * K + 8 * (kc0 + c)) * 2
+                                                              : 0x7ffffff0;
+      t[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int q = i * 64 * SS_WAVES + tid, m = q / (AROW / 16), c = q % (AROW / 16);
+      if (c < ncw) *(u32x4*)(smem + AROW * m + 16 * (c ^ m)) = t[i];
+    }
+  }
+  __syncthreads();
+
+  // B staging of the wave: 16 rows of 256 bytes, 16-byte chunk c of row r stored at
+  // c ^ 2 (r % 8), so that the transposed reads (4 rows x 32 bytes per 16 lanes) are free of
+  // bank conflicts. Tile t: 16-lane group g reads k rows 4g + j/4, columns 16t + 4 (j%4) ..
+  uint8_t* const my = smem + AL + wave * WB;
+  int wr[4], rd[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int r = 4 * p + g;
+    wr[p] = 256 * r + 16 * (j ^ (2 * (r & 7)));
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int r = 4 * g + (j >> 2), c = 2 * t + ((j & 3) >> 1);
+    rd[t] = 256 * r + 16 * (c ^ (2 * (r & 7))) + 8 * (j & 1);
+  }
+  const uint8_t* const a_row = smem + AROW * j + 8 * (g & 1);
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{};
+  auto process = [&](const u32x4 (&cb)[4], int b) {
+    const u32x2 av = *(const u32x2*)(a_row + 16 * ((2 * b + (g >> 1)) ^ j));
+#pragma unroll
+    for (int p = 0; p < 4; ++p) *(u32x4*)(my + wr[p]) = cb[p];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      acc[t] = MT::mma(av, __builtin_bit_cast(u32x2, lds_read_tr16((const uint16_t*)(my + rd[t]))),
+                       acc[t]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  if (wave < nbk) process(rb0, wave);
+  for (int b = wave + SS_WAVES; b < nbk; b += SS_WAVES) {
+    u32x4 cb[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) cb[p] = rn[p];
+    load(rn, b + SS_WAVES < nbk ? kb_lo + b + SS_WAVES : KB);
+    process(cb, b);
+  }
+  __syncthreads();  // every wave is done with A and its staging before the reduction reuses them
+
+  // lane holds column 16t + lane%16, rows 4 (lane/16) + i
+  float(*red)[16][SS_NT + 1] = (float(*)[16][SS_NT + 1])smem;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][4 * g + i][16 * t + j] = acc[t][i];
+  __syncthreads();
+  // thread: row tid/32, columns 4 (tid%32) .. + 3 of the strip
+  const int orow = tid >> 5, ocol = 4 * (tid & 31);
+  f32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < SS_WAVES; ++w) s += red[w][orow][ocol + i];
+    v[i] = s;
+  }
+  if (nsplit > 1) {
+    // The tiles go to memory and come back with sc0 sc1 (write-through stores, loads that miss
+    // in every cache), so the exchange needs no cache write-back or invalidation: a wait for the
+    // stores before the arrival, and the loads issued after it.
+    st_cp<CP_SC01>(part, (blockIdx.x * SS_PART + 4 * tid) * 4, __builtin_bit_cast(u32x4, v));
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): the tile has been written
+    unsigned* const last = (unsigned*)(smem + LDS - 4);
+    __syncthreads();
+    if (tid == 0) *last = atomicAdd(&arrivals[strip], 1u) == (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!*last) return;
+    f32x4 tot = {};
+    for (int sp = 0; sp < nsplit; ++sp)
+      tot += sp == split ? v
+                         : __builtin_bit_cast(f32x4, ld_cp<CP_SC01>(
+                                                         part, ((sp * nstrips + strip) * SS_PART +
+                                                                4 * tid) * 4));
+    v = tot;
+    if (tid == 0) atomicExch(&arrivals[strip], 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (orow < M && n0 + ocol + i < N) store_out<OUT>(C, (int64_t)orow * N + n0 + ocol + i, v[i]);
+}
+
 // Generic fallback for shapes the vector kernels cannot take (K or N not a multiple of 8,
 // unaligned pointers): one thread per output, fp32 accumulation in k order.
 template <bool BF16, bool TRANS_B, int OUT>
@@ -525,11 +725,89 @@ __global__ __launch_bounds__(256) void gemm_generic(const uint16_t* __restrict__
   store_out<OUT>(C, idx, s);
 }
 
+}  // namespace
+
+// Workspace of gemm_skinny_split, one instance per GPU (a device that loads this code object
+// holds its own copy until the process ends; 16 MB): SS_SLOTS slots of partial tiles and arrival
+// counters. The counters start at zero and every call leaves them at zero. In host code the names
+// only identify the symbols; the device addresses come from hipGetSymbolAddress.
+static __device__ __align__(256) float ss_partials[SS_SLOTS][SS_MAX_WG][SS_PART];
+static __device__ __align__(256) unsigned ss_arrivals[SS_SLOTS][SS_MAX_WG];
+
+namespace {
+
+constexpr int kSsDevices = 64;
+struct SsDevice {
+  std::once_flag once;
+  hipError_t err = hipSuccess;
+  float* part = nullptr;
+  unsigned* arrivals = nullptr;
+  bool used[SS_SLOTS] = {};
+  hipStream_t owner[SS_SLOTS] = {};
+};
+SsDevice g_ss[kSsDevices];
+std::mutex g_ss_mu;
+
+// The workspace slot of stream `s` on the current device: the one it owns, else a free one that
+// it then owns. False when every slot is owned by another stream (or the lookup failed), and the
+// caller takes gemm_skinny.
+bool ss_slot(hipStream_t s, float** part, unsigned** arrivals) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSsDevices) return false;
+  SsDevice& d = g_ss[dev];
+  std::call_once(d.once, [&d]() {
+    void* p = nullptr;
+    void* q = nullptr;
+    d.err = hipGetSymbolAddress(&p, HIP_SYMBOL(ss_partials));
+    if (d.err == hipSuccess) d.err = hipGetSymbolAddress(&q, HIP_SYMBOL(ss_arrivals));
+    d.part = (float*)p;
+    d.arrivals = (unsigned*)q;
+  });
+  if (d.err != hipSuccess) return false;
+  std::lock_guard<std::mutex> lk(g_ss_mu);
+  int slot = -1;
+  for (int i = 0; i < SS_SLOTS && slot < 0; ++i)
+    if (d.used[i] && d.owner[i] == s) slot = i;
+  for (int i = 0; i < SS_SLOTS && slot < 0; ++i)
+    if (!d.used[i]) {
+      d.used[i] = true;
+      d.owner[i] = s;
+      slot = i;
+    }
+  if (slot < 0) return false;
+  *part = d.part + (size_t)slot * SS_MAX_WG * SS_PART;
+  *arrivals = d.arrivals + (size_t)slot * SS_MAX_WG;
+  return true;
+}
+
+// Split count of gemm_skinny_split for N x K (0: the shape does not fit it): about one
+// workgroup per CU without a second round, at least 16 blocks (256 k) and at most SS_AMAX_K of
+// k per workgroup.
+int ss_nsplit(int N, int K) {
+  const int nstrips = (N + SS_NT - 1) / SS_NT;
+  const int KB = (K + SS_BK - 1) / SS_BK;
+  int ns = std::max(1, std::min(SS_MAX_SPLIT, 256 / nstrips));
+  ns = std::min(ns, std::max(1, KB / 16));
+  ns = std::max(ns, (KB + SS_AMAX_K / SS_BK - 1) / (SS_AMAX_K / SS_BK));
+  if (ns > SS_MAX_SPLIT || (ns > 1 && (int64_t)nstrips * ns > SS_MAX_WG)) return 0;
+  return ns;
+}
+
 template <bool BF16, bool TRANS_B, int OUT>
 int launch(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t s) {
   const bool vec = tlm_aligned(A, 16) && tlm_aligned(B, 16) && K % 8 == 0 &&
                    (TRANS_B || N % 8 == 0);
-  if (vec && M <= 16) {
+  int ns = 0;
+  float* part = nullptr;
+  unsigned* arrivals = nullptr;
+  if (vec && M <= 16 && !TRANS_B && K > 0 && (int64_t)(K + 2 * SS_BK) * N * 2 < 0x7ffffff0)
+    ns = ss_nsplit(N, K);
+  if (ns > 1 && !ss_slot(s, &part, &arrivals)) ns = 0;
+  if (ns > 0) {
+    const int nstrips = (N + SS_NT - 1) / SS_NT;
+    gemm_skinny_split<BF16, OUT><<<(unsigned)(nstrips * ns), 64 * SS_WAVES, 0, s>>>(
+        (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, ns, part, arrivals);
+  } else if (vec && M <= 16) {
     gemm_skinny<BF16, TRANS_B, OUT><<<(unsigned)((N + SK_NT - 1) / SK_NT), 64 * SK_WAVES, 0, s>>>(
         (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
   } else if (vec && (int64_t)BM * K * 2 < 0x7ffffff0 &&
