@@ -106,7 +106,11 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * trans_b == 1: B is [N,K] row-major (ppl_gemm transpose_B=True).
  * in_dtype: F16 | BF16; out_dtype: F16 | BF16 | F32. The fp32 program
  * (tpu_demo/matmul/tpu_test_matmul_fp32.py:9-31) copies its fp32 A/B tiles to fp16 before
- * ppl_gemm: tlm_cast to F16, then this with out_dtype F32. */
+ * ppl_gemm: tlm_cast to F16, then this with out_dtype F32.
+ * M <= 16 with trans_b == 0 splits K over several workgroups whose partial tiles meet in a
+ * library-owned device workspace (16 MB per GPU, 4 slots): each stream owns one slot, so calls
+ * on one stream are ordered and calls that overlap use different slots; further streams take an
+ * unsplit kernel. The result does not depend on the split's timing (bitwise reproducible). */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
              int out_dtype, int trans_b, void* stream);
 
