@@ -563,7 +563,7 @@ __global__ __launch_bounds__(64 * SS_WAVES) void gemm_skinny_split(
   constexpr int AL = SS_AMAX_K * 16 * 2;
   constexpr int WB = SS_BK * SS_NT * 2;
   constexpr int LDS = AL + SS_WAVES * WB;
-  static_assert(LDS >= SS_WAVES * 16 * (SS_NT + 1) * 4 + 4, "reduction and flag alias the LDS");
+  static_assert(LDS >= SS_WAVES * SS_NT * 16 * 4 + 4, "reduction and flag alias the LDS");
   __shared__ __attribute__((aligned(16))) uint8_t smem[LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, j = lane & 15;
@@ -664,23 +664,17 @@ __global__ __launch_bounds__(64 * SS_WAVES) void gemm_skinny_split(
   }
   __syncthreads();  // every wave is done with A and its staging before the reduction reuses them
 
-  // lane holds column 16t + lane%16, rows 4 (lane/16) + i
-  float(*red)[16][SS_NT + 1] = (float(*)[16][SS_NT + 1])smem;
+  // The 8 waves' tiles are summed through LDS as [wave][column][16 rows]: a lane's accumulator
+  // (column 16t + lane%16, rows 4 (lane/16) .. + 3) is one 16-byte write, and a thread's share
+  // of the sum (column tid/4, rows 4 (tid%4) .. + 3) one 16-byte read per wave.
+  f32x4* const red = (f32x4*)smem;
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][4 * g + i][16 * t + j] = acc[t][i];
+  for (int t = 0; t < 8; ++t) red[(wave * SS_NT + 16 * t + j) * 4 + g] = acc[t];
   __syncthreads();
-  // thread: row tid/32, columns 4 (tid%32) .. + 3 of the strip
-  const int orow = tid >> 5, ocol = 4 * (tid & 31);
-  f32x4 v;
+  const int ocol = tid >> 2, orow = 4 * (tid & 3);
+  f32x4 v = red[tid];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < SS_WAVES; ++w) s += red[w][orow][ocol + i];
-    v[i] = s;
-  }
+  for (int w = 1; w < SS_WAVES; ++w) v += red[w * SS_NT * 4 + tid];
   if (nsplit > 1) {
     // The tiles go to memory and come back with sc0 sc1 (write-through stores, loads that miss
     // in every cache), so the exchange needs no cache write-back or invalidation: a wait for the
@@ -703,7 +697,7 @@ __global__ __launch_bounds__(64 * SS_WAVES) void gemm_skinny_split(
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (orow < M && n0 + ocol + i < N) store_out<OUT>(C, (int64_t)orow * N + n0 + ocol + i, v[i]);
+    if (orow + i < M && n0 + ocol < N) store_out<OUT>(C, (int64_t)(orow + i) * N + n0 + ocol, v[i]);
 }
 
 // Generic fallback for shapes the vector kernels cannot take (K or N not a multiple of 8,
