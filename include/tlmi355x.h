@@ -110,7 +110,9 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * M <= 16 with trans_b == 0 splits K over several workgroups whose partial tiles meet in a
  * library-owned device workspace (16 MB per GPU, 4 slots): each stream owns one slot, so calls
  * on one stream are ordered and calls that overlap use different slots; further streams take an
- * unsplit kernel. The result does not depend on the split's timing (bitwise reproducible). */
+ * unsplit kernel. A HIP graph keeps the slot of the stream it was captured on, so its replays
+ * must not overlap each other or other work of that stream. The result does not depend on the
+ * split's timing (bitwise reproducible). */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
              int out_dtype, int trans_b, void* stream);
 

@@ -527,7 +527,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
 // adds the tiles in split order (the result does not depend on arrival order), writes C and
 // resets the counter to zero. The workspace is a file-scope device array with SS_SLOTS slots;
 // each stream that runs this kernel on a device owns one slot, so calls that overlap are on
-// different streams and never share a slot. A further stream takes gemm_skinny.
+// different streams and never share a slot. A further stream takes gemm_skinny. A HIP graph
+// keeps the slot of the stream it was captured on.
 constexpr int SS_WAVES = 8;
 constexpr int SS_NT = 128;
 constexpr int SS_BK = 16;
