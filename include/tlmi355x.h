@@ -112,7 +112,8 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * on one stream are ordered and calls that overlap use different slots; further streams take an
  * unsplit kernel. A HIP graph keeps the slot of the stream it was captured on, so its replays
  * must not overlap each other or other work of that stream. The result does not depend on the
- * split's timing (bitwise reproducible). */
+ * split's timing: a stream's calls are bitwise reproducible (the unsplit kernel of a stream
+ * without a slot sums in another order, so its last bits can differ from the split kernel's). */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
              int out_dtype, int trans_b, void* stream);
 

@@ -118,6 +118,38 @@ def test_gemm_skinny_concurrent_streams():
         torch_assert_close(c.cpu(), ref.matmul_ref(x, y), atol=1e-2, rtol=1e-2)
 
 
+def test_gemm_skinny_split_graph_replays():
+    """A skinny GEMM captured in a HIP graph (no memset node: the split kernel's arrival counters
+    are reset by the kernel) gives, on every replay, the bits of the same call run eagerly on
+    the capture stream, with eager skinny GEMMs of other shapes run between the replays. (The
+    capture stream owns a workspace slot, or takes the unsplit kernel when earlier streams of
+    the process hold all slots; the eager call on that stream takes the same path.)"""
+    g = torch.Generator().manual_seed(23)
+    a_h = (torch.rand(16, 4096, generator=g) * 2 - 1).half()
+    b_h = (torch.rand(4096, 6144, generator=g) * 2 - 1).half()
+    a, b = a_h.to(DEV), b_h.to(DEV)
+    c = torch.zeros(16, 6144, dtype=torch.float16, device=DEV)
+    ref_c = torch.empty_like(c)
+    graph, side = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.gemm(a, b, ref_c)
+        with torch.cuda.graph(graph, stream=side):
+            ops.gemm(a, b, c)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    torch_assert_close(ref_c.cpu(), ref.matmul_ref(a_h, b_h), atol=1e-2, rtol=1e-2)
+    x = torch.randn(8, 2048, device=DEV).half()
+    y = torch.randn(2048, 3000, device=DEV).half()
+    for _ in range(3):
+        c.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, ref_c)
+        ops.gemm(x, y, torch.empty(8, 3000, dtype=torch.float16, device=DEV))
+        torch.cuda.synchronize()
+
+
 def test_gemm_generic_path_odd_k():
     """K not a multiple of 8 takes the scalar fallback kernel."""
     g = torch.Generator().manual_seed(14)
