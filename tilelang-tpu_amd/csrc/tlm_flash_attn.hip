@@ -1123,7 +1123,11 @@ int launch_generic(const void* q, const void* k, const void* v, void* o, int B, 
 // the merge of those stored (rounded) values, as the program's combine reads them back:
 // O = sum_s O_s 2^(lse_s - lse), lse = log2 sum_s 2^(lse_s) (taken here as a running merge).
 constexpr int FA_MAX_PARTS = 8;  // internal parts per program split
-template <bool BF16>
+// RA > 0: every part of every split (r == RA, ns RA <= FA_ALL_PARTS) is requested before any is
+// used, so a thread waits for one memory latency instead of one per split; RA == 0: any r, one
+// split's parts at a time.
+constexpr int FA_ALL_PARTS = 16;
+template <bool BF16, int RA>
 __global__ __launch_bounds__(256) void fa_split_combine(const float* __restrict__ part,
                                                         const float* __restrict__ lse,
                                                         uint16_t* __restrict__ glse,
@@ -1143,28 +1147,14 @@ __global__ __launch_bounds__(256) void fa_split_combine(const float* __restrict_
   const int nsi = ns * r;
   float M = -INFINITY, L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < ns; ++sp) {
-    // every part of the split requested before any is used
-    float lv[FA_MAX_PARTS];
-    f32x4 pv[FA_MAX_PARTS];
-#pragma unroll
-    for (int j = 0; j < FA_MAX_PARTS; ++j) {
-      lv[j] = -INFINITY;
-      pv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (j < r) {
-        const int64_t pi = row * nsi + sp * r + j;
-        lv[j] = lse[pi];
-        pv[j] = *(const f32x4*)(part + pi * D + 4 * c);
-      }
-    }
+  // split sp from its parts (lse lv, output pv; absent parts have lse -inf and weigh 0)
+  auto merge_split = [&](int sp, const float* lv, const f32x4* pv, int np) {
     float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < FA_MAX_PARTS; ++j) m = fmaxf(m, lv[j]);
+    for (int j = 0; j < np; ++j) m = fmaxf(m, lv[j]);
     float l = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
     if (m != -INFINITY) {
-#pragma unroll
-      for (int j = 0; j < FA_MAX_PARTS; ++j) {
+      for (int j = 0; j < np; ++j) {
         const float w = fast_exp2(lv[j] - m);  // 0 for an empty or absent part
         l += w;
         o += pv[j] * w;
@@ -1183,6 +1173,39 @@ __global__ __launch_bounds__(256) void fa_split_combine(const float* __restrict_
       L = L * a + w;
       acc = acc * a + f32x4{HH::lo(pk[0]), HH::hi(pk[0]), HH::lo(pk[1]), HH::hi(pk[1])} * w;
       M = Mn;
+    }
+  };
+  if constexpr (RA > 0) {
+    float la[FA_ALL_PARTS];
+    f32x4 pa[FA_ALL_PARTS];
+#pragma unroll
+    for (int k = 0; k < FA_ALL_PARTS; ++k) {
+      la[k] = -INFINITY;
+      pa[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (k < nsi) {
+        la[k] = lse[row * nsi + k];
+        pa[k] = *(const f32x4*)(part + (row * nsi + k) * D + 4 * c);
+      }
+    }
+#pragma unroll
+    for (int sp = 0; sp < FA_ALL_PARTS / RA; ++sp)
+      if (sp < ns) merge_split(sp, la + sp * RA, pa + sp * RA, RA);
+  } else {
+    for (int sp = 0; sp < ns; ++sp) {
+      // every part of the split requested before any is used
+      float lv[FA_MAX_PARTS];
+      f32x4 pv[FA_MAX_PARTS];
+#pragma unroll
+      for (int j = 0; j < FA_MAX_PARTS; ++j) {
+        lv[j] = -INFINITY;
+        pv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (j < r) {
+          const int64_t pi = row * nsi + sp * r + j;
+          lv[j] = lse[pi];
+          pv[j] = *(const f32x4*)(part + pi * D + 4 * c);
+        }
+      }
+      merge_split(sp, lv, pv, FA_MAX_PARTS);
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
@@ -1404,14 +1427,25 @@ extern "C" int tlm_flash_attn_splitkv_fwd(const void* q, const void* k, const vo
   if (rc != TLM_OK) return rc;
   const int64_t nthr = rows * (D / 4);
   const dim3 grid((unsigned)((nthr + 255) / 256));
-  if (bf)
-    fa_split_combine<true><<<grid, 256, 0, st>>>(part, lse, (uint16_t*)glse,
-                                                 (uint16_t*)o_partial, (uint16_t*)o, rows,
-                                                 (int)S_q, (int)H, (int)D, num_split, r);
-  else
-    fa_split_combine<false><<<grid, 256, 0, st>>>(part, lse, (uint16_t*)glse,
-                                                  (uint16_t*)o_partial, (uint16_t*)o, rows,
-                                                  (int)S_q, (int)H, (int)D, num_split, r);
+  auto combine = [&](auto kern) {
+    kern<<<grid, 256, 0, st>>>(part, lse, (uint16_t*)glse, (uint16_t*)o_partial, (uint16_t*)o,
+                               rows, (int)S_q, (int)H, (int)D, num_split, r);
+  };
+  // all parts in one round when r is 1, 2, 4 or 8 and ns r <= FA_ALL_PARTS
+  const bool all = num_split * r <= FA_ALL_PARTS && (r & (r - 1)) == 0;
+  if (bf) {
+    if (all && r == 1) combine(fa_split_combine<true, 1>);
+    else if (all && r == 2) combine(fa_split_combine<true, 2>);
+    else if (all && r == 4) combine(fa_split_combine<true, 4>);
+    else if (all && r == 8) combine(fa_split_combine<true, 8>);
+    else combine(fa_split_combine<true, 0>);
+  } else {
+    if (all && r == 1) combine(fa_split_combine<false, 1>);
+    else if (all && r == 2) combine(fa_split_combine<false, 2>);
+    else if (all && r == 4) combine(fa_split_combine<false, 4>);
+    else if (all && r == 8) combine(fa_split_combine<false, 8>);
+    else combine(fa_split_combine<false, 0>);
+  }
   TLM_LAUNCH_CHECK("tlm_flash_attn_splitkv_fwd (combine)");
   return TLM_OK;
 }
