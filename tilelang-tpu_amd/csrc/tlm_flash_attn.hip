@@ -434,7 +434,9 @@ constexpr int PP_RSRC_WORD3 = 0x00020000;         // raw buffer, 32-bit data for
 // re-read its tiles from L2. Non-temporal loads measured 4-5% slower for causal and, for full
 // attention, 1-2% faster at S 2048, neutral for head-major and grouped-query, 3-4% slower for
 // ragged batches (1,038-1,044 against 1,069-1,084 TFLOP/s), whose counted fetches rose from
-// 1.12 to 1.77 times the algorithmic bytes (grouped-query: 1.88 to 2.45).
+// 1.12 to 1.77 times the algorithmic bytes (grouped-query: 1.88 to 2.45). Split-KV parts whose
+// tiles are each read by one workgroup (one query tile, no shared K / V heads) load them
+// non-temporally: a stand-alone copy of that read pattern streamed 6.2 against 5.1 TB/s.
 constexpr int PP_KV_CP = CP_PLAIN;
 static_assert(8 * 32 * PP_OP * 2 <= PP_SMEM, "epilogue staging must fit in the rings");
 
@@ -491,7 +493,8 @@ TLM_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false>
+// NT (split parts whose K / V tiles are each read by one workgroup): non-temporal K / V loads.
+template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false, bool NT = false>
 __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__ Q,
                                                    const uint16_t* __restrict__ K,
                                                    const uint16_t* __restrict__ V,
@@ -604,7 +607,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
     for (int r = 0; r < 4; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rsrc, (__attribute__((address_space(3))) void*)(dlds + slot * PP_TILE + r * 1024), 16,
-          doff[r], 0, 0, PP_KV_CP);
+          doff[r], 0, 0, NT ? CP_NT : PP_KV_CP);
   };
 
   // ---- operand read addresses (LDS byte addresses of the current K / V stage; row-block offsets
@@ -873,7 +876,7 @@ __global__ __launch_bounds__(512, 1) void fa_fwd_pp(const uint16_t* __restrict__
   }
 }
 
-template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false>
+template <bool BF16, bool CAUSAL, bool OUT32, bool SPLIT = false, bool NT = false>
 int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S, int H, int Hkv,
               float sc, const SeqMap& sm, hipStream_t st, const FaSplit& sp = FaSplit{}) {
   const int64_t nqt = (S + PP_BQ - 1) / PP_BQ;
@@ -883,7 +886,7 @@ int launch_pp(const void* q, const void* k, const void* v, void* o, int B, int S
     tlm_set_error("tlm_flash_attn_fwd: problem too large");
     return TLM_EINVAL;
   }
-  fa_fwd_pp<BF16, CAUSAL, OUT32, SPLIT><<<(unsigned)nwg, 512, 0, st>>>(
+  fa_fwd_pp<BF16, CAUSAL, OUT32, SPLIT, NT><<<(unsigned)nwg, 512, 0, st>>>(
       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, o, B, S, H, Hkv, sc, sm, sp);
   TLM_LAUNCH_CHECK("tlm_flash_attn_fwd");
   return TLM_OK;
@@ -1409,12 +1412,18 @@ extern "C" int tlm_flash_attn_splitkv_fwd(const void* q, const void* k, const vo
   const int64_t rows = B * S_q * H;
   float* part = (float*)ws;
   float* lse = part + rows * num_split * r * D;
+  const bool once = (S_q + PP_BQ - 1) / PP_BQ == 1 && H_kv == H;  // each K / V tile read once
   const FaSplit sp{lse, num_split * r, r, per, per_i};
   const SeqMap sm{nullptr, nullptr, (int)S_q, (int)S_kv, H * D, H_kv * D, D, D};
   const float sc = (float)((double)sm_scale * 1.4426950408889634);
   hipStream_t st = (hipStream_t)stream;
   const bool bf = dtype == TLM_BF16;
-  if (D == 128)
+  if (D == 128 && once)
+    rc = bf ? launch_pp<true, false, true, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                       (int)H_kv, sc, sm, st, sp)
+            : launch_pp<false, false, true, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
+                                                        (int)H_kv, sc, sm, st, sp);
+  else if (D == 128)
     rc = bf ? launch_pp<true, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
                                                  (int)H_kv, sc, sm, st, sp)
             : launch_pp<false, false, true, true>(q, k, v, part, (int)B, (int)S_q, (int)H,
