@@ -687,12 +687,21 @@ __global__ __launch_bounds__(64 * SS_WAVES) void gemm_skinny_split(
     if (tid == 0) *last = atomicAdd(&arrivals[strip], 1u) == (unsigned)(nsplit - 1);
     __syncthreads();
     if (!*last) return;
+    // every other tile requested before any is added (one memory latency, not one per split;
+    // nsplit and split are uniform, so the tests are scalar branches); the sum runs in split
+    // order
+    f32x4 pt[SS_MAX_SPLIT];
+#pragma unroll
+    for (int sp = 0; sp < SS_MAX_SPLIT; ++sp) {
+      pt[sp] = v;
+      if (sp < nsplit && sp != split)
+        pt[sp] = __builtin_bit_cast(
+            f32x4, ld_cp<CP_SC01>(part, ((sp * nstrips + strip) * SS_PART + 4 * tid) * 4));
+    }
     f32x4 tot = {};
-    for (int sp = 0; sp < nsplit; ++sp)
-      tot += sp == split ? v
-                         : __builtin_bit_cast(f32x4, ld_cp<CP_SC01>(
-                                                         part, ((sp * nstrips + strip) * SS_PART +
-                                                                4 * tid) * 4));
+#pragma unroll
+    for (int sp = 0; sp < SS_MAX_SPLIT; ++sp)
+      if (sp < nsplit) tot += pt[sp];
     v = tot;
     if (tid == 0) atomicExch(&arrivals[strip], 0u);
   }
