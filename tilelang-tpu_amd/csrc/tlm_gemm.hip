@@ -518,9 +518,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
 // 256-byte segments over half of K at 6.3 TB/s, and a workgroup per CU is needed (one CU alone
 // streams about 38 GB/s). Within a workgroup the 8 waves take interleaved 16-row blocks (16 x
 // 128 halves = 4 KB, one block in flight per wave), each one v_mfma_f32_16x16x16 per 16 columns.
-// The workgroup's part of A (16 rows x at most 2048 k) is staged in LDS once, after the first B
-// block is requested: per-block A fragments read from the cache were measured to cost 2.5 us of
-// 24 at 16 x 14336 x 4096.
+// The workgroup's part of A (16 rows x at most 2048 k) is staged in LDS once, after each wave's
+// first two B blocks are requested: per-block A fragments read from the cache were measured to
+// cost 2.5 us of 24 at 16 x 14336 x 4096.
 //
 // The nsplit partial 16 x 128 tiles of a strip meet in a workspace: every workgroup stores its
 // tile and counts itself in with an atomic on the strip's arrival counter; the last to arrive
