@@ -111,7 +111,9 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * library-owned device workspace (16 MB per GPU, 4 slots): each stream owns one slot, so calls
  * on one stream are ordered and calls that overlap use different slots; further streams take an
  * unsplit kernel. A HIP graph keeps the slot of the stream it was captured on, so its replays
- * must not overlap each other or other work of that stream. The result does not depend on the
+ * must not overlap each other or other work of that stream. Slots are keyed by the stream handle:
+ * a stream created after another is destroyed can get the same handle and inherits its slot, so
+ * a stream is destroyed only once its calls have finished. The result does not depend on the
  * split's timing: a stream's calls are bitwise reproducible (the unsplit kernel of a stream
  * without a slot sums in another order, so its last bits can differ from the split kernel's). */
 int tlm_gemm(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int in_dtype,
