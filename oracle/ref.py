@@ -116,7 +116,10 @@ def ppl_add_ref(a: torch.Tensor, b: torch.Tensor, out_dtype=None) -> torch.Tenso
 
 # ------------------------------------------------------------------------------------------------
 # RoPE — tables per tpu_demo/tpu_test_rope_bf16.py:53-74 (make_rope_cos_sin), computed in fp32;
-# rotation per rope_ref_torch (:76-92).
+# rotation as the program computes it: ppl_rope_add (codegen_ppl.cc:1809-1848: out[2i] =
+# e1[2i] + e2[2i+1], out[2i+1] = o1[2i+1] + o2[2i]) over the tiles x*cos, -x*sin, x*cos, x*sin
+# (tpu_test_rope_bf16.py:28-45). With the demo's paired tables (cos[2i] = cos[2i+1], sin alike)
+# this is rope_ref_torch (:76-92).
 def rope_cos_sin(C: int, W: int, base: float = 10000.0, pos_start: int = 0,
                  dtype=torch.bfloat16):
     assert W % 2 == 0
@@ -137,10 +140,11 @@ def rope_ref(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Ten
         cf = cf.view(cf.shape[0], *([1] * (xf.dim() - 2)), cf.shape[-1])
         sf = sf.view(sf.shape[0], *([1] * (xf.dim() - 2)), sf.shape[-1])
     xe, xo = xf[..., 0::2], xf[..., 1::2]
-    c, s = cf[..., 0::2], sf[..., 0::2]
+    ce, co = cf[..., 0::2], cf[..., 1::2]
+    se, so = sf[..., 0::2], sf[..., 1::2]
     out = torch.empty_like(xf.expand(*torch.broadcast_shapes(xf.shape, cf.shape)))
-    out[..., 0::2] = xe * c - xo * s
-    out[..., 1::2] = xo * c + xe * s
+    out[..., 0::2] = xe * ce - xo * so
+    out[..., 1::2] = xo * co + xe * se
     return out.to(x.dtype)
 
 

@@ -541,3 +541,162 @@ def test_symbolic_program_still_fails_at_compile_time():
 
     with pytest.raises(UnsupportedProgram):
         tilelang.compile(mix, out_idx=-1)
+
+
+# ------------------------------------------------------------------------------------------------
+# The dedicated families take parameter roles from the data flow and compile only the expression
+# their kernel computes (anything else is rejected or goes to the general elementwise program).
+
+
+def test_rope_output_first_program_roles():
+    """tpu_demo/ppl/rope/rope_bf16.py:8-13 puts the output first."""
+    k = tilelang.compile(programs.rope(64, 16, 128, 64, out_first=True), out_idx=[0])
+    a = k.plan.attrs
+    assert (a["q"], a["cos"], a["sin"], a["q_out"], a["k"]) == (1, 2, 3, 0, None)
+    assert k.out_idx == [0]
+
+
+def _rope_variant(e2_kind="neg_x", cos_pos=None, C=128, W=64, Bc=64, Bw=16):
+    dt = "bfloat16"
+
+    @T.prim_func
+    def main(X: T.Tensor((C, W), dt), CO: T.Tensor((C, W), dt), SI: T.Tensor((C, W), dt),
+             O: T.Tensor((C, W), dt)):
+        with T.Kernel(T.ceildiv(C, Bc), T.ceildiv(W, Bw), is_cpu=True) as (bx, by):
+            x, c, s = (T.alloc_shared((Bc, Bw), dt) for _ in range(3))
+            T.ppl_copy(X[bx * Bc, by * Bw], x)
+            T.ppl_copy(CO[cos_pos(bx, by) if cos_pos else (bx * Bc, by * Bw)], c)
+            T.ppl_copy(SI[bx * Bc, by * Bw], s)
+            xc, xs, xn, e2, o = (T.alloc_shared((Bc, Bw), dt) for _ in range(5))
+            T.ppl_mul(xc, x, c)
+            T.ppl_mul(xs, x, s)
+            if e2_kind == "neg_x":       # the demo: (-x) * sin
+                T.ppl_mul_C(xn, x, -1.0)
+                T.ppl_mul(e2, xn, s)
+            elif e2_kind == "neg_prod":  # -(x * sin)
+                T.ppl_mul_C(e2, xs, -1.0)
+            elif e2_kind == "no_neg":    # x * sin: not a rotation
+                T.ppl_mul(e2, x, s)
+            elif e2_kind == "cos":       # (-x) * cos: the tables mixed up
+                T.ppl_mul_C(xn, x, -1.0)
+                T.ppl_mul(e2, xn, c)
+            T.ppl_rope_add(o, xc, e2, xc, xs)
+            T.ppl_copy(o, O[bx * Bc, by * Bw])
+
+    return main
+
+
+def test_rope_operand_forms():
+    for kind in ("neg_x", "neg_prod"):
+        a = recognize(_rope_variant(kind)).attrs
+        assert (a["q"], a["cos"], a["sin"], a["q_out"]) == (0, 1, 2, 3)
+    for kind in ("no_neg", "cos"):
+        with pytest.raises(UnsupportedProgram, match="ppl_rope_add"):
+            recognize(_rope_variant(kind))
+
+
+def test_rope_tables_at_another_tile_rejected():
+    # cos taken at the transposed tile position of a square grid
+    prog = _rope_variant(cos_pos=lambda bx, by: (by * 64, bx * 64), C=128, W=128, Bc=64, Bw=64)
+    with pytest.raises(UnsupportedProgram, match="grid position"):
+        recognize(prog)
+
+
+def _swiglu_variant(with_gate_factor):
+    C = W = 64
+    dt = "float32"
+
+    @T.prim_func
+    def main(G: T.Tensor((C, W), dt), U: T.Tensor((C, W), dt), O: T.Tensor((C, W), dt)):
+        with T.Kernel(T.ceildiv(C, 32), T.ceildiv(W, 32), is_cpu=True) as (bx, by):
+            g, u, e, ones, den, sig, out = (T.alloc_shared((32, 32), dt) for _ in range(7))
+            T.ppl_fill(ones, T.float32(1.0))
+            T.ppl_copy(G[bx * 32, by * 32], g)
+            T.ppl_copy(U[bx * 32, by * 32], u)
+            T.ppl_mul_C(e, g, T.float32(-1.0))
+            T.ppl_exp2(e)
+            T.ppl_add(den, e, ones)
+            T.ppl_div(sig, g if with_gate_factor else ones, den)
+            T.ppl_mul(out, sig, u)
+            T.ppl_copy(out, O[bx * 32, by * 32])
+
+    return main
+
+
+def test_swiglu_expression_checked():
+    p = recognize(_swiglu_variant(True))
+    assert p.family == "swiglu" and (p.attrs["gate"], p.attrs["up"]) == (0, 1)
+    # up * sigmoid(gate) is not SwiGLU: the general elementwise program computes it as written
+    assert recognize(_swiglu_variant(False)).family == "elementwise"
+
+
+def _rmsnorm_variant(kind):
+    M, N, dt = 64, 128, "float32"
+
+    def body(A, Wt, B):
+        with T.Kernel(T.ceildiv(M, 32), is_cpu=True) as (bx,):
+            x = T.alloc_shared((32, N), dt)
+            sq = T.alloc_shared((32, N), dt)
+            ss = T.alloc_shared((32, 1), dt)
+            T.ppl_copy(A[bx * 32, 0], x)
+            T.ppl_mul(sq, x, x)
+            T.ppl_reduce_sum(sq, ss, dim=1)
+            T.ppl_mul_C(ss, ss, T.float32(1.0 / N))
+            T.ppl_add_C(ss, ss, T.float32(1e-6))
+            T.ppl_rsqrt(ss, ss)
+            if kind != "no_x":
+                T.ppl_mul(x, x, ss)
+            else:
+                T.ppl_mul(x, sq, ss)  # x * x scaled: not RMSNorm
+            if kind == "weight":
+                w = T.alloc_shared((1, N), dt)
+                T.ppl_copy(Wt[0], w)
+                T.ppl_mul(x, x, w)
+            T.ppl_copy(x, B[bx * 32, 0])
+
+    if kind == "plain" or kind == "no_x":
+        @T.prim_func
+        def main(A: T.Tensor((M, N), dt), B: T.Tensor((M, N), dt)):
+            body(A, None, B)
+    else:
+        @T.prim_func
+        def main(A: T.Tensor((M, N), dt), Wt: T.Tensor((N,), dt), B: T.Tensor((M, N), dt)):
+            body(A, Wt, B)
+    return main
+
+
+def test_rmsnorm_expression_checked():
+    assert recognize(_rmsnorm_variant("plain")).attrs["w"] is None
+    assert recognize(_rmsnorm_variant("weight")).attrs["w"] == 1
+    # a weight parameter the program never applies is not multiplied in by the kernel either
+    with pytest.raises(UnsupportedProgram, match="stored value"):
+        recognize(_rmsnorm_variant("unused_weight"))
+    with pytest.raises(UnsupportedProgram, match="stored value"):
+        recognize(_rmsnorm_variant("no_x"))
+
+
+def test_sigmoid_expression_checked():
+    C = W = 64
+
+    @T.prim_func
+    def twice(G_in: T.Tensor((C, W), "float32"), G_out: T.Tensor((C, W), "float32")):
+        with T.Kernel(T.ceildiv(C, 32), T.ceildiv(W, 32), is_cpu=True) as (bx, by):
+            x, y = T.alloc_shared((32, 32), "float32"), T.alloc_shared((32, 32), "float32")
+            T.ppl_copy(G_in[bx * 32, by * 32], x)
+            T.ppl_sigmoid(y, x)
+            T.ppl_mul_C(y, y, T.float32(2.0))
+            T.ppl_copy(y, G_out[bx * 32, by * 32])
+
+    assert recognize(programs.sigmoid(32, 32, C, W)).family == "sigmoid"
+    assert recognize(twice).family == "elementwise"
+
+
+def test_region_of_an_access_with_a_slice():
+    """Point indices of an access that has a slice span one element; an access of point indices
+    only takes the tile's extents on its trailing dims (tilelang/language/copy.py:40-62)."""
+    from tilelang.language import ir
+    buf = ir.Buffer("b", (10, 4, 128), "bfloat16", "global")
+    st, ex = buf[3:7, 2, :].region((4, 128))
+    assert [int(ir.const_value(e)) for e in ex] == [4, 1, 128]
+    st, ex = buf[3, 2, 0].region((4, 128))
+    assert [int(ir.const_value(e)) for e in ex] == [1, 4, 128]

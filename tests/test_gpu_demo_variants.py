@@ -102,6 +102,14 @@ def test_rope_fp32_fp16(dtype, tol, C, W):
     out = torch.zeros(C, W, dtype=tdt)
     assert k(x, cos, sin, out) == 0
     torch_assert_close(out, ref.rope_ref(x, cos, sin), atol=tol, rtol=tol)
+    # tables whose even and odd entries differ (ppl_rope_add's strided adds), output first
+    # (tpu_demo/ppl/rope/rope_{fp16,fp32}.py:8-13)
+    cos, sin = (torch.randn(C, W, generator=_gen(67)).to(tdt) for _ in range(2))
+    k = tilelang.compile(programs.rope(64, 16, C, W, dtype=dtype, out_first=True), out_idx=[0],
+                         target="tpu")
+    out = torch.zeros(C, W, dtype=tdt)
+    assert k(out, x, cos, sin) == 0
+    torch_assert_close(out, ref.rope_ref(x, cos, sin), atol=3 * tol, rtol=tol)
 
 
 @pytest.mark.parametrize("C,W", [(1024, 1024), (37, 11)])

@@ -108,6 +108,34 @@ def test_rope_qk(tokens, hq, hk, dim):
     _ulp_close(k_out, ek, 8e-3)
 
 
+def test_rope_output_first_program():
+    """tpu_demo/ppl/rope/rope_bf16.py:8-13 order (G_out, G_in, G_cos, G_sin), TPU convention."""
+    C, W = 128, 64
+    k = tilelang.compile(programs.rope(64, 16, C, W, out_first=True), out_idx=[0], target="tpu")
+    x = torch.randn(C, W, generator=torch.Generator().manual_seed(15)).to(torch.bfloat16)
+    cos, sin = ref.rope_cos_sin(C, W)
+    out = torch.zeros(C, W, dtype=torch.bfloat16)
+    assert k(out, x, cos, sin) == 0
+    exp = ref.rope_ref(x, cos, sin)
+    torch_assert_close(out, exp, atol=1e-2, rtol=1e-2)
+    _ulp_close(out, exp, 8e-3)
+
+
+@pytest.mark.parametrize("tokens,hq,hk,dim", [(40, 4, 2, 128), (9, 3, 1, 40)])
+def test_rope_unpaired_tables(tokens, hq, hk, dim):
+    """Tables whose even and odd entries differ: the odd output takes cos[2i+1] and the even
+    output sin[2i+1], as ppl_rope_add's strided adds do (16-byte and scalar kernels)."""
+    g = torch.Generator().manual_seed(16)
+    q = torch.randn(tokens, hq, dim, generator=g).to(torch.bfloat16)
+    kk = torch.randn(tokens, hk, dim, generator=g).to(torch.bfloat16)
+    cos, sin = (torch.randn(tokens, dim, generator=g).to(torch.bfloat16) for _ in range(2))
+    k = tilelang.compile(programs.rope_qk(tokens, hq, hk, dim), out_idx=[4, 5])
+    q_out, k_out = k(q.to(DEV), kk.to(DEV), cos.to(DEV), sin.to(DEV))
+    for got, x in ((q_out, q), (k_out, kk)):
+        exp = ref.rope_ref(x, cos, sin)
+        torch_assert_close(got.cpu(), exp, atol=2e-2, rtol=8e-3)
+
+
 def test_rope_position_zero_is_identity():
     w = workloads.rope(4, 8, 128, seed=8)
     k = tilelang.compile(programs.rope_qk(4, 8, 8, 128), out_idx=[4, 5])

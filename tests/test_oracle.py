@@ -106,6 +106,25 @@ def test_rope_vs_complex_rotation_and_invariants():
     assert np.allclose(np.abs(out[..., 0::2] + 1j * out[..., 1::2]), np.abs(z), atol=1e-4)
 
 
+def test_rope_unpaired_tables_follow_rope_add():
+    """Tables whose pairs differ: brute force over the program's tiles and the two strided adds
+    of ppl_rope_add (codegen_ppl.cc:1809-1848), element by element in fp64."""
+    g = torch.Generator().manual_seed(41)
+    x, c, s = (torch.randn(3, 10, generator=g) for _ in range(3))
+    out = ref.rope_ref(x, c, s).double().numpy()
+    X, C, S = (t.double().numpy() for t in (x, c, s))
+    for r in range(3):
+        xc = [X[r, j] * C[r, j] for j in range(10)]
+        xns = [(-X[r, j]) * S[r, j] for j in range(10)]
+        xs = [X[r, j] * S[r, j] for j in range(10)]
+        for i in range(5):
+            assert abs(out[r, 2 * i] - (xc[2 * i] + xns[2 * i + 1])) < 1e-5
+            assert abs(out[r, 2 * i + 1] - (xc[2 * i + 1] + xs[2 * i])) < 1e-5
+    # and a wrong pairing (the even table entries for both outputs) differs
+    alt = X[:, 0::2] * C[:, 0::2] - X[:, 1::2] * S[:, 0::2]
+    assert np.abs(alt - out[:, 0::2]).max() > 1e-2
+
+
 # ----------------------------------------------------------------------------------------- SwiGLU
 def test_swiglu_vs_numpy_and_limits():
     g = torch.Generator().manual_seed(5)

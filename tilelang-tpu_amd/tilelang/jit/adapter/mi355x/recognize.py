@@ -149,6 +149,79 @@ def _index(pf, buf) -> int:
     raise UnsupportedProgram(f"{buf!r} is not a parameter")
 
 
+def _symbolic(pf):
+    """The values a program stores, as expressions over its parameters: a list of
+    (parameter index, expression) per store to a parameter, in program order, or None when the
+    program uses an op outside the elementwise / row-reduce / rope vocabulary.
+
+    Tiles are followed through the program in order, so a tile written twice (``x = x * r``)
+    carries its latest value. Expressions are tuples: ("load", i) for a tile copied from
+    parameter i, ("const", v), (op, a, b) for add / sub / mul / div (operands of add and mul in a
+    canonical order), ("add_C" / "mul_C", a, ("const", v)), ("exp", a), ("rsqrt", a),
+    ("sigmoid", a), ("rsum", a) for a row sum and ("rope", e1, e2, o1, o2). Casts between tile
+    dtypes and loop structure do not appear: a split-K accumulation ``acc = acc + rsum(x * x)``
+    over a loop reads as one step from the filled accumulator. The dedicated families compare
+    these expressions with the computation their kernel performs, and take their parameter
+    roles from them rather than from parameter positions."""
+    val: Dict[int, tuple] = {}
+    stores: List[tuple] = []
+
+    def get(b):
+        b = _buf(b)
+        return val.get(id(b), ("?",)) if b is not None else ("?",)
+
+    def sym(op, a, b):
+        if op in ("add", "mul") and repr(b) < repr(a):
+            a, b = b, a
+        return (op, a, b)
+
+    for op in _ops(pf):
+        n = op.name
+        if n in _COPY:
+            sb, db = _buf(op.args[0]), _buf(op.args[1])
+            if sb is None or db is None:
+                return None
+            if sb.scope == "global" and db.scope == "global":
+                return None
+            if sb.scope == "global":
+                val[id(db)] = ("load", _index(pf, sb))
+            elif db.scope == "global":
+                stores.append((_index(pf, db), get(sb)))
+            else:
+                val[id(db)] = get(sb)
+        elif n in _FILL_OPS:
+            val[id(_buf(op.args[0]))] = ("const", _const(op.args[1]))
+        elif n in ("ppl_add", "ppl_sub", "ppl_mul", "ppl_div"):
+            val[id(_buf(op.args[0]))] = sym(n[4:], get(op.args[1]), get(op.args[2]))
+        elif n in ("ppl_add_C", "ppl_mul_C"):
+            val[id(_buf(op.args[0]))] = (n[4:], get(op.args[1]), ("const", _const(op.args[2])))
+        elif n == "ppl_exp":
+            val[id(_buf(op.args[0]))] = ("exp", get(op.args[0]))
+        elif n in ("ppl_rsqrt", "ppl_sigmoid"):
+            val[id(_buf(op.args[0]))] = (n[4:], get(op.args[1]))
+        elif n == "ppl_reduce_sum":
+            if op.kwargs.get("dim", 1) not in (1, -1):
+                return None
+            val[id(_buf(op.args[1]))] = ("rsum", get(op.args[0]))
+        elif n == "ppl_rope_add":
+            val[id(_buf(op.args[0]))] = ("rope",) + tuple(get(a) for a in op.args[1:5])
+        else:
+            return None
+    return stores
+
+
+def _neg(e) -> tuple:
+    return ("mul_C", e, ("const", -1.0))
+
+
+def _mul(a, b) -> tuple:
+    return ("mul", a, b) if repr(a) <= repr(b) else ("mul", b, a)
+
+
+def _add(a, b) -> tuple:
+    return ("add", a, b) if repr(a) <= repr(b) else ("add", b, a)
+
+
 def _shape(b: Buffer):
     return tuple(int(ir.const_value(s)) for s in b.shape)
 
@@ -282,6 +355,23 @@ def _rmsnorm(pf, names) -> Plan:
             w = p
         else:
             _fail(fam, f"unexpected parameter {p!r}")
+    # the stored value, as the program computes it: x * rsqrt(rowsum(x * x) * inv + eps),
+    # times w when there is a weight (the row sum optionally accumulated into a zero-filled sum)
+    X = ("load", _index(pf, x))
+    S = ("rsum", _mul(X, X))
+    R = [("rsqrt", ("add_C", ("mul_C", s_, ("const", inv)), ("const", eps)))
+         for s_ in (S, _add(("const", 0.0), S))]
+    want = [sorted(map(repr, [X, r] + ([] if w is None else [("load", _index(pf, w))])))
+            for r in R]
+    stores = _symbolic(pf)
+
+    def factors(e):
+        return factors(e[1]) + factors(e[2]) if e[0] == "mul" else [e]
+
+    if not stores or any(o != _index(pf, y) or sorted(map(repr, factors(e))) not in want
+                         for o, e in stores):
+        _fail(fam, "the stored value is not x * rsqrt(mean(x * x) + eps)" +
+              ("" if w is None else " * w"))
     outs = [_index(pf, y)]
     return Plan(fam, pf.params, outs, dict(
         x=_index(pf, x), w=None if w is None else _index(pf, w), y=outs[0], eps=eps,
@@ -289,66 +379,143 @@ def _rmsnorm(pf, names) -> Plan:
 
 
 def _swiglu(pf, names) -> Plan:
+    """out = up * (gate / (exp(-gate) + 1)) (tpu_test_swiglu_bf16.py:41-49), with the roles of
+    gate and up read from the stored expression. Another expression is not this kernel's (the
+    caller then tries the general elementwise program)."""
     fam = "swiglu"
-    exp_ops = [op for op in _ops(pf, ("ppl_exp",))]
-    if len(exp_ops) != 1:
-        _fail(fam, "expected one ppl_exp2")
-    ebuf = _buf(exp_ops[0].args[0])
-    # exp input = -gate: find mul_C(-1) producing ebuf
-    neg = [op for op in _ops(pf, ("ppl_mul_C",)) if _buf(op.args[0]) is ebuf]
-    if not neg or _const(neg[0].args[2]) != -1.0:
-        _fail(fam, "exp argument is not -gate")
-    gate = _source_param(pf, _buf(neg[0].args[1]))
-    writes = _written_params(pf)
-    reads = [p for p in pf.params if all(p is not w for w in writes)]
-    if gate is None or len(writes) != 1 or len(reads) != 2:
+    stores = _symbolic(pf)
+    if not stores or len(stores) != 1:
+        _fail(fam, "expected one stored tile")
+    o, e = stores[0]
+    gate = up = None
+    if e[0] == "mul":
+        for u, q in ((e[1], e[2]), (e[2], e[1])):
+            if u[0] == "load" and q[0] == "div" and q[1][0] == "load" and q[1] != u and \
+                    q == ("div", q[1], _add(("exp", _neg(q[1])), ("const", 1.0))):
+                gate, up = q[1][1], u[1]
+    if gate is None:
+        _fail(fam, "the stored tile is not up * (gate / (exp(-gate) + 1))")
+    P = pf.params
+    gate, up, out = P[gate], P[up], P[o]
+    if len(P) != 3:
         _fail(fam, "expected (gate, up) -> out")
-    up = reads[0] if reads[1] is gate else reads[1]
-    out = writes[0]
     if not (_shape(gate) == _shape(up) == _shape(out)):
         _fail(fam, "gate, up, out shapes differ")
     if not (gate.dtype == up.dtype == out.dtype) or gate.dtype not in ("bfloat16", "float16",
                                                                        "float32"):
         _fail(fam, "dtypes must all be bfloat16, all float16 or all float32")
-    return Plan(fam, pf.params, [_index(pf, out)], dict(
+    maps = []
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if sb is not None and db is not None and (sb.scope == "global") != (db.scope == "global"):
+            maps.append(_tile_map(pf, src, db) if sb.scope == "global" else
+                        _tile_map(pf, dst, sb))
+    if not maps or maps[0] is None or any(m != maps[0] for m in maps):
+        _fail(fam, "the tile copies of gate, up and out are not at one grid position")
+    return Plan(fam, P, [_index(pf, out)], dict(
         gate=_index(pf, gate), up=_index(pf, up), out=_index(pf, out),
         n=math.prod(_shape(gate)), dtype=gate.dtype))
 
 
+def _rope_term(e1, e2, o1, o2):
+    """(x, cos, sin) parameter indices when the ppl_rope_add operands are the demo's tiles
+    x*cos, -(x*sin), x*cos, x*sin (tpu_test_rope_bf16.py:28-45) of three distinct parameters,
+    else None. The negation may sit on the product, on x or on sin."""
+    if e1 != o1 or e1[0] != "mul" or o2[0] != "mul":
+        return None
+    a, b, c, d = e1[1], e1[2], o2[1], o2[2]
+    if any(t[0] != "load" for t in (a, b, c, d)):
+        return None
+    common = {a, b} & {c, d}
+    if len(common) != 1:
+        return None
+    x = common.pop()
+    cos = b if a == x else a
+    sin = d if c == x else c
+    if len({x, cos, sin}) != 3:
+        return None
+    if e2 not in (_neg(o2), _mul(_neg(x), sin), _mul(x, _neg(sin))):
+        return None
+    return x[1], cos[1], sin[1]
+
+
 def _rope(pf, names) -> Plan:
+    """Parameter roles come from the data flow into ppl_rope_add, not from positions: the
+    reference's ppl/rope programs take (G_out, G_in, G_cos, G_sin), the tpu_test_rope demos
+    (G_in, G_cos, G_sin, G_out)."""
     fam = "rope"
-    n = len(pf.params)
-    if n == 4:
-        x, c, s, o = pf.params
-        if not (_shape(x) == _shape(c) == _shape(s) == _shape(o)) or len(_shape(x)) != 2:
+    stores = _symbolic(pf)
+    if not stores or len(stores) > 2:
+        _fail(fam, "expected one stored rope tile (x) or two (q and k)")
+    terms = []
+    for o, e in stores:
+        t = _rope_term(*e[1:]) if e[0] == "rope" else None
+        if t is None:
+            _fail(fam, "the stored tile is not ppl_rope_add(out, x*cos, -x*sin, x*cos, x*sin) of "
+                       "one input and one cos / sin table pair")
+        terms.append(t + (o,))
+    P = pf.params
+    # every global tile copy must address the output tile's grid position (tables without the
+    # head dimension of a 3-D q / k)
+    maps: Dict[int, list] = {}
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if sb is None or db is None:
+            _fail(fam, "copy operands must be buffers")
+        if sb.scope == "global" and db.scope != "global":
+            maps.setdefault(_index(pf, sb), []).append(_tile_map(pf, src, db))
+        elif db.scope == "global" and sb.scope != "global":
+            maps.setdefault(_index(pf, db), []).append(_tile_map(pf, dst, sb))
+
+    def same_position(x, c, s, o):
+        mo = maps.get(o, [None])
+        if len(mo) != 1 or mo[0] is None:
+            return False
+        mo = mo[0]
+        tab = mo if len(mo) == 2 else [mo[0], mo[-1]]
+        return all(m == mo for m in maps.get(x, [None])) and \
+            all(m == tab for m in maps.get(c, [None]) + maps.get(s, [None]))
+
+    if len(terms) == 1:
+        x, c, s, o = terms[0]
+        if len(P) != 4:
+            _fail(fam, "the one-tensor form takes x, cos, sin and out (4 parameters)")
+        if not (_shape(P[x]) == _shape(P[c]) == _shape(P[s]) == _shape(P[o])) or \
+                len(_shape(P[x])) != 2:
             _fail(fam, "the 4-parameter form takes x, cos, sin, out of one [C, W] shape")
-        C, W = _shape(x)
-        attrs = dict(q=0, k=None, cos=1, sin=2, q_out=3, k_out=None, tokens=C, heads_q=1,
+        C, W = _shape(P[x])
+        attrs = dict(q=x, k=None, cos=c, sin=s, q_out=o, k_out=None, tokens=C, heads_q=1,
                      heads_k=0, dim=W)
-        outs = [3]
-    elif n == 6:
-        q, k, c, s, qo, ko = pf.params
-        if _shape(c) != _shape(s) or len(_shape(c)) != 2:
-            _fail(fam, "cos/sin must be [tokens, dim]")
-        T, W = _shape(c)
-        if _shape(q)[0] != T or _shape(q)[-1] != W or _shape(k)[0] != T or _shape(k)[-1] != W:
-            _fail(fam, "q/k must be [tokens, heads, dim] matching the tables")
-        if _shape(qo) != _shape(q) or _shape(ko) != _shape(k):
-            _fail(fam, "outputs must match q and k")
-        hq = math.prod(_shape(q)[1:-1])
-        hk = math.prod(_shape(k)[1:-1])
-        attrs = dict(q=0, k=1, cos=2, sin=3, q_out=4, k_out=5, tokens=T, heads_q=hq, heads_k=hk,
-                     dim=W)
-        outs = [4, 5]
+        outs = [o]
     else:
-        _fail(fam, "expected (x, cos, sin, out) or (q, k, cos, sin, q_out, k_out)")
-    dts = {p.dtype for p in pf.params}
+        (xq, c, s, oq), (xk, c2, s2, ok) = terms
+        if (c, s) != (c2, s2) or xq == xk or oq == ok or len(P) != 6:
+            _fail(fam, "the q+k form rotates two inputs into two outputs with one table pair "
+                       "(6 parameters)")
+        if _shape(P[c]) != _shape(P[s]) or len(_shape(P[c])) != 2:
+            _fail(fam, "cos/sin must be [tokens, dim]")
+        T_, W = _shape(P[c])
+        for xi, oi in ((xq, oq), (xk, ok)):
+            xs = _shape(P[xi])
+            if len(xs) < 2 or xs[0] != T_ or xs[-1] != W or _shape(P[oi]) != xs:
+                _fail(fam, "q/k must be [tokens, heads, dim] matching the tables and outputs")
+        attrs = dict(q=xq, k=xk, cos=c, sin=s, q_out=oq, k_out=ok, tokens=T_,
+                     heads_q=math.prod(_shape(P[xq])[1:-1]),
+                     heads_k=math.prod(_shape(P[xk])[1:-1]), dim=W)
+        outs = sorted((oq, ok))
+    for x, c, s, o in terms:
+        if not same_position(x, c, s, o):
+            _fail(fam, f"the tile copies of {P[x]!r}, its tables and {P[o]!r} are not at one "
+                       f"grid position")
+    dts = {p.dtype for p in P}
     if len(dts) != 1 or next(iter(dts)) not in ("bfloat16", "float16", "float32"):
         _fail(fam, f"all parameters must share one of bfloat16 / float16 / float32, got {dts}")
     if attrs["dim"] % 2:
         _fail(fam, "dim must be even")
     attrs["dtype"] = next(iter(dts))
-    return Plan(fam, pf.params, outs, attrs)
+    return Plan(fam, P, outs, attrs)
 
 
 def _gemm(pf, names) -> Plan:
@@ -888,6 +1055,8 @@ def _sigmoid(pf, names) -> Plan:
         _fail(fam, "expected one input and one output of the same shape")
     if x.dtype != y.dtype or x.dtype not in ("float32", "float16", "bfloat16"):
         _fail(fam, f"dtypes {x.dtype} -> {y.dtype} (float32, float16 or bfloat16, matching)")
+    if _symbolic(pf) != [(_index(pf, y), ("sigmoid", ("load", _index(pf, x))))]:
+        _fail(fam, "the program stores something other than sigmoid(x)")
     return Plan(fam, pf.params, [_index(pf, y)], dict(
         x=_index(pf, x), y=_index(pf, y), n=math.prod(_shape(x)), dtype=x.dtype))
 
@@ -968,14 +1137,50 @@ def _grid_var_extent(pf, e) -> Optional[int]:
     """Extent of the kernel grid dimension whose variable is ``e`` (None if it is not one)."""
     if not isinstance(e, Expr) or e.op != "var" or not pf.kernels:
         return None
-    k = pf.kernels[0]
-    for v, ext in zip(k.vars, k.extents):
-        if v is e or (isinstance(v, Expr) and v.args[0] == e.args[0]):
-            try:
-                return int(ir.const_value(ext))
-            except (TypeError, ValueError):
+    # the kernel that binds this variable object (a program may launch several kernels, each
+    # with its own bx, by), else a variable of the same name in the first kernel
+    pairs = [(v, ext) for k in pf.kernels for v, ext in zip(k.vars, k.extents) if v is e]
+    if not pairs:
+        k = pf.kernels[0]
+        pairs = [(v, ext) for v, ext in zip(k.vars, k.extents)
+                 if isinstance(v, Expr) and v.args[0] == e.args[0]]
+    if not pairs:
+        return None
+    try:
+        return int(ir.const_value(pairs[0][1]))
+    except (TypeError, ValueError):
+        return None
+
+
+def _eval_int(e, v):
+    """Integer value of an index expression of +, -, * with every variable set to ``v``."""
+    if isinstance(e, bool):
+        return None
+    if isinstance(e, int):
+        return e
+    if isinstance(e, Expr):
+        if e.op == "const" and isinstance(e.args[0], int):
+            return e.args[0]
+        if e.op == "var":
+            return v
+        if e.op in ("add", "sub", "mul") and len(e.args) == 2:
+            a, b = _eval_int(e.args[0], v), _eval_int(e.args[1], v)
+            if a is None or b is None:
                 return None
+            return a + b if e.op == "add" else a - b if e.op == "sub" else a * b
     return None
+
+
+def _extent_value(ex) -> Optional[int]:
+    """A region extent as an integer: a constant, or a slice length such as
+    ``(bx + 1) * 32 - bx * 32`` that takes one value whatever the grid variables (checked at
+    three settings of them); None otherwise."""
+    try:
+        return int(ir.const_value(ex))
+    except (TypeError, ValueError):
+        pass
+    vals = {_eval_int(ex, v) for v in (0, 1, 7)}
+    return vals.pop() if len(vals) == 1 and None not in vals else None
 
 
 def _tile_map(pf, access, tile: Buffer):
@@ -991,10 +1196,7 @@ def _tile_map(pf, access, tile: Buffer):
     starts, exts = access.region(tile.shape)
     out = []
     for d, (st, ex) in enumerate(zip(starts, exts)):
-        try:
-            t = int(ir.const_value(ex))
-        except (TypeError, ValueError):
-            t = None
+        t = _extent_value(ex)
         try:
             s0 = int(ir.const_value(st))
         except (TypeError, ValueError):
@@ -1002,13 +1204,16 @@ def _tile_map(pf, access, tile: Buffer):
         if s0 == 0 and (t == dims[d] or dims[d] == 1):
             out.append(None)
             continue
-        if not (isinstance(st, Expr) and st.op == "mul"):
+        if isinstance(st, Expr) and st.op == "var":  # a grid variable alone: unit tiles
+            var, c = st, 1
+        elif isinstance(st, Expr) and st.op == "mul":
+            a, b = st.args
+            var, c = (a, b) if isinstance(b, Expr) and b.op == "const" else (b, a)
+            if not (isinstance(c, Expr) and c.op == "const"):
+                return None
+            c = int(c.args[0])
+        else:
             return None
-        a, b = st.args
-        var, c = (a, b) if isinstance(b, Expr) and b.op == "const" else (b, a)
-        if not (isinstance(c, Expr) and c.op == "const"):
-            return None
-        c = int(c.args[0])
         if t is None:
             tdims = list(tile.shape)
             t = int(ir.const_value(tdims[d - (len(dims) - len(tdims))])) if len(tdims) else 1

@@ -468,13 +468,14 @@ class BufferAccess(Expr):
             else:
                 starts.append(ix)
                 extents.append(None)
-        if fallback_extents is not None:
+        # An access with a slice is a region whose point indices span one element; an access of
+        # point indices only takes the tile's extents on its trailing dims and 1 on the leading
+        # ones (tilelang/language/copy.py:40-62).
+        if fallback_extents is not None and all(e is None for e in extents):
             fb = list(fallback_extents)
-            # align from the right, ignoring unit dims of the tile
             j = len(fb) - 1
             for d in range(len(extents) - 1, -1, -1):
-                if extents[d] is None:
-                    extents[d] = fb[j] if j >= 0 else 1
+                extents[d] = fb[j] if j >= 0 else 1
                 j -= 1
         extents = [1 if e is None else e for e in extents]
         return starts, extents

@@ -259,16 +259,30 @@ def _rope_tile(x_src, cos_src, sin_src, dst, shape, dtype):
     T.ppl_copy(out, dst)
 
 
-def rope(Block_c, Block_w, C, W, dtype="bfloat16"):
+def rope(Block_c, Block_w, C, W, dtype="bfloat16", out_first=False):
+    """tpu_test_rope_bf16.py:5-51 (G_in, G_cos, G_sin, G_out); out_first gives the parameter
+    order of tpu_demo/ppl/rope/rope_{bf16,fp16,fp32}.py:8-13 (G_out, G_in, G_cos, G_sin)."""
     shape = (C, W)
 
-    @T.prim_func
-    def rope_kernel(G_in: T.Tensor(shape, dtype), G_cos: T.Tensor(shape, dtype),
-                    G_sin: T.Tensor(shape, dtype), G_out: T.Tensor(shape, dtype)):
+    def body(G_in, G_cos, G_sin, G_out):
         with T.Kernel(T.ceildiv(C, Block_c), T.ceildiv(W, Block_w), is_cpu=True) as (bx, by):
             _rope_tile(G_in[bx * Block_c, by * Block_w], G_cos[bx * Block_c, by * Block_w],
                        G_sin[bx * Block_c, by * Block_w], G_out[bx * Block_c, by * Block_w],
                        (Block_c, Block_w), dtype)
+
+    if out_first:
+
+        @T.prim_func
+        def rope_out_first(G_out: T.Tensor(shape, dtype), G_in: T.Tensor(shape, dtype),
+                           G_cos: T.Tensor(shape, dtype), G_sin: T.Tensor(shape, dtype)):
+            body(G_in, G_cos, G_sin, G_out)
+
+        return rope_out_first
+
+    @T.prim_func
+    def rope_kernel(G_in: T.Tensor(shape, dtype), G_cos: T.Tensor(shape, dtype),
+                    G_sin: T.Tensor(shape, dtype), G_out: T.Tensor(shape, dtype)):
+        body(G_in, G_cos, G_sin, G_out)
 
     return rope_kernel
 
@@ -284,8 +298,9 @@ def rope_qk(tokens, heads_q, heads_k, W, Block_t=64, dtype="bfloat16"):
                        K_out: T.Tensor((tokens, heads_k, W), dtype)):
         for X, Y, H in ((Q, Q_out, heads_q), (K, K_out, heads_k)):
             with T.Kernel(T.ceildiv(tokens, Block_t), H, is_cpu=True) as (bx, by):
-                _rope_tile(X[bx * Block_t, by, 0], COS[bx * Block_t, 0], SIN[bx * Block_t, 0],
-                           Y[bx * Block_t, by, 0], (Block_t, W), dtype)
+                tok = slice(bx * Block_t, (bx + 1) * Block_t)
+                _rope_tile(X[tok, by, :], COS[tok, :], SIN[tok, :], Y[tok, by, :], (Block_t, W),
+                           dtype)
 
     return rope_qk_kernel
 
