@@ -700,3 +700,120 @@ def test_region_of_an_access_with_a_slice():
     assert [int(ir.const_value(e)) for e in ex] == [4, 1, 128]
     st, ex = buf[3, 2, 0].region((4, 128))
     assert [int(ir.const_value(e)) for e in ex] == [1, 4, 128]
+
+
+def _gemm_variant(kind, M=64, N=64, K=128, BM=32, BN=32, BK=32):
+    dt = "float16"
+
+    @T.prim_func
+    def main(A: T.Tensor((M, K), dt), B: T.Tensor((K, N), dt), C: T.Tensor((M, N), dt)):
+        with T.Kernel(T.ceildiv(N, BN), T.ceildiv(M, BM), is_cpu=True) as (bx, by):
+            a_s = T.alloc_shared((BM, BK), dt)
+            b_s = T.alloc_shared((BK, BN), dt)
+            acc = T.alloc_shared((BM, BN), "float32")
+            c_s = T.alloc_shared((BM, BN), dt)
+            if kind != "clear_inside":
+                T.ppl_fill(acc, T.float32(0))
+            nk = T.ceildiv(K, BK) - (1 if kind == "short_k" else 0)
+            for k in T.Pipelined(nk, num_stages=2):
+                if kind == "clear_inside":
+                    T.ppl_fill(acc, T.float32(0))
+                ra = bx if kind == "a_rows_by_bx" else by
+                T.ppl_copy(A[ra * BM, k * BK], a_s)
+                T.ppl_copy(B[k * BK, bx * BN], b_s)
+                T.ppl_gemm(a_s, b_s, acc)
+            T.ppl_copy(acc, c_s)
+            T.ppl_copy(c_s, C[by * BM, bx * BN])
+
+    return main
+
+
+def test_gemm_tiles_and_k_coverage_checked():
+    assert recognize(_gemm_variant("ok")).attrs["K"] == 128
+    for kind, msg in (("short_k", "all of K"), ("a_rows_by_bx", "all of K"),
+                      ("clear_inside", "cleared inside")):
+        with pytest.raises(UnsupportedProgram, match=msg):
+            recognize(_gemm_variant(kind))
+    # 2xAcc with an odd k-tile count: the fold every second tile never takes the last one
+    with pytest.raises(UnsupportedProgram, match="last k tile"):
+        recognize(programs.matmul_fp8(256, 256, 192, two_acc=True))
+
+
+def _reduce_variant(N, BN, clear=True, looped=False):
+    M, BM = 64, 32
+
+    @T.prim_func
+    def main(X: T.Tensor((M, N), "float16"), Y: T.Tensor((M, 1), "float16")):
+        with T.Kernel(1, T.ceildiv(M, BM), is_cpu=True) as (bx, by):
+            xs = T.alloc_shared((BM, BN), "float16")
+            ys = T.alloc_shared((BM, 1), "float16")
+            if looped:
+                T.ppl_fill(ys, T.float16(-65504.0))
+                for k in T.serial(T.ceildiv(N, BN)):
+                    T.ppl_copy(X[by * BM, k * BN], xs)
+                    T.ppl_reduce_max(xs, ys, 1, False)
+            else:
+                T.ppl_copy(X[by * BM, 0], xs)
+                T.ppl_reduce_max(xs, ys, 1, clear)
+            T.ppl_copy(ys, Y[by * BM, 0])
+
+    return main
+
+
+def test_row_reduce_whole_rows():
+    """tpu_test_reduce_max.py reduces one whole-row tile; a narrower tile reduces part of the
+    row, a reduction without clear also takes the output's contents."""
+    assert recognize(_reduce_variant(64, 64)).family == "row_reduce"
+    with pytest.raises(UnsupportedProgram, match="whole rows"):
+        recognize(_reduce_variant(128, 64))
+    with pytest.raises(UnsupportedProgram, match="clearing reduction"):
+        recognize(_reduce_variant(64, 64, clear=False))
+    with pytest.raises(UnsupportedProgram, match="clearing reduction"):
+        recognize(_reduce_variant(128, 64, looped=True))
+
+
+def test_rmsnorm_whole_rows():
+    """A row tile narrower than the row, or a looped row sum that is not accumulated."""
+    M, N = 64, 128
+
+    def prog(kind):
+        @T.prim_func
+        def main(A: T.Tensor((M, N), "float32"), B: T.Tensor((M, N), "float32")):
+            with T.Kernel(T.ceildiv(M, 32), is_cpu=True) as (bx,):
+                w = 64 if kind != "ok" else N
+                x = T.alloc_shared((32, w), "float32")
+                sq = T.alloc_shared((32, w), "float32")
+                ss = T.alloc_shared((32, 1), "float32")
+                if kind == "overwrite":
+                    for k in T.serial(N // w):
+                        T.ppl_copy(A[bx * 32, k * w], x)
+                        T.ppl_mul(sq, x, x)
+                        T.ppl_reduce_sum(sq, ss, dim=1)
+                else:
+                    T.ppl_copy(A[bx * 32, 0], x)
+                    T.ppl_mul(sq, x, x)
+                    T.ppl_reduce_sum(sq, ss, dim=1)
+                T.ppl_mul_C(ss, ss, T.float32(1.0 / N))
+                T.ppl_add_C(ss, ss, T.float32(1e-6))
+                T.ppl_rsqrt(ss, ss)
+                if kind == "overwrite":
+                    for k in T.serial(N // w):
+                        T.ppl_copy(A[bx * 32, k * w], x)
+                        T.ppl_mul(x, x, ss)
+                        T.ppl_copy(x, B[bx * 32, k * w])
+                else:
+                    T.ppl_mul(x, x, ss)
+                    T.ppl_copy(x, B[bx * 32, 0])
+        return main
+
+    assert recognize(prog("ok")).family == "rmsnorm"
+    with pytest.raises(UnsupportedProgram, match="whole rows"):
+        recognize(prog("narrow"))
+    with pytest.raises(UnsupportedProgram, match="accumulate"):
+        recognize(prog("overwrite"))
+
+
+def test_flashattn_visits_every_key_block():
+    assert recognize(programs.flashattn(1, 2, 256, 64, False, 64, 64)).family == "flashattn"
+    with pytest.raises(UnsupportedProgram, match="every key"):
+        recognize(programs.flashattn(1, 2, 256, 64, False, 64, 64, kv_blocks=3))

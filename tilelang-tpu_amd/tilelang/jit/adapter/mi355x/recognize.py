@@ -199,10 +199,13 @@ def _symbolic(pf):
             val[id(_buf(op.args[0]))] = ("exp", get(op.args[0]))
         elif n in ("ppl_rsqrt", "ppl_sigmoid"):
             val[id(_buf(op.args[0]))] = (n[4:], get(op.args[1]))
-        elif n == "ppl_reduce_sum":
+        elif n in ("ppl_reduce_sum", "ppl_reduce_max", "reduce_sum", "reduce_max"):
             if op.kwargs.get("dim", 1) not in (1, -1):
                 return None
-            val[id(_buf(op.args[1]))] = ("rsum", get(op.args[0]))
+            r = ("rsum" if "sum" in n else "rmax", get(op.args[0]))
+            if not op.kwargs.get("clear", True):  # accumulates into the output's contents
+                r = ("acc_" + r[0], get(op.args[1]), r)
+            val[id(_buf(op.args[1]))] = r
         elif n == "ppl_rope_add":
             val[id(_buf(op.args[0]))] = ("rope",) + tuple(get(a) for a in op.args[1:5])
         else:
@@ -372,6 +375,25 @@ def _rmsnorm(pf, names) -> Plan:
                          for o, e in stores):
         _fail(fam, "the stored value is not x * rsqrt(mean(x * x) + eps)" +
               ("" if w is None else " * w"))
+    # whole rows: every copy of x and every store to y spans the row (one tile, or column
+    # tiles stepped by a loop), all at one row-tile position; a row sum taken inside a loop is
+    # accumulated into a sum filled outside it (else only the last column tile would count)
+    rows = []
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        for g, t in ((src, db), (dst, sb)):
+            gb = _buf(g)
+            if gb is x or gb is y:
+                if t.scope == "global" or not _covers_rows(op, g, t, N):
+                    _fail(fam, f"a tile copy of {gb!r} does not span whole rows")
+                rows.append(_tile_map(pf, g, t, skip=-1))
+    if not rows or rows[0] is None or any(r != rows[0] for r in rows):
+        _fail(fam, "the tile copies of x and y are not at one row-tile position")
+    if red[0].loops:
+        fills = [op for op in _ops(pf, _FILL_OPS) if _buf(op.args[0]) is acc]
+        if len(fills) != 1 or any(lp in (fills[0].loops or ()) for lp in red[0].loops):
+            _fail(fam, "a row sum inside a loop must accumulate into a sum cleared outside it")
     outs = [_index(pf, y)]
     return Plan(fam, pf.params, outs, dict(
         x=_index(pf, x), w=None if w is None else _index(pf, w), y=outs[0], eps=eps,
@@ -579,6 +601,49 @@ def _gemm(pf, names) -> Plan:
                 all(e.args[0] is not op.args[0] for e in loads):
             _fail(fam, f"element store into {op.args[0]!r} is not the accumulator fold "
                        "acc2[i, j] += acc[i, j]; epilogues are not part of the gemm kernel")
+    # The tiles multiplied are the kernel's: A's row tile and B's column tile at C's tile
+    # position, both stepped over all of K by the loop around the gemm, into an accumulator
+    # cleared before that loop. (A clear inside it keeps only the tiles after the last clear,
+    # unless a fold into a second accumulator precedes it, and that fold must run on the last
+    # k tile: example_tilelang_gemm_fp8_2xAcc.py:36-44 folds every 128 / block_K tiles.)
+    kd_b = 1 if tb else 0
+    cmap = None
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if db is C and sb.scope != "global":
+            cmap = _tile_map(pf, dst, sb)
+    if cmap is None:
+        _fail(fam, "C is not stored as one tile of a grid covering it")
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if db.scope == "global" or sb not in (A, B) or (sb is A and sb is B):
+            continue
+        kd = 1 if sb is A else kd_b
+        m = _tile_map(pf, src, db, skip=kd)
+        if m is None or not _covers_rows(op, src, db, K, d=kd) or \
+                m[1 - kd] != (cmap[0] if sb is A else cmap[1]):
+            _fail(fam, f"the tile copies of {sb!r} do not step over all of K at C's tile "
+                       "position")
+    loops = g[0].loops or ()
+    folded = any(op.name == "store" for op in _ops(pf))
+    for op in _ops(pf, _FILL_OPS):
+        if _buf(op.args[0]) is acc and any(lp in (op.loops or ()) for lp in loops) and not folded:
+            _fail(fam, "the accumulator is cleared inside the k loop")
+    if loops:
+        names, last = [], {}
+        for lp in loops:
+            for v, ext in zip(lp.vars, lp.extents):
+                n = _extent_value(ext)
+                if n is None or not isinstance(v, Expr):
+                    _fail(fam, "k loop without a static extent")
+                last[v.args[0]] = n - 1
+        for op in pf.ops:
+            if op.name == "branch" and any(lp in (op.loops or ()) for lp in loops):
+                if not _eval_env(op.args[0], last):
+                    _fail(fam, "a branch inside the k loop is not taken on the last k tile, so "
+                               "the program leaves its last tiles out of C")
     return Plan(fam, pf.params, [_index(pf, C)], dict(
         a=_index(pf, A), b=_index(pf, B), c=_index(pf, C), M=M, N=N, K=K, trans_b=bool(tb),
         in_dtype=A.dtype, out_dtype=C.dtype,
@@ -666,6 +731,22 @@ def _flashattn(pf, names) -> Plan:
                     sm_scale = cs[0] / LOG2E_REF
         if sm_scale is None:
             _fail(fam, "could not read the softmax scale")
+    # Output's tile is stored where Q's tile was read, and without a causal bound the K and V
+    # tiles step over every key
+    qm = om = None
+    seqd = 2 if bhsd else 1
+    for op in _ops(pf, _COPY):
+        src, dst = op.args[0], op.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if sb is Q and db.scope != "global":
+            qm = _tile_map(pf, src, db)
+        elif db is O and sb.scope != "global":
+            om = _tile_map(pf, dst, sb)
+        elif sb in (K, V) and db.scope != "global" and not causal and \
+                not _covers_rows(op, src, db, kshp[seqd], d=seqd):
+            _fail(fam, f"the tile copies of {sb!r} do not step over every key")
+    if qm is None or qm != om:
+        _fail(fam, "Output's tile is not stored at the position its Q tile was read from")
     if bhsd:
         # example_mha_fwd_bhsd.py:50-55 masks with q_idx = bx * block_M + i + seq_kv - seq_q
         # while its loop bound (:139-141) stops at key (bx + 1) * block_M and its reference
@@ -1113,6 +1194,26 @@ def _row_reduce(pf, names) -> Plan:
     xs, ys = _shape(x), _shape(y)
     if math.prod(ys) != math.prod(xs[:-1]):
         _fail(fam, f"Y{ys} does not hold one value per row of X{xs}")
+    # one reduction of whole rows, stored as computed: a tile narrower than the row (or a
+    # reduction repeated over column tiles) reduces only part of each row, and a max that does
+    # not clear its output also takes the output's previous contents
+    if op.loops or ("max" in op.name and not op.kwargs.get("clear", True)):
+        _fail(fam, "expected one clearing reduction outside loops")
+    want = ("rsum" if "sum" in op.name else "rmax", ("load", _index(pf, x)))
+    if _symbolic(pf) != [(_index(pf, y), want)]:
+        _fail(fam, "the program stores something other than the row reduction of X")
+    maps = []
+    for cop in _ops(pf, _COPY):
+        src, dst = cop.args[0], cop.args[1]
+        sb, db = _buf(src), _buf(dst)
+        if sb is x:
+            if not _covers_rows(cop, src, db, xs[-1]):
+                _fail(fam, "the tile copy of X does not span whole rows")
+            maps.append(_tile_map(pf, src, db, skip=-1))
+        elif db is y:
+            maps.append(_tile_map(pf, dst, sb, skip=-1))
+    if len(maps) != 2 or maps[0] is None or maps[0][:-1] != maps[1][:len(maps[0]) - 1]:
+        _fail(fam, "the tile copies of X and Y are not at one row-tile position")
     if x.dtype not in ("float32", "float16", "bfloat16") or \
             y.dtype not in ("float32", "float16", "bfloat16"):
         _fail(fam, f"dtypes {x.dtype} -> {y.dtype}")
@@ -1183,12 +1284,73 @@ def _extent_value(ex) -> Optional[int]:
     return vals.pop() if len(vals) == 1 and None not in vals else None
 
 
-def _tile_map(pf, access, tile: Buffer):
+def _eval_env(e, env: Dict[str, int]):
+    """Integer value of an index expression of +, -, * with variables from ``env`` (others 0)."""
+    if isinstance(e, bool):
+        return None
+    if isinstance(e, int):
+        return e
+    if isinstance(e, Expr):
+        if e.op == "const" and isinstance(e.args[0], int):
+            return e.args[0]
+        if e.op == "var":
+            return env.get(e.args[0], 0)
+        if e.op in _INT_OPS and len(e.args) == 2:
+            a, b = _eval_env(e.args[0], env), _eval_env(e.args[1], env)
+            if a is None or b is None or (e.op in ("mod", "floordiv") and b == 0):
+                return None
+            return int(_INT_OPS[e.op](a, b))
+    return None
+
+
+_INT_OPS = {"add": lambda a, b: a + b, "sub": lambda a, b: a - b, "mul": lambda a, b: a * b,
+            "mod": lambda a, b: a % b, "floordiv": lambda a, b: a // b,
+            "eq": lambda a, b: a == b, "ne": lambda a, b: a != b, "lt": lambda a, b: a < b,
+            "le": lambda a, b: a <= b, "gt": lambda a, b: a > b, "ge": lambda a, b: a >= b,
+            "and": lambda a, b: bool(a) and bool(b), "or": lambda a, b: bool(a) or bool(b)}
+
+
+def _covers_rows(op, access, tile: Buffer, ncols: int, d: int = -1) -> bool:
+    """Whether the tile copy ``access`` of ``op`` reads or writes whole rows of its parameter
+    over all iterations of the loops around it: column starts 0, w, 2w, ... (in any order, each
+    once) for a tile w columns wide, together spanning the ``ncols`` columns. ``d`` names
+    another dimension to check the same way (the k dimension of a GEMM operand)."""
+    if isinstance(access, Buffer):
+        return True
+    starts, exts = access.region(tile.shape)
+    w = _extent_value(exts[d])
+    if w is None or w <= 0:
+        return False
+    names, ranges = [], []
+    for lp in op.loops or ():
+        for v, ext in zip(lp.vars, lp.extents):
+            n = _extent_value(ext)
+            if n is None or n <= 0 or not isinstance(v, Expr):
+                return False
+            names.append(v.args[0])
+            ranges.append(n)
+    if math.prod(ranges) > 4096:
+        return False
+    cols = []
+    for it in range(math.prod(ranges)):
+        env, r = {}, it
+        for name, n in zip(names, ranges):
+            env[name], r = r % n, r // n
+        c = _eval_env(starts[d], env)
+        if c is None:
+            return False
+        cols.append(c)
+    e = len(cols)
+    return sorted(cols) == [i * w for i in range(e)] and (e - 1) * w < ncols <= e * w
+
+
+def _tile_map(pf, access, tile: Buffer, skip: Optional[int] = None):
     """Grid mapping of the tile copy ``access`` of a global parameter, or None when the copy is
     not the (i, j)-th tile of a grid that covers the parameter exactly. Per dimension the entry
     is None (the whole or unit dimension, or a tile as long as the dimension) or (grid variable
     name, tile extent) for a start of grid_var * t with extent t and a grid extent of
-    ceil(dim / t)."""
+    ceil(dim / t). ``skip``: a dimension that is not examined (entry None), such as the
+    column dimension of a copy stepped over columns by a loop."""
     buf = access.buffer if isinstance(access, BufferAccess) else access
     dims = _shape(buf)
     if isinstance(access, Buffer):
@@ -1196,6 +1358,9 @@ def _tile_map(pf, access, tile: Buffer):
     starts, exts = access.region(tile.shape)
     out = []
     for d, (st, ex) in enumerate(zip(starts, exts)):
+        if skip is not None and d == skip % len(dims):
+            out.append(None)
+            continue
         t = _extent_value(ex)
         try:
             s0 = int(ir.const_value(st))

@@ -484,10 +484,12 @@ def deepseek_mlp_fp32(Block_bs, Block_h, Block_i, batch_seq, hidden_size, interm
 
 
 def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
-              dtype="bfloat16", gemm_dtype=None):
+              dtype="bfloat16", gemm_dtype=None, kv_blocks=None):
     """tpu_test_flashattn_bf16.py:14-135 (fp16 twin); dtype float32 with gemm_dtype float16
     gives tpu_test_flashattn_fp32.py: Q, K, V tiles and P copied to fp16 tiles for the two
-    ppl_gemm, softmax state, acc_o and the output in fp32."""
+    ppl_gemm, softmax state, acc_o and the output in fp32. kv_blocks (non-causal) sets the
+    number of key blocks the loop visits (default all: a program over fewer attends to a
+    prefix of the keys, which the recogniser rejects)."""
     scale = (1.0 / dim) ** 0.5
     shape = [batch, seq_len, heads, dim]
     acc = "float32"
@@ -517,7 +519,7 @@ def flashattn(batch, heads, seq_len, dim, is_causal, block_M=128, block_N=128,
             T.ppl_fill(l, T.float32(0))
             T.ppl_fill(m, -T.infinity(acc))
             n_kv = (T.min(T.ceildiv(seq_len, block_N), T.ceildiv((bx + 1) * block_M, block_N))
-                    if is_causal else T.ceildiv(seq_len, block_N))
+                    if is_causal else kv_blocks or T.ceildiv(seq_len, block_N))
             for k in T.Pipelined(n_kv, num_stages=2):
                 T.ppl_copy(K[bz, k * block_N:(k + 1) * block_N, by, :], k_s)
                 T.ppl_fill(s, T.float32(0))
