@@ -817,3 +817,44 @@ def test_flashattn_visits_every_key_block():
     assert recognize(programs.flashattn(1, 2, 256, 64, False, 64, 64)).family == "flashattn"
     with pytest.raises(UnsupportedProgram, match="every key"):
         recognize(programs.flashattn(1, 2, 256, 64, False, 64, 64, kv_blocks=3))
+
+
+def test_mlp_expression_checked():
+    """The down projection must multiply up * silu(gate); silu(gate) * gate is another MLP."""
+    M, Hd, I, dt, acc = 16, 64, 128, "bfloat16", "float32"
+
+    def prog(second):
+        @T.prim_func
+        def main(output: T.Tensor((M, Hd), dt), x: T.Tensor((M, Hd), dt),
+                 gate_weight: T.Tensor((I, Hd), dt), up_weight: T.Tensor((I, Hd), dt),
+                 down_weight: T.Tensor((Hd, I), dt)):
+            with T.Kernel(1, 1, 1, is_cpu=True) as (bx, by, bz):
+                xb = T.alloc_shared((M, Hd), dt)
+                wg, wu = T.alloc_shared((I, Hd), dt), T.alloc_shared((I, Hd), dt)
+                wd = T.alloc_shared((Hd, I), dt)
+                g16, u16 = T.alloc_shared((M, I), dt), T.alloc_shared((M, I), dt)
+                d16, h16 = T.alloc_shared((M, Hd), dt), T.alloc_shared((M, I), dt)
+                g32, u32, s32, h32, neg, ones, den = (T.alloc_shared((M, I), acc)
+                                                      for _ in range(7))
+                T.ppl_fill(ones, T.float32(1.0))
+                T.ppl_copy(x[0:M, 0:Hd], xb)
+                T.ppl_copy(gate_weight[0:I, 0:Hd], wg)
+                T.ppl_copy(up_weight[0:I, 0:Hd], wu)
+                T.ppl_copy(down_weight[0:Hd, 0:I], wd)
+                T.ppl_gemm(xb, wg, g16, transpose_B=True)
+                T.ppl_copy(g16, g32)
+                T.ppl_mul_C(neg, g32, T.float32(-1.0))
+                T.ppl_exp2(neg)
+                T.ppl_add(den, neg, ones)
+                T.ppl_div(s32, g32, den)
+                T.ppl_gemm(xb, wu, u16, transpose_B=True)
+                T.ppl_copy(u16, u32)
+                T.ppl_mul(h32, s32, u32 if second == "up" else g32)
+                T.ppl_copy(h32, h16)
+                T.ppl_gemm(h16, wd, d16, transpose_B=True)
+                T.ppl_copy(d16, output[0:M, 0:Hd])
+        return main
+
+    assert recognize(prog("up")).family == "mlp"
+    with pytest.raises(UnsupportedProgram, match="silu"):
+        recognize(prog("gate"))

@@ -149,10 +149,12 @@ def _index(pf, buf) -> int:
     raise UnsupportedProgram(f"{buf!r} is not a parameter")
 
 
-def _symbolic(pf):
+def _symbolic(pf, gemms: Optional[List] = None):
     """The values a program stores, as expressions over its parameters: a list of
     (parameter index, expression) per store to a parameter, in program order, or None when the
-    program uses an op outside the elementwise / row-reduce / rope vocabulary.
+    program uses an op outside the elementwise / row-reduce / rope vocabulary (or a gemm, when
+    ``gemms`` is None; otherwise each gemm appends (op, ("gemm", a, b)) to it and its result
+    tile takes that value).
 
     Tiles are followed through the program in order, so a tile written twice (``x = x * r``)
     carries its latest value. Expressions are tuples: ("load", i) for a tile copied from
@@ -208,6 +210,10 @@ def _symbolic(pf):
             val[id(_buf(op.args[1]))] = r
         elif n == "ppl_rope_add":
             val[id(_buf(op.args[0]))] = ("rope",) + tuple(get(a) for a in op.args[1:5])
+        elif n in _GEMM and gemms is not None:
+            r = ("gemm", get(op.args[0]), get(op.args[1]))
+            gemms.append((op, r))
+            val[id(_buf(op.args[2]))] = r
         else:
             return None
     return stores
@@ -881,6 +887,19 @@ def _mlp(pf, names) -> Plan:
         _fail(fam, "the projections must multiply and store 16-bit tiles of one dtype (the "
                    "parameter dtype for 16-bit parameters)")
     operand = next(iter(tdt)) if dt == "float32" else None
+    # what the down projection multiplies and what is stored: up * (gate / (exp(-gate) + 1))
+    # of the two projections of x, and the down projection of it
+    recs: List[tuple] = []
+    stores = _symbolic(pf, recs)
+    ex = {id(op): r for op, r in recs}
+    G, U, D = ex.get(id(gate)), ex.get(id(up)), ex.get(id(down))
+    if stores is None or None in (G, U, D) or \
+            D[1] != _mul(U, ("div", G, _add(("exp", _neg(G)), ("const", 1.0)))) or \
+            stores != [(_index(pf, out), D)] or G[1] != ("load", _index(pf, x)) or \
+            U[1] != G[1] or G[2] != ("load", _index(pf, wg)) or \
+            U[2] != ("load", _index(pf, wu)) or D[2] != ("load", _index(pf, wd)):
+        _fail(fam, "the program does not store down(up * silu(gate)) of x's gate and up "
+                   "projections")
     bh, bi = _shape(a[i])[1], _shape(_buf(gate.args[1]))[0]
     if bh != Hd or bi != I:
         _fail(fam, f"blocks of {bh} hidden / {bi} intermediate columns: each workgroup reduces "
