@@ -134,3 +134,26 @@ def test_grouped_kv_heads_equal_repeated_heads(D):
     torch_assert_close(outs[0][2].float(),
                        ref.mha_inference_ref(q.cpu(), rep(kk).cpu(), rep(v).cpu()),
                        atol=1e-2, rtol=1e-2)
+
+
+def test_one_kernel_on_two_streams():
+    """One compiled program called on two streams whose work overlaps: each stream has its own
+    workspace, so both results equal the program's on their own inputs."""
+    B, H, Sq, Skv, D, ns = 1, 8, 64, 2048, 128, 4
+    k = tilelang.compile(programs.mha_inference(B, H, Sq, Skv, D), out_idx=[5])
+    ins = [_qkv(B, Sq, Skv, H, D, 120 + i) for i in range(2)]
+    dev_ins = [tuple(x.to(DEV) for x in qkv) for qkv in ins]
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = []
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for s, (q, kk, v) in zip(streams, dev_ins):
+            with torch.cuda.stream(s):
+                glse = torch.empty(B, H, ns, Sq, dtype=torch.float16, device=DEV)
+                part = torch.empty(B, Sq, H, ns, D, dtype=torch.float16, device=DEV)
+                outs.append(k(q, kk, v, glse, part))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        q, kk, v = ins[i % 2]
+        torch_assert_close(o.cpu().float(), ref.mha_inference_ref(q, kk, v), atol=1e-2,
+                           rtol=1e-2)

@@ -114,3 +114,24 @@ def test_upstream_program_generic_heads():
     g, op = torch.empty(B, H, 1, dtype=torch.float16), torch.empty(B, H, 1, dv, dtype=torch.float16)
     out = k(*(x.to(DEV) for x in (q, qpe, kv, kpe, g, op))).cpu()
     torch_assert_close(out, ref.mla_decode_nopage_ref(q, qpe, kv, kpe), atol=1e-2, rtol=1e-2)
+
+
+def test_one_kernel_on_two_streams():
+    """One compiled program on two streams whose work overlaps: each stream keeps its own
+    workspace and identity table, so both results are the program's on their own inputs."""
+    B, H, S, dv, dpe = 4, 128, 1024, 512, 64
+    k = tilelang.compile(programs.mla_decode_nopage(B, H, S, dv, dpe, num_split=1), out_idx=[6])
+    ins = [_inputs(B, H, S, dv, dpe, 130 + i) for i in range(2)]
+    dev_ins = [tuple(x.to(DEV) for x in t) for t in ins]
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = []
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for s, (q, qpe, kv, kpe) in zip(streams, dev_ins):
+            with torch.cuda.stream(s):
+                glse = torch.empty(B, H, 1, dtype=torch.float16, device=DEV)
+                opart = torch.empty(B, H, 1, dv, dtype=torch.float16, device=DEV)
+                outs.append(k(q, qpe, kv, kpe, glse, opart))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        torch_assert_close(o.cpu(), ref.mla_decode_nopage_ref(*ins[i % 2]), atol=1e-2, rtol=1e-2)

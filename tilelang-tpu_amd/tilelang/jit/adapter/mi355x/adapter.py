@@ -41,6 +41,12 @@ def _eval_extent(s, env):
     return int(ir.const_value(v))
 
 
+def _stream_key(dev):
+    """Workspaces are kept per device and stream: the kernels of one stream run in order, so a
+    stream's calls can share its workspace, while calls on two streams may overlap."""
+    return (dev, torch.cuda.current_stream(dev).cuda_stream)
+
+
 def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     a = plan.attrs
     f = plan.family
@@ -65,7 +71,7 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
         q = t[a["q"]]
         need = ops.flash_attn_splitkv_workspace_bytes(a["B"], a["S"], a["S_kv"], a["H"], a["D"],
                                                       a["num_split"])
-        key = (q.device, "splitkv")
+        key = (_stream_key(q.device), "splitkv")
         ws = workspace_cache.get(key)
         if ws is None or ws.numel() < need:
             ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
@@ -110,10 +116,10 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
         q = t[a["q"]]
         dev = q.device
         need = ops.mla_workspace_bytes(a["B"], a["Hq"], a["dv"], a["num_split"])
-        ws = workspace_cache.get(dev)
+        ws = workspace_cache.get(_stream_key(dev))
         if ws is None or ws.numel() < need:
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
-            workspace_cache[dev] = ws
+            workspace_cache[_stream_key(dev)] = ws
         kvs = None if a["kv_scale"] is None else t[a["kv_scale"]]
         B, Hq, dv, dpe = a["B"], a["Hq"], a["dv"], a["dpe"]
         if a["paged"]:
@@ -121,8 +127,8 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
             qq, qpe, o = q, t[a["q_pe"]], t[a["o"]]
         else:
             # non-paged cache [B, S, 1, d]: token t of sequence b is row b * S + t, i.e. one page
-            # of S tokens per sequence under the identity table (kept per device and shape)
-            key = (dev, "identity", B, a["seqlen_kv"])
+            # of S tokens per sequence under the identity table (kept per device, stream and shape)
+            key = (_stream_key(dev), "identity", B, a["seqlen_kv"])
             if key not in workspace_cache:
                 workspace_cache[key] = (
                     torch.arange(B, dtype=torch.int32, device=dev).view(B, 1),
