@@ -115,7 +115,12 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
     elif f == "mla":
         q = t[a["q"]]
         dev = q.device
-        need = ops.mla_workspace_bytes(a["B"], a["Hq"], a["dv"], a["num_split"])
+        # A program that does not write its partials leaves the key split to the kernels: about
+        # one workgroup per CU (B * splits workgroups), as the balanced FP8 decode and the split
+        # kernel both launch. The split program writes one partial per split of its own
+        # partition, so it runs with its num_split.
+        ns = a["num_split"] if a.get("partials") else max(1, min(64, -(-256 // max(1, a["B"]))))
+        need = ops.mla_workspace_bytes(a["B"], a["Hq"], a["dv"], ns)
         ws = workspace_cache.get(_stream_key(dev))
         if ws is None or ws.numel() < need:
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
@@ -143,8 +148,8 @@ def _run_plan(plan, t: List[torch.Tensor], workspace_cache: dict):
             if not a["paged"]:
                 g = g.view(B, Hq, a["num_split"])
                 op = op.view(B, Hq, a["num_split"], dv)
-        ops.mla_decode(qq, qpe, t[a["kv"]], t[a["k_pe"]], bt, sl, o, ws, a["page"],
-                       a["num_split"], a["sm_scale"], kvs, glse=g, o_partial=op,
+        ops.mla_decode(qq, qpe, t[a["kv"]], t[a["k_pe"]], bt, sl, o, ws, a["page"], ns,
+                       a["sm_scale"], kvs, glse=g, o_partial=op,
                        part_block=a.get("part_block", 64))
     elif f == "elementwise":
         ops.elementwise([t[i] for i in a["inputs"]], a["bcast"], [t[i] for i in a["outputs"]],
