@@ -374,6 +374,45 @@ __global__ __launch_bounds__(256) void mla_partial_combine(
                                        HO::pack(acc[2] * inv, acc[3] * inv)};
 }
 
+// The same combine over the fp8 decode's segments (tlm_mla_fp8_launch_segments): split s of
+// sequence b, head h is row (b ns + s) Hq + h of seg_o (bf16, normalised, times kv_scale) and
+// seg_lse (fp32, -inf for a split without tokens).
+template <int PK, bool OUT_BF16>
+__global__ __launch_bounds__(128) void mla_segment_combine(
+    const uint16_t* __restrict__ seg_o, const float* __restrict__ seg_lse, void* __restrict__ glse,
+    void* __restrict__ opart, uint16_t* __restrict__ out, int num_split, int Hq) {
+  using PS = part_store<PK>;
+  using HO = h16<OUT_BF16>;
+  using HB = h16<true>;
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / Hq, h = bh % Hq;
+  const int d = threadIdx.x * 4;
+  float M = -INFINITY, L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < num_split; ++s) {
+    const int64_t srow = (b * num_split + s) * Hq + h;
+    const float l0 = seg_lse[srow];
+    if (threadIdx.x == 0) PS::put_lse(glse, bh * num_split + s, l0);
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (l0 != -INFINITY) {
+      const u32x2 x = *(const u32x2*)(seg_o + srow * MLA_DV + d);
+      v = f32x4{HB::lo(x[0]), HB::hi(x[0]), HB::lo(x[1]), HB::hi(x[1])};
+    }
+    const f32x4 vr = PS::put4(opart, (bh * num_split + s) * MLA_DV + d, v);
+    const float lr = PS::round(l0);  // the stored values, as read back
+    if (lr != -INFINITY) {
+      const float Mn = fmaxf(M, lr);
+      const float a = fast_exp2(M - Mn), w = fast_exp2(lr - Mn);  // a = 0 while M = -inf
+      L = L * a + w;
+      acc = acc * a + vr * w;
+      M = Mn;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  *(u32x2*)(out + bh * MLA_DV + d) = u32x2{HO::pack(acc[0] * inv, acc[1] * inv),
+                                           HO::pack(acc[2] * inv, acc[3] * inv)};
+}
+
 // ------------------------------------------------------------------------------------------------
 // Paged gather: one 64-lane wave per token row; rows resolved through the block table exactly
 // as the decode kernel resolves them (example_mla_decode_paged.py:62-63).
@@ -551,6 +590,22 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
                        void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
                        int num_split, float score_scale, const float* kv_scale, bool q_bf16,
                        bool o_bf16, void* stream);
+size_t tlm_mla_fp8_segments_workspace_bytes(int64_t B, int64_t Hq, int num_split, int par);
+int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_stride,
+                                int64_t q_pe_stride, const void* kv, const void* k_pe,
+                                int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                                const int32_t* block_table, const int32_t* seqlens, void* ws,
+                                int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                                int num_split, int par, float score_scale,
+                                const float* kv_scale, bool q_bf16, void* stream,
+                                const uint16_t** seg_o, const float** seg_lse);
+
+// Ranges of the split programs' fp8 path: the program's splits, or more when that leaves CUs
+// idle (about 256 workgroups over all head groups)
+static int mla_seg_par(int64_t B, int num_split) {
+  const int64_t fill = (256 + std::max<int64_t>(B, 1) - 1) / std::max<int64_t>(B, 1);
+  return (int)std::max<int64_t>(num_split, std::min<int64_t>(64, fill));
+}
 
 // Workspace bytes of the two paths: the fp8 matrix-core path (fp8 KV, page a multiple of 64, Hq
 // a multiple of 64; its own layout) and the split path (fp32 partial outputs + log2-sum-exp,
@@ -561,9 +616,11 @@ static size_t mla_split_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int n
 
 extern "C" size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split) {
   if (B <= 0 || Hq <= 0 || dv <= 0 || num_split <= 0) return 0;
-  // the larger of the two layouts serves both paths
-  return std::max(mla_split_workspace_bytes(B, Hq, dv, num_split),
-                  tlm_mla_fp8_workspace_bytes(B, Hq, num_split));
+  // the largest layout serves every path (the split programs' fp8 path included)
+  return std::max({mla_split_workspace_bytes(B, Hq, dv, num_split),
+                   tlm_mla_fp8_workspace_bytes(B, Hq, num_split),
+                   tlm_mla_fp8_segments_workspace_bytes(B, Hq, num_split,
+                                                        mla_seg_par(B, num_split))});
 }
 
 // The matrix-core kernels take dv = 512, dpe = 64, Hq a multiple of 64 and 16-byte aligned Q / KV
@@ -645,6 +702,38 @@ static int mla_run(const char* fn, const void* q, const void* q_pe, int64_t q_st
   const bool partials = glse != nullptr && opart != nullptr;
   const bool fast = mla_fast_shape(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
                                    kpe_stride, o, Hq, dv, dpe, kv_dtype);
+  if (partials && fast && kv_dtype == TLM_F8E4M3 && part_block == 64 &&
+      dv == MLA_DV && tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride) &&
+      tlm_mla_fp8_segments_workspace_bytes(B, Hq, num_split, mla_seg_par(B, num_split)) > 0 &&
+      ws_bytes >= tlm_mla_fp8_segments_workspace_bytes(B, Hq, num_split,
+                                                       mla_seg_par(B, num_split))) {
+    // the program's partition (64-token blocks) on the balanced 128-head fp8 decode: each split
+    // is a segment of its sequence, then the partials and Output as above
+    const uint16_t* seg_o = nullptr;
+    const float* seg_lse = nullptr;
+    int rc = tlm_mla_fp8_launch_segments(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
+                                         kpe_stride, kv_rows, block_table, seqlens, ws, B, Hq,
+                                         page, max_pages, num_split, mla_seg_par(B, num_split),
+                                         sc, kv_scale, q_dtype == TLM_BF16, stream, &seg_o,
+                                         &seg_lse);
+    if (rc == TLM_OK) {
+      hipStream_t st = (hipStream_t)stream;
+      auto comb = [&](auto kern) {
+        kern<<<(unsigned)(B * Hq), MLA_DV / 4, 0, st>>>(seg_o, seg_lse, glse, opart,
+                                                        (uint16_t*)o, num_split, (int)Hq);
+      };
+      const bool ob = o_dtype == TLM_BF16;
+      if (p_dtype == TLM_F32)
+        ob ? comb(mla_segment_combine<2, true>) : comb(mla_segment_combine<2, false>);
+      else if (p_dtype == TLM_BF16)
+        ob ? comb(mla_segment_combine<1, true>) : comb(mla_segment_combine<1, false>);
+      else
+        ob ? comb(mla_segment_combine<0, true>) : comb(mla_segment_combine<0, false>);
+      TLM_LAUNCH_CHECK("tlm_mla_decode (segment combine)");
+      return TLM_OK;
+    }
+    if (rc != TLM_EUNSUPPORTED) return rc;
+  }
   if (partials) {
     // the program's own split partition, its partials stored, Output from the stored values
     if (ws_bytes < mla_split_workspace_bytes(B, Hq, dv, num_split)) {

@@ -273,7 +273,30 @@ struct F8Args {
   int lmax;           // seqlens are clamped to [0, lmax = max_pages * page]
   float score_scale;  // sm_scale * log2(e)
   const float* kv_scale;
+  // Split programs (glse / Output_partial written): the decode runs over B = batch * nsp
+  // segments, segment v being split v % nsp of sequence v / nsp in the program's partition;
+  // `out` then holds each segment's normalised rows (bf16) and seg_lse its log2 sum-exp.
+  // nsp == 1, seg_lse == nullptr: the segments are the sequences.
+  int nsp;
+  float* seg_lse;
 };
+
+// Segment v: its sequence, first token, valid tokens and 64-token tiles (Lraw: the sequence's
+// cache length). Split s of a sequence of T 64-token blocks takes T / nsp blocks, one more for
+// s < T % nsp, starting after the earlier splits' blocks (example_mla_decode_paged.py:140-144
+// with block_N = 64).
+struct F8Seg {
+  int b, start, len, ntiles;
+};
+TLM_DEV int f8_seq(const F8Args& a, int v) { return a.nsp == 1 ? v : v / a.nsp; }
+TLM_DEV F8Seg f8_seg(const F8Args& a, int v, int Lraw) {
+  const int L = max(0, min(Lraw, a.lmax));
+  if (a.nsp == 1) return F8Seg{v, 0, L, (L + F8_TILE - 1) / F8_TILE};
+  const int b = v / a.nsp, sp = v - b * a.nsp;
+  const int tb = (L + F8_TILE - 1) / F8_TILE, bps = tb / a.nsp, rem = tb - bps * a.nsp;
+  const int n = bps + (sp < rem ? 1 : 0), st = (bps * sp + min(sp, rem)) * F8_TILE;
+  return F8Seg{b, st, max(0, min(n * F8_TILE, L - st)), n};
+}
 
 constexpr int F8_QROW = 2 * (F8_DV + F8_DPE);  // bytes per (sequence, head) in qsplit
 
@@ -306,10 +329,7 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
     const int t = threadIdx.x;
     const int per = (a.B + 255) / 256;
     const int b0 = min(a.B, t * per), b1 = min(a.B, b0 + per);
-    auto tiles = [&](int b) {
-      const int L = max(0, min(a.seqlens[b], a.lmax));
-      return (L + F8_TILE - 1) / F8_TILE;
-    };
+    auto tiles = [&](int v) { return f8_seg(a, v, a.seqlens[f8_seq(a, v)]).ntiles; };
     auto cost = [&](int n) { return n ? n + F8_PIECE_COST : 0; };
     int32_t sum = 0, vsum = 0;
     for (int b = b0; b < b1; ++b) {
@@ -356,7 +376,7 @@ __global__ __launch_bounds__(256) void mla_fp8_prep(const F8Args a, int nq) {
   using H = h16<Q_BF16>;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)(blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)a.B * a.Hq) return;
+  if (row >= (int64_t)(a.B / a.nsp) * a.Hq) return;
   // lane: latent dims 8 lane .. +7; lanes 0..7 also rope dims 8 lane .. +7
   const u32x4 wl = *(const u32x4*)(a.q + row * a.q_stride + 8 * lane);
   const bool has_pe = lane < 8;
@@ -1018,11 +1038,12 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
         if (a.cu[mid] <= tj) blo = mid; else bhi = mid - 1;
       }
       tab_b = blo;
-      const int L = max(0, min(a.seqlens[blo], a.lmax));
-      const int tok0 = (tj - a.cu[blo]) * F8_TILE;
-      const int valid = min(F8_TILE, L - tok0);
+      const F8Seg sg = f8_seg(a, blo, a.seqlens[f8_seq(a, blo)]);
+      const int tok0 = (tj - a.cu[blo]) * F8_TILE;  // within the segment
+      const int valid = min(F8_TILE, sg.len - tok0);
+      const int tk = sg.start + tok0;  // within the sequence
       const int64_t row0 =
-          (int64_t)a.bt[(int64_t)blo * a.max_pages + tok0 / a.page] * a.page + tok0 % a.page;
+          (int64_t)a.bt[(int64_t)sg.b * a.max_pages + tk / a.page] * a.page + tk % a.page;
       int64_t nrow = min((int64_t)valid, a.kv_rows - row0);
       if (row0 < 0 || nrow < 0) nrow = 0;
       tab_lo = (uint32_t)row0;
@@ -1187,8 +1208,9 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
       cb_lo = cb_hi;
       cb_hi = ldc(a.cu + cb + 1);
     }
-    L = max(0, min(ldc(a.seqlens + cb), a.lmax));
-    const int64_t qr0 = (int64_t)cb * a.Hq + head0;  // the wave's first Q row (uniform)
+    const F8Seg sg = f8_seg(a, cb, ldc(a.seqlens + f8_seq(a, cb)));
+    L = sg.len;
+    const int64_t qr0 = (int64_t)sg.b * a.Hq + head0;  // the wave's first Q row (uniform)
     const uint8_t* qs = a.qsplit + (qr0 + hh) * F8_QROW;
 #pragma unroll
     for (int s = 0; s < 9; ++s) qhi[s] = *(const i32x8*)(qs + 64 * s + 32 * hf);
@@ -1448,7 +1470,8 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
     const int64_t sb = (int64_t)g * F8_SLOTS + slot;
     uint16_t* const rows = complete ? a.out + ((int64_t)cb * a.Hq + head0) * F8_DV
                                     : a.part_o + (sb * a.Hq + head0) * F8_DV;
-    float* const lse_at = complete ? nullptr : a.part_lse + sb * a.Hq + head;
+    float* const lse_at = !complete ? a.part_lse + sb * a.Hq + head
+                          : a.seg_lse ? a.seg_lse + (int64_t)cb * a.Hq + head : nullptr;
     const float lse = mref + __log2f(lsum), w = kvs / lsum;
     if (t < t_hi) begin_piece();
     wg_barrier();
@@ -1476,6 +1499,7 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   const int64_t V = ldc(a.vcu + a.B), v0 = ldc(a.vcu + b), v1 = ldc(a.vcu + b + 1);
   if (v0 == v1) {
     *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
+    if (a.seg_lse && d0 == 0) a.seg_lse[row] = -INFINITY;
     return;
   }
   const int64_t G = a.G;
@@ -1540,6 +1564,7 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   const float inv = 1.0f / l;
   acc[0] *= inv;
   acc[1] *= inv;
+  if (a.seg_lse && d0 == 0) a.seg_lse[row] = m + __log2f(l);
   st_cp<F8_CMB_STORE_CP>(a.out + row * F8_DV, 2 * d0,
                          u32x4{H::pack(acc[0][0], acc[0][1]), H::pack(acc[0][2], acc[0][3]),
                                H::pack(acc[1][0], acc[1][1]), H::pack(acc[1][2], acc[1][3])});
@@ -1581,15 +1606,24 @@ bool tlm_mla_fp8_applies(int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
          kpe_stride <= (1 << 24) && B * tiles_per_seq <= INT32_MAX;
 }
 
-// Returns TLM_EUNSUPPORTED (launching nothing) when the shape is outside this kernel's domain.
-int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
-                       const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
-                       int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
-                       void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
-                       int num_split, float score_scale, const float* kv_scale, bool q_bf16,
-                       bool o_bf16, void* stream) {
-  if (!tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride))
-    return TLM_EUNSUPPORTED;
+// Workspace of the split programs' path (tlm_mla_fp8_launch_segments): the fp8 path's layout over
+// B * num_split segments and the ranges of `par` (Q terms still per sequence), then each
+// segment's bf16 rows and fp32 lse.
+size_t tlm_mla_fp8_segments_workspace_bytes(int64_t B, int64_t Hq, int num_split, int par) {
+  if (Hq % W_HEADS) return 0;
+  const int64_t Bv = B * num_split;
+  const size_t G = (size_t)f8_ranges(B, Hq, par);
+  return f8_cu_bytes(Bv, (int64_t)G) + f8_q_bytes(B, Hq) +
+         G * F8_SLOTS * (size_t)Hq * (F8_DV * sizeof(uint16_t) + sizeof(float)) +
+         f8_align((size_t)Bv * Hq * F8_DV * sizeof(uint16_t)) + f8_align((size_t)Bv * Hq * 4);
+}
+
+namespace {
+
+F8Args f8_args(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+               const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+               int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens, int64_t page,
+               int64_t max_pages, float score_scale, const float* kv_scale) {
   F8Args a;
   a.q = (const uint16_t*)q;
   a.q_pe = (const uint16_t*)q_pe;
@@ -1602,24 +1636,33 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
   a.kv_rows = kv_rows;
   a.bt = block_table;
   a.seqlens = seqlens;
-  const int64_t G = f8_ranges(B, Hq, num_split);
-  a.cu = (int32_t*)ws;
-  a.vcu = a.cu + (B + 1);
-  a.range_t = (int32_t*)((char*)ws + f8_align((size_t)(B + 1) * 8));
-  a.qsplit = (uint8_t*)ws + f8_cu_bytes(B, G);
-  a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
-  a.part_lse = (float*)((char*)ws + f8_cu_bytes(B, G) + f8_q_bytes(B, Hq));
-  a.part_o = (uint16_t*)(a.part_lse + G * F8_SLOTS * Hq);
-  a.out = (uint16_t*)o;
-  a.B = (int)B;
-  a.Hq = (int)Hq;
   a.page = (int)page;
   a.max_pages = (int)max_pages;
-  a.G = (int)G;
   a.lmax = (int)(max_pages * page);
   a.score_scale = score_scale;
   a.kv_scale = kv_scale;
-  hipStream_t st = (hipStream_t)stream;
+  a.nsp = 1;
+  a.seg_lse = nullptr;
+  return a;
+}
+
+// Prep, decode and combine over B * nsp segments (nsp splits of each of B sequences) cut into G
+// ranges; the workspace starts with the prefixes and range starts, then the Q terms of the B
+// sequences and the partial slots of the G ranges.
+int f8_run(F8Args& a, void* ws, int64_t B, int64_t Hq, int nsp, int64_t G, bool q_bf16,
+           bool o_bf16, hipStream_t st) {
+  const int64_t Bv = B * nsp;
+  a.cu = (int32_t*)ws;
+  a.vcu = a.cu + (Bv + 1);
+  a.range_t = (int32_t*)((char*)ws + f8_align((size_t)(Bv + 1) * 8));
+  a.qsplit = (uint8_t*)ws + f8_cu_bytes(Bv, G);
+  a.qexp = (int32_t*)(a.qsplit + f8_align((size_t)B * Hq * F8_QROW));
+  a.part_lse = (float*)((char*)ws + f8_cu_bytes(Bv, G) + f8_q_bytes(B, Hq));
+  a.part_o = (uint16_t*)(a.part_lse + G * F8_SLOTS * Hq);
+  a.B = (int)Bv;
+  a.Hq = (int)Hq;
+  a.G = (int)G;
+  a.nsp = nsp;
   const int HG = (int)(Hq / f8_group_heads(Hq));
   const int nq = (int)((B * Hq + 3) / 4);
   if (q_bf16)
@@ -1639,9 +1682,57 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
     mla_fp8_decode<false><<<grid, 512, 0, st>>>(a);
   }
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
-  const dim3 cgrid((unsigned)((B * Hq + 3) / 4));
+  const dim3 cgrid((unsigned)((Bv * Hq + 3) / 4));
   if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
   else mla_fp8_combine<false><<<cgrid, 256, 0, st>>>(a);
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 combine)");
   return TLM_OK;
+}
+
+}  // namespace
+
+// Returns TLM_EUNSUPPORTED (launching nothing) when the shape is outside this kernel's domain.
+int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
+                       const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
+                       int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
+                       void* o, void* ws, int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                       int num_split, float score_scale, const float* kv_scale, bool q_bf16,
+                       bool o_bf16, void* stream) {
+  if (!tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride))
+    return TLM_EUNSUPPORTED;
+  F8Args a = f8_args(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
+                     block_table, seqlens, page, max_pages, score_scale, kv_scale);
+  a.out = (uint16_t*)o;
+  // num_split sets the ranges (B * num_split workgroups over all head groups), not a partition
+  return f8_run(a, ws, B, Hq, 1, f8_ranges(B, Hq, num_split), q_bf16, o_bf16,
+                (hipStream_t)stream);
+}
+
+// The split programs' partition (num_split segments per sequence, example_mla_decode_paged.py:
+// 140-144 with block_N = 64) on the 128-head decode, balanced over f8_ranges(B, Hq, par) ranges:
+// each segment's normalised rows (bf16, times kv_scale) go to *seg_o and its log2 sum-exp to
+// *seg_lse, rows (b num_split + s) Hq + head, both inside the workspace. Returns
+// TLM_EUNSUPPORTED (launching nothing) outside this path's domain.
+int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_stride,
+                                int64_t q_pe_stride, const void* kv, const void* k_pe,
+                                int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
+                                const int32_t* block_table, const int32_t* seqlens, void* ws,
+                                int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
+                                int num_split, int par, float score_scale,
+                                const float* kv_scale, bool q_bf16, void* stream,
+                                const uint16_t** seg_o, const float** seg_lse) {
+  if (!tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride) || Hq % W_HEADS ||
+      num_split < 1 || B * num_split > INT32_MAX / 2)
+    return TLM_EUNSUPPORTED;
+  F8Args a = f8_args(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows,
+                     block_table, seqlens, page, max_pages, score_scale, kv_scale);
+  const int64_t Bv = B * num_split;
+  const int64_t G = f8_ranges(B, Hq, par);
+  char* tail = (char*)ws + f8_cu_bytes(Bv, G) + f8_q_bytes(B, Hq) +
+               G * F8_SLOTS * (size_t)Hq * (F8_DV * sizeof(uint16_t) + sizeof(float));
+  a.out = (uint16_t*)tail;
+  a.seg_lse = (float*)(tail + f8_align((size_t)Bv * Hq * F8_DV * sizeof(uint16_t)));
+  *seg_o = a.out;
+  *seg_lse = a.seg_lse;
+  return f8_run(a, ws, B, Hq, num_split, G, q_bf16, true, (hipStream_t)stream);
 }
