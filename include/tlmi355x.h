@@ -310,8 +310,8 @@ int tlm_elementwise(const void* const* in, const int* in_dtype, const int* in_bc
  *   per-(sequence, head) kernel that needs no workspace.
  * A non-paged cache [B, S, 1, d] (examples/deepseek_mla/example_mla_decode.py) is the paged
  *   layout with page = S, max_pages = 1 and block_table[b, 0] = b.
- * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned; the larger of
- *   the two paths' layouts). */
+ * ws must hold tlm_mla_workspace_bytes(...) bytes (device memory, caller-owned; the largest of
+ *   the paths' layouts, the split programs' fp8 path of tlm_mla_decode_ex included). */
 int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
                    const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
                    int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens, void* o,
@@ -332,8 +332,11 @@ int tlm_mla_decode(const void* q, const void* q_pe, int64_t q_stride, int64_t q_
  *   sum-exp of the scaled scores (exp2 domain), both rounded to p_dtype; o is the combine of the
  *   stored values. A split without tokens stores -inf and zeros (the reference divides 0 by 0
  *   there). dv must be a multiple of 4. With glse and o_partial both NULL this is
- *   tlm_mla_decode. The partials path runs the program's partition on the split kernels (not the
- *   balanced fp8 path); ws as for tlm_mla_decode. Other arguments as tlm_mla_decode. */
+ *   tlm_mla_decode. With fp8 KV, part_block 64, Hq a multiple of 128, dv 512 / dpe 64 and a
+ *   workspace of tlm_mla_workspace_bytes(...) the program's splits run as segments of their
+ *   sequences on the balanced 128-head fp8 decode (glse then sums the e4m3-rounded P that
+ *   weighs the split's output: within ~0.1 of the exact log2 sum-exp); other requests run the
+ *   program's partition on the split kernels. Other arguments as tlm_mla_decode. */
 int tlm_mla_decode_ex(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_stride,
                       const void* kv, const void* k_pe, int64_t kv_stride, int64_t kpe_stride,
                       int64_t kv_rows, const int32_t* block_table, const int32_t* seqlens,
