@@ -736,6 +736,46 @@ def bench_mla(args, dev, flush, cpu):
     return res
 
 
+def bench_mla_program(args, dev, flush, cpu):
+    """The reference's split MLA program (example_mla_decode_paged.py with num_split 4, fp8 KV,
+    bf16 Q / Output, fp32 glse / Output_partial as it declares them) through tilelang.compile
+    at the MLA config: the drop-in path, partials written. Priced against HBM with the
+    partials it writes counted in its bytes."""
+    import tilelang
+    from tilelang.testing import programs, workloads
+    w = workloads.mla()
+    a = w.attrs
+    B, Hq, dv, dpe, page, mp = a["B"], a["Hq"], a["dv"], a["dpe"], a["page"], a["max_pages"]
+    ns = 4
+    k = tilelang.compile(programs.mla_decode(B, Hq, 1, mp * page, dv, dpe, 64, 64, ns, page,
+                                             dtype="bfloat16", kv_dtype="float8_e4m3",
+                                             out_dtype="bfloat16"), out_idx=[8])
+    sum_l = int(w.tensors["seqlens"].sum())
+    nbytes = sum_l * (dv + dpe) + B * Hq * (dv + dpe) * 2 + B * Hq * dv * 2 + \
+        w.tensors["block_table"].numel() * 4 + B * 4 + B * Hq * ns * (dv + 1) * 4
+    sets = []
+    for _ in range(_copies_for(nbytes)):
+        T = w.tensors
+        pool = T["kv"].view(B * mp * page, 1, dv + dpe)
+        sets.append((T["q"][..., :dv].contiguous().to(dev), T["q"][..., dv:].contiguous().to(dev),
+                     pool[..., :dv].contiguous().to(dev), pool[..., dv:].contiguous().to(dev),
+                     T["block_table"].to(dev), T["seqlens"].to(dev),
+                     torch.empty(B, Hq, ns, device=dev), torch.empty(B, Hq, ns, dv, device=dev),
+                     torch.empty(B, Hq, dv, dtype=torch.bfloat16, device=dev),
+                     T["kv_scale"].to(dev)))
+    fns = [lambda s=s: k(*s) for s in sets]
+    pmc_launches(args, fns, "mla_program")
+    ms, how = time_steps(fns, args.steps, args.warmup)
+    mean_ms, med_ms = time_launches(fns, 50, flush)
+    return {"workload": "mla_split_program_fp8_b64_h128_d576_split4", "value":
+            nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
+            "dtype": "fp8e4m3 (kv; q as two e4m3 terms, p as one)",
+            "roofline": roofline("hbm", nbytes / (mean_ms * 1e-3) / 1e9, "GB/s", HBM_PEAK_GBS),
+            "kernel_ms_mean": mean_ms, "kernel_ms_flushed_median": med_ms, "timing": how,
+            "algorithmic_bytes": nbytes, "path": "tilelang.compile (TPU convention, all "
+            "parameters on the device)"}
+
+
 def bench_copy(args, dev, flush, cpu):
     """Calibration kernel for the HBM counters: a 1 GiB device-to-device copy (torch's copy
     kernel) reads 1 GiB and writes 1 GiB."""
@@ -853,11 +893,12 @@ BENCHES = {
     "flashattn_bhsd": bench_flashattn_bhsd,
     "gemm_fp8": bench_gemm_fp8,
     "mla": bench_mla,
+    "mla_program": bench_mla_program,
     "kv_append": bench_kv_append,
 }
 ORDER = ["gemm", "gemm_skinny", "rmsnorm", "rope", "swiglu", "flashattn", "flashattn_s2048",
          "flashattn_gqa", "flashattn_varlen", "flashattn_bhsd", "flashattn_inference", "gemm_fp8",
-         "mla", "kv_append"]
+         "mla", "mla_program", "kv_append"]
 
 
 def main():
