@@ -144,6 +144,31 @@ TLM_DEV u32x4 ld_cp(const void* base, int off) {
                                                                            0, CP));
 }
 
+// Stores of a split program's partials (glse / Output_partial) in its dtype, PK: 0 fp16, 1 bf16,
+// 2 fp32 (stored unrounded). round() and put4() return the values as a later read gives them back.
+template <int PK>
+struct part_store {
+  static TLM_DEV float round(float x) {
+    if constexpr (PK == 2) return x;
+    else return h16<PK == 1>::to_f32(h16<PK == 1>::from_f32(x));
+  }
+  static TLM_DEV void put_lse(void* g, int64_t i, float x) {
+    if constexpr (PK == 2) ((float*)g)[i] = x;
+    else ((uint16_t*)g)[i] = (uint16_t)h16<PK == 1>::from_f32(x);
+  }
+  static TLM_DEV f32x4 put4(void* p, int64_t i, f32x4 v) {
+    if constexpr (PK == 2) {
+      *(f32x4*)((float*)p + i) = v;
+      return v;
+    } else {
+      using H = h16<PK == 1>;
+      const u32x2 pk = {H::pack(v[0], v[1]), H::pack(v[2], v[3])};
+      *(u32x2*)((uint16_t*)p + i) = pk;
+      return f32x4{H::lo(pk[0]), H::hi(pk[0]), H::lo(pk[1]), H::hi(pk[1])};
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------------------------
 // Host-side error plumbing (defined in tlm_capi.hip).
 void tlm_set_error(const char* fmt, ...);

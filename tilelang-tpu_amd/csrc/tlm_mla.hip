@@ -314,30 +314,8 @@ __global__ __launch_bounds__(128) void mla_combine_kernel(const float* __restric
 // reads them back: O = sum_s O_s 2^(lse_s - lse), lse = log2 sum_s 2^(lse_s - max) + max. A split
 // without tokens stores lse -inf and zeros (the reference divides 0 by 0 there). One workgroup
 // per (sequence, head), 4 dims per thread.
-// PK: storage of the partials, 0 fp16, 1 bf16, 2 fp32 (stored unrounded).
-template <int PK>
-struct part_store {
-  static TLM_DEV float round(float x) {
-    if constexpr (PK == 2) return x;
-    else return h16<PK == 1>::to_f32(h16<PK == 1>::from_f32(x));
-  }
-  static TLM_DEV void put_lse(void* g, int64_t i, float x) {
-    if constexpr (PK == 2) ((float*)g)[i] = x;
-    else ((uint16_t*)g)[i] = (uint16_t)h16<PK == 1>::from_f32(x);
-  }
-  // stores four values and returns them as read back
-  static TLM_DEV f32x4 put4(void* p, int64_t i, f32x4 v) {
-    if constexpr (PK == 2) {
-      *(f32x4*)((float*)p + i) = v;
-      return v;
-    } else {
-      using H = h16<PK == 1>;
-      const u32x2 pk = {H::pack(v[0], v[1]), H::pack(v[2], v[3])};
-      *(u32x2*)((uint16_t*)p + i) = pk;
-      return f32x4{H::lo(pk[0]), H::hi(pk[0]), H::lo(pk[1]), H::hi(pk[1])};
-    }
-  }
-};
+// PK: storage of the partials, 0 fp16, 1 bf16, 2 fp32 (stored unrounded; part_store in
+// tlm_common.h).
 
 template <int PK, bool OUT_BF16>
 __global__ __launch_bounds__(256) void mla_partial_combine(
@@ -372,45 +350,6 @@ __global__ __launch_bounds__(256) void mla_partial_combine(
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   *(u32x2*)(out + bh * dv + d) = u32x2{HO::pack(acc[0] * inv, acc[1] * inv),
                                        HO::pack(acc[2] * inv, acc[3] * inv)};
-}
-
-// The same combine over the fp8 decode's segments (tlm_mla_fp8_launch_segments): split s of
-// sequence b, head h is row (b ns + s) Hq + h of seg_o (bf16, normalised, times kv_scale) and
-// seg_lse (fp32, -inf for a split without tokens).
-template <int PK, bool OUT_BF16>
-__global__ __launch_bounds__(128) void mla_segment_combine(
-    const uint16_t* __restrict__ seg_o, const float* __restrict__ seg_lse, void* __restrict__ glse,
-    void* __restrict__ opart, uint16_t* __restrict__ out, int num_split, int Hq) {
-  using PS = part_store<PK>;
-  using HO = h16<OUT_BF16>;
-  using HB = h16<true>;
-  const int64_t bh = blockIdx.x;
-  const int64_t b = bh / Hq, h = bh % Hq;
-  const int d = threadIdx.x * 4;
-  float M = -INFINITY, L = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < num_split; ++s) {
-    const int64_t srow = (b * num_split + s) * Hq + h;
-    const float l0 = seg_lse[srow];
-    if (threadIdx.x == 0) PS::put_lse(glse, bh * num_split + s, l0);
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (l0 != -INFINITY) {
-      const u32x2 x = *(const u32x2*)(seg_o + srow * MLA_DV + d);
-      v = f32x4{HB::lo(x[0]), HB::hi(x[0]), HB::lo(x[1]), HB::hi(x[1])};
-    }
-    const f32x4 vr = PS::put4(opart, (bh * num_split + s) * MLA_DV + d, v);
-    const float lr = PS::round(l0);  // the stored values, as read back
-    if (lr != -INFINITY) {
-      const float Mn = fmaxf(M, lr);
-      const float a = fast_exp2(M - Mn), w = fast_exp2(lr - Mn);  // a = 0 while M = -inf
-      L = L * a + w;
-      acc = acc * a + vr * w;
-      M = Mn;
-    }
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-  *(u32x2*)(out + bh * MLA_DV + d) = u32x2{HO::pack(acc[0] * inv, acc[1] * inv),
-                                           HO::pack(acc[2] * inv, acc[3] * inv)};
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -597,8 +536,8 @@ int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_strid
                                 const int32_t* block_table, const int32_t* seqlens, void* ws,
                                 int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
                                 int num_split, int par, float score_scale,
-                                const float* kv_scale, bool q_bf16, void* stream,
-                                const uint16_t** seg_o, const float** seg_lse);
+                                const float* kv_scale, bool q_bf16, void* glse, void* o_partial,
+                                int p_dtype, void* o, bool o_bf16, void* stream);
 
 // Ranges of the split programs' fp8 path: the program's splits, or more when that leaves CUs
 // idle (about 256 workgroups over all head groups)
@@ -709,29 +648,10 @@ static int mla_run(const char* fn, const void* q, const void* q_pe, int64_t q_st
                                                        mla_seg_par(B, num_split))) {
     // the program's partition (64-token blocks) on the balanced 128-head fp8 decode: each split
     // is a segment of its sequence, then the partials and Output as above
-    const uint16_t* seg_o = nullptr;
-    const float* seg_lse = nullptr;
-    int rc = tlm_mla_fp8_launch_segments(q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride,
-                                         kpe_stride, kv_rows, block_table, seqlens, ws, B, Hq,
-                                         page, max_pages, num_split, mla_seg_par(B, num_split),
-                                         sc, kv_scale, q_dtype == TLM_BF16, stream, &seg_o,
-                                         &seg_lse);
-    if (rc == TLM_OK) {
-      hipStream_t st = (hipStream_t)stream;
-      auto comb = [&](auto kern) {
-        kern<<<(unsigned)(B * Hq), MLA_DV / 4, 0, st>>>(seg_o, seg_lse, glse, opart,
-                                                        (uint16_t*)o, num_split, (int)Hq);
-      };
-      const bool ob = o_dtype == TLM_BF16;
-      if (p_dtype == TLM_F32)
-        ob ? comb(mla_segment_combine<2, true>) : comb(mla_segment_combine<2, false>);
-      else if (p_dtype == TLM_BF16)
-        ob ? comb(mla_segment_combine<1, true>) : comb(mla_segment_combine<1, false>);
-      else
-        ob ? comb(mla_segment_combine<0, true>) : comb(mla_segment_combine<0, false>);
-      TLM_LAUNCH_CHECK("tlm_mla_decode (segment combine)");
-      return TLM_OK;
-    }
+    const int rc = tlm_mla_fp8_launch_segments(
+        q, q_pe, q_stride, q_pe_stride, kv, k_pe, kv_stride, kpe_stride, kv_rows, block_table,
+        seqlens, ws, B, Hq, page, max_pages, num_split, mla_seg_par(B, num_split), sc, kv_scale,
+        q_dtype == TLM_BF16, glse, opart, p_dtype, o, o_dtype == TLM_BF16, stream);
     if (rc != TLM_EUNSUPPORTED) return rc;
   }
   if (partials) {

@@ -1482,29 +1482,19 @@ __global__ __launch_bounds__(256, 1) void mla_fp8_decode_w32(const F8Args a) {
   }
 }
 
-// Merge the partial slots of every sequence that spans more than one range; zero-length
-// sequences produce zeros. Thread = (sequence, head, 8 dims); a workgroup covers 4 heads.
-template <bool O_BF16>
-__global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
-  // the wave's (sequence, head) row is wave-uniform: its range bookkeeping runs on the scalar
-  // unit once per wave
-  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (row >= (int64_t)a.B * a.Hq) return;
-  const int b = (int)(row / a.Hq), head = (int)(row % a.Hq);
-  const int d0 = 8 * (threadIdx.x & 63);
-  using H = h16<O_BF16>;
-  uint16_t* o = a.out + row * F8_DV + d0;
-  // positions on the cost line (see the prep kernel): the sequence covers [v0, v1), its first
-  // tile at v0 + F8_PIECE_COST; range g starts at cost position floor(g V / G)
-  const int64_t V = ldc(a.vcu + a.B), v0 = ldc(a.vcu + b), v1 = ldc(a.vcu + b + 1);
-  if (v0 == v1) {
-    *(u32x4*)o = u32x4{0u, 0u, 0u, 0u};
-    if (a.seg_lse && d0 == 0) a.seg_lse[row] = -INFINITY;
-    return;
-  }
+// Online merge of the partial slots of sequence (or segment) v, head `head`, dims d0 .. d0 + 7:
+// 0 when v has no tiles, 1 when it lies inside one range (the decode kernel wrote its row), else
+// 2 with the running max m, the sum l of 2^(lse - m) and the weighted sum acc (unnormalised).
+// v and head are wave-uniform, so the range bookkeeping runs on the scalar unit.
+TLM_DEV int f8_merge(const F8Args& a, int v, int head, int d0, float& m, float& l,
+                     f32x4 (&acc)[2]) {
+  // positions on the cost line (see the prep kernel): v covers [v0, v1), its first tile at
+  // v0 + F8_PIECE_COST; range g starts at cost position floor(g V / G)
+  const int64_t V = ldc(a.vcu + a.B), v0 = ldc(a.vcu + v), v1 = ldc(a.vcu + v + 1);
+  if (v0 == v1) return 0;
   const int64_t G = a.G;
   const int64_t g0 = div_floor((v0 + F8_PIECE_COST + 1) * G - 1, V), g1 = div_floor(v1 * G - 1, V);
-  if (g0 == g1) return;  // whole sequence inside one range: written by the decode kernel
+  if (g0 == g1) return 1;
   // range starts floor(g V / G) stepped incrementally: floor(g V / G) + V / G, plus one when the
   // remainder (g V) mod G wraps
   const int64_t tq = div_floor(V, G), tr = V - tq * G;
@@ -1523,8 +1513,9 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
   // batch are all requested before any is used, so a call waits for about one memory latency
   // per batch (a sequence spans at most a few ranges at the usual split counts).
   constexpr int F8_CMB = 8;
-  float m = -INFINITY, l = 0.f;
-  f32x4 acc[2] = {};
+  m = -INFINITY;
+  l = 0.f;
+  acc[0] = acc[1] = f32x4{};
   for (int64_t gb = g0; gb <= g1; gb += F8_CMB) {
     float lv[F8_CMB];
     u32x4 pv[F8_CMB];
@@ -1561,13 +1552,86 @@ __global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
     }
     m = mb;
   }
+  return 2;
+}
+
+// Merge the partial slots of every sequence that spans more than one range; zero-length
+// sequences produce zeros. Thread = (sequence, head, 8 dims); a workgroup covers 4 heads.
+template <bool O_BF16>
+__global__ __launch_bounds__(256) void mla_fp8_combine(const F8Args a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.Hq) return;
+  const int b = (int)(row / a.Hq), head = (int)(row % a.Hq);
+  const int d0 = 8 * (threadIdx.x & 63);
+  using H = h16<O_BF16>;
+  float m, l;
+  f32x4 acc[2];
+  const int r = f8_merge(a, b, head, d0, m, l, acc);
+  if (r == 0) {
+    *(u32x4*)(a.out + row * F8_DV + d0) = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  if (r == 1) return;  // whole sequence inside one range: written by the decode kernel
   const float inv = 1.0f / l;
   acc[0] *= inv;
   acc[1] *= inv;
-  if (a.seg_lse && d0 == 0) a.seg_lse[row] = m + __log2f(l);
   st_cp<F8_CMB_STORE_CP>(a.out + row * F8_DV, 2 * d0,
                          u32x4{H::pack(acc[0][0], acc[0][1]), H::pack(acc[0][2], acc[0][3]),
                                H::pack(acc[1][0], acc[1][1]), H::pack(acc[1][2], acc[1][3])});
+}
+
+// The split programs' combine over segments (example_mla_decode_paged.py:186-221): wave =
+// (sequence b, head), thread = 8 dims. Split s is segment b ns + s: its row and lse come from
+// the decode kernel (inside one range), from the merge of its pieces, or are -inf and zeros (no
+// tokens). Each is stored to Output_partial [b, h, s, :] / glse [b, h, s] in the program's dtype
+// (PK as part_store), and Output is the merge of the stored values as read back.
+template <int PK, bool O_BF16>
+__global__ __launch_bounds__(256) void mla_fp8_segment_combine(const F8Args a, void* glse,
+                                                               void* opart, uint16_t* out,
+                                                               int ns) {
+  using PS = part_store<PK>;
+  using HO = h16<O_BF16>;
+  const int lane = threadIdx.x & 63;
+  const int64_t bh = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (bh >= (int64_t)(a.B / ns) * a.Hq) return;
+  const int b = (int)(bh / a.Hq), head = (int)(bh % a.Hq);
+  const int d0 = 8 * lane;
+  float M = -INFINITY, L = 0.f;
+  f32x4 tot[2] = {};
+  for (int sp = 0; sp < ns; ++sp) {
+    const int v = b * ns + sp;
+    float m, l, lse = -INFINITY;
+    f32x4 o[2] = {};
+    const int r = f8_merge(a, v, head, d0, m, l, o);
+    if (r == 1) {
+      const int64_t row = (int64_t)v * a.Hq + head;
+      lse = a.seg_lse[row];
+      const u32x4 x = *(const u32x4*)(a.out + row * F8_DV + d0);
+      o[0] = bf16x4_to_f32(u32x2{x[0], x[1]});
+      o[1] = bf16x4_to_f32(u32x2{x[2], x[3]});
+    } else if (r == 2) {
+      lse = m + __log2f(l);
+      const float inv = 1.0f / l;
+      o[0] *= inv;
+      o[1] *= inv;
+    }
+    if (lane == 0) PS::put_lse(glse, bh * ns + sp, lse);
+    const f32x4 s0 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0, o[0]);
+    const f32x4 s1 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0 + 4, o[1]);
+    const float lr = PS::round(lse);  // the stored values, as read back
+    if (lr != -INFINITY) {
+      const float Mn = fmaxf(M, lr);
+      const float c = __builtin_amdgcn_exp2f(M - Mn), w = __builtin_amdgcn_exp2f(lr - Mn);
+      L = L * c + w;
+      tot[0] = tot[0] * c + s0 * w;
+      tot[1] = tot[1] * c + s1 * w;
+      M = Mn;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  *(u32x4*)(out + bh * F8_DV + d0) =
+      u32x4{HO::pack(tot[0][0] * inv, tot[0][1] * inv), HO::pack(tot[0][2] * inv, tot[0][3] * inv),
+            HO::pack(tot[1][0] * inv, tot[1][1] * inv), HO::pack(tot[1][2] * inv, tot[1][3] * inv)};
 }
 
 size_t f8_align(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -1650,7 +1714,7 @@ F8Args f8_args(const void* q, const void* q_pe, int64_t q_stride, int64_t q_pe_s
 // ranges; the workspace starts with the prefixes and range starts, then the Q terms of the B
 // sequences and the partial slots of the G ranges.
 int f8_run(F8Args& a, void* ws, int64_t B, int64_t Hq, int nsp, int64_t G, bool q_bf16,
-           bool o_bf16, hipStream_t st) {
+           bool o_bf16, hipStream_t st, bool combine = true) {
   const int64_t Bv = B * nsp;
   a.cu = (int32_t*)ws;
   a.vcu = a.cu + (Bv + 1);
@@ -1682,6 +1746,7 @@ int f8_run(F8Args& a, void* ws, int64_t B, int64_t Hq, int nsp, int64_t G, bool 
     mla_fp8_decode<false><<<grid, 512, 0, st>>>(a);
   }
   TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 decode)");
+  if (!combine) return TLM_OK;
   const dim3 cgrid((unsigned)((Bv * Hq + 3) / 4));
   if (o_bf16) mla_fp8_combine<true><<<cgrid, 256, 0, st>>>(a);
   else mla_fp8_combine<false><<<cgrid, 256, 0, st>>>(a);
@@ -1709,18 +1774,17 @@ int tlm_mla_fp8_launch(const void* q, const void* q_pe, int64_t q_stride, int64_
 }
 
 // The split programs' partition (num_split segments per sequence, example_mla_decode_paged.py:
-// 140-144 with block_N = 64) on the 128-head decode, balanced over f8_ranges(B, Hq, par) ranges:
-// each segment's normalised rows (bf16, times kv_scale) go to *seg_o and its log2 sum-exp to
-// *seg_lse, rows (b num_split + s) Hq + head, both inside the workspace. Returns
-// TLM_EUNSUPPORTED (launching nothing) outside this path's domain.
+// 140-144 with block_N = 64) on the 128-head decode, balanced over f8_ranges(B, Hq, par) ranges,
+// then mla_fp8_segment_combine: glse / o_partial of p_dtype (TLM_F16 / TLM_BF16 / TLM_F32) and
+// Output o. Returns TLM_EUNSUPPORTED (launching nothing) outside this path's domain.
 int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_stride,
                                 int64_t q_pe_stride, const void* kv, const void* k_pe,
                                 int64_t kv_stride, int64_t kpe_stride, int64_t kv_rows,
                                 const int32_t* block_table, const int32_t* seqlens, void* ws,
                                 int64_t B, int64_t Hq, int64_t page, int64_t max_pages,
                                 int num_split, int par, float score_scale,
-                                const float* kv_scale, bool q_bf16, void* stream,
-                                const uint16_t** seg_o, const float** seg_lse) {
+                                const float* kv_scale, bool q_bf16, void* glse, void* o_partial,
+                                int p_dtype, void* o, bool o_bf16, void* stream) {
   if (!tlm_mla_fp8_applies(B, Hq, page, max_pages, kv_stride, kpe_stride) || Hq % W_HEADS ||
       num_split < 1 || B * num_split > INT32_MAX / 2)
     return TLM_EUNSUPPORTED;
@@ -1728,11 +1792,24 @@ int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_strid
                      block_table, seqlens, page, max_pages, score_scale, kv_scale);
   const int64_t Bv = B * num_split;
   const int64_t G = f8_ranges(B, Hq, par);
+  // segments inside one range leave their row (bf16) and lse here for the segment combine
   char* tail = (char*)ws + f8_cu_bytes(Bv, G) + f8_q_bytes(B, Hq) +
                G * F8_SLOTS * (size_t)Hq * (F8_DV * sizeof(uint16_t) + sizeof(float));
   a.out = (uint16_t*)tail;
   a.seg_lse = (float*)(tail + f8_align((size_t)Bv * Hq * F8_DV * sizeof(uint16_t)));
-  *seg_o = a.out;
-  *seg_lse = a.seg_lse;
-  return f8_run(a, ws, B, Hq, num_split, G, q_bf16, true, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = f8_run(a, ws, B, Hq, num_split, G, q_bf16, true, st, false);
+  if (rc) return rc;
+  const dim3 cgrid((unsigned)((B * Hq + 3) / 4));
+  auto comb = [&](auto kern) {
+    kern<<<cgrid, 256, 0, st>>>(a, glse, o_partial, (uint16_t*)o, num_split);
+  };
+  if (p_dtype == TLM_F32)
+    o_bf16 ? comb(mla_fp8_segment_combine<2, true>) : comb(mla_fp8_segment_combine<2, false>);
+  else if (p_dtype == TLM_BF16)
+    o_bf16 ? comb(mla_fp8_segment_combine<1, true>) : comb(mla_fp8_segment_combine<1, false>);
+  else
+    o_bf16 ? comb(mla_fp8_segment_combine<0, true>) : comb(mla_fp8_segment_combine<0, false>);
+  TLM_LAUNCH_CHECK("tlm_mla_decode (fp8 segment combine)");
+  return TLM_OK;
 }
