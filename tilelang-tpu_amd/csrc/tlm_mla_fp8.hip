@@ -1616,8 +1616,16 @@ __global__ __launch_bounds__(256) void mla_fp8_segment_combine(const F8Args a, v
       o[1] *= inv;
     }
     if (lane == 0) PS::put_lse(glse, bh * ns + sp, lse);
-    const f32x4 s0 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0, o[0]);
-    const f32x4 s1 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0 + 4, o[1]);
+    f32x4 s0, s1;
+    if constexpr (PK == 2) {  // fp32 partials: written once, stored non-temporally (~2.5%)
+      __builtin_nontemporal_store(o[0], (f32x4*)opart + ((bh * ns + sp) * F8_DV + d0) / 4);
+      __builtin_nontemporal_store(o[1], (f32x4*)opart + ((bh * ns + sp) * F8_DV + d0) / 4 + 1);
+      s0 = o[0];
+      s1 = o[1];
+    } else {
+      s0 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0, o[0]);
+      s1 = PS::put4(opart, (bh * ns + sp) * F8_DV + d0 + 4, o[1]);
+    }
     const float lr = PS::round(lse);  // the stored values, as read back
     if (lr != -INFINITY) {
       const float Mn = fmaxf(M, lr);
