@@ -107,8 +107,8 @@ int tlm_rope(const void* q, const void* k, const void* cos_t, const void* sin_t,
  * in_dtype: F16 | BF16; out_dtype: F16 | BF16 | F32. The fp32 program
  * (tpu_demo/matmul/tpu_test_matmul_fp32.py:9-31) copies its fp32 A/B tiles to fp16 before
  * ppl_gemm: tlm_cast to F16, then this with out_dtype F32.
- * M <= 16 with trans_b == 0 splits K over several workgroups whose partial tiles meet in a
- * library-owned device workspace (16 MB per GPU, 4 slots): each stream owns one slot, so calls
+ * M <= 16 with trans_b == 0 (and with trans_b == 1 when the output has few 64-column strips)
+ * splits K over several workgroups whose partial tiles meet in a library-owned device workspace (16 MB per GPU, 4 slots): each stream owns one slot, so calls
  * on one stream are ordered and calls that overlap use different slots; further streams take an
  * unsplit kernel. A HIP graph keeps the slot of the stream it was captured on, so its replays
  * must not overlap each other or other work of that stream. Slots are keyed by the stream handle:

@@ -96,6 +96,26 @@ def test_gemm_skinny_split_repeatable():
         assert torch.equal(c, c0)
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 14336), (5, 1000, 2056), (1, 64, 8192),
+                                   (16, 520, 4104)])
+def test_gemm_skinny_bt_split(M, N, K):
+    """M <= 16 with B^T and few 64-column strips splits K over several workgroups per strip
+    (one per CU in all); the partial tiles meet in split order: parity with the oracle, and
+    reruns (with other split calls in between) are bitwise equal."""
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.rand(M, K, generator=g) * 2 - 1).half()
+    b = (torch.rand(N, K, generator=g) * 2 - 1).half()
+    c0 = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    ops.gemm(a.to(DEV), b.to(DEV), c0, trans_b=True)
+    torch_assert_close(c0.cpu(), ref.matmul_ref(a, b.t().contiguous()), atol=1e-2, rtol=1e-2)
+    x = torch.randn(3, 1000, device=DEV).half()
+    ops.gemm(x, torch.randn(200, 1000, device=DEV).half(),
+             torch.empty(3, 200, dtype=torch.float16, device=DEV), trans_b=True)
+    c1 = torch.empty_like(c0)
+    ops.gemm(a.to(DEV), b.to(DEV), c1, trans_b=True)
+    assert torch.equal(c1, c0)
+
+
 def test_gemm_skinny_concurrent_streams():
     """Each stream owns one workspace slot of the split skinny kernel (4 per device); further
     streams take the unsplit kernel. Six streams run skinny GEMMs at the same time, twice over,

@@ -417,7 +417,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_256x256(const uint16_t* __re
 // into operand layout. The next block's loads are issued before the current block's MFMAs.
 // The 8 partial 16x64 tiles are summed through LDS at the end. B is read once per call, with
 // non-temporal loads: 3% faster back to back, and a single launch after a cache flush 27 against
-// 48 us at 16 x 14336 x 4096.
+// 48 us at 16 x 14336 x 4096. With nsplit > 1 (B^T with few strips) the workgroups of a strip
+// take 1/nsplit of K each and their tiles meet as in gemm_skinny_split (split order, last
+// arriver).
+constexpr int SS_WAVES = 8;
+constexpr int SS_NT = 128;
+constexpr int SS_BK = 16;
+constexpr int SS_AMAX_K = 2048;  // k range of one workgroup: its A is 64 KB of LDS
+constexpr int SS_MAX_SPLIT = 16;
+constexpr int SS_SLOTS = 4;
+constexpr int SS_MAX_WG = 512;   // workgroups of one call that publish a partial tile
+constexpr int SS_PART = 16 * SS_NT;
 constexpr int SK_WAVES = 8;
 constexpr int SK_NT = 64;
 constexpr int SK_BK = 32;
@@ -428,14 +438,20 @@ template <bool BF16, bool TRANS_B, int OUT>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __restrict__ A,
                                                             const uint16_t* __restrict__ B,
                                                             void* __restrict__ C, int M, int N,
-                                                            int K) {
+                                                            int K, int nsplit, float* part,
+                                                            unsigned* arrivals) {
   using MT = mfma16_t<BF16>;
   using v8 = typename MT::v8;
   __shared__ __attribute__((aligned(16))) uint16_t sbuf[SK_WAVES][SK_BK * SK_BPITCH];
   __shared__ float red[SK_WAVES][16][SK_NT + 1];
+  __shared__ unsigned last_arrival;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * SK_NT;
-  const int KB = (K + SK_BK - 1) / SK_BK;
+  const int nstrips = (N + SK_NT - 1) / SK_NT;
+  const int strip = blockIdx.x % nstrips, split = blockIdx.x / nstrips;
+  const int n0 = strip * SK_NT;
+  const int KBall = (K + SK_BK - 1) / SK_BK;
+  const int kb_lo = (int)((int64_t)split * KBall / nsplit);
+  const int KB = (int)((int64_t)(split + 1) * KBall / nsplit);  // this split's blocks end
   const int am = lane & 15, ak = 8 * (lane >> 4);
   // row-major B block loads: 32 rows x 64 cols = 4 vectors per lane (rows lane/8 + 8p)
   const int br = lane >> 3, bc = (lane & 7) * 8;
@@ -465,7 +481,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
   };
 
   uint16_t* my = sbuf[wave];
-  int kb = wave;
+  int kb = kb_lo + wave;
   if (kb < KB) load(kb);
   for (; kb < KB; kb += SK_WAVES) {
     const u32x4 ca = ra;
@@ -501,12 +517,53 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][16 * t + (lane & 15)] = acc[t][i];
   __syncthreads();
-  for (int o = threadIdx.x; o < 16 * SK_NT; o += 64 * SK_WAVES) {
-    const int r = o / SK_NT, c = o % SK_NT;
+  constexpr int PER = 16 * SK_NT / (64 * SK_WAVES);  // outputs per thread
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int o = threadIdx.x + i * 64 * SK_WAVES, r = o / SK_NT, c = o % SK_NT;
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < SK_WAVES; ++w) s += red[w][r][c];
-    if (r < M && n0 + c < N) store_out<OUT>(C, (int64_t)r * N + n0 + c, s);
+    v[i] = s;
+  }
+  if (nsplit > 1) {
+    // the strip's tiles meet in the workspace: sc0 sc1 stores (written through), a wait for
+    // them before the arrival, sc0 sc1 loads (missing every cache) after it; the sum runs in
+    // split order
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc(part, (short)0, 0x7fffffff, RSRC_WORD3);
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __builtin_bit_cast(uint32_t, v[i]), rp,
+          (int)((blockIdx.x * SS_PART + threadIdx.x + i * 64 * SK_WAVES) * 4), 0, CP_SC01);
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): the tile has been written
+    __syncthreads();
+    if (threadIdx.x == 0)
+      last_arrival = atomicAdd(&arrivals[strip], 1u) == (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!last_arrival) return;
+    float t[PER] = {};
+    for (int sp = 0; sp < nsplit; ++sp) {  // uniform
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        float x = v[i];
+        if (sp != split)
+          x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+              rp, (int)(((sp * nstrips + strip) * SS_PART + threadIdx.x + i * 64 * SK_WAVES) * 4),
+              0, CP_SC01));
+        t[i] += x;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = t[i];
+    if (threadIdx.x == 0) atomicExch(&arrivals[strip], 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int o = threadIdx.x + i * 64 * SK_WAVES, r = o / SK_NT, c = o % SK_NT;
+    if (r < M && n0 + c < N) store_out<OUT>(C, (int64_t)r * N + n0 + c, v[i]);
   }
 }
 
@@ -529,14 +586,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_skinny(const uint16_t* __r
 // each stream that runs this kernel on a device owns one slot, so calls that overlap are on
 // different streams and never share a slot. A further stream takes gemm_skinny. A HIP graph
 // keeps the slot of the stream it was captured on.
-constexpr int SS_WAVES = 8;
-constexpr int SS_NT = 128;
-constexpr int SS_BK = 16;
-constexpr int SS_AMAX_K = 2048;  // k range of one workgroup: its A is 64 KB of LDS
-constexpr int SS_MAX_SPLIT = 16;
-constexpr int SS_SLOTS = 4;
-constexpr int SS_MAX_WG = 512;   // workgroups of one call that publish a partial tile
-constexpr int SS_PART = 16 * SS_NT;
 
 template <bool BF16>
 struct mfma16k16_t;
@@ -797,6 +846,16 @@ int ss_nsplit(int N, int K) {
   return ns;
 }
 
+// Split count of gemm_skinny for B^T (1: no split): about one workgroup per CU when the 64-column
+// strips are fewer, at least 8 blocks (256 k) per workgroup.
+int sk_nsplit(int N, int K) {
+  const int nstrips = (N + SK_NT - 1) / SK_NT;
+  const int KB = (K + SK_BK - 1) / SK_BK;
+  int ns = std::max(1, std::min(SS_MAX_SPLIT, 256 / nstrips));
+  ns = std::min(ns, std::max(1, KB / 8));
+  return (int64_t)nstrips * ns > SS_MAX_WG ? 1 : ns;
+}
+
 template <bool BF16, bool TRANS_B, int OUT>
 int launch(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t s) {
   const bool vec = tlm_aligned(A, 16) && tlm_aligned(B, 16) && K % 8 == 0 &&
@@ -812,8 +871,11 @@ int launch(const void* A, const void* B, void* C, int M, int N, int K, hipStream
     gemm_skinny_split<BF16, OUT><<<(unsigned)(nstrips * ns), 64 * SS_WAVES, 0, s>>>(
         (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, ns, part, arrivals);
   } else if (vec && M <= 16) {
-    gemm_skinny<BF16, TRANS_B, OUT><<<(unsigned)((N + SK_NT - 1) / SK_NT), 64 * SK_WAVES, 0, s>>>(
-        (const uint16_t*)A, (const uint16_t*)B, C, M, N, K);
+    int nk = TRANS_B ? sk_nsplit(N, K) : 1;
+    if (nk > 1 && !ss_slot(s, &part, &arrivals)) nk = 1;
+    gemm_skinny<BF16, TRANS_B, OUT><<<(unsigned)((N + SK_NT - 1) / SK_NT * nk), 64 * SK_WAVES, 0,
+                                      s>>>((const uint16_t*)A, (const uint16_t*)B, C, M, N, K, nk,
+                                           part, arrivals);
   } else if (vec && (int64_t)BM * K * 2 < 0x7ffffff0 &&
              (TRANS_B ? (int64_t)BN * K * 2 : (int64_t)BK * N * 2) < 0x7ffffff0) {
     // the LDS-DMA offsets of a 256-row panel (or a 64-row k-tile of row-major B) are 32-bit
