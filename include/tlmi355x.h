@@ -346,7 +346,7 @@ int tlm_mla_decode_ex(const void* q, const void* q_pe, int64_t q_stride, int64_t
                       int o_dtype, void* glse, void* o_partial, int64_t part_block, int p_dtype,
                       void* stream);
 
-/* Workspace bytes that tlm_mla_decode needs for (B, Hq, dv, num_split). */
+/* Workspace bytes that tlm_mla_decode and tlm_mla_decode_ex need for (B, Hq, dv, num_split). */
 size_t tlm_mla_workspace_bytes(int64_t B, int64_t Hq, int64_t dv, int num_split);
 
 /* Bytes of the library-owned scratch of tlm_mla_decode_noalloc (per GPU). */
