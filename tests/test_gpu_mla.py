@@ -120,9 +120,10 @@ def test_split_program_partials_with_empty_splits():
     torch_assert_close(out, exp, atol=2e-2, rtol=2e-2)
 
 
-def test_fp8_program_through_compile():
+@pytest.mark.parametrize("ns", [4, 8])
+def test_fp8_program_through_compile(ns):
     B, Hq, max_pages, page = 4, 128, 8, 64
-    prog = programs.mla_decode(B, Hq, 1, max_pages * page, 512, 64, 64, 64, 4, page,
+    prog = programs.mla_decode(B, Hq, 1, max_pages * page, 512, 64, 64, 64, ns, page,
                                dtype="bfloat16", kv_dtype="float8_e4m3", out_dtype="bfloat16")
     k = tilelang.compile(prog, out_idx=[8])
     assert k.plan.attrs["kv_dtype"] == "float8_e4m3" and k.plan.attrs["kv_scale"] == 9
@@ -130,8 +131,8 @@ def test_fp8_program_through_compile():
                       seed=32)
     T = w.tensors
     pool = T["kv"].view(B * max_pages * page, 1, 576)
-    glse = torch.empty(B, Hq, 4, device=DEV)
-    opart = torch.empty(B, Hq, 4, 512, device=DEV)
+    glse = torch.empty(B, Hq, ns, device=DEV)
+    opart = torch.empty(B, Hq, ns, 512, device=DEV)
     out = k(T["q"][..., :512].contiguous().to(DEV), T["q"][..., 512:].contiguous().to(DEV),
             pool[..., :512].contiguous().to(DEV), pool[..., 512:].contiguous().to(DEV),
             T["block_table"].to(DEV), T["seqlens"].to(DEV), glse, opart,
@@ -145,7 +146,7 @@ def test_fp8_program_through_compile():
     # the program's fp32 partials: each split's output (times kv_scale) and log2 sum-exp
     _, (g_ref, p_ref) = ref.mla_split_combine_ref(
         T["q"][..., :512], T["q"][..., 512:], T["kv"][:, :512], T["kv"][:, 512:],
-        T["block_table"], T["seqlens"], page, 1 / math.sqrt(576), 4, block_n=64,
+        T["block_table"], T["seqlens"], page, 1 / math.sqrt(576), ns, block_n=64,
         kv_scale=float(T["kv_scale"]), store_dtype=torch.float32)
     _check_fp8_partials(glse.cpu(), opart.cpu(), g_ref, p_ref)
 

@@ -539,11 +539,13 @@ int tlm_mla_fp8_launch_segments(const void* q, const void* q_pe, int64_t q_strid
                                 const float* kv_scale, bool q_bf16, void* glse, void* o_partial,
                                 int p_dtype, void* o, bool o_bf16, void* stream);
 
-// Ranges of the split programs' fp8 path: the program's splits, or more when that leaves CUs
-// idle (about 256 workgroups over all head groups)
+// Ranges of the split programs' fp8 path, whatever the program's split count: about 256
+// workgroups over all head groups (f8_ranges(B, Hq, par) = B * par / head groups); the ranges
+// are balanced over the B * num_split segments, so one range may hold several of them
 static int mla_seg_par(int64_t B, int num_split) {
+  (void)num_split;
   const int64_t fill = (256 + std::max<int64_t>(B, 1) - 1) / std::max<int64_t>(B, 1);
-  return (int)std::max<int64_t>(num_split, std::min<int64_t>(64, fill));
+  return (int)std::min<int64_t>(64, fill);
 }
 
 // Workspace bytes of the two paths: the fp8 matrix-core path (fp8 KV, page a multiple of 64, Hq
