@@ -299,3 +299,43 @@ def test_out_of_pool_rows_read_as_zero():
     ops.paged_gather(kvb, bt.to(DEV), T["seqlens"].to(DEV), cu.to(DEV), out, 64)
     assert int(out[64:].sum()) == 0
     assert torch.equal(out[:64].cpu(), T["kv"].view(torch.uint8)[int(bt[0, 0]) * 64:][:64])
+
+
+def _split_program_cases(n, seed):
+    import random
+    r = random.Random(seed)
+    return [(r.randint(1, 6), r.choice([128, 256]), r.choice([2, 3, 5, 8]), r.choice([64, 128]),
+             r.choice([4, 8]), 200 + i) for i in range(n)]
+
+
+@pytest.mark.parametrize("B,Hq,ns,page,mp,seed", _split_program_cases(6, seed=909))
+def test_fp8_split_program_random(B, Hq, ns, page, mp, seed):
+    """The split program on the segment path over random batches (lengths 0 .. the table's
+    reach, several splits empty): partials and Output against the oracle."""
+    print(f"split program B={B} Hq={Hq} ns={ns} page={page} pages={mp} seed={seed}", flush=True)
+    w = workloads.mla(B=B, Hq=Hq, max_pages=mp, page=page, min_len=0, max_len=mp * page,
+                      seed=seed)
+    T = w.tensors
+    prog = programs.mla_decode(B, Hq, 1, mp * page, 512, 64, 64, 64, ns, page,
+                               dtype="bfloat16", kv_dtype="float8_e4m3", out_dtype="bfloat16")
+    k = tilelang.compile(prog, out_idx=[8])
+    pool = T["kv"].view(B * mp * page, 1, 576)
+    glse = torch.full((B, Hq, ns), float("nan"), device=DEV)
+    opart = torch.full((B, Hq, ns, 512), float("nan"), device=DEV)
+    out = k(T["q"][..., :512].contiguous().to(DEV), T["q"][..., 512:].contiguous().to(DEV),
+            pool[..., :512].contiguous().to(DEV), pool[..., 512:].contiguous().to(DEV),
+            T["block_table"].to(DEV), T["seqlens"].to(DEV), glse, opart,
+            T["kv_scale"].to(DEV)).cpu()
+    sc = 1 / math.sqrt(576)
+    _, (g_ref, p_ref) = ref.mla_split_combine_ref(
+        T["q"][..., :512], T["q"][..., 512:], T["kv"][:, :512], T["kv"][:, 512:],
+        T["block_table"], T["seqlens"], page, sc, ns, block_n=64,
+        kv_scale=float(T["kv_scale"]), store_dtype=torch.float32)
+    _check_fp8_partials(glse.cpu(), opart.cpu(), g_ref, p_ref)
+    exp = ref.mla_decode_ref(T["q"][..., :512], T["q"][..., 512:], T["kv"][:, :512],
+                             T["kv"][:, 512:], T["block_table"], T["seqlens"], page, sc,
+                             float(T["kv_scale"]))
+    live = T["seqlens"] > 0
+    assert torch.equal(out[~live].float(), torch.zeros_like(out[~live].float()))
+    if live.any():
+        assert _rel_rms(out[live], exp[live]) < FP8_REL_RMS
